@@ -1,0 +1,108 @@
+/*
+ * CPU oracle for the Qwen3 attention hot path (TEST INFRASTRUCTURE ONLY).
+ *
+ * This library is the checker: only tests, the smoke entry and the bench's
+ * CPU-baseline leg may load it. The product path (engine-mlx_amd/) never calls
+ * it and never falls back to it.
+ *
+ * It restates, in plain C, the semantics of the MLX primitives the reference
+ * calls on this path (reference: dangranaz/engine-mlx 0.1.18):
+ *   - mlx_fast_rms_norm           crates/mlx-ffi/src/ops/real/blas.rs:5-9
+ *   - mlx_fast_rope(_dynamic)     crates/mlx-ffi/src/ops/real/blas.rs:67-80
+ *       (traditional=false, base=theta, scale=1.0, dims=head_dim)
+ *   - static KV write             crates/serve/src/compiled.rs:157-161 (scatter_single)
+ *                                 crates/serve/src/forward_qwen3.rs:124-142 (slice_update)
+ *   - masked / causal SDPA        crates/mlx-ffi/src/ops/real/transform.rs:8-29 ("array" mask)
+ *                                 crates/mlx-ffi/src/ops/real/blas.rs:82-101 ("causal")
+ *   - op order norm -> transpose -> rope -> write -> sdpa
+ *                                 crates/serve/src/forward_qwen3.rs:52-152
+ *
+ * bf16 tensors are passed as uint16_t bit patterns (IEEE bfloat16, RNE).
+ *
+ * Layouts (all contiguous, row-major):
+ *   qkv    [B, T, (Hq + 2*Hkv) * D]   fused projection output, order q | k | v
+ *   q      [B, Hq, Tq, D]             attention-ordered queries
+ *   cache  [B, Hkv, cap, D]           static K (and V) cache
+ *   out    [B, Tq, Hq * D]            attention output, o_proj input layout
+ *
+ * Parity pins: see the header comment of each function (tests/test_oracle.py
+ * holds the checks).
+ */
+#ifndef EMA_ORACLE_H
+#define EMA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORA_FLAG_NO_NORM 1u /* q_norm/k_norm are None (optional_qk_norm no-op) */
+#define ORA_FLAG_NO_ROPE 2u /* NoPE layer (apply_rope with use_rope=false)     */
+
+/* bf16 <-> f32 (RNE, NaN kept quiet). */
+uint16_t ora_f32_to_bf16(float f);
+float ora_bf16_to_f32(uint16_t h);
+void ora_f32_to_bf16_array(const float* in, uint16_t* out, size_t n);
+void ora_bf16_to_f32_array(const uint16_t* in, float* out, size_t n);
+
+/* Counter-based N(mean, std) generator (splitmix64 -> Box-Muller), rounded
+ * to bf16. Element i depends only on (seed, i). */
+void ora_fill_normal_bf16(uint16_t* out, size_t n, uint64_t seed, float mean, float std);
+void ora_fill_normal_f32(float* out, size_t n, uint64_t seed, float mean, float std);
+
+/* RMSNorm over the last axis, MLX fast::rms_norm semantics:
+ *   y = bf16( w * bf16( x * rsqrt(mean(x^2) + eps) ) ), statistics in f64. */
+void ora_rms_norm(const uint16_t* x, const uint16_t* w, int64_t rows, int D, float eps,
+                  uint16_t* out);
+
+/* Non-traditional (split-half) RoPE on rows of length D, MLX fast::rope
+ * semantics with dims=D, scale=1: pair (x[i], x[i+D/2]) rotated by
+ * angle = pos * theta^(-2i/D), inv-frequency and angle formed in f32.
+ * x is [rows, D]; pos[r] is the absolute position of row r. */
+void ora_rope(const uint16_t* x, const int32_t* pos, int64_t rows, int D, float theta,
+              uint16_t* out);
+
+/* Fused pre-attention step for B sequences of T new tokens:
+ *   q,k <- rms_norm (unless NO_NORM), q,k <- rope at off[b]+t (unless NO_ROPE),
+ *   q_out[b,h,t,:] = q ; kcache[b,h,off[b]+t,:] = k ; vcache[...] = v.
+ * Rows of the caches outside [off[b], off[b]+T) are left untouched.
+ * Returns 0, or -1 if some off[b] < 0 or off[b] + T > cap. */
+int ora_pre_attention(const uint16_t* qkv, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                      float eps, float theta, const int32_t* off, int B, int T, int Hq, int Hkv,
+                      int D, uint32_t flags, uint16_t* q_out, uint16_t* kcache, uint16_t* vcache,
+                      int cap);
+
+/* Scaled dot-product attention over the static cache, GQA mapping
+ * q-head h -> kv-head h / (Hq/Hkv).
+ * For batch b, keys live in [kv_begin[b], kv_len[b]) (kv_begin may be NULL = 0).
+ * causal != 0: query row i may see key j only if j <= kv_len[b] - Tq + i
+ *              (query block aligned to the end of the key range, MLX "causal").
+ * causal == 0: every key in range is visible (the decode mask of
+ *              crates/serve/src/engine_ext.rs:237-260 reduces to this with
+ *              kv_len = offset + 1).
+ * A query row with no visible key yields zeros.
+ * precision 0: f64 scores/softmax/PV (the accurate oracle).
+ * precision 1: f32 scores/softmax/PV (MLX CPU-stream arithmetic), OpenMP over
+ *              (b, head, row); used as the timed CPU baseline. */
+void ora_sdpa(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache,
+              const int32_t* kv_len, const int32_t* kv_begin, int B, int Hq, int Hkv, int Tq,
+              int D, int cap, float scale, int causal, int precision, uint16_t* out);
+
+/* Split-K building blocks (flash-decoding). For one query vector q[D] and
+ * keys rows [0, n) of K/V (row stride D): m = max_j s_j, l = sum_j exp(s_j - m),
+ * acc = sum_j exp(s_j - m) v_j with s_j = scale * q.k_j, all in f64. */
+void ora_sdpa_partial(const uint16_t* q, const uint16_t* k, const uint16_t* v, int n, int D,
+                      float scale, double* m, double* l, double* acc);
+/* Merge P partials by log-sum-exp; writes out[D] = (sum_p e^{m_p-M} acc_p) / (sum_p e^{m_p-M} l_p). */
+void ora_lse_merge(const double* m, const double* l, const double* acc, int P, int D,
+                   double* out);
+
+/* Number of OpenMP threads ora_sdpa(precision=1) uses. */
+int ora_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,197 @@
+"""numpy front end of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
+``bench.py`` import this module; it is the checker, never the product.
+bf16 tensors are numpy ``uint16`` arrays holding IEEE bfloat16 bit patterns.
+The C functions behind each wrapper cite the reference files they restate
+(``oracle/ema_oracle.h``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+FLAG_NO_NORM = 1
+FLAG_NO_ROPE = 2
+
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+
+
+def build() -> None:
+    """Compile liboracle.so with the recipe in oracle/Makefile."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library not built: {_LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(_LIB_PATH)
+        L.ora_f32_to_bf16.restype = ctypes.c_uint16
+        L.ora_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.ora_bf16_to_f32.restype = ctypes.c_float
+        L.ora_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.ora_f32_to_bf16_array.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+        L.ora_bf16_to_f32_array.argtypes = [_u16p, _f32p, ctypes.c_size_t]
+        L.ora_fill_normal_bf16.argtypes = [_u16p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
+        L.ora_fill_normal_f32.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
+        L.ora_rms_norm.argtypes = [_u16p, _u16p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _u16p]
+        L.ora_rope.argtypes = [_u16p, _i32p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _u16p]
+        L.ora_pre_attention.restype = ctypes.c_int
+        L.ora_pre_attention.argtypes = [
+            _u16p, _u16p, _u16p, ctypes.c_float, ctypes.c_float, _i32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint32,
+            _u16p, _u16p, _u16p, ctypes.c_int,
+        ]
+        L.ora_sdpa.argtypes = [
+            _u16p, _u16p, _u16p, _i32p, _i32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_float, ctypes.c_int, ctypes.c_int, _u16p,
+        ]
+        L.ora_sdpa_partial.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f64p, _f64p, _f64p]
+        L.ora_lse_merge.argtypes = [_f64p, _f64p, _f64p, ctypes.c_int, ctypes.c_int, _f64p]
+        L.ora_num_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, t):
+    return a.ctypes.data_as(t)
+
+
+def _c(a: np.ndarray, dtype) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    if a.dtype != dtype:
+        raise TypeError(f"expected {dtype}, got {a.dtype}")
+    return a
+
+
+# ------------------------------------------------------------------ bf16
+def bf16_from_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().ora_f32_to_bf16_array(_p(x, _f32p), _p(out, _u16p), x.size)
+    return out
+
+
+def f32_from_bf16(h) -> np.ndarray:
+    h = _c(np.asarray(h), np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().ora_bf16_to_f32_array(_p(h, _u16p), _p(out, _f32p), h.size)
+    return out
+
+
+def normal_bf16(shape, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.uint16)
+    lib().ora_fill_normal_bf16(_p(out, _u16p), out.size, seed & 0xFFFFFFFFFFFFFFFF, mean, std)
+    return out
+
+
+def normal_f32(shape, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    lib().ora_fill_normal_f32(_p(out, _f32p), out.size, seed & 0xFFFFFFFFFFFFFFFF, mean, std)
+    return out
+
+
+# ------------------------------------------------------------------ ops
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = _c(x, np.uint16)
+    w = _c(w, np.uint16)
+    D = x.shape[-1]
+    out = np.empty_like(x)
+    lib().ora_rms_norm(_p(x, _u16p), _p(w, _u16p), x.size // D, D, eps, _p(out, _u16p))
+    return out
+
+
+def rope(x: np.ndarray, pos: np.ndarray, theta: float) -> np.ndarray:
+    """x: [rows, D] bf16; pos: [rows] int32 absolute positions."""
+    x = _c(x, np.uint16)
+    D = x.shape[-1]
+    rows = x.size // D
+    pos = _c(np.asarray(pos, dtype=np.int32).reshape(rows), np.int32)
+    out = np.empty_like(x)
+    lib().ora_rope(_p(x, _u16p), _p(pos, _i32p), rows, D, theta, _p(out, _u16p))
+    return out
+
+
+def pre_attention(qkv, q_norm_w, k_norm_w, eps, theta, off, Hq, Hkv, kcache, vcache, flags=0):
+    """qkv [B,T,(Hq+2Hkv)*D] bf16; caches [B,Hkv,cap,D] bf16 updated in place.
+
+    Returns q_out [B,Hq,T,D]. Raises ValueError when off+T exceeds the capacity.
+    """
+    qkv = _c(qkv, np.uint16)
+    B, T, F = qkv.shape
+    D = F // (Hq + 2 * Hkv)
+    cap = kcache.shape[2]
+    off = _c(np.asarray(off, dtype=np.int32).reshape(B), np.int32)
+    qw = _c(q_norm_w if q_norm_w is not None else np.zeros(D, np.uint16), np.uint16)
+    kw = _c(k_norm_w if k_norm_w is not None else np.zeros(D, np.uint16), np.uint16)
+    assert kcache.flags.c_contiguous and vcache.flags.c_contiguous
+    q_out = np.empty((B, Hq, T, D), dtype=np.uint16)
+    rc = lib().ora_pre_attention(
+        _p(qkv, _u16p), _p(qw, _u16p), _p(kw, _u16p), eps, theta, _p(off, _i32p),
+        B, T, Hq, Hkv, D, flags, _p(q_out, _u16p), _p(kcache, _u16p), _p(vcache, _u16p), cap,
+    )
+    if rc != 0:
+        raise ValueError("static KV overflow")
+    return q_out
+
+
+def sdpa(q, kcache, vcache, kv_len, scale, causal, kv_begin=None, precision=0) -> np.ndarray:
+    """q [B,Hq,Tq,D]; caches [B,Hkv,cap,D]; kv_len [B]. Returns out [B,Tq,Hq*D] bf16."""
+    q = _c(q, np.uint16)
+    kcache = _c(kcache, np.uint16)
+    vcache = _c(vcache, np.uint16)
+    B, Hq, Tq, D = q.shape
+    Hkv, cap = kcache.shape[1], kcache.shape[2]
+    kv_len = _c(np.asarray(kv_len, dtype=np.int32).reshape(B), np.int32)
+    kb = None
+    if kv_begin is not None:
+        kb = _c(np.asarray(kv_begin, dtype=np.int32).reshape(B), np.int32)
+    out = np.empty((B, Tq, Hq * D), dtype=np.uint16)
+    lib().ora_sdpa(
+        _p(q, _u16p), _p(kcache, _u16p), _p(vcache, _u16p), _p(kv_len, _i32p),
+        _p(kb, _i32p) if kb is not None else None,
+        B, Hq, Hkv, Tq, D, cap, scale, int(bool(causal)), precision, _p(out, _u16p),
+    )
+    return out
+
+
+def sdpa_partial(q, k, v, scale):
+    """One query q[D] against key/value rows k,v [n,D]: returns (m, l, acc[D]) in f64."""
+    q = _c(q, np.uint16)
+    k = _c(k, np.uint16)
+    v = _c(v, np.uint16)
+    n, D = k.shape
+    m = ctypes.c_double()
+    l = ctypes.c_double()
+    acc = np.empty(D, dtype=np.float64)
+    lib().ora_sdpa_partial(_p(q, _u16p), _p(k, _u16p), _p(v, _u16p), n, D, scale,
+                           ctypes.byref(m), ctypes.byref(l), _p(acc, _f64p))
+    return m.value, l.value, acc
+
+
+def lse_merge(ms, ls, accs) -> np.ndarray:
+    ms = np.ascontiguousarray(ms, dtype=np.float64)
+    ls = np.ascontiguousarray(ls, dtype=np.float64)
+    accs = np.ascontiguousarray(accs, dtype=np.float64)
+    P, D = accs.shape
+    out = np.empty(D, dtype=np.float64)
+    lib().ora_lse_merge(_p(ms, _f64p), _p(ls, _f64p), _p(accs, _f64p), P, D, _p(out, _f64p))
+    return out
+
+
+def num_threads() -> int:
+    return int(lib().ora_num_threads())
