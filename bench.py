@@ -1,0 +1,290 @@
+#!/usr/bin/env python3
+"""Benchmark of the engine-mlx attention hot path on one MI355X.
+
+Headline workload (the metric's decode half): Qwen3-8B-shape batched decode
+step, batch 32, 32 query / 8 KV heads, head_dim 128, bf16 static cache of
+capacity 8192 per sequence, valid lengths uniform in [512, 8192] (seed 1234).
+One step = the fused pre-attention for one new token per sequence (q/k
+RMSNorm, RoPE, K/V written at offset len-1) followed by decode attention over
+len positions. value = algorithmic bytes of the step / step time.
+
+The other shapes are measured after it and reported under "secondary"
+(prefill TFLOP/s for the metric's prefill half, the remaining configurations).
+Inputs are synthetic (seeded normal), already resident in HBM.
+
+python bench.py [--steps K] [--warmup W] [--only primary] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "engine-mlx_amd"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+METRIC = "decode attn GB/s (% of 8 TB/s) + prefill attn TFLOP/s, Qwen3-8B shapes"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk"], default="all")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+class Ctx:
+    def __init__(self):
+        import torch
+
+        self.torch = torch
+        self.dev = torch.device("cuda:0")
+        self.gen = torch.Generator(device=self.dev)
+        self.gen.manual_seed(2024)
+
+    def randn(self, shape, mean=0.0, std=1.0):
+        t = self.torch.randn(shape, generator=self.gen, device=self.dev, dtype=self.torch.float32)
+        return (t * std + mean).to(self.torch.bfloat16)
+
+    def i32(self, values):
+        return self.torch.tensor(list(map(int, values)), dtype=self.torch.int32, device=self.dev)
+
+
+def time_calls(torch, fn, steps, warmup):
+    """Average ms per call of fn() with HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+# ---------------------------------------------------------------- decode
+def decode_bytes(lengths, Hq, Hkv, D):
+    B = len(lengths)
+    return sum(2 * Hkv * int(L) * D * 2 for L in lengths) + 2 * B * Hq * D * 2
+
+
+def pre_bytes(B, T, Hq, Hkv, D):
+    return B * T * ((Hq + 2 * Hkv) * D * 2 + Hq * D * 2 + 2 * Hkv * D * 2)
+
+
+def primary(ctx, ema, args):
+    torch = ctx.torch
+    import numpy as np
+
+    B, Hq, Hkv, D, cap = 32, 32, 8, 128, 8192
+    lengths = np.random.default_rng(1234).integers(512, 8193, size=B)
+    off = lengths - 1
+    log(f"[bench] decode step B={B} {Hq}q/{Hkv}kv D={D} cap={cap} sum(L)={int(lengths.sum())}")
+    cache = ema.StaticCache(B, Hkv, cap, D, k=ctx.randn((B, Hkv, cap, D)), v=ctx.randn((B, Hkv, cap, D)))
+    qkv = ctx.randn((B, 1, (Hq + 2 * Hkv) * D))
+    qw = ctx.randn((D,), 1.0, 0.02)
+    kw = ctx.randn((D,), 1.0, 0.02)
+    off_d, len_d = ctx.i32(off), ctx.i32(lengths)
+    q = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=ctx.dev)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = torch.empty(ema.decode_workspace_size(B, Hq, Hkv, D, cap), dtype=torch.uint8, device=ctx.dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def pre():
+        ema.pre_attention(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, q_out=q)
+
+    def attn():
+        ema.decode_attention(q, cache, len_d, cap, scale, out=out, workspace=ws)
+
+    for _ in range(args.warmup):
+        pre()
+        attn()
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t0.record()
+    for i in range(K):
+        pre()
+        ev[i][0].record()
+        attn()
+        ev[i][1].record()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = t0.elapsed_time(t1) / K
+    ms_attn = sum(a.elapsed_time(b) for a, b in ev) / K
+    ab = decode_bytes(lengths, Hq, Hkv, D)
+    sb = ab + pre_bytes(B, 1, Hq, Hkv, D)
+    res = {
+        "lengths_sum": int(lengths.sum()), "step_bytes": sb, "attn_bytes": ab,
+        "ms_per_step": ms_step, "attn_ms": ms_attn, "wall_s": wall,
+        "step_gbs": sb / (ms_step * 1e-3) / 1e9, "attn_gbs": ab / (ms_attn * 1e-3) / 1e9,
+    }
+    log(f"[bench] decode step {ms_step*1e3:.1f} us ({res['step_gbs']:.0f} GB/s); "
+        f"attention {ms_attn*1e3:.1f} us ({res['attn_gbs']:.0f} GB/s, {res['attn_gbs']/HBM_PEAK_GBS:.1%} of HBM)")
+    state = dict(cache=cache, q=q, lengths=lengths, Hq=Hq, Hkv=Hkv, D=D, cap=cap, scale=scale, bytes=ab)
+    return res, state
+
+
+def cpu_baseline(state, seconds):
+    """The oracle's f32 SDPA (MLX CPU-stream arithmetic, OpenMP) on the same decode workload."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    import torch
+
+    cache = state["cache"]
+    kc = cache.k.view(torch.int16).cpu().numpy().view(np.uint16)
+    vc = cache.v.view(torch.int16).cpu().numpy().view(np.uint16)
+    q = state["q"].view(torch.int16).cpu().numpy().view(np.uint16)
+    L = np.asarray(state["lengths"], np.int32)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t = time.perf_counter()
+        oracle.sdpa(q, kc, vc, L, state["scale"], False, precision=1)
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() > t_end or len(times) >= 20:
+            break
+    med = statistics.median(times)
+    return {
+        "value": state["bytes"] / med / 1e9, "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
+        "sample": f"the full batch-32 decode attention (same lengths, {len(times)} runs, median {med*1e3:.1f} ms): "
+                  "oracle f32 SDPA, bf16 inputs, OpenMP over (sequence, kv head)",
+    }
+
+
+# ------------------------------------------------------------- secondary
+def prefill_flops(Hq, D, T, off):
+    return 4 * Hq * D * (T * off + T * (T + 1) // 2)
+
+
+def bench_prefill(ctx, ema, name, B, Hq, Hkv, D, cap, T, off, steps=20):
+    torch = ctx.torch
+    cache = ema.StaticCache(B, Hkv, cap, D, k=ctx.randn((B, Hkv, cap, D)), v=ctx.randn((B, Hkv, cap, D)))
+    q = ctx.randn((B, Hq, T, D))
+    qo = ctx.i32([off] * B)
+    out = torch.empty((B, T, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ms = time_calls(torch, lambda: ema.prefill_attention(q, cache, qo, causal=True, out=out), steps, 5)
+    fl = B * prefill_flops(Hq, D, T, off)
+    tf = fl / (ms * 1e-3) / 1e12
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s ({tf/BF16_PEAK_TFLOPS:.1%} of bf16 peak)")
+    return {"workload": name, "us": ms * 1e3, "tflops": tf, "frac_of_peak": tf / BF16_PEAK_TFLOPS, "flops": fl}
+
+
+def bench_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
+    torch = ctx.torch
+    cache = ema.StaticCache(B, Hkv, cap, D, k=ctx.randn((B, Hkv, cap, D)), v=ctx.randn((B, Hkv, cap, D)))
+    q = ctx.randn((B, Hq, D))
+    ld = ctx.i32(lengths)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = torch.empty(ema.decode_workspace_size(B, Hq, Hkv, D, cap), dtype=torch.uint8, device=ctx.dev)
+    ms = time_calls(torch, lambda: ema.decode_attention(q, cache, ld, int(max(lengths)), out=out, workspace=ws),
+                    steps, 5)
+    by = decode_bytes(lengths, Hq, Hkv, D)
+    gbs = by / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM)")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
+
+
+def bench_pre(ctx, ema, name, T, Hq, Hkv, D, cap, steps=20):
+    torch = ctx.torch
+    cache = ema.StaticCache(1, Hkv, cap, D)
+    # qkv = x W for x [T, 2048] ~ N(0,1), W ~ N(0, 1/sqrt(2048)): the projection is outside the path
+    x = ctx.randn((T, 2048))
+    w = ctx.randn((2048, (Hq + 2 * Hkv) * D), 0.0, 1.0 / math.sqrt(2048))
+    qkv = (x @ w).reshape(1, T, -1).contiguous()
+    qw, kw = ctx.randn((D,), 1.0, 0.02), ctx.randn((D,), 1.0, 0.02)
+    off = ctx.i32([0])
+    q = torch.empty((1, Hq, T, D), dtype=torch.bfloat16, device=ctx.dev)
+    ms = time_calls(torch, lambda: ema.pre_attention(qkv, qw, kw, 1e-6, 1e6, off, Hq, cache, q_out=q), steps, 5)
+    by = pre_bytes(1, T, Hq, Hkv, D)
+    gbs = by / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {gbs:.0f} GB/s")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for {max(args.gpus, world)}); the attention path here is "
+              "single-GPU and has no multi-GPU mode.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    import ema_attn as ema
+
+    ema.lib()
+    ctx = Ctx()
+    res, state = primary(ctx, ema, args)
+    secondary = []
+    if args.only in ("all", "prefill"):
+        secondary.append(bench_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_qwen3_8b", 1, 32, 8, 128, 4096, 2048, 0))
+    if args.only == "all":
+        secondary.append(bench_prefill(ctx, ema, "prefill_causal_T2048_16q8kv_qwen3_1p7b", 1, 16, 8, 128, 4096, 2048, 0))
+        secondary.append(bench_pre(ctx, ema, "pre_attention_T2048_16q8kv", 2048, 16, 8, 128, 4096))
+        secondary.append(bench_decode(ctx, ema, "decode_B1_16q8kv_L1024_cap4096", 1, 16, 8, 128, 4096, [1024]))
+    if args.only in ("all", "decode_long"):
+        secondary.append(bench_decode(ctx, ema, "decode_B8_32q4kv_L32768", 8, 32, 4, 128, 32768, [32768] * 8))
+    if args.only in ("all", "prefill_chunk"):
+        secondary.append(bench_prefill(ctx, ema, "prefill_chunk_off14336_T2048_64q8kv", 1, 64, 8, 128, 16384, 2048,
+                                       14336, steps=10))
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle f32 SDPA on the host)")
+        cpu = cpu_baseline(state, args.cpu_seconds)
+        log(f"[bench] CPU baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(res["step_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) q/K/V and qkv, norm weights 1+N(0,0.02), lengths U[512,8192] seed 1234",
+        "config": {
+            "workload": "qwen3_8b_batched_decode_step: pre-attention (T=1) + decode attention",
+            "batch": 32, "n_heads": 32, "n_kv_heads": 8, "head_dim": 128, "capacity": 8192,
+            "lengths_sum": res["lengths_sum"], "parallelism": "single_gpu",
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "decode attention (decode_kernel + decode_merge_kernel)",
+            "achieved": round(res["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(res["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "attn_us": round(res["attn_ms"] * 1e3, 2), "attn_bytes": res["attn_bytes"],
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

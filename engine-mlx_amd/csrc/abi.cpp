@@ -1,0 +1,209 @@
+// C ABI of the attention hot path: argument validation and dispatch.
+//
+// Error behaviour follows the reference's FFI wrapper: every call returns a
+// status, 0 = OK (crates/mlx-ffi/src/ops/real/mod.rs:35-40 turns a non-zero
+// mlx-c status into "MLX op '<op>' failed with code <n>"); here the message
+// is kept in a thread-local string readable through ema_last_error().
+// Validation runs on the host before any HIP call, so every argument error is
+// reported without touching the GPU.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "ema_common.hpp"
+
+namespace ema {
+
+static thread_local char g_err[512] = "";
+
+int32_t set_error(int32_t code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int32_t check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return EMA_OK;
+  return set_error(EMA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+uint64_t decode_header_bytes();
+
+}  // namespace ema
+
+using namespace ema;
+
+namespace {
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
+  if (!c) return set_error(EMA_ERR_INVALID_ARG, "%s: cache descriptor is null", op);
+  if (!c->k || !c->v) return set_error(EMA_ERR_INVALID_ARG, "%s: KV cache is empty (null K/V buffer)", op);
+  if (c->dtype != EMA_DTYPE_BF16) return set_error(EMA_ERR_INVALID_ARG, "%s: cache dtype must be bf16", op);
+  if (c->batch <= 0 || c->n_kv_heads <= 0 || c->capacity <= 0 || c->head_dim <= 0)
+    return set_error(EMA_ERR_SHAPE, "%s: cache dims must be positive (batch=%d n_kv_heads=%d capacity=%d head_dim=%d)",
+                     op, c->batch, c->n_kv_heads, c->capacity, c->head_dim);
+  if (c->head_dim % 8 != 0) return set_error(EMA_ERR_SHAPE, "%s: head_dim %d is not a multiple of 8", op, c->head_dim);
+  if (c->stride_pos < c->head_dim || c->stride_pos % 8 || c->stride_head % 8 || c->stride_batch % 8 ||
+      c->stride_head < 0 || c->stride_batch < 0)
+    return set_error(EMA_ERR_SHAPE, "%s: cache strides must be >= head_dim and multiples of 8 elements", op);
+  if (!aligned16(c->k) || !aligned16(c->v)) return set_error(EMA_ERR_INVALID_ARG, "%s: cache buffers must be 16-byte aligned", op);
+  return EMA_OK;
+}
+
+int32_t check_heads(const char* op, int32_t Hq, int32_t Hkv) {
+  if (Hq <= 0 || Hkv <= 0) return set_error(EMA_ERR_SHAPE, "%s: head counts must be positive (n_heads=%d n_kv_heads=%d)", op, Hq, Hkv);
+  if (Hq % Hkv) return set_error(EMA_ERR_SHAPE, "%s: n_heads %d is not a multiple of n_kv_heads %d", op, Hq, Hkv);
+  return EMA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ema_last_error(void) { return g_err; }
+
+const char* ema_version(void) { return "ema_attn 0.1.0 (gfx950)"; }
+
+int32_t ema_kvcache_init(ema_kvcache_desc* d, void* k, void* v, int32_t batch, int32_t n_kv_heads,
+                         int32_t capacity, int32_t head_dim) {
+  if (!d) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_init: descriptor is null");
+  memset(d, 0, sizeof(*d));
+  d->k = k;
+  d->v = v;
+  d->batch = batch;
+  d->n_kv_heads = n_kv_heads;
+  d->capacity = capacity;
+  d->head_dim = head_dim;
+  d->stride_pos = head_dim;
+  d->stride_head = (int64_t)capacity * head_dim;
+  d->stride_batch = (int64_t)n_kv_heads * capacity * head_dim;
+  d->dtype = EMA_DTYPE_BF16;
+  return check_cache("ema_kvcache_init", d);
+}
+
+int32_t ema_kvcache_alloc(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads, int32_t capacity,
+                          int32_t head_dim) {
+  if (!out) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_alloc: descriptor is null");
+  memset(out, 0, sizeof(*out));
+  if (batch <= 0 || n_kv_heads <= 0 || capacity <= 0 || head_dim <= 0 || head_dim % 8)
+    return set_error(EMA_ERR_SHAPE, "ema_kvcache_alloc: bad dims (batch=%d n_kv_heads=%d capacity=%d head_dim=%d)",
+                     batch, n_kv_heads, capacity, head_dim);
+  const size_t bytes = (size_t)batch * n_kv_heads * capacity * head_dim * 2;
+  void *k = nullptr, *v = nullptr;
+  int32_t rc = check_hip(hipMalloc(&k, bytes), "ema_kvcache_alloc: hipMalloc K");
+  if (rc) return rc;
+  rc = check_hip(hipMalloc(&v, bytes), "ema_kvcache_alloc: hipMalloc V");
+  if (rc) {
+    (void)hipFree(k);
+    return rc;
+  }
+  rc = check_hip(hipMemset(k, 0, bytes), "ema_kvcache_alloc: zero K");
+  if (!rc) rc = check_hip(hipMemset(v, 0, bytes), "ema_kvcache_alloc: zero V");
+  if (rc) {
+    (void)hipFree(k);
+    (void)hipFree(v);
+    return rc;
+  }
+  return ema_kvcache_init(out, k, v, batch, n_kv_heads, capacity, head_dim);
+}
+
+int32_t ema_kvcache_free(ema_kvcache_desc* d) {
+  if (!d) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_free: descriptor is null");
+  int32_t rc = EMA_OK;
+  if (d->k) rc = check_hip(hipFree(d->k), "ema_kvcache_free: K");
+  if (d->v) {
+    int32_t r2 = check_hip(hipFree(d->v), "ema_kvcache_free: V");
+    rc = rc ? rc : r2;
+  }
+  memset(d, 0, sizeof(*d));
+  return rc;
+}
+
+int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* d, uint64_t* bytes) {
+  if (!bytes) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_memory_bytes: output is null");
+  int32_t rc = check_cache("ema_kvcache_memory_bytes", d);
+  if (rc) return rc;
+  *bytes = 2ull * d->batch * d->n_kv_heads * d->capacity * d->head_dim * 2ull;
+  return EMA_OK;
+}
+
+int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                          float eps, float theta, const int32_t* offsets, int32_t batch, int32_t n_tokens,
+                          int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, uint32_t flags, void* q_out,
+                          const ema_kvcache_desc* cache) {
+  const char* op = "ema_pre_attention";
+  int32_t rc = check_cache(op, cache);
+  if (rc) return rc;
+  if (!qkv || !q_out || !offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null qkv/q_out/offsets", op);
+  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE)) return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
+  if (!(flags & EMA_PRE_NO_NORM) && (!q_norm_w || !k_norm_w))
+    return set_error(EMA_ERR_INVALID_ARG, "%s: norm weights are null (pass EMA_PRE_NO_NORM for models without q/k norm)", op);
+  if ((rc = check_heads(op, n_heads, n_kv_heads))) return rc;
+  if (batch <= 0 || n_tokens <= 0) return set_error(EMA_ERR_SHAPE, "%s: batch=%d n_tokens=%d must be positive", op, batch, n_tokens);
+  if (batch != cache->batch || n_kv_heads != cache->n_kv_heads || head_dim != cache->head_dim)
+    return set_error(EMA_ERR_SHAPE, "%s: shape (batch=%d n_kv_heads=%d head_dim=%d) does not match the cache (%d, %d, %d)",
+                     op, batch, n_kv_heads, head_dim, cache->batch, cache->n_kv_heads, cache->head_dim);
+  if (n_tokens > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: static KV overflow: %d tokens exceed capacity %d", op, n_tokens, cache->capacity);
+  if (!(eps >= 0.f) || !(theta > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: eps must be >= 0 and theta > 0", op);
+  if (!aligned16(qkv) || !aligned16(q_out)) return set_error(EMA_ERR_INVALID_ARG, "%s: qkv/q_out must be 16-byte aligned", op);
+  return launch_pre_attention((hipStream_t)stream, qkv, q_norm_w, k_norm_w, eps, theta, offsets, batch, n_tokens,
+                              n_heads, n_kv_heads, head_dim, flags, q_out, *cache);
+}
+
+int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                  int32_t max_len, uint64_t* bytes) {
+  const char* op = "ema_decode_workspace_size";
+  if (!bytes) return set_error(EMA_ERR_INVALID_ARG, "%s: output is null", op);
+  int32_t rc = check_heads(op, n_heads, n_kv_heads);
+  if (rc) return rc;
+  if (batch <= 0 || head_dim <= 0 || max_len < 0) return set_error(EMA_ERR_SHAPE, "%s: bad dims", op);
+  DecodePlan p = plan_decode(batch, n_heads, n_kv_heads, head_dim, max_len);
+  *bytes = decode_header_bytes() + p.part_bytes;
+  return EMA_OK;
+}
+
+int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
+                             const int32_t* lengths, int32_t max_len, int32_t n_heads, float scale, void* out,
+                             void* workspace, uint64_t workspace_bytes) {
+  const char* op = "ema_decode_attention";
+  int32_t rc = check_cache(op, cache);
+  if (rc) return rc;
+  if (!q || !out || !lengths) return set_error(EMA_ERR_INVALID_ARG, "%s: null q/out/lengths", op);
+  if ((rc = check_heads(op, n_heads, cache->n_kv_heads))) return rc;
+  if (max_len < 0 || max_len > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: max_len %d outside [0, capacity %d]", op, max_len, cache->capacity);
+  if (!(scale > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: scale must be > 0", op);
+  if (!aligned16(q) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: q/out must be 16-byte aligned", op);
+  DecodePlan p = plan_decode(cache->batch, n_heads, cache->n_kv_heads, cache->head_dim, max_len);
+  const uint64_t need = decode_header_bytes() + p.part_bytes;
+  if (!workspace || workspace_bytes < need)
+    return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes needed, %llu given", op,
+                     (unsigned long long)need, (unsigned long long)(workspace ? workspace_bytes : 0));
+  if (!aligned16(workspace)) return set_error(EMA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", op);
+  return launch_decode((hipStream_t)stream, q, *cache, lengths, n_heads, scale, out, workspace, p);
+}
+
+int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
+                              const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads, float scale,
+                              uint32_t flags, void* out) {
+  const char* op = "ema_prefill_attention";
+  int32_t rc = check_cache(op, cache);
+  if (rc) return rc;
+  if (!q || !out || !q_offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null q/out/q_offsets", op);
+  if (flags & ~(EMA_PREFILL_CAUSAL | EMA_PREFILL_CHUNK_ONLY))
+    return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
+  if ((rc = check_heads(op, n_heads, cache->n_kv_heads))) return rc;
+  if (n_tokens <= 0) return set_error(EMA_ERR_SHAPE, "%s: n_tokens %d must be positive", op, n_tokens);
+  if (n_tokens > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: %d tokens exceed capacity %d", op, n_tokens, cache->capacity);
+  if (!(scale > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: scale must be > 0", op);
+  if (!aligned16(q) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: q/out must be 16-byte aligned", op);
+  return launch_prefill((hipStream_t)stream, q, *cache, q_offsets, n_tokens, n_heads, scale, flags, out);
+}
+
+}  // extern "C"

@@ -1,0 +1,85 @@
+// Shared device/host helpers for the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ema_attn.h"
+
+namespace ema {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// bf16 bits -> f32 (exact).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// f32 -> bf16 bits, round to nearest even, NaN kept quiet (same rule as the oracle).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// 16x16x32 bf16 MFMA, f32 accumulate. Lane layout (checked on gfx950):
+//   A[16 x 32]: lane l holds row l%16, k = 8*(l/16) .. +7
+//   B[32 x 16]: lane l holds col l%16, k = 8*(l/16) .. +7
+//   C[16 x 16]: lane l holds col l%16, rows 4*(l/16) .. +3
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// 32x32x16 bf16 MFMA. Lane layout (checked on gfx950):
+//   A[32 x 16]: lane l holds row l%32, k = 8*(l/32) .. +7
+//   B[16 x 32]: lane l holds col l%32, k = 8*(l/32) .. +7
+//   C[32 x 32]: lane l holds col l%32, rows (i%4) + 8*(i/4) + 4*(l/32), i = 0..15
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, 64));
+}
+
+}  // namespace ema
+
+// ---------------------------------------------------------------- host side
+namespace ema {
+
+// Sets the thread-local error message and returns `code`.
+int32_t set_error(int32_t code, const char* fmt, ...);
+// Maps a HIP error to EMA_ERR_HIP with context, or returns EMA_OK.
+int32_t check_hip(hipError_t e, const char* what);
+
+int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, const void* kw,
+                             float eps, float theta, const int32_t* off, int B, int T, int Hq,
+                             int Hkv, int D, uint32_t flags, void* q_out,
+                             const ema_kvcache_desc& c);
+
+struct DecodePlan {
+  int workers;        // independent wave workers over the flattened (b, kv-head, tile) space
+  int segments;       // B * Hkv
+  uint64_t part_bytes;  // partial (m, l, o) slots: (workers + segments) pieces
+};
+DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len);
+int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, const int32_t* len,
+                      int Hq, float scale, void* out, void* ws, const DecodePlan& plan);
+
+int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
+                       const int32_t* q_off, int T, int Hq, float scale, uint32_t flags,
+                       void* out);
+
+}  // namespace ema

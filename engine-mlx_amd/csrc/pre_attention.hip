@@ -1,0 +1,208 @@
+// Fused Qwen3 pre-attention for gfx950: q/k RMSNorm, split-half RoPE and the
+// in-place K/V write at the sequence offset, one pass over the fused qkv
+// activation.
+//
+// Replaces the op chain of crates/serve/src/forward_qwen3.rs:56-68 + :124-142
+// (prefill: slice, reshape, rms_norm, transpose, rope_dynamic, slice_update)
+// and crates/serve/src/compiled.rs:134-161 (decode: dsplit, rms_norm, rope,
+// scatter_single). Arithmetic follows MLX fast::rms_norm / fast::rope
+// (crates/mlx-ffi/src/ops/real/blas.rs:5-9, :67-80): f32 statistics, the
+// normalised value rounded to bf16 before the weight multiply, RoPE angle
+// pos * 2^(-(i/(D/2)) * log2(theta)) formed in f32.
+//
+// Mapping: one 16-lane group per head vector (b, t, h), h over the
+// Hq + 2*Hkv heads of the fused row; lane j holds elements
+// [j*E, j*E+E) and [D/2 + j*E, D/2 + j*E + E) with E = D/32, so each RoPE pair
+// sits in one lane and each half of the row is one contiguous 2*D-byte access
+// per group. HBM-bound: every byte of qkv is read once, q/k/v written once.
+#include "ema_common.hpp"
+
+namespace ema {
+namespace {
+
+template <int E>
+struct Vec;
+template <>
+struct Vec<2> {
+  typedef uint32_t T;
+  static __device__ __forceinline__ void load(const uint16_t* p, uint16_t* x) {
+    uint32_t w = *(const uint32_t*)p;
+    x[0] = (uint16_t)w;
+    x[1] = (uint16_t)(w >> 16);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const uint16_t* x) {
+    *(uint32_t*)p = (uint32_t)x[0] | ((uint32_t)x[1] << 16);
+  }
+};
+template <>
+struct Vec<4> {
+  static __device__ __forceinline__ void load(const uint16_t* p, uint16_t* x) {
+    u32x2 w = *(const u32x2*)p;
+    for (int i = 0; i < 2; ++i) {
+      x[2 * i] = (uint16_t)w[i];
+      x[2 * i + 1] = (uint16_t)(w[i] >> 16);
+    }
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const uint16_t* x) {
+    u32x2 w;
+    for (int i = 0; i < 2; ++i) w[i] = (uint32_t)x[2 * i] | ((uint32_t)x[2 * i + 1] << 16);
+    *(u32x2*)p = w;
+  }
+};
+template <>
+struct Vec<8> {
+  static __device__ __forceinline__ void load(const uint16_t* p, uint16_t* x) {
+    u32x4 w = *(const u32x4*)p;
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = (uint16_t)w[i];
+      x[2 * i + 1] = (uint16_t)(w[i] >> 16);
+    }
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const uint16_t* x) {
+    u32x4 w;
+    for (int i = 0; i < 4; ++i) w[i] = (uint32_t)x[2 * i] | ((uint32_t)x[2 * i + 1] << 16);
+    *(u32x4*)p = w;
+  }
+};
+
+struct PreArgs {
+  const uint16_t* qkv;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const int32_t* off;
+  uint16_t* q_out;
+  uint16_t* kc;
+  uint16_t* vc;
+  int64_t sb, sh, sp;
+  int64_t nvec;
+  float eps;
+  float log2_theta;
+  int B, T, Hq, Hkv, cap;
+  uint32_t flags;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
+  constexpr int HALF = D / 2;
+  constexpr int E = D / 32;
+  const int lane16 = threadIdx.x & 15;
+  const int64_t vec = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  if (vec >= a.nvec) return;  // whole 16-lane groups exit together
+  const int H = a.Hq + 2 * a.Hkv;
+  const int h = (int)(vec % H);
+  const int64_t bt = vec / H;
+  const int t = (int)(bt % a.T);
+  const int b = (int)(bt / a.T);
+  const int off = a.off[b];
+  const int pos = off + t;
+  const bool in_cap = off >= 0 && (int64_t)off + a.T <= a.cap;
+
+  const uint16_t* src = a.qkv + vec * D;
+  uint16_t x[2 * E];
+  Vec<E>::load(src + lane16 * E, x);
+  Vec<E>::load(src + HALF + lane16 * E, x + E);
+
+  if (h >= a.Hq + a.Hkv) {  // v: bit copy into the cache row
+    if (!in_cap) return;
+    const int kh = h - a.Hq - a.Hkv;
+    uint16_t* dst = a.vc + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)pos * a.sp;
+    Vec<E>::store(dst + lane16 * E, x);
+    Vec<E>::store(dst + HALF + lane16 * E, x + E);
+    return;
+  }
+  const bool is_q = h < a.Hq;
+  float y[2 * E];
+  if (!(a.flags & EMA_PRE_NO_NORM)) {
+    float ss = 0.f;
+    for (int e = 0; e < 2 * E; ++e) {
+      const float f = bf16_to_f32(x[e]);
+      ss += f * f;
+    }
+    ss += __shfl_xor(ss, 8, 16);
+    ss += __shfl_xor(ss, 4, 16);
+    ss += __shfl_xor(ss, 2, 16);
+    ss += __shfl_xor(ss, 1, 16);
+    const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+    const uint16_t* w = is_q ? a.qw : a.kw;
+    uint16_t wv[2 * E];
+    Vec<E>::load(w + lane16 * E, wv);
+    Vec<E>::load(w + HALF + lane16 * E, wv + E);
+    for (int e = 0; e < 2 * E; ++e) {
+      const float n = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32(x[e]) * inv));
+      y[e] = bf16_to_f32((uint16_t)f32_to_bf16_bits(n * bf16_to_f32(wv[e])));
+    }
+  } else {
+    for (int e = 0; e < 2 * E; ++e) y[e] = bf16_to_f32(x[e]);
+  }
+  uint16_t o[2 * E];
+  if (!(a.flags & EMA_PRE_NO_ROPE)) {
+    for (int e = 0; e < E; ++e) {
+      const int i = lane16 * E + e;
+      const float inv_freq = exp2f(-((float)i / (float)HALF) * a.log2_theta);
+      const float ang = (float)pos * inv_freq;
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      const float x1 = y[e], x2 = y[E + e];
+      o[e] = (uint16_t)f32_to_bf16_bits(x1 * cs - x2 * sn);
+      o[E + e] = (uint16_t)f32_to_bf16_bits(x1 * sn + x2 * cs);
+    }
+  } else {
+    for (int e = 0; e < 2 * E; ++e) o[e] = (uint16_t)f32_to_bf16_bits(y[e]);
+  }
+  uint16_t* dst;
+  if (is_q) {
+    dst = a.q_out + (((int64_t)b * a.Hq + h) * a.T + t) * D;
+  } else {
+    if (!in_cap) return;
+    dst = a.kc + (int64_t)b * a.sb + (int64_t)(h - a.Hq) * a.sh + (int64_t)pos * a.sp;
+  }
+  Vec<E>::store(dst + lane16 * E, o);
+  Vec<E>::store(dst + HALF + lane16 * E, o + E);
+}
+
+}  // namespace
+
+int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, const void* kw,
+                             float eps, float theta, const int32_t* off, int B, int T, int Hq,
+                             int Hkv, int D, uint32_t flags, void* q_out,
+                             const ema_kvcache_desc& c) {
+  PreArgs a;
+  a.qkv = (const uint16_t*)qkv;
+  a.qw = (const uint16_t*)qw;
+  a.kw = (const uint16_t*)kw;
+  a.off = off;
+  a.q_out = (uint16_t*)q_out;
+  a.kc = (uint16_t*)c.k;
+  a.vc = (uint16_t*)c.v;
+  a.sb = c.stride_batch;
+  a.sh = c.stride_head;
+  a.sp = c.stride_pos;
+  a.nvec = (int64_t)B * T * (Hq + 2 * Hkv);
+  a.eps = eps;
+  a.log2_theta = log2f(theta);
+  a.B = B;
+  a.T = T;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.cap = c.capacity;
+  a.flags = flags;
+  const int threads = 256;
+  const int64_t blocks = (a.nvec + 15) / 16;
+  if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many head vectors");
+  switch (D) {
+    case 64:
+      hipLaunchKernelGGL(pre_attention_kernel<64>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      break;
+    case 128:
+      hipLaunchKernelGGL(pre_attention_kernel<128>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      break;
+    case 256:
+      hipLaunchKernelGGL(pre_attention_kernel<256>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      break;
+    default:
+      return set_error(EMA_ERR_UNSUPPORTED, "ema_pre_attention: head_dim %d not supported (64/128/256)", D);
+  }
+  return check_hip(hipGetLastError(), "ema_pre_attention launch");
+}
+
+}  // namespace ema

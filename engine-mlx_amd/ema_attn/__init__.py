@@ -1,0 +1,211 @@
+"""Python binding of the ema_attn C ABI (include/ema_attn.h).
+
+Thin ctypes layer used by the tests and the benchmark: tensors are torch
+device tensors (bf16 / int32), every call goes through ``libema_attn.so`` and
+fails loudly when the library is missing or a call returns an error. There is
+no fallback path.
+
+The names mirror the reference's API for this path:
+``KvCache``/``StaticCache`` (crates/kvcache/src/lib.rs:52-76) and
+``gqa_attention`` (crates/attention/src/gqa.rs:62-107) minus the projections.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libema_attn.so")
+
+EMA_OK = 0
+EMA_ERR_INVALID_ARG = -1
+EMA_ERR_SHAPE = -2
+EMA_ERR_CAPACITY = -3
+EMA_ERR_WORKSPACE = -4
+EMA_ERR_UNSUPPORTED = -5
+EMA_ERR_HIP = -6
+
+EMA_DTYPE_BF16 = 1
+EMA_PRE_NO_NORM = 1
+EMA_PRE_NO_ROPE = 2
+EMA_PREFILL_CAUSAL = 1
+EMA_PREFILL_CHUNK_ONLY = 2
+
+EXPORTED = (
+    "ema_last_error", "ema_version", "ema_kvcache_init", "ema_kvcache_alloc", "ema_kvcache_free",
+    "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
+    "ema_decode_attention", "ema_prefill_attention",
+)
+
+
+class EmaError(RuntimeError):
+    def __init__(self, code: int, op: str, msg: str):
+        super().__init__(f"{op} failed with code {code}: {msg}")
+        self.code = code
+        self.op = op
+        self.msg = msg
+
+
+class KvCacheDesc(ctypes.Structure):
+    _fields_ = [
+        ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("batch", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32),
+        ("capacity", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("stride_batch", ctypes.c_int64), ("stride_head", ctypes.c_int64),
+        ("stride_pos", ctypes.c_int64), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"ema_attn HIP library not built: {LIB_PATH} (run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i32, u32, f32, u64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float, ctypes.c_uint64
+        D = ctypes.POINTER(KvCacheDesc)
+        sig = {
+            "ema_last_error": (ctypes.c_char_p, []),
+            "ema_version": (ctypes.c_char_p, []),
+            "ema_kvcache_init": (i32, [D, vp, vp, i32, i32, i32, i32]),
+            "ema_kvcache_alloc": (i32, [D, i32, i32, i32, i32]),
+            "ema_kvcache_free": (i32, [D]),
+            "ema_kvcache_memory_bytes": (i32, [D, ctypes.POINTER(u64)]),
+            "ema_pre_attention": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, i32, i32, i32, u32, vp, D]),
+            "ema_decode_workspace_size": (i32, [i32, i32, i32, i32, i32, ctypes.POINTER(u64)]),
+            "ema_decode_attention": (i32, [vp, vp, D, vp, i32, i32, f32, vp, vp, u64]),
+            "ema_prefill_attention": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().ema_last_error().decode()
+
+
+def version() -> str:
+    return lib().ema_version().decode()
+
+
+def _check(rc: int, op: str) -> None:
+    if rc != EMA_OK:
+        raise EmaError(rc, op, last_error())
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+class StaticCache:
+    """Static pre-allocated bf16 KV cache of one layer, [B, Hkv, cap, D].
+
+    Mirrors the reference's static KV state (crates/serve/src/engine.rs:31-42,
+    alloc_kv_static at crates/serve/src/engine_ext.rs:266-306) behind the
+    KvCache trait surface (crates/kvcache/src/lib.rs:52-76): ``len`` is the
+    number of valid positions per sequence, ``reset`` only rewinds the offsets
+    (stale rows stay and are excluded by length, engine_ext.rs:218-228).
+    """
+
+    def __init__(self, batch: int, n_kv_heads: int, capacity: int, head_dim: int, device="cuda",
+                 k=None, v=None):
+        import torch
+
+        shape = (batch, n_kv_heads, capacity, head_dim)
+        self.k = k if k is not None else torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.v = v if v is not None else torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.desc = KvCacheDesc()
+        _check(lib().ema_kvcache_init(ctypes.byref(self.desc), _ptr(self.k), _ptr(self.v), batch, n_kv_heads,
+                                      capacity, head_dim), "ema_kvcache_init")
+        self.offsets = [0] * batch
+
+    @property
+    def capacity(self) -> int:
+        return self.desc.capacity
+
+    def len(self) -> int:
+        return max(self.offsets) if self.offsets else 0
+
+    def is_empty(self) -> bool:
+        return self.len() == 0
+
+    def reset(self) -> None:
+        self.offsets = [0] * len(self.offsets)
+
+    def memory_bytes(self) -> int:
+        out = ctypes.c_uint64()
+        _check(lib().ema_kvcache_memory_bytes(ctypes.byref(self.desc), ctypes.byref(out)), "ema_kvcache_memory_bytes")
+        return out.value
+
+
+def pre_attention(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: StaticCache, flags=0,
+                  q_out=None, stream=None):
+    """qkv [B,T,(Hq+2Hkv)*D] bf16; offsets int32 device [B]. Returns q_out [B,Hq,T,D]."""
+    import torch
+
+    B, T, F = qkv.shape
+    D = cache.desc.head_dim
+    Hkv = cache.desc.n_kv_heads
+    if q_out is None:
+        q_out = torch.empty((B, n_heads, T, D), dtype=torch.bfloat16, device=qkv.device)
+    _check(lib().ema_pre_attention(_stream(stream), _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), eps, theta,
+                                   _ptr(offsets), B, T, n_heads, Hkv, D, flags, _ptr(q_out),
+                                   ctypes.byref(cache.desc)), "ema_pre_attention")
+    return q_out
+
+
+def decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_len) -> int:
+    out = ctypes.c_uint64()
+    _check(lib().ema_decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_len, ctypes.byref(out)),
+           "ema_decode_workspace_size")
+    return out.value
+
+
+def decode_attention(q, cache: StaticCache, lengths, max_len, scale=None, out=None, workspace=None, stream=None):
+    """q [B,Hq,D] (or [B,Hq,1,D]) bf16; lengths int32 device [B]. Returns out [B, Hq*D]."""
+    import torch
+
+    B, Hq = q.shape[0], q.shape[1]
+    D = cache.desc.head_dim
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        n = decode_workspace_size(B, Hq, cache.desc.n_kv_heads, D, max_len)
+        workspace = torch.empty(n, dtype=torch.uint8, device=q.device)
+    _check(lib().ema_decode_attention(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(lengths), max_len, Hq,
+                                      scale, _ptr(out), _ptr(workspace), workspace.numel()), "ema_decode_attention")
+    return out
+
+
+def prefill_attention(q, cache: StaticCache, q_offsets, scale=None, causal=True, chunk_only=False, out=None,
+                      stream=None):
+    """q [B,Hq,T,D] bf16; q_offsets int32 device [B]. Returns out [B,T,Hq*D]."""
+    import torch
+
+    B, Hq, T, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty((B, T, Hq * D), dtype=torch.bfloat16, device=q.device)
+    flags = (EMA_PREFILL_CAUSAL if causal else 0) | (EMA_PREFILL_CHUNK_ONLY if chunk_only else 0)
+    _check(lib().ema_prefill_attention(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(q_offsets), T, Hq,
+                                       scale, flags, _ptr(out)), "ema_prefill_attention")
+    return out

@@ -1,0 +1,157 @@
+/*
+ * ema_attn — MI355X (gfx950) attention hot path of engine-mlx, C ABI.
+ *
+ * Replaces, for the Qwen3 attention path, the MLX primitives the reference
+ * reaches through mlx-c (dangranaz/engine-mlx 0.1.18):
+ *
+ *   reference call (file:line)                                  replaced by
+ *   ----------------------------------------------------------  ----------------------
+ *   MlxCtx::rms_norm   crates/mlx-ffi/src/ops/real/blas.rs:5-9  ema_pre_attention
+ *   MlxCtx::rope_dynamic / rope            blas.rs:67-80        ema_pre_attention
+ *   MlxCtx::scatter_single  crates/mlx-ffi/src/ops/real/slice.rs:106-113
+ *                                                               ema_pre_attention (T=1)
+ *   MlxCtx::slice_update    slice.rs:78-88                      ema_pre_attention (T>1)
+ *   MlxCtx::sdpa_masked  crates/mlx-ffi/src/ops/real/transform.rs:8-29
+ *                                                               ema_decode_attention
+ *   MlxCtx::sdpa(causal=true)  blas.rs:82-101                   ema_prefill_attention
+ *   static KV buffers  crates/serve/src/engine_ext.rs:266-306   ema_kvcache_*
+ *   KvCache::memory_bytes  crates/kvcache/src/lib.rs:75         ema_kvcache_memory_bytes
+ *
+ * Conventions
+ *   - Every entry point returns int32_t: EMA_OK (0) or a negative EMA_ERR_*.
+ *     On error, ema_last_error() returns a thread-local message (the analogue
+ *     of the reference's "MLX op '<op>' failed with code <n>",
+ *     crates/mlx-ffi/src/ops/real/mod.rs:35-40).
+ *   - Eager and stream-ordered: work is enqueued on `stream` (a hipStream_t;
+ *     NULL = the default stream). Nothing synchronises the host.
+ *   - No allocation inside the hot calls (pre_attention, decode, prefill);
+ *     buffers and workspace are owned by the caller. Re-entrant on distinct
+ *     streams; the only global state is the thread-local error string.
+ *   - bf16 = IEEE bfloat16 (RNE). Device pointers must be 16-byte aligned and
+ *     head_dim-contiguous.
+ *   - Masking is by valid length: the additive bf16 mask of
+ *     crates/serve/src/engine_ext.rs:237-260 (0 for p <= offset, -1e9 beyond)
+ *     is exactly a length offset+1, because exp(-1e9 - m) is 0 in f32.
+ */
+#ifndef EMA_ATTN_H
+#define EMA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EMA_OK 0
+#define EMA_ERR_INVALID_ARG (-1) /* null pointer, bad enum, misaligned      */
+#define EMA_ERR_SHAPE (-2)       /* inconsistent or unsupported dimensions   */
+#define EMA_ERR_CAPACITY (-3)    /* write/read beyond the static capacity    */
+#define EMA_ERR_WORKSPACE (-4)   /* workspace missing or too small           */
+#define EMA_ERR_UNSUPPORTED (-5) /* valid but not implemented (e.g. head_dim)*/
+#define EMA_ERR_HIP (-6)         /* HIP runtime error (launch, malloc)       */
+
+#define EMA_DTYPE_BF16 1
+
+/* ema_pre_attention flags */
+#define EMA_PRE_NO_NORM 1u /* q_norm/k_norm are None: crates/ops/src/attention.rs:57-76 */
+#define EMA_PRE_NO_ROPE 2u /* NoPE layer (use_rope=false): crates/ops/src/rope.rs:38-40  */
+
+/* ema_prefill_attention flags */
+#define EMA_PREFILL_CAUSAL 1u     /* MLX "causal", query block end-aligned to the keys   */
+#define EMA_PREFILL_CHUNK_ONLY 2u /* keys limited to the new chunk [q_off, q_off+T):
+                                     crates/serve/src/forward_qwen3.rs:150 attends only
+                                     the freshly projected k/v; without this flag the
+                                     whole cache [0, q_off+T) is attended, as
+                                     gqa_attention does (crates/attention/src/gqa.rs:100-106) */
+
+typedef void* ema_stream_t; /* hipStream_t */
+
+#ifndef EMA_API
+#define EMA_API __attribute__((visibility("default")))
+#endif
+
+/* Static KV cache of one layer: K and V of logical shape
+ * [batch, n_kv_heads, capacity, head_dim], bf16, head_dim contiguous.
+ * Owned by the caller (the reference allocates these once at MAX_CAP,
+ * crates/serve/src/engine_ext.rs:266-306, and reuses them across requests). */
+typedef struct ema_kvcache_desc {
+  void* k;
+  void* v;
+  int32_t batch;
+  int32_t n_kv_heads;
+  int32_t capacity;
+  int32_t head_dim;
+  int64_t stride_batch; /* in elements */
+  int64_t stride_head;  /* in elements */
+  int64_t stride_pos;   /* in elements, >= head_dim */
+  int32_t dtype;        /* EMA_DTYPE_BF16 */
+  int32_t reserved;
+} ema_kvcache_desc;
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+EMA_API const char* ema_last_error(void);
+/* Library version string. */
+EMA_API const char* ema_version(void);
+
+/* Fill a descriptor for caller-owned contiguous K/V buffers. */
+EMA_API int32_t ema_kvcache_init(ema_kvcache_desc* desc, void* k, void* v, int32_t batch,
+                         int32_t n_kv_heads, int32_t capacity, int32_t head_dim);
+/* Allocate zeroed device K/V buffers (zeros_bf16 in alloc_kv_static,
+ * crates/serve/src/engine_ext.rs:273-278). Not for the hot path. */
+EMA_API int32_t ema_kvcache_alloc(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads,
+                          int32_t capacity, int32_t head_dim);
+/* Free buffers obtained from ema_kvcache_alloc and clear the descriptor. */
+EMA_API int32_t ema_kvcache_free(ema_kvcache_desc* desc);
+/* Bytes held by K and V (KvCache::memory_bytes, crates/kvcache/src/lib.rs:75). */
+EMA_API int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* desc, uint64_t* bytes);
+
+/* Fused Qwen3 pre-attention for `batch` sequences of `n_tokens` new tokens.
+ *   qkv      [batch, n_tokens, (n_heads + 2*n_kv_heads) * head_dim] bf16, order q|k|v
+ *            (fused projection output, crates/serve/src/forward/projection.rs:105-128)
+ *   q_norm_w, k_norm_w  [head_dim] bf16 (ignored with EMA_PRE_NO_NORM)
+ *   offsets  device int32 [batch]: position of the first new token
+ *   q_out    [batch, n_heads, n_tokens, head_dim] bf16
+ * Per head vector: RMSNorm over head_dim (eps), split-half RoPE at offsets[b]+t
+ * (base theta), then K and V are written into cache rows [offsets[b], offsets[b]+n_tokens).
+ * Replaces forward_qwen3.rs:56-68,124-142 and compiled.rs:134-161.
+ * Offsets are read on the device; offsets[b] + n_tokens > capacity writes nothing
+ * for that sequence (callers guard on the host as decode_compiled.rs:18-20 does). */
+EMA_API int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_norm_w,
+                          const void* k_norm_w, float eps, float theta, const int32_t* offsets,
+                          int32_t batch, int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads,
+                          int32_t head_dim, uint32_t flags, void* q_out,
+                          const ema_kvcache_desc* cache);
+
+/* Workspace (bytes) ema_decode_attention needs for this shape. */
+EMA_API int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_t n_kv_heads,
+                                  int32_t head_dim, int32_t max_len, uint64_t* bytes);
+
+/* Batched single-token decode attention over the static cache
+ * (MlxCtx::sdpa_masked with the static mask, compiled.rs:163 / decode_eager.rs:140).
+ *   q        [batch, n_heads, head_dim] bf16 (post norm/RoPE)
+ *   lengths  device int32 [batch]: valid positions (offset + 1 after the write);
+ *            clamped to [0, capacity]; a sequence with 0 valid positions yields zeros
+ *   max_len  host upper bound of lengths (sizes the split; <= capacity)
+ *   out      [batch, n_heads * head_dim] bf16 (the o_proj input layout)
+ * GQA: q head h reads kv head h / (n_heads / n_kv_heads). */
+EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
+                             const int32_t* lengths, int32_t max_len, int32_t n_heads,
+                             float scale, void* out, void* workspace, uint64_t workspace_bytes);
+
+/* Prefill / chunked-prefill attention over the static cache
+ * (MlxCtx::sdpa(causal), blas.rs:82-101 via forward_qwen3.rs:150 and
+ * attend_and_project, crates/ops/src/attention.rs:162-177).
+ *   q          [batch, n_heads, n_tokens, head_dim] bf16
+ *   q_offsets  device int32 [batch]: cache position of the first query; keys
+ *              [0, q_offsets[b] + n_tokens) (or [q_offsets[b], ...) with CHUNK_ONLY)
+ *   out        [batch, n_tokens, n_heads * head_dim] bf16
+ * With EMA_PREFILL_CAUSAL, query i sees key j iff j <= q_offsets[b] + i. */
+EMA_API int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
+                              const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads,
+                              float scale, uint32_t flags, void* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EMA_ATTN_H */

@@ -1,0 +1,155 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/ema_attn.h declares, and rejects bad arguments on the host with the
+documented status codes and messages (no HIP call is reached)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ema_attn.h")
+
+
+@pytest.fixture(scope="module")
+def ema():
+    import ema_attn
+
+    if not os.path.exists(ema_attn.LIB_PATH):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "engine-mlx_amd")], check=True)
+    ema_attn.lib()
+    return ema_attn
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"EMA_API\s+[\w\s\*]+?\b(ema_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_set(ema):
+    assert declared_symbols() == sorted(ema.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(ema):
+    out = subprocess.run(["nm", "-D", "--defined-only", ema.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s(ema_\w+)$", out, re.M))
+    missing = [s for s in declared_symbols() if s not in exported]
+    assert not missing, missing
+    # internal C++ helpers stay hidden
+    assert not [s for s in exported if s not in ema.EXPORTED]
+
+
+def test_version_and_empty_error(ema):
+    assert "gfx950" in ema.version()
+
+
+def _desc(ema, k=0x10000, v=0x20000, B=2, Hkv=8, cap=64, D=128):
+    d = ema.KvCacheDesc()
+    rc = ema.lib().ema_kvcache_init(ctypes.byref(d), k, v, B, Hkv, cap, D)
+    return rc, d
+
+
+def test_kvcache_init_and_memory_bytes(ema):
+    rc, d = _desc(ema)
+    assert rc == ema.EMA_OK
+    assert (d.stride_pos, d.stride_head, d.stride_batch) == (128, 64 * 128, 8 * 64 * 128)
+    n = ctypes.c_uint64()
+    assert ema.lib().ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 8 * 64 * 128 * 2
+
+
+def test_empty_cache_is_rejected(ema):
+    """Same contract text as ConcatCache::get (crates/kvcache/src/concat.rs:54)."""
+    rc, d = _desc(ema, k=0, v=0)
+    assert rc == ema.EMA_ERR_INVALID_ARG
+    assert "KV cache is empty" in ema.last_error()
+
+
+def test_bad_shapes_and_alignment(ema):
+    rc, _ = _desc(ema, D=100)
+    assert rc == ema.EMA_ERR_SHAPE
+    rc, _ = _desc(ema, k=0x10008)
+    assert rc == ema.EMA_ERR_INVALID_ARG and "aligned" in ema.last_error()
+    rc, _ = _desc(ema, cap=0)
+    assert rc == ema.EMA_ERR_SHAPE
+
+
+def test_workspace_size_scales_with_shape(ema):
+    a = ema.decode_workspace_size(32, 32, 8, 128, 8192)
+    b = ema.decode_workspace_size(1, 16, 8, 128, 1024)
+    assert a > b > 0
+    with pytest.raises(ema.EmaError) as e:
+        ema.decode_workspace_size(1, 12, 8, 128, 1024)
+    assert e.value.code == ema.EMA_ERR_SHAPE and "multiple" in e.value.msg
+
+
+def test_decode_argument_errors(ema):
+    L = ema.lib()
+    _, d = _desc(ema)
+    good = 0x40000
+    # GQA mapping needs n_heads % n_kv_heads == 0
+    rc = L.ema_decode_attention(None, good, ctypes.byref(d), good, 64, 12, 0.088, good, good, 1 << 30)
+    assert rc == ema.EMA_ERR_SHAPE
+    # max_len beyond the static capacity (decode_compiled.rs:18-20 overflow guard)
+    rc = L.ema_decode_attention(None, good, ctypes.byref(d), good, 65, 16, 0.088, good, good, 1 << 30)
+    assert rc == ema.EMA_ERR_CAPACITY and "capacity" in ema.last_error()
+    # workspace too small
+    rc = L.ema_decode_attention(None, good, ctypes.byref(d), good, 64, 16, 0.088, good, good, 16)
+    assert rc == ema.EMA_ERR_WORKSPACE and "workspace" in ema.last_error()
+    # null q
+    rc = L.ema_decode_attention(None, None, ctypes.byref(d), good, 64, 16, 0.088, good, good, 1 << 30)
+    assert rc == ema.EMA_ERR_INVALID_ARG
+    # null descriptor
+    rc = L.ema_decode_attention(None, good, None, good, 64, 16, 0.088, good, good, 1 << 30)
+    assert rc == ema.EMA_ERR_INVALID_ARG
+
+
+def test_pre_attention_argument_errors(ema):
+    L = ema.lib()
+    _, d = _desc(ema)
+    g = 0x40000
+    # norm weights required unless NO_NORM
+    rc = L.ema_pre_attention(None, g, None, None, 1e-6, 1e6, g, 2, 4, 16, 8, 128, 0, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_INVALID_ARG and "norm" in ema.last_error()
+    # batch mismatch with the cache
+    rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 3, 4, 16, 8, 128, 0, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_SHAPE
+    # more tokens than the static capacity
+    rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 2, 65, 16, 8, 128, 0, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_CAPACITY and "overflow" in ema.last_error()
+    # unknown flag bits
+    rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 2, 4, 16, 8, 128, 8, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_INVALID_ARG
+
+
+def test_prefill_argument_errors(ema):
+    L = ema.lib()
+    _, d = _desc(ema)
+    g = 0x40000
+    rc = L.ema_prefill_attention(None, g, ctypes.byref(d), g, 0, 16, 0.088, 1, g)
+    assert rc == ema.EMA_ERR_SHAPE
+    rc = L.ema_prefill_attention(None, g, ctypes.byref(d), g, 65, 16, 0.088, 1, g)
+    assert rc == ema.EMA_ERR_CAPACITY
+    rc = L.ema_prefill_attention(None, g, ctypes.byref(d), g, 8, 16, 0.088, 4, g)
+    assert rc == ema.EMA_ERR_INVALID_ARG
+    rc = L.ema_prefill_attention(None, g, ctypes.byref(d), g, 8, 16, -1.0, 1, g)
+    assert rc == ema.EMA_ERR_INVALID_ARG
+
+
+def test_errors_are_thread_local(ema):
+    import threading
+
+    L = ema.lib()
+    _, d = _desc(ema)
+    L.ema_prefill_attention(None, 0x40000, ctypes.byref(d), 0x40000, 0, 16, 0.088, 1, 0x40000)
+    main_msg = ema.last_error()
+    seen = {}
+
+    def worker():
+        seen["msg"] = ema.last_error()
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    assert main_msg and seen["msg"] == ""

@@ -1,0 +1,317 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Tolerance (bf16 outputs vs the f64 oracle): max-abs 2e-2, mean-abs 2e-3.
+KV-cache write positions, V rows and masking are bit-exact; post-RoPE K rows
+may differ from the oracle by the last bf16 bit (f32 op order, sincos ulp) and
+are held to the same 2e-2 / 2e-3 bound.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import assert_close, dev, f32, host, say, scale_of
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ema():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import ema_attn
+
+    ema_attn.lib()
+    return ema_attn
+
+
+def make_cache(ema, kc: np.ndarray, vc: np.ndarray):
+    B, Hkv, cap, D = kc.shape
+    return ema.StaticCache(B, Hkv, cap, D, k=dev(kc), v=dev(vc))
+
+
+# ------------------------------------------------------------ pre-attention
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+def test_pre_attention_small(ema, ora, D, flags):
+    import torch
+
+    B, T, Hq, Hkv, cap = 2, 5, 4, 2, 16
+    say(f"pre_attention small D={D} flags={flags}")
+    qkv = ora.normal_bf16((B, T, (Hq + 2 * Hkv) * D), seed=100 + D + flags)
+    qw = ora.normal_bf16(D, seed=101, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=102, mean=1.0, std=0.02)
+    off = np.array([3, 9], np.int32)
+    junk = ora.normal_bf16((B, Hkv, cap, D), seed=103)
+    kr, vr = junk.copy(), junk.copy()
+    q_ref = ora.pre_attention(qkv, qw, kw, 1e-6, 1e6, off, Hq, Hkv, kr, vr, flags=flags)
+    cache = make_cache(ema, junk, junk)
+    q = ema.pre_attention(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, cache, flags=flags)
+    torch.cuda.synchronize()
+    kg, vg = host(cache.k), host(cache.v)
+    assert np.array_equal(vg, vr), "V rows must be a bit copy at [off, off+T)"
+    for b in range(B):
+        rows = np.r_[0:off[b], off[b] + T:cap]
+        assert np.array_equal(kg[b][:, rows], junk[b][:, rows]), "rows outside the write changed"
+    assert_close(host(q), q_ref, "q_out")
+    assert_close(kg, kr, "k cache")
+    if flags & 2 and flags & 1:  # pure copy: bit exact
+        assert np.array_equal(kg, kr) and np.array_equal(host(q), q_ref)
+
+
+def test_pre_attention_prefill_shape(ema, ora):
+    """2048 tokens, 16q/8kv, written at offset 0 of a 4096-capacity cache."""
+    import torch
+
+    B, T, Hq, Hkv, D, cap = 1, 2048, 16, 8, 128, 4096
+    say("pre_attention T=2048 16q/8kv cap 4096")
+    qkv = ora.normal_bf16((B, T, (Hq + 2 * Hkv) * D), seed=110)
+    qw = ora.normal_bf16(D, seed=111, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=112, mean=1.0, std=0.02)
+    off = np.zeros(B, np.int32)
+    kr = np.zeros((B, Hkv, cap, D), np.uint16)
+    vr = kr.copy()
+    q_ref = ora.pre_attention(qkv, qw, kw, 1e-6, 1e6, off, Hq, Hkv, kr, vr)
+    cache = ema.StaticCache(B, Hkv, cap, D)
+    q = ema.pre_attention(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, cache)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(cache.v), vr)
+    assert np.all(host(cache.k)[:, :, T:] == 0)
+    assert_close(host(q), q_ref, "q_out")
+    assert_close(host(cache.k)[:, :, :T], kr[:, :, :T], "k cache")
+    ulp = np.abs(host(cache.k).astype(np.int32) - kr.astype(np.int32))
+    say(f"  k rows differing from the oracle bits: {np.count_nonzero(ulp)} of {ulp.size}, max {ulp.max()} ulp")
+    assert ulp.max() <= 1
+
+
+def test_pre_attention_decode_positions(ema, ora):
+    """Decode write: one token per sequence at its own offset (scatter_single)."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 32, 32, 8, 128, 512
+    rng = np.random.default_rng(5)
+    off = rng.integers(0, cap, size=B).astype(np.int32)
+    off[0], off[1] = 0, cap - 1
+    say("pre_attention decode B=32 ragged offsets")
+    qkv = ora.normal_bf16((B, 1, (Hq + 2 * Hkv) * D), seed=120)
+    qw = ora.normal_bf16(D, seed=121, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=122, mean=1.0, std=0.02)
+    base = ora.normal_bf16((B, Hkv, cap, D), seed=123)
+    kr, vr = base.copy(), base.copy()
+    q_ref = ora.pre_attention(qkv, qw, kw, 1e-6, 1e6, off, Hq, Hkv, kr, vr)
+    cache = make_cache(ema, base, base)
+    q = ema.pre_attention(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, cache)
+    torch.cuda.synchronize()
+    kg = host(cache.k)
+    assert np.array_equal(host(cache.v), vr)
+    changed = np.any(kg != base, axis=(1, 3))
+    for b in range(B):
+        rows = np.nonzero(changed[b])[0]
+        assert set(rows.tolist()) <= {int(off[b])}
+    assert_close(host(q), q_ref, "q_out")
+    assert_close(kg, kr, "k cache")
+
+
+def test_pre_attention_overflow_writes_nothing(ema, ora):
+    import torch
+
+    B, T, Hq, Hkv, D, cap = 2, 4, 2, 1, 128, 8
+    qkv = ora.normal_bf16((B, T, (Hq + 2 * Hkv) * D), seed=130)
+    base = ora.normal_bf16((B, Hkv, cap, D), seed=131)
+    cache = make_cache(ema, base, base)
+    off = np.array([5, 2], np.int32)  # sequence 0 would overflow (5 + 4 > 8)
+    ema.pre_attention(dev(qkv), None, None, 1e-6, 1e6, dev(off), Hq, cache, flags=3)
+    torch.cuda.synchronize()
+    kg = host(cache.k)
+    assert np.array_equal(kg[0], base[0])
+    assert not np.array_equal(kg[1], base[1])
+
+
+# ------------------------------------------------------------------ decode
+def _decode_case(ema, ora, B, Hq, Hkv, D, cap, lengths, seed, outliers=False, poison=False, max_len=None):
+    import torch
+
+    q = ora.normal_bf16((B, Hq, 1, D), seed=seed)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 1)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 2)
+    if outliers:  # 1% of K entries x8 before bf16 rounding
+        kf = ora.normal_f32((B, Hkv, cap, D), seed=seed + 1)
+        sel = np.random.default_rng(seed).random(kf.shape, dtype=np.float32) < 0.01
+        kf[sel] *= 8.0
+        kc = ora.bf16_from_f32(kf)
+        del kf, sel
+    L = np.asarray(lengths, np.int32)
+    ref = ora.sdpa(q, kc, vc, L, scale_of(D), False)
+    if poison:
+        for b in range(B):
+            kc[b, :, L[b]:] = 0x7FC0
+            vc[b, :, L[b]:] = 0x7FC0
+    cache = make_cache(ema, kc, vc)
+    out = ema.decode_attention(dev(q), cache, dev(L), int(max_len or L.max()))
+    torch.cuda.synchronize()
+    return host(out), ref
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+def test_decode_small(ema, ora, G):
+    B, Hkv, D, cap = 6, 2, 128, 160
+    lengths = [1, 31, 32, 33, 100, 160]
+    say(f"decode small G={G} lengths={lengths}")
+    got, ref = _decode_case(ema, ora, B, Hkv * G, Hkv, D, cap, lengths, seed=200 + G)
+    assert_close(got, ref, f"decode G={G}")
+
+
+def test_decode_stale_tail_is_bit_exact(ema, ora):
+    """Rows >= len poisoned with NaN give bit-identical output (mask exactness)."""
+    B, Hq, Hkv, D, cap = 4, 8, 2, 128, 256
+    lengths = [7, 64, 65, 200]
+    say("decode stale-tail NaN poison")
+    clean, ref = _decode_case(ema, ora, B, Hq, Hkv, D, cap, lengths, seed=210)
+    dirty, _ = _decode_case(ema, ora, B, Hq, Hkv, D, cap, lengths, seed=210, poison=True)
+    assert np.array_equal(clean, dirty)
+    assert_close(clean, ref, "decode clean")
+
+
+def test_decode_zero_length_gives_zeros(ema, ora):
+    got, _ = _decode_case(ema, ora, 3, 4, 2, 128, 64, [0, 10, 0], seed=220, max_len=64)
+    assert np.all(got[0] == 0) and np.all(got[2] == 0) and np.any(got[1] != 0)
+
+
+@pytest.mark.parametrize("max_len", [33, 100, 1000, 4096])
+def test_decode_split_invariance(ema, ora, max_len):
+    """Different max_len hints change the worker split; results stay within tolerance."""
+    B, Hq, Hkv, D, cap = 3, 16, 8, 128, 4096
+    lengths = [33, 1, 29]
+    say(f"decode split max_len={max_len}")
+    got, ref = _decode_case(ema, ora, B, Hq, Hkv, D, cap, lengths, seed=230, max_len=max_len)
+    assert_close(got, ref, f"decode max_len={max_len}")
+
+
+def test_decode_qwen3_1p7b_shape(ema, ora):
+    """batch 1, 16q/8kv, D 128, cap 4096, 1024 valid positions."""
+    say("decode B1 16q/8kv cap 4096 L 1024")
+    got, ref = _decode_case(ema, ora, 1, 16, 8, 128, 4096, [1024], seed=240, poison=True)
+    assert_close(got, ref, "decode 1.7B shape")
+
+
+def test_decode_qwen3_8b_batched_shape(ema, ora):
+    """batch 32, 32q/8kv, cap 8192, lengths uniform in [512, 8192]."""
+    L = np.random.default_rng(1234).integers(512, 8193, size=32)
+    say(f"decode B32 32q/8kv cap 8192 ragged sum(L)={int(L.sum())}")
+    got, ref = _decode_case(ema, ora, 32, 32, 8, 128, 8192, L, seed=250, max_len=8192)
+    assert_close(got, ref, "decode 8B batched")
+
+
+def test_decode_qwen3_30b_long_context_shape(ema, ora):
+    """batch 8, 32q/4kv (G 8), cap = len = 32768, 1% of K entries x8."""
+    say("decode B8 32q/4kv L 32768 outliers")
+    got, ref = _decode_case(ema, ora, 8, 32, 4, 128, 32768, [32768] * 8, seed=260, outliers=True)
+    assert_close(got, ref, "decode 30B long context")
+
+
+# ----------------------------------------------------------------- prefill
+def _prefill_case(ema, ora, B, Hq, Hkv, D, cap, T, q_off, causal, chunk_only, seed, heads=None):
+    import torch
+
+    q = ora.normal_bf16((B, Hq, T, D), seed=seed)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 1)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 2)
+    qo = np.asarray(q_off, np.int32)
+    cache = make_cache(ema, kc, vc)
+    out = host(ema.prefill_attention(dev(q), cache, dev(qo), causal=causal, chunk_only=chunk_only))
+    torch.cuda.synchronize()
+    kv_len = qo + T
+    kv_begin = qo if chunk_only else None
+    if heads is None:
+        ref = ora.sdpa(q, kc, vc, kv_len, scale_of(D), causal, kv_begin=kv_begin)
+        return out, ref
+    G = Hq // Hkv
+    kvh = sorted({h // G for h in heads})
+    sel = [h for kh in kvh for h in range(kh * G, kh * G + G)]
+    ref = ora.sdpa(q[:, sel].copy(), kc[:, kvh].copy(), vc[:, kvh].copy(), kv_len, scale_of(D), causal,
+                   kv_begin=kv_begin)
+    o = out.reshape(B, T, Hq, D)[:, :, sel].reshape(B, T, len(sel) * D)
+    return o, ref
+
+
+@pytest.mark.parametrize("T,q_off,causal,chunk", [
+    (1, 0, True, False), (5, 0, True, False), (64, 0, True, False), (128, 0, True, False),
+    (200, 0, True, False), (200, 37, True, False), (77, 100, True, True), (130, 50, False, False),
+    (300, 0, False, True),
+])
+@pytest.mark.parametrize("G", [1, 2, 8])
+def test_prefill_small(ema, ora, T, q_off, causal, chunk, G):
+    B, Hkv, D, cap = 2, 2, 128, 512
+    say(f"prefill small T={T} q_off={q_off} causal={causal} chunk={chunk} G={G}")
+    got, ref = _prefill_case(ema, ora, B, Hkv * G, Hkv, D, cap, T, [q_off, q_off // 2], causal, chunk,
+                             seed=300 + T + G)
+    assert_close(got, ref, f"prefill T={T}")
+
+
+def test_prefill_qwen3_1p7b_2k(ema, ora):
+    """1 x 2048 tokens, 16q/8kv, causal from offset 0 (heads 0-3 checked)."""
+    say("prefill T=2048 16q/8kv causal")
+    got, ref = _prefill_case(ema, ora, 1, 16, 8, 128, 4096, 2048, [0], True, False, seed=310, heads=[0, 3])
+    assert_close(got, ref, "prefill 2k")
+
+
+def test_prefill_chunk_on_existing_cache_sampled_rows(ema, ora):
+    """64q/8kv, 14336 cached + 2048 new (16384 capacity); sampled rows of two heads."""
+    import torch
+
+    B, Hq, Hkv, D, cap, T, off = 1, 64, 8, 128, 16384, 2048, 14336
+    say("prefill chunked 64q/8kv off 14336 T 2048")
+    q = ora.normal_bf16((B, Hq, T, D), seed=320)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=321)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=322)
+    cache = make_cache(ema, kc, vc)
+    out = host(ema.prefill_attention(dev(q), cache, dev(np.array([off], np.int32)), causal=True))
+    torch.cuda.synchronize()
+    out = out.reshape(T, Hq, D)
+    rows = np.r_[0:4, 1021:1025, T - 4:T]
+    for h in (0, 37):
+        for i in rows:
+            ref = ora.sdpa(q[:, h:h + 1, i:i + 1].copy(), kc[:, h // 8:h // 8 + 1].copy(),
+                           vc[:, h // 8:h // 8 + 1].copy(), [off + i + 1], scale_of(D), False)
+            assert_close(out[i, h][None], ref.reshape(1, D), f"row {i} head {h}")
+
+
+def test_prefill_rows_match_decode_on_gpu(ema, ora):
+    """Causal prefill row i equals decode with len = off + i + 1 on the same cache."""
+    import torch
+
+    B, Hq, Hkv, D, cap, T, off = 1, 8, 2, 128, 1024, 96, 500
+    q = ora.normal_bf16((B, Hq, T, D), seed=330)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=331)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=332)
+    cache = make_cache(ema, kc, vc)
+    pre = host(ema.prefill_attention(dev(q), cache, dev(np.array([off], np.int32)), causal=True))
+    for i in (0, 17, 95):
+        dec = host(ema.decode_attention(dev(q[:, :, i].copy()), cache, dev(np.array([off + i + 1], np.int32)),
+                                        off + i + 1))
+        torch.cuda.synchronize()
+        assert_close(pre[:, i], dec, f"row {i}", max_abs=1e-2, mean_abs=1e-3)
+
+
+# --------------------------------------------------------------- full step
+def test_decode_step_pre_attention_then_attention(ema, ora):
+    """The decode step: write one token per sequence, then attend over len = off + 1."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 8, 32, 8, 128, 2048
+    rng = np.random.default_rng(77)
+    off = rng.integers(0, cap, size=B).astype(np.int32)
+    say("decode step B=8 pre-attention + attention")
+    qkv = ora.normal_bf16((B, 1, (Hq + 2 * Hkv) * D), seed=400)
+    qw = ora.normal_bf16(D, seed=401, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=402, mean=1.0, std=0.02)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=403)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=404)
+    kr, vr = kc.copy(), vc.copy()
+    q_ref = ora.pre_attention(qkv, qw, kw, 1e-6, 1e6, off, Hq, Hkv, kr, vr)
+    ref = ora.sdpa(q_ref, kr, vr, off + 1, scale_of(D), False)
+    cache = make_cache(ema, kc, vc)
+    q = ema.pre_attention(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, cache)
+    out = ema.decode_attention(q, cache, dev(off + 1), cap)
+    torch.cuda.synchronize()
+    assert_close(host(out), ref, "decode step")
