@@ -1,0 +1,150 @@
+// C++ host API of the attention hot path: the reference's KvCache trait and
+// gqa_attention, restated over the ema_attn C ABI.
+//
+//   reference (dangranaz/engine-mlx 0.1.18)                  here
+//   -------------------------------------------------------  ----------------------------
+//   trait KvCache            crates/kvcache/src/lib.rs:52-76  class KvCache
+//   static KV state + alloc  crates/serve/src/engine.rs:31-42,
+//                            crates/serve/src/engine_ext.rs:266-306
+//                                                            class StaticCache
+//   struct GqaConfig         crates/attention/src/gqa.rs:27-42  struct GqaConfig
+//   struct GqaWeights        crates/attention/src/gqa.rs:45-53  struct GqaWeights (q/k norm only)
+//   fn gqa_attention         crates/attention/src/gqa.rs:62-107 gqa_attention
+//   fn sliding_window_attention crates/attention/src/sliding_window.rs:40-50
+//                                                            sliding_window_attention
+//
+// The projections (q/k/v/o_proj quantised matmuls) are outside this path:
+// gqa_attention takes the fused projection output qkv [1, T, (Hq+2Hkv)*D] and
+// returns the attention output [1, T, Hq*D] that o_proj consumes.
+// Errors are thrown as ema::Error with the reference's message texts
+// ("KV cache is empty", "static KV overflow offset=.. cap=..").
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "ema_attn.h"
+
+#define EMA_HOST_API __attribute__((visibility("default")))
+
+namespace ema {
+
+class EMA_HOST_API Error : public std::runtime_error {
+ public:
+  Error(int32_t code, const std::string& msg) : std::runtime_error(msg), code_(code) {}
+  int32_t code() const { return code_; }
+
+ private:
+  int32_t code_;
+};
+
+// Analogue of MlxCtx for this path: the HIP stream work is enqueued on.
+struct Ctx {
+  ema_stream_t stream = nullptr;
+};
+
+// Analogue of mlx_array for this path: a non-owning view of a bf16 device
+// tensor. `strides` are in elements; empty means contiguous.
+struct Array {
+  void* data = nullptr;
+  std::vector<int64_t> shape;
+  std::vector<int64_t> strides;
+  int64_t numel() const;
+};
+
+class EMA_HOST_API KvCache {
+ public:
+  virtual ~KvCache() = default;
+  // Append new K and V, shape [1, n_kv_heads, seq_len, head_dim] (attention order).
+  virtual void append(const Ctx& ctx, const Array& k, const Array& v) = 0;
+  // The full accumulated K and V, [1, n_kv_heads, total_seq, head_dim].
+  virtual std::pair<Array, Array> get(const Ctx& ctx) const = 0;
+  virtual size_t len() const = 0;
+  bool is_empty() const { return len() == 0; }
+  virtual void reset() = 0;
+  virtual size_t memory_bytes() const = 0;
+};
+
+// Static pre-allocated bf16 cache of one layer, [1, Hkv, capacity, head_dim],
+// allocated zeroed once (alloc_kv_static) and reused: reset() rewinds the
+// offset only, stale rows stay and are excluded by the valid length.
+class EMA_HOST_API StaticCache final : public KvCache {
+ public:
+  StaticCache(int32_t n_kv_heads, int32_t capacity, int32_t head_dim);
+  ~StaticCache() override;
+  StaticCache(const StaticCache&) = delete;
+  StaticCache& operator=(const StaticCache&) = delete;
+
+  void append(const Ctx& ctx, const Array& k, const Array& v) override;
+  std::pair<Array, Array> get(const Ctx& ctx) const override;
+  size_t len() const override { return (size_t)offset_; }
+  void reset() override { offset_ = 0; }
+  size_t memory_bytes() const override;
+
+  int32_t capacity() const { return desc_.capacity; }
+  int32_t n_kv_heads() const { return desc_.n_kv_heads; }
+  int32_t head_dim() const { return desc_.head_dim; }
+  const ema_kvcache_desc& desc() const { return desc_; }
+  // Device pointer to the int32 value p, 0 <= p <= capacity: the analogue of
+  // the pre-built static_offsets scalars (crates/serve/src/engine_ext.rs:293-299),
+  // so a step passes its offset without a host-to-device copy.
+  const int32_t* device_position(int32_t p) const;
+  // Record that rows [offset, offset + n) were written in place.
+  void advance(int32_t n);
+
+  // Scratch owned by the cache for gqa_attention (grown on demand, outside
+  // the steady state): q [Hq * T * D], output [T * Hq * D], decode workspace.
+  void* q_scratch(size_t bytes);
+  void* out_scratch(size_t bytes);
+  void* decode_workspace(int32_t n_heads, uint64_t* bytes);
+
+ private:
+  ema_kvcache_desc desc_{};
+  int32_t offset_ = 0;
+  int32_t* positions_ = nullptr;  // device int32 [capacity + 1] = 0, 1, ..., capacity
+  void* q_buf_ = nullptr;
+  size_t q_bytes_ = 0;
+  void* o_buf_ = nullptr;
+  size_t o_bytes_ = 0;
+  void* ws_ = nullptr;
+  uint64_t ws_bytes_ = 0;
+};
+
+struct GqaConfig {
+  int32_t n_heads = 0;
+  int32_t n_kv_heads = 0;
+  int32_t head_dim = 0;
+  float rope_theta = 1e6f;
+  float norm_eps = 1e-6f;
+  bool use_rope = true;
+};
+
+// Only the parts of GqaWeights this path consumes: the optional per-head
+// q/k RMSNorm weights ([head_dim] bf16 device views).
+struct GqaWeights {
+  std::optional<Array> q_norm;
+  std::optional<Array> k_norm;
+};
+
+struct SlidingWindowConfig {
+  GqaConfig gqa;
+  size_t window_size = 0;
+};
+
+// qkv [1, T, (Hq + 2*Hkv) * head_dim] -> attention output [1, T, Hq * head_dim]
+// (a view into cache-owned scratch, valid until the next call on this cache).
+// T > 1: causal attention over the cache rows [0, offset + T); T == 1: decode
+// over offset + 1 rows. K/V are written at [offset, offset + T) and the cache
+// length advances to offset + T.
+EMA_HOST_API Array gqa_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights, StaticCache& cache,
+                                 const GqaConfig& config, int32_t offset);
+
+EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights,
+                                            StaticCache& cache, const SlidingWindowConfig& config, int32_t offset);
+
+}  // namespace ema
