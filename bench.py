@@ -63,15 +63,26 @@ class Ctx:
 
 
 def time_calls(torch, fn, steps, warmup):
-    """Average ms per call of fn() with HIP events on the current stream."""
+    """Average ms per call of fn(): `steps` calls captured in one HIP graph and
+    replayed, timed with HIP events on the replay stream, so host launch cost
+    is not in the figure."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        fn()
-    e1.record()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(steps):
+                fn()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        graph.replay()  # warm replay
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
 
@@ -101,7 +112,7 @@ def primary(ctx, ema, args):
     off_d, len_d = ctx.i32(off), ctx.i32(lengths)
     q = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=ctx.dev)
     out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
-    ws = torch.empty(ema.decode_workspace_size(B, Hq, Hkv, D, cap), dtype=torch.uint8, device=ctx.dev)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
     scale = 1.0 / math.sqrt(D)
 
     def pre():
@@ -196,7 +207,7 @@ def bench_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
     q = ctx.randn((B, Hq, D))
     ld = ctx.i32(lengths)
     out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
-    ws = torch.empty(ema.decode_workspace_size(B, Hq, Hkv, D, cap), dtype=torch.uint8, device=ctx.dev)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
     ms = time_calls(torch, lambda: ema.decode_attention(q, cache, ld, int(max(lengths)), out=out, workspace=ws),
                     steps, 5)
     by = decode_bytes(lengths, Hq, Hkv, D)

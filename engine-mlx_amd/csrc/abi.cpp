@@ -29,8 +29,6 @@ int32_t check_hip(hipError_t e, const char* what) {
   return set_error(EMA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-uint64_t decode_header_bytes();
-
 }  // namespace ema
 
 using namespace ema;
@@ -163,7 +161,7 @@ int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_t n_kv_h
   if (rc) return rc;
   if (batch <= 0 || head_dim <= 0 || max_len < 0) return set_error(EMA_ERR_SHAPE, "%s: bad dims", op);
   DecodePlan p = plan_decode(batch, n_heads, n_kv_heads, head_dim, max_len);
-  *bytes = decode_header_bytes() + p.part_bytes;
+  *bytes = decode_workspace_bytes(p);
   return EMA_OK;
 }
 
@@ -180,7 +178,7 @@ int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcac
   if (!(scale > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: scale must be > 0", op);
   if (!aligned16(q) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: q/out must be 16-byte aligned", op);
   DecodePlan p = plan_decode(cache->batch, n_heads, cache->n_kv_heads, cache->head_dim, max_len);
-  const uint64_t need = decode_header_bytes() + p.part_bytes;
+  const uint64_t need = decode_workspace_bytes(p);
   if (!workspace || workspace_bytes < need)
     return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes needed, %llu given", op,
                      (unsigned long long)need, (unsigned long long)(workspace ? workspace_bytes : 0));

@@ -10,13 +10,17 @@
 // Work split. The valid rows of every (sequence b, kv head kh) pair form a
 // "segment" of ceil(len_b / 32) tiles of 32 positions. All segments are laid
 // end to end and the flattened tile range is cut into W equal slices, one per
-// wave ("worker"), so ragged lengths cost no load imbalance. A worker walks its
-// slice; each maximal run inside one segment is a "piece" whose online-softmax
-// state (m, l, unnormalised o) goes to partial slot (w + segment index), which
-// is unique because w and the segment index never both stay constant from one
-// piece to the next. A segment covered by a single worker is normalised and
-// written directly; the others are combined by decode_merge_kernel
-// (log-sum-exp merge).
+// workgroup, so ragged lengths cost no load imbalance. A workgroup walks its
+// slice; each maximal run inside one segment is a "piece". The four waves of
+// the workgroup take the piece's tiles in turn, each keeping its own
+// online-softmax state, and combine the four states through LDS at the end of
+// the piece. A segment covered by a single workgroup is normalised and written
+// directly; otherwise the combined state (m, l, unnormalised o) goes to
+// partial slot (w + segment index) -- unique because w and the segment index
+// never both stay constant from one piece to the next -- and
+// decode_merge_kernel folds the slots of each segment by log-sum-exp after the
+// kernel boundary, which is also what makes the partials of other XCDs
+// visible without cache maintenance inside the kernel.
 //
 // Per 32-position tile a wave issues 16 MFMA 16x16x32 (bf16 in, f32 acc):
 //   S^T[pos, g] = K[pos, :] . Q^T[:, g]    A = K rows (straight from HBM),
@@ -41,7 +45,7 @@ constexpr int kTile = 32;
 constexpr int kWaves = 4;       // waves per workgroup, each an independent worker
 constexpr int kMaxB = 1024;     // batch rows held in the LDS prefix table
 constexpr int kPieceStride = kD + 4;  // floats per (piece, head): m, l, pad, pad, o[D]
-constexpr int kHeaderInts = kMaxB + 8;
+constexpr int kMaxWorkers = 512;      // workgroups of the split (and staging rows of the merge)
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -49,7 +53,6 @@ struct DecodeArgs {
   const uint16_t* v;
   const int32_t* len;
   uint16_t* out;
-  int32_t* hdr;  // workspace header: tile prefix per batch row, then total
   float* part;   // partial slots
   int64_t sb, sh, sp;
   float qk_scale;  // scale * log2(e): scores live in the log2 domain
@@ -99,15 +102,34 @@ __device__ void build_prefix(const DecodeArgs& a, int32_t* pre) {
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *(const u32x4*)p; }
 
+__device__ __forceinline__ bool worker_nonempty(int64_t w, int64_t total, int W) {
+  return worker_begin(w, total, W) < worker_begin(w + 1, total, W);
+}
+
+// LDS used to combine the four waves' states at the end of a piece.
+struct Combine {
+  float m[kWaves][16];
+  float l[kWaves][16];
+  float o[kWaves][16][kD];
+};
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t pre[kMaxB + 1];
+  __shared__ Combine cmb;
   build_prefix(a, pre);
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.hdr[i] = pre[i];
 
-  const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (w >= a.W) return;
+  // sequences with no valid position produce zeros (nothing else visits them)
+  if (blockIdx.x == 0) {
+    const int row_words = a.Hq * kD / 2;
+    for (int b = 0; b < a.B; ++b)
+      if (clamp_len(a.len[b], a.cap) == 0)
+        for (int i = threadIdx.x; i < row_words; i += blockDim.x) ((uint32_t*)(a.out + (int64_t)b * a.Hq * kD))[i] = 0u;
+  }
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int w = blockIdx.x;
   const int64_t total = pre[a.B];
   if (total == 0) return;
   int64_t t = worker_begin(w, total, a.W);
@@ -121,7 +143,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int krow0 = 8 * (m >> 2) + (m & 3);
 
   while (t < t_end) {
-    // locate the segment containing tile t (uniform across the wave)
+    // locate the segment containing tile t (uniform across the workgroup)
     int lo = 0, hi = a.B;  // largest b with pre[b] <= t
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
@@ -152,6 +174,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const u32x4 v = ld16(qh + 8 * (4 * s + c));
         qop[s] = as_bf16x8(g < a.G ? v : z);
       }
+      wait_vmem();
     }
 
     float m_run = -INFINITY, l_run = 0.f;
@@ -174,9 +197,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     };
 
-    load_tile(tile0, kc, vc);
-    for (int tile = tile0; tile < tile1; ++tile) {
-      if (tile + 1 < tile1) load_tile(tile + 1, kn, vn);
+    // this wave's tiles of the piece: tile0 + wave, + kWaves, ...
+    const int first = tile0 + wave;
+    if (first < tile1) load_tile(first, kc, vc);
+    for (int tile = first; tile < tile1; tile += kWaves) {
+      const bool more = tile + kWaves < tile1;
+      if (more) load_tile(tile + kWaves, kn, vn);
       const int p0 = tile * kTile;
 
       f32x4 sc[2];
@@ -185,22 +211,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int s = 0; s < 4; ++s) acc = mfma16(as_bf16x8(kc[r][s]), qop[s], acc);
         sc[r] = acc;
       }
+      // running max on raw scores (scale > 0), exponent as one fma
       float x[8];
       float mx = -INFINITY;
       for (int r = 0; r < 2; ++r)
         for (int i = 0; i < 4; ++i) {
           const int pos = p0 + 8 * c + 4 * r + i;
-          const float v = pos < L ? sc[r][i] * a.qk_scale : -INFINITY;
+          const float v = pos < L ? sc[r][i] : -INFINITY;
           x[4 * r + i] = v;
           mx = fmaxf(mx, v);
         }
       mx = wave_max_xor(mx, 16);
       mx = wave_max_xor(mx, 32);
-      const float m_new = fmaxf(m_run, mx);
+      const float m_new = fmaxf(m_run, mx * a.qk_scale);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       float psum = 0.f;
       for (int e = 0; e < 8; ++e) {
-        x[e] = __builtin_amdgcn_exp2f(x[e] - m_new);
+        x[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a.qk_scale, -m_new));
         psum += x[e];
       }
       l_run = l_run * alpha + psum;
@@ -218,13 +245,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int j = 0; j < 8; ++j) {
         u32x4 av;
         for (int tt = 0; tt < 4; ++tt) {
-          const uint32_t lo = vc[2 * tt][j >> 1];
-          const uint32_t hi = vc[2 * tt + 1][j >> 1];
-          av[tt] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+          const uint32_t lo2 = vc[2 * tt][j >> 1];
+          const uint32_t hi2 = vc[2 * tt + 1][j >> 1];
+          av[tt] = (j & 1) ? ((lo2 >> 16) | (hi2 & 0xffff0000u)) : ((lo2 & 0xffffu) | (hi2 << 16));
         }
         o[j] = mfma16(as_bf16x8(av), pop, o[j]);
       }
-      if (tile + 1 < tile1) {
+      if (more) {
         for (int r = 0; r < 2; ++r)
           for (int s = 0; s < 4; ++s) kc[r][s] = kn[r][s];
         for (int kk = 0; kk < 8; ++kk) vc[kk] = vn[kk];
@@ -234,83 +261,125 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float l_tot = l_run + __shfl_xor(l_run, 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
 
-    // lane (g, c) holds O[g][32c + 8i + j] = o[j][i]
+    // publish this wave's state: lane (g, c) holds O[g][32c + 8i + j] = o[j][i]
+    if (c == 0) {
+      cmb.m[wave][g] = m_run;
+      cmb.l[wave][g] = l_tot;
+    }
+    for (int i = 0; i < 4; ++i) {
+      float* dst = &cmb.o[wave][g][32 * c + 8 * i];
+      *(f32x4*)dst = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
+      *(f32x4*)(dst + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
+    }
+    __syncthreads();
+
+    // combine the four waves; thread e covers (head e / 128, dim e % 128)
     const bool single = worker_of(seg_first, total, a.W) == worker_of(seg_end - 1, total, a.W);
-    if (g < a.G) {
+    const int64_t s = (int64_t)b * a.Hkv + kh;
+    for (int e = tid; e < a.G * kD; e += blockDim.x) {
+      const int gg = e / kD, d = e % kD;
+      float M = -INFINITY;
+      for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, cmb.m[ww][gg]);
+      float Lsum = 0.f, acc = 0.f;
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const float sc = __builtin_amdgcn_exp2f(cmb.m[ww][gg] - M);  // idle waves: m = -inf -> 0
+        Lsum += sc * cmb.l[ww][gg];
+        acc += sc * cmb.o[ww][gg][d];
+      }
       if (single) {
-        const float inv = 1.0f / l_tot;
-        uint16_t* dst = a.out + ((int64_t)b * a.Hq + (int64_t)kh * a.G + g) * kD + 32 * c;
-        for (int i = 0; i < 4; ++i) {
-          u32x4 wv;
-          for (int jj = 0; jj < 4; ++jj) wv[jj] = pack_bf16x2(o[2 * jj][i] * inv, o[2 * jj + 1][i] * inv);
-          *(u32x4*)(dst + 8 * i) = wv;
-        }
+        a.out[((int64_t)b * a.Hq + (int64_t)kh * a.G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(acc / Lsum);
       } else {
-        const int64_t piece = (int64_t)w + (int64_t)b * a.Hkv + kh;
-        float* P = a.part + (piece * a.G + g) * kPieceStride;
-        if (c == 0) {
-          P[0] = m_run;
-          P[1] = l_tot;
+        float* P = a.part + (((int64_t)w + s) * a.G + gg) * kPieceStride;
+        if (d == 0) {
+          P[0] = M;
+          P[1] = Lsum;
         }
-        for (int i = 0; i < 4; ++i) {
-          float* dst = P + 4 + 32 * c + 8 * i;
-          *(f32x4*)dst = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
-          *(f32x4*)(dst + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
-        }
+        P[4 + d] = acc;
       }
     }
+    __syncthreads();  // cmb is reused by the next piece
     t = piece_end;
   }
 }
 
-// One wave per (segment, query head): log-sum-exp merge of the pieces of
-// segments that span several workers; zero output for empty segments.
+// One workgroup per segment that spans several workgroups: log-sum-exp merge
+// of its partial slots. The (m, l) pairs of all pieces are staged in LDS by
+// the whole workgroup first, so each output element then streams its piece
+// values with independent loads.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t sg = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  const int S = a.B * a.Hkv;
-  if (sg >= (int64_t)S * a.G) return;
-  const int s = (int)(sg / a.G);
-  const int g = (int)(sg % a.G);
-  const int b = s / a.Hkv;
-  const int kh = s % a.Hkv;
-  uint32_t* dst = (uint32_t*)(a.out + ((int64_t)b * a.Hq + (int64_t)kh * a.G + g) * kD) + lane;
+  __shared__ int32_t pre[kMaxB + 1];
+  __shared__ float sm[kMaxWorkers * 2];  // per (piece, head): m, then l in the second half
+  build_prefix(a, pre);
+  const int64_t total = pre[a.B];
+  const int64_t s = blockIdx.x;
+  const int b = (int)(s / a.Hkv), kh = (int)(s % a.Hkv);
   const int L = clamp_len(a.len[b], a.cap);
-  if (L == 0) {
-    *dst = 0u;
-    return;
-  }
+  if (L == 0 || total == 0) return;
   const int nb = (L + kTile - 1) / kTile;
-  const int64_t total = a.hdr[a.B];
-  const int64_t seg_first = a.hdr[b] + (int64_t)kh * nb;
+  const int64_t seg_first = pre[b] + (int64_t)kh * nb;
   const int64_t seg_end = seg_first + nb;
-  const int64_t w0 = worker_of(seg_first, total, a.W);
-  const int64_t w1 = worker_of(seg_end - 1, total, a.W);
-  if (w0 == w1) return;  // written by the decode kernel
-  float M = -INFINITY;
-  for (int64_t w = w0; w <= w1; ++w) {
-    if (worker_begin(w, total, a.W) == worker_begin(w + 1, total, a.W)) continue;
-    const float* P = a.part + ((w + s) * a.G + g) * kPieceStride;
-    M = fmaxf(M, P[0]);
+  const int w0 = (int)worker_of(seg_first, total, a.W);
+  const int w1 = (int)worker_of(seg_end - 1, total, a.W);
+  if (w0 == w1) return;  // written directly by decode_kernel
+  const int P = w1 - w0 + 1;
+  const int G = a.G;
+  // pieces are processed in chunks that fit the staging area
+  const int chunk = kMaxWorkers * 2 / (2 * G);
+  float M_acc[kD * 16 / 256], L_acc[kD * 16 / 256], O_acc[kD * 16 / 256];
+  const int per_thread = (G * kD + blockDim.x - 1) / blockDim.x;
+  for (int i = 0; i < per_thread; ++i) {
+    M_acc[i] = -INFINITY;
+    L_acc[i] = 0.f;
+    O_acc[i] = 0.f;
   }
-  float lsum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int64_t w = w0; w <= w1; ++w) {
-    if (worker_begin(w, total, a.W) == worker_begin(w + 1, total, a.W)) continue;
-    const float* P = a.part + ((w + s) * a.G + g) * kPieceStride;
-    const float sc = __builtin_amdgcn_exp2f(P[0] - M);
-    lsum += sc * P[1];
-    o0 += sc * P[4 + 2 * lane];
-    o1 += sc * P[5 + 2 * lane];
+  for (int c0 = 0; c0 < P; c0 += chunk) {
+    const int n = P - c0 < chunk ? P - c0 : chunk;
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < n * G; idx += blockDim.x) {
+      const int w = w0 + c0 + idx / G, gg = idx % G;
+      float m = -INFINITY, l = 0.f;
+      if (worker_nonempty(w, total, a.W)) {  // empty workers wrote nothing this call
+        const float* Pp = a.part + (((int64_t)w + s) * G + gg) * kPieceStride;
+        m = Pp[0];
+        l = Pp[1];
+      }
+      sm[idx] = m;
+      sm[kMaxWorkers + idx] = l;
+    }
+    __syncthreads();
+    for (int i = 0; i < per_thread; ++i) {
+      const int e = threadIdx.x + i * blockDim.x;
+      if (e >= G * kD) break;
+      const int gg = e / kD, d = e % kD;
+      float Mc = M_acc[i];
+      for (int p = 0; p < n; ++p) Mc = fmaxf(Mc, sm[p * G + gg]);
+      const float r = __builtin_amdgcn_exp2f(M_acc[i] - Mc);
+      float lsum = L_acc[i] * r, acc = O_acc[i] * r;
+#pragma unroll 8
+      for (int p = 0; p < n; ++p) {
+        const float sc = __builtin_amdgcn_exp2f(sm[p * G + gg] - Mc);  // empty pieces: 0
+        lsum += sc * sm[kMaxWorkers + p * G + gg];
+        const float v = a.part[(((int64_t)w0 + c0 + p + s) * G + gg) * kPieceStride + 4 + d];
+        acc += sc == 0.f ? 0.f : sc * v;  // stale slots of empty pieces never leak in
+      }
+      M_acc[i] = Mc;
+      L_acc[i] = lsum;
+      O_acc[i] = acc;
+    }
   }
-  const float inv = 1.0f / lsum;
-  *dst = pack_bf16x2(o0 * inv, o1 * inv);
+  for (int i = 0; i < per_thread; ++i) {
+    const int e = threadIdx.x + i * blockDim.x;
+    if (e >= G * kD) break;
+    const int gg = e / kD, d = e % kD;
+    a.out[((int64_t)b * a.Hq + (int64_t)kh * G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(O_acc[i] / L_acc[i]);
+  }
 }
 
 int max_workers() {
   static int w = [] {
     const char* e = getenv("EMA_DECODE_WORKERS");
     int v = e ? atoi(e) : 0;
-    return v > 0 ? v : 2048;
+    return v > 0 && v <= kMaxWorkers ? v : kMaxWorkers;
   }();
   return w;
 }
@@ -319,8 +388,10 @@ int max_workers() {
 
 DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len) {
   DecodePlan p;
+  // at least one tile per wave of each workgroup
   const int64_t tiles = (int64_t)B * Hkv * ((max_len + kTile - 1) / kTile);
-  int64_t w = tiles < max_workers() ? tiles : max_workers();
+  const int64_t want = (tiles + kWaves - 1) / kWaves;
+  int64_t w = want < max_workers() ? want : max_workers();
   if (w < 1) w = 1;
   p.workers = (int)w;
   p.segments = B * Hkv;
@@ -329,7 +400,7 @@ DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len) {
   return p;
 }
 
-uint64_t decode_header_bytes() { return (uint64_t)kHeaderInts * sizeof(int32_t); }
+uint64_t decode_workspace_bytes(const DecodePlan& p) { return p.part_bytes; }
 
 int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, const int32_t* len,
                       int Hq, float scale, void* out, void* ws, const DecodePlan& plan) {
@@ -346,8 +417,7 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.v = (const uint16_t*)c.v;
   a.len = len;
   a.out = (uint16_t*)out;
-  a.hdr = (int32_t*)ws;
-  a.part = (float*)((char*)ws + decode_header_bytes());
+  a.part = (float*)ws;
   a.sb = c.stride_batch;
   a.sh = c.stride_head;
   a.sp = c.stride_pos;
@@ -358,14 +428,14 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.G = G;
   a.cap = c.capacity;
   a.W = plan.workers;
-  const int blocks = (plan.workers + kWaves - 1) / kWaves;
-  hipLaunchKernelGGL(decode_kernel, dim3(blocks), dim3(kWaves * 64), 0, s, a);
+  hipLaunchKernelGGL(decode_kernel, dim3(plan.workers), dim3(kWaves * 64), 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");
   if (rc) return rc;
-  const int64_t merge_waves = (int64_t)plan.segments * G;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((merge_waves + kWaves - 1) / kWaves)),
-                     dim3(kWaves * 64), 0, s, a);
-  return check_hip(hipGetLastError(), "ema_decode_attention merge launch");
+  if (plan.workers > 1) {
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(plan.segments), dim3(256), 0, s, a);
+    rc = check_hip(hipGetLastError(), "ema_decode_attention merge launch");
+  }
+  return rc;
 }
 
 }  // namespace ema

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   // heaviest (latest) query blocks first
   const int qb = a.nqb - 1 - (int)(blockIdx.x % a.nqb);
   const int h = (int)((blockIdx.x / a.nqb) % a.Hq);
@@ -91,6 +91,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   {
     const uint16_t* qp = a.q + (((int64_t)b * a.Hq + h) * a.T + qr_c) * kD + 8 * hh;
     for (int s = 0; s < 8; ++s) qop[s] = as_bf16x8(ld16(qp + 16 * s));
+    wait_vmem();
   }
 
   const uint16_t* Kg = a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh;
@@ -143,44 +144,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (active) {
       const uint16_t* Kt = Ks + buf * kKTile;
       const uint16_t* Vt = Vs + buf * kVTile;
+      // two independent accumulation chains (sub-tiles kt = 0, 1), interleaved
       f32x16 sc[2];
-      for (int kt = 0; kt < 2; ++kt) {
-        f32x16 acc;
-        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-        const uint16_t* kp = Kt + (kt * 32 + (lane & 31)) * kKStride + 8 * hh;
-        for (int s = 0; s < 8; ++s) acc = mfma32(as_bf16x8(*(const u32x4*)(kp + 16 * s)), qop[s], acc);
-        sc[kt] = acc;
-      }
-      // scale + mask; key of slot i in sub-tile kt: kbase + 32kt + (i%4) + 8(i/4) + 4hh
+      for (int kt = 0; kt < 2; ++kt)
+        for (int i = 0; i < 16; ++i) sc[kt][i] = 0.f;
+      const uint16_t* kp = Kt + (lane & 31) * kKStride + 8 * hh;
+      for (int s = 0; s < 8; ++s)
+        for (int kt = 0; kt < 2; ++kt)
+          sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(kp + kt * 32 * kKStride + 16 * s)), qop[s], sc[kt]);
+      // mask on raw scores; key of slot i in sub-tile kt: kbase + 32kt + (i%4) + 8(i/4) + 4hh
       const bool need_mask = kbase < kv_begin || kbase + kBN > kv_len ||
                              (causal && kbase + kBN - 1 > wave_first_abs);
-      float mx = -INFINITY;
-      for (int kt = 0; kt < 2; ++kt)
-        for (int i = 0; i < 16; ++i) {
-          float x = sc[kt][i] * a.qk_scale;
-          if (need_mask) {
+      if (need_mask) {
+        for (int kt = 0; kt < 2; ++kt)
+          for (int i = 0; i < 16; ++i) {
             const int key = kbase + 32 * kt + (i & 3) + 8 * (i >> 2) + 4 * hh;
             const bool ok = key >= kv_begin && key < kv_len && (!causal || key <= q_abs);
-            x = ok ? x : -INFINITY;
+            sc[kt][i] = ok ? sc[kt][i] : -INFINITY;
           }
-          sc[kt][i] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = wave_max_xor(mx, 32);
-      const float m_new = fmaxf(m_run, mx);
-      // a row with nothing visible yet keeps m = -inf; use 0 as the exp base then
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      }
+      float mx = -INFINITY;
+      for (int kt = 0; kt < 2; ++kt)
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[kt][i]);
+      mx = wave_max_xor(mx, 32) * a.qk_scale;  // scale > 0: max commutes with it
+      // Lazy rescale: the running max (log2 domain) moves only when a row's max
+      // grows by more than 8, so p = 2^(s - m) stays <= 256 and the O/l rescale
+      // is skipped for most blocks. Any m gives the same normalised result.
+      if (__any(mx > m_run + 8.f)) {
+        const float m_new = mx > m_run + 8.f ? mx : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf -> 0
+        l_run *= alpha;
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        m_run = m_new;
+      }
+      // rows with nothing visible yet keep m = -inf: use 0 as the base (all p = 0)
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
       float psum = 0.f;
       for (int kt = 0; kt < 2; ++kt)
         for (int i = 0; i < 16; ++i) {
-          const float p = __builtin_amdgcn_exp2f(sc[kt][i] - m_use);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][i], a.qk_scale, -m_use));
           sc[kt][i] = p;
           psum += p;
         }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      l_run += psum;
 
       // PV: step st covers S^T slots 8*(st&1) .. +7 of sub-tile st>>1
       for (int st = 0; st < 4; ++st) {

@@ -177,6 +177,14 @@ def decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_len) -> int:
     return out.value
 
 
+def decode_workspace(batch, n_heads, n_kv_heads, head_dim, max_len, device="cuda", stream=None):
+    """Allocate a decode workspace (reusable across calls on one stream)."""
+    import torch
+
+    n = decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_len)
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
 def decode_attention(q, cache: StaticCache, lengths, max_len, scale=None, out=None, workspace=None, stream=None):
     """q [B,Hq,D] (or [B,Hq,1,D]) bf16; lengths int32 device [B]. Returns out [B, Hq*D]."""
     import torch
@@ -188,8 +196,7 @@ def decode_attention(q, cache: StaticCache, lengths, max_len, scale=None, out=No
     if out is None:
         out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=q.device)
     if workspace is None:
-        n = decode_workspace_size(B, Hq, cache.desc.n_kv_heads, D, max_len)
-        workspace = torch.empty(n, dtype=torch.uint8, device=q.device)
+        workspace = decode_workspace(B, Hq, cache.desc.n_kv_heads, D, max_len, device=q.device, stream=stream)
     _check(lib().ema_decode_attention(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(lengths), max_len, Hq,
                                       scale, _ptr(out), _ptr(workspace), workspace.numel()), "ema_decode_attention")
     return out

@@ -123,10 +123,11 @@ EMA_API int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const vo
                           int32_t head_dim, uint32_t flags, void* q_out,
                           const ema_kvcache_desc* cache);
 
-/* Workspace (bytes) ema_decode_attention needs for this shape. */
+/* Workspace (bytes) ema_decode_attention needs for this shape: per-piece
+ * partial softmax states of the split (no initialisation needed; calls that
+ * share one workspace must not overlap). */
 EMA_API int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_t n_kv_heads,
                                   int32_t head_dim, int32_t max_len, uint64_t* bytes);
-
 /* Batched single-token decode attention over the static cache
  * (MlxCtx::sdpa_masked with the static mask, compiled.rs:163 / decode_eager.rs:140).
  *   q        [batch, n_heads, head_dim] bf16 (post norm/RoPE)

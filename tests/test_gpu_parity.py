@@ -195,6 +195,28 @@ def test_decode_split_invariance(ema, ora, max_len):
     assert_close(got, ref, f"decode max_len={max_len}")
 
 
+def test_decode_workspace_reuse_is_clean(ema, ora):
+    """Reusing one workspace across calls with different lengths (stale partial
+    slots from earlier calls) gives the same bits as fresh workspaces."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 4, 32, 8, 128, 2048
+    q = ora.normal_bf16((B, Hq, 1, D), seed=235)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=236)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=237)
+    cache = make_cache(ema, kc, vc)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+    qd = dev(q)
+    for lengths in ([2048, 1, 700, 1500], [64, 2048, 2048, 3], [2048] * 4, [1500, 900, 33, 1]):
+        L = np.asarray(lengths, np.int32)
+        say(f"decode workspace reuse lengths={lengths}")
+        shared = host(ema.decode_attention(qd, cache, dev(L), cap, workspace=ws))
+        fresh = host(ema.decode_attention(qd, cache, dev(L), cap))
+        torch.cuda.synchronize()
+        assert np.array_equal(shared, fresh)
+        assert_close(shared, ora.sdpa(q, kc, vc, L, scale_of(D), False), "reused workspace")
+
+
 def test_decode_qwen3_1p7b_shape(ema, ora):
     """batch 1, 16q/8kv, D 128, cap 4096, 1024 valid positions."""
     say("decode B1 16q/8kv cap 4096 L 1024")
@@ -323,3 +345,45 @@ def test_decode_step_pre_attention_then_attention(ema, ora):
     out = ema.decode_attention(q, cache, dev(off + 1), cap)
     torch.cuda.synchronize()
     assert_close(host(out), ref, "decode step")
+
+
+def test_graph_replay_matches_eager(ema, ora):
+    """The decode step (pre-attention + decode) captured in a HIP graph: every
+    replay, with eager work and synchronisation in between, equals the eager result."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 4, 16, 8, 128, 1024
+    off = np.array([100, 1023, 0, 512], np.int32)
+    qkv = dev(ora.normal_bf16((B, 1, (Hq + 2 * Hkv) * D), seed=500))
+    qw = dev(ora.normal_bf16(D, seed=501, mean=1.0, std=0.02))
+    kw = dev(ora.normal_bf16(D, seed=502, mean=1.0, std=0.02))
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=503)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=504)
+    cache = make_cache(ema, kc, vc)
+    off_d, len_d = dev(off), dev(off + 1)
+    q = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device="cuda")
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+
+    def step():
+        ema.pre_attention(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, q_out=q)
+        ema.decode_attention(q, cache, len_d, cap, out=out, workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    eager = host(out).copy()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), eager), f"replay {i}"
+        step()  # eager work between replays
+        torch.cuda.synchronize()
