@@ -17,6 +17,11 @@
 //                                          after exp, unmoved)
 // Each lane therefore owns one query row's scores, running max, row sum and
 // 64 output accumulators; the row max needs one xor-32 exchange per block.
+//
+// Two workgroups share a CU (2 waves per SIMD). The MFMA sections run at raised
+// wave priority (s_setprio 1) and the softmax at normal priority, so when both
+// waves of a SIMD are ready the arbiter issues the matrix work first and the
+// other wave's softmax VALU fills the gaps (ping-pong between the two waves).
 #include "ema_common.hpp"
 
 namespace ema {
@@ -30,6 +35,7 @@ constexpr int kVStride = kD + 32; // LDS row stride of the V tile: conflict-free
 constexpr int kKTile = kBN * kKStride;
 constexpr int kVTile = kBN * kVStride;
 constexpr int kLdsBytes = 2 * (kKTile + kVTile) * 2;
+constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dispatched round-robin
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -55,11 +61,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  // heaviest (latest) query blocks first
-  const int qb = a.nqb - 1 - (int)(blockIdx.x % a.nqb);
-  const int h = (int)((blockIdx.x / a.nqb) % a.Hq);
-  const int b = (int)(blockIdx.x / ((unsigned)a.nqb * a.Hq));
-  const int kh = h / a.G;
+  // Grid mapping. Workgroups are dispatched round-robin over the 8 XCDs (x % 8), each
+  // with its own L2. When the (batch, kv head) groups divide evenly over the XCDs, all
+  // query heads of a group run on the group's XCD, so its K/V stream is read from HBM
+  // once and served from that L2 to every workgroup that attends over it. Inside an XCD
+  // (or over the whole grid otherwise) work items are ranked heaviest first (a later
+  // query block sees more keys) and the second half of the local index range takes the
+  // ranks in reverse, so the two workgroups that share a CU (local indices i and
+  // i + n/2 when they are resident together) carry complementary causal work.
+  const int groups = a.B * a.Hkv;
+  const bool by_xcd = groups % kXcds == 0 && gridDim.x % kXcds == 0;
+  const int64_t x = blockIdx.x;
+  const int64_t n_local = by_xcd ? gridDim.x / kXcds : gridDim.x;
+  const int64_t li = by_xcd ? x / kXcds : x;
+  const int64_t half = (n_local + 1) / 2;
+  const int64_t rank = li < half ? li : n_local - 1 - (li - half);
+  const int groups_local = by_xcd ? groups / kXcds : groups;
+  const int per_qb = groups_local * a.G;
+  const int qb = a.nqb - 1 - (int)(rank / per_qb);
+  const int rest = (int)(rank % per_qb);
+  const int grp_id = by_xcd ? (rest / a.G) * kXcds + (int)(x % kXcds) : rest / a.G;
+  const int b = grp_id / a.Hkv;
+  const int h = (grp_id % a.Hkv) * a.G + rest % a.G;
+  const int kh = grp_id % a.Hkv;
 
   int q_off = a.q_off[b];
   q_off = q_off < 0 ? 0 : q_off;
@@ -94,28 +118,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     wait_vmem();
   }
 
-  const uint16_t* Kg = a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh;
-  const uint16_t* Vg = a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh;
+  const char* Kg = (const char*)(a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh);
+  const char* Vg = (const char*)(a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh);
+  const int64_t blk_bytes = (int64_t)kBN * a.sp * 2;
 
-  // global -> register staging: 4 K chunks + 4 V chunks of 16 B per thread
+  // global -> register staging: the thread owns rows rr + 16i (i < 4) of a block at
+  // 16-byte column cc, for K and for V
+  const int rr = tid >> 4, cc = (tid & 15) * 8;
+  uint32_t toff[4];
+  for (int i = 0; i < 4; ++i) toff[i] = (uint32_t)(((int64_t)(rr + 16 * i) * a.sp + cc) * 2);
   u32x4 kst[4], vst[4];
   auto gload = [&](int blk) {
     const int base = blk * kBN;
-    for (int i = 0; i < 4; ++i) {
-      const int id = tid + 256 * i;
-      int r = base + (id >> 4);
-      r = r < kv_len ? r : kv_len - 1;
-      const int col = (id & 15) * 8;
-      kst[i] = ld16(Kg + (int64_t)r * a.sp + col);
-      vst[i] = ld16(Vg + (int64_t)r * a.sp + col);
+    if (base + kBN <= kv_len) {  // whole block valid: uniform block base + 32-bit offsets
+      const char* kp = Kg + (int64_t)blk * blk_bytes;
+      const char* vp = Vg + (int64_t)blk * blk_bytes;
+      for (int i = 0; i < 4; ++i) {
+        kst[i] = *(const u32x4*)(kp + toff[i]);
+        vst[i] = *(const u32x4*)(vp + toff[i]);
+      }
+    } else {  // tail block: clamp rows to the last valid one (masked later)
+      for (int i = 0; i < 4; ++i) {
+        int r = base + rr + 16 * i;
+        r = r < kv_len ? r : kv_len - 1;
+        kst[i] = *(const u32x4*)(Kg + ((int64_t)r * a.sp + cc) * 2);
+        vst[i] = *(const u32x4*)(Vg + ((int64_t)r * a.sp + cc) * 2);
+      }
     }
   };
   auto sstore = [&](int buf) {
     for (int i = 0; i < 4; ++i) {
-      const int id = tid + 256 * i;
-      const int r = id >> 4, col = (id & 15) * 8;
-      *(u32x4*)(Ks + buf * kKTile + r * kKStride + col) = kst[i];
-      *(u32x4*)(Vs + buf * kVTile + r * kVStride + col) = vst[i];
+      *(u32x4*)(Ks + buf * kKTile + (rr + 16 * i) * kKStride + cc) = kst[i];
+      *(u32x4*)(Vs + buf * kVTile + (rr + 16 * i) * kVStride + cc) = vst[i];
     }
   };
 
@@ -149,9 +183,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int kt = 0; kt < 2; ++kt)
         for (int i = 0; i < 16; ++i) sc[kt][i] = 0.f;
       const uint16_t* kp = Kt + (lane & 31) * kKStride + 8 * hh;
+      __builtin_amdgcn_s_setprio(1);
       for (int s = 0; s < 8; ++s)
         for (int kt = 0; kt < 2; ++kt)
           sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(kp + kt * 32 * kKStride + 16 * s)), qop[s], sc[kt]);
+      __builtin_amdgcn_s_setprio(0);
       // mask on raw scores; key of slot i in sub-tile kt: kbase + 32kt + (i%4) + 8(i/4) + 4hh
       const bool need_mask = kbase < kv_begin || kbase + kBN > kv_len ||
                              (causal && kbase + kBN - 1 > wave_first_abs);
@@ -189,6 +225,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       l_run += psum;
 
       // PV: step st covers S^T slots 8*(st&1) .. +7 of sub-tile st>>1
+      __builtin_amdgcn_s_setprio(1);
       for (int st = 0; st < 4; ++st) {
         const int kt = st >> 1, q2 = st & 1;
         u32x4 pw;
@@ -207,6 +244,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if (more) sstore(buf ^ 1);
     __syncthreads();
   }

@@ -278,6 +278,15 @@ def test_prefill_small(ema, ora, T, q_off, causal, chunk, G):
     assert_close(got, ref, f"prefill T={T}")
 
 
+@pytest.mark.parametrize("causal,chunk", [(True, False), (False, False), (True, True)])
+def test_prefill_xcd_grid_mapping(ema, ora, causal, chunk):
+    """batch x kv heads a multiple of 8 (the XCD-grouped grid order), ragged offsets."""
+    B, Hq, Hkv, D, cap, T = 4, 8, 2, 128, 640, 300
+    say(f"prefill xcd mapping causal={causal} chunk={chunk}")
+    got, ref = _prefill_case(ema, ora, B, Hq, Hkv, D, cap, T, [0, 37, 300, 129], causal, chunk, seed=340)
+    assert_close(got, ref, "prefill xcd mapping")
+
+
 def test_prefill_qwen3_1p7b_2k(ema, ora):
     """1 x 2048 tokens, 16q/8kv, causal from offset 0 (heads 0-3 checked)."""
     say("prefill T=2048 16q/8kv causal")
