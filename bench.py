@@ -4,15 +4,20 @@
 Headline workload (the metric's decode half): Qwen3-8B-shape batched decode
 step, batch 32, 32 query / 8 KV heads, head_dim 128, bf16 static cache of
 capacity 8192 per sequence, valid lengths uniform in [512, 8192] (seed 1234).
-One step = the fused pre-attention for one new token per sequence (q/k
-RMSNorm, RoPE, K/V written at offset len-1) followed by decode attention over
-len positions. value = algorithmic bytes of the step / step time.
+One step = the pre-attention for one new token per sequence (q/k RMSNorm,
+RoPE, K/V written at offset len-1) and decode attention over len positions,
+issued as one fused ema_decode_step call. value = algorithmic bytes of the
+step / step time.
 
 The other shapes are measured after it and reported under "secondary"
 (prefill TFLOP/s for the metric's prefill half, the remaining configurations).
 Inputs are synthetic (seeded normal), already resident in HBM.
 
-python bench.py [--steps K] [--warmup W] [--only primary] [--no-cpu-baseline]
+python bench.py [--steps K] [--warmup W] [--only primary] [--no-cpu-baseline] [--calibrate-copy]
+
+--calibrate-copy first copies 1 GiB device-to-device (torch), so a FETCH_SIZE /
+WRITE_SIZE counter profile of the same command holds a copy kernel of known
+size to scale the counters by.
 """
 import argparse
 import json
@@ -42,6 +47,7 @@ def parse():
     p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk"], default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--calibrate-copy", action="store_true")
     return p.parse_args()
 
 
@@ -115,41 +121,39 @@ def primary(ctx, ema, args):
     ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
     scale = 1.0 / math.sqrt(D)
 
-    def pre():
-        ema.pre_attention(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, q_out=q)
+    def step():
+        ema.decode_step(qkv2d, qw, kw, 1e-6, 1e6, off_d, Hq, cache, cap, scale, out=out, workspace=ws)
 
-    def attn():
-        ema.decode_attention(q, cache, len_d, cap, scale, out=out, workspace=ws)
-
+    qkv2d = qkv.reshape(B, -1)
     for _ in range(args.warmup):
-        pre()
-        attn()
+        step()
     torch.cuda.synchronize()
+    # One step is one ema_decode_step call (two kernels on this stream), so the
+    # events around the K timed steps also give the call's average duration.
     K = args.steps
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t0.record()
-    for i in range(K):
-        pre()
-        ev[i][0].record()
-        attn()
-        ev[i][1].record()
+    for _ in range(K):
+        step()
     t1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_step = t0.elapsed_time(t1) / K
-    ms_attn = sum(a.elapsed_time(b) for a, b in ev) / K
+    ms_call = ms_step
     ab = decode_bytes(lengths, Hq, Hkv, D)
     sb = ab + pre_bytes(B, 1, Hq, Hkv, D)
     res = {
         "lengths_sum": int(lengths.sum()), "step_bytes": sb, "attn_bytes": ab,
-        "ms_per_step": ms_step, "attn_ms": ms_attn, "wall_s": wall,
-        "step_gbs": sb / (ms_step * 1e-3) / 1e9, "attn_gbs": ab / (ms_attn * 1e-3) / 1e9,
+        "ms_per_step": ms_step, "call_ms": ms_call, "wall_s": wall,
+        "step_gbs": sb / (ms_step * 1e-3) / 1e9, "call_gbs": sb / (ms_call * 1e-3) / 1e9,
     }
-    log(f"[bench] decode step {ms_step*1e3:.1f} us ({res['step_gbs']:.0f} GB/s); "
-        f"attention {ms_attn*1e3:.1f} us ({res['attn_gbs']:.0f} GB/s, {res['attn_gbs']/HBM_PEAK_GBS:.1%} of HBM)")
+    log(f"[bench] fused decode step {ms_step*1e3:.1f} us per step ({res['step_gbs']:.0f} GB/s); "
+        f"per call {ms_call*1e3:.1f} us ({res['call_gbs']:.0f} GB/s, {res['call_gbs']/HBM_PEAK_GBS:.1%} of HBM)")
+    # q of the last step, for the CPU baseline (same inputs the GPU attended with)
+    ema.pre_attention(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, q_out=q)
+    torch.cuda.synchronize()
     state = dict(cache=cache, q=q, lengths=lengths, Hq=Hq, Hkv=Hkv, D=D, cap=cap, scale=scale, bytes=ab)
     return res, state
 
@@ -216,6 +220,35 @@ def bench_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
     return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
 
 
+def bench_decode_pair(ctx, ema, name, steps=20):
+    """The same batch-32 step as two calls: ema_pre_attention (T=1) + ema_decode_attention."""
+    import numpy as np
+
+    torch = ctx.torch
+    B, Hq, Hkv, D, cap = 32, 32, 8, 128, 8192
+    lengths = np.random.default_rng(1234).integers(512, 8193, size=B)
+    cache = ema.StaticCache(B, Hkv, cap, D, k=ctx.randn((B, Hkv, cap, D)), v=ctx.randn((B, Hkv, cap, D)))
+    qkv = ctx.randn((B, 1, (Hq + 2 * Hkv) * D))
+    qw, kw = ctx.randn((D,), 1.0, 0.02), ctx.randn((D,), 1.0, 0.02)
+    off_d, len_d = ctx.i32(lengths - 1), ctx.i32(lengths)
+    q = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=ctx.dev)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+
+    def pair():
+        ema.pre_attention(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, q_out=q)
+        ema.decode_attention(q, cache, len_d, cap, out=out, workspace=ws)
+
+    ms = time_calls(torch, pair, steps, 5)
+    ms_attn = time_calls(torch, lambda: ema.decode_attention(q, cache, len_d, cap, out=out, workspace=ws), steps, 5)
+    by = decode_bytes(lengths, Hq, Hkv, D)
+    sb = by + pre_bytes(B, 1, Hq, Hkv, D)
+    log(f"[bench] {name}: step {ms*1e3:.1f} us ({sb/(ms*1e-3)/1e9:.0f} GB/s); decode attention alone "
+        f"{ms_attn*1e3:.1f} us ({by/(ms_attn*1e-3)/1e9:.0f} GB/s)")
+    return {"workload": name, "us": ms * 1e3, "gbs": sb / (ms * 1e-3) / 1e9, "attn_us": ms_attn * 1e3,
+            "attn_gbs": by / (ms_attn * 1e-3) / 1e9, "frac_of_peak": by / (ms_attn * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
 def bench_pre(ctx, ema, name, T, Hq, Hkv, D, cap, steps=20):
     torch = ctx.torch
     cache = ema.StaticCache(1, Hkv, cap, D)
@@ -249,6 +282,13 @@ def main():
 
     ema.lib()
     ctx = Ctx()
+    if args.calibrate_copy:  # a copy kernel of known size (1 GiB read + 1 GiB write)
+        src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     res, state = primary(ctx, ema, args)
     secondary = []
     if args.only in ("all", "prefill"):
@@ -257,6 +297,7 @@ def main():
         secondary.append(bench_prefill(ctx, ema, "prefill_causal_T2048_16q8kv_qwen3_1p7b", 1, 16, 8, 128, 4096, 2048, 0))
         secondary.append(bench_pre(ctx, ema, "pre_attention_T2048_16q8kv", 2048, 16, 8, 128, 4096))
         secondary.append(bench_decode(ctx, ema, "decode_B1_16q8kv_L1024_cap4096", 1, 16, 8, 128, 4096, [1024]))
+        secondary.append(bench_decode_pair(ctx, ema, "decode_B32_32q8kv_unfused_pre_attention_plus_attention"))
     if args.only in ("all", "decode_long"):
         secondary.append(bench_decode(ctx, ema, "decode_B8_32q4kv_L32768", 8, 32, 4, 128, 32768, [32768] * 8))
     if args.only in ("all", "prefill_chunk"):
@@ -281,15 +322,15 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) q/K/V and qkv, norm weights 1+N(0,0.02), lengths U[512,8192] seed 1234",
         "config": {
-            "workload": "qwen3_8b_batched_decode_step: pre-attention (T=1) + decode attention",
+            "workload": "qwen3_8b_batched_decode_step: pre-attention (T=1) + decode attention (fused ema_decode_step)",
             "batch": 32, "n_heads": 32, "n_kv_heads": 8, "head_dim": 128, "capacity": 8192,
             "lengths_sum": res["lengths_sum"], "parallelism": "single_gpu",
         },
         "roofline": {
-            "bound": "hbm", "kernel": "decode attention (decode_kernel + decode_merge_kernel)",
-            "achieved": round(res["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(res["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-            "attn_us": round(res["attn_ms"] * 1e3, 2), "attn_bytes": res["attn_bytes"],
+            "bound": "hbm", "kernel": "ema_decode_step (decode_kernel<fused> + decode_merge_kernel)",
+            "achieved": round(res["call_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(res["call_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "call_us": round(res["call_ms"] * 1e3, 2), "call_bytes": res["step_bytes"],
         },
         "cpu_baseline": cpu,
         "secondary": secondary,

@@ -186,6 +186,33 @@ int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcac
   return launch_decode((hipStream_t)stream, q, *cache, lengths, n_heads, scale, out, workspace, p);
 }
 
+int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                        float eps, float theta, const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                        uint32_t flags, float scale, const ema_kvcache_desc* cache, void* out, void* workspace,
+                        uint64_t workspace_bytes) {
+  const char* op = "ema_decode_step";
+  int32_t rc = check_cache(op, cache);
+  if (rc) return rc;
+  if (!qkv || !out || !offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null qkv/out/offsets", op);
+  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE)) return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
+  if (!(flags & EMA_PRE_NO_NORM) && (!q_norm_w || !k_norm_w))
+    return set_error(EMA_ERR_INVALID_ARG, "%s: norm weights are null (pass EMA_PRE_NO_NORM for models without q/k norm)", op);
+  if ((rc = check_heads(op, n_heads, cache->n_kv_heads))) return rc;
+  if (max_len < 0 || max_len > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: max_len %d outside [0, capacity %d]", op, max_len, cache->capacity);
+  if (!(eps >= 0.f) || !(theta > 0.f) || !(scale > 0.f))
+    return set_error(EMA_ERR_INVALID_ARG, "%s: eps must be >= 0, theta and scale > 0", op);
+  if (!aligned16(qkv) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: qkv/out must be 16-byte aligned", op);
+  DecodePlan p = plan_decode(cache->batch, n_heads, cache->n_kv_heads, cache->head_dim, max_len);
+  const uint64_t need = decode_workspace_bytes(p);
+  if (!workspace || workspace_bytes < need)
+    return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes needed, %llu given", op,
+                     (unsigned long long)need, (unsigned long long)(workspace ? workspace_bytes : 0));
+  if (!aligned16(workspace)) return set_error(EMA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", op);
+  FusedPre f{qkv, q_norm_w, k_norm_w, offsets, eps, theta, flags};
+  return launch_decode((hipStream_t)stream, nullptr, *cache, nullptr, n_heads, scale, out, workspace, p, &f);
+}
+
 int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                               const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads, float scale,
                               uint32_t flags, void* out) {

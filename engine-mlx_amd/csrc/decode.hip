@@ -53,10 +53,19 @@ struct DecodeArgs {
   const uint16_t* v;
   const int32_t* len;
   uint16_t* out;
+  int32_t* hdr;  // workspace header: tile prefix per batch row (pre[0..B]) for the merge
   float* part;   // partial slots
   int64_t sb, sh, sp;
   float qk_scale;  // scale * log2(e): scores live in the log2 domain
   int B, Hq, Hkv, G, cap, W;
+  // fused decode step only: the pre-attention inputs; lengths are off[b] + 1
+  const uint16_t* qkv;  // [B, (Hq + 2*Hkv) * D]
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const int32_t* off;
+  float eps, log2_theta;
+  uint32_t flags;
+  int fused;
 };
 
 __device__ __forceinline__ int64_t worker_of(int64_t t, int64_t total, int W) {
@@ -68,6 +77,12 @@ __device__ __forceinline__ int64_t worker_begin(int64_t w, int64_t total, int W)
 
 __device__ __forceinline__ int clamp_len(int L, int cap) { return L < 0 ? 0 : (L > cap ? cap : L); }
 
+// Valid positions of sequence b: the given length, or offset + 1 in the fused step
+// (the new token is written at the offset before attention reads it).
+__device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
+  return clamp_len(a.fused ? a.off[b] + 1 : a.len[b], a.cap);
+}
+
 // Tile prefix over batch rows (tiles of all kv heads of rows < b), computed by
 // the whole workgroup. pre[B] is the total tile count.
 __device__ void build_prefix(const DecodeArgs& a, int32_t* pre) {
@@ -78,7 +93,7 @@ __device__ void build_prefix(const DecodeArgs& a, int32_t* pre) {
   int32_t local = 0;
   for (int i = 0; i < chunk; ++i) {
     const int b = b0 + i;
-    if (b < a.B) local += ((clamp_len(a.len[b], a.cap) + kTile - 1) / kTile) * a.Hkv;
+    if (b < a.B) local += ((seq_len(a, b) + kTile - 1) / kTile) * a.Hkv;
   }
   part[tid] = local;
   __syncthreads();
@@ -93,7 +108,7 @@ __device__ void build_prefix(const DecodeArgs& a, int32_t* pre) {
     const int b = b0 + i;
     if (b < a.B) {
       pre[b] = run;
-      run += ((clamp_len(a.len[b], a.cap) + kTile - 1) / kTile) * a.Hkv;
+      run += ((seq_len(a, b) + kTile - 1) / kTile) * a.Hkv;
     }
   }
   if (tid == 255) pre[a.B] = part[255];
@@ -101,9 +116,10 @@ __device__ void build_prefix(const DecodeArgs& a, int32_t* pre) {
 }
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *(const u32x4*)p; }
-
-__device__ __forceinline__ bool worker_nonempty(int64_t w, int64_t total, int W) {
-  return worker_begin(w, total, W) < worker_begin(w + 1, total, W);
+// K/V rows are read exactly once per call: non-temporal (streaming) loads keep them
+// from displacing reusable lines (measured: ~10% faster on the batch-32 and 32k shapes).
+__device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
+  return __builtin_nontemporal_load((const u32x4*)p);
 }
 
 // LDS used to combine the four waves' states at the end of a piece.
@@ -113,16 +129,56 @@ struct Combine {
   float o[kWaves][16][kD];
 };
 
+// RMSNorm + split-half RoPE of the head vector whose dims 8*(4s + c) + j (s < 4, j < 8)
+// this lane holds in x[8s + j] (c = lane / 16; the four lanes of one head together
+// hold all 128 dims, and dims d, d + 64 -- a RoPE pair -- sit in one lane as s, s + 2).
+// Same arithmetic as the pre-attention kernel: f32 statistics, normalised value
+// rounded to bf16 before the weight multiply; cs_tab[i] = (cos, sin) of the angle
+// pos * 2^(-(i/64) log2 theta) formed in f32.
+__device__ __forceinline__ void norm_rope_q(const DecodeArgs& a, float (&x)[32], const uint16_t* w, int c,
+                                            const float2* cs_tab) {
+  if (!(a.flags & EMA_PRE_NO_NORM)) {
+    float ss = 0.f;
+    for (int e = 0; e < 32; ++e) ss += x[e] * x[e];
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const u32x4 wv = ld16(w + 8 * (4 * s2 + c));
+      for (int j = 0; j < 8; ++j) {
+        const float n = bf16_to_f32((uint16_t)f32_to_bf16_bits(x[8 * s2 + j] * inv));
+        const float wj = (j & 1) ? bf16_hi(wv[j >> 1]) : bf16_lo(wv[j >> 1]);
+        x[8 * s2 + j] = bf16_to_f32((uint16_t)f32_to_bf16_bits(n * wj));
+      }
+    }
+  }
+  if (!(a.flags & EMA_PRE_NO_ROPE)) {
+    for (int s2 = 0; s2 < 2; ++s2)
+      for (int j = 0; j < 8; ++j) {
+        const int i = 8 * (4 * s2 + c) + j;  // < 64; partner i + 64 is slot s2 + 2
+        const float cs = cs_tab[i].x, sn = cs_tab[i].y;
+        const float x1 = x[8 * s2 + j], x2 = x[8 * (s2 + 2) + j];
+        x[8 * s2 + j] = x1 * cs - x2 * sn;
+        x[8 * (s2 + 2) + j] = x1 * sn + x2 * cs;
+      }
+  }
+}
+
+template <bool kFused>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
+  __shared__ __attribute__((aligned(16))) uint16_t new_kv[2][kD];  // fused: the new token's k, v
+  __shared__ float2 rope_cs[kD / 2];                                 // fused: RoPE (cos, sin) at the offset
   build_prefix(a, pre);
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.hdr[i] = pre[i];
 
   // sequences with no valid position produce zeros (nothing else visits them)
   if (blockIdx.x == 0) {
     const int row_words = a.Hq * kD / 2;
     for (int b = 0; b < a.B; ++b)
-      if (clamp_len(a.len[b], a.cap) == 0)
+      if (seq_len(a, b) == 0)
         for (int i = threadIdx.x; i < row_words; i += blockDim.x) ((uint32_t*)(a.out + (int64_t)b * a.Hq * kD))[i] = 0u;
   }
 
@@ -131,9 +187,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int w = blockIdx.x;
   const int64_t total = pre[a.B];
-  if (total == 0) return;
-  int64_t t = worker_begin(w, total, a.W);
-  const int64_t t_end = worker_begin(w + 1, total, a.W);
+  // never more workers than tiles, so every worker's slice is non-empty
+  const int W = (int)(total < a.W ? total : a.W);
+  if (w >= W) return;
+  int64_t t = worker_begin(w, total, W);
+  const int64_t t_end = worker_begin(w + 1, total, W);
 
   const int g = lane & 15;  // query head inside the kv group (B-operand column)
   const int c = lane >> 4;  // 16-lane group
@@ -150,7 +208,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (pre[mid] <= t) lo = mid; else hi = mid;
     }
     const int b = lo;
-    const int L = clamp_len(a.len[b], a.cap);
+    const int L = seq_len(a, b);
     const int nb = (L + kTile - 1) / kTile;
     const int64_t rel = t - pre[b];
     const int kh = (int)(rel / nb);
@@ -163,20 +221,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint16_t* Kb = a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh;
     const uint16_t* Vb = a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh;
 
-    // B operand: Q^T, k index of step s <-> dims 8*(4s + c) .. +7
-    bf16x8 qop[4];
-    {
-      // columns g >= G are zero padding; their (clamped, in-bounds) loads are discarded
-      const int gc = g < a.G ? g : 0;
-      const uint16_t* qh = a.q + ((int64_t)b * a.Hq + (int64_t)kh * a.G + gc) * kD;
-      for (int s = 0; s < 4; ++s) {
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        const u32x4 v = ld16(qh + 8 * (4 * s + c));
-        qop[s] = as_bf16x8(g < a.G ? v : z);
-      }
-      wait_vmem();
-    }
-
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 o[8];
     for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -188,22 +232,104 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         int p = p0 + krow0 + 4 * r;
         p = p < L ? p : L - 1;
         const uint16_t* row = Kb + (int64_t)p * a.sp;
-        for (int s = 0; s < 4; ++s) kr[r][s] = ld16(row + 8 * (4 * s + c));
+        for (int s = 0; s < 4; ++s) kr[r][s] = ld16_stream(row + 8 * (4 * s + c));
       }
       for (int kk = 0; kk < 8; ++kk) {
         int p = p0 + 8 * c + kk;
         p = p < L ? p : L - 1;
-        vr[kk] = ld16(Vb + (int64_t)p * a.sp + 8 * m);
+        vr[kk] = ld16_stream(Vb + (int64_t)p * a.sp + 8 * m);
       }
     };
 
-    // this wave's tiles of the piece: tile0 + wave, + kWaves, ...
+    // q loads, then this wave's first tile loads, then the q work: the work below
+    // runs while the tile is in flight. B operand Q^T: step s <-> dims 8*(4s + c) .. +7;
+    // columns g >= G are zero padding (their clamped, in-bounds loads are discarded).
     const int first = tile0 + wave;
+    const int gc = g < a.G ? g : 0;
+    const int F = (a.Hq + 2 * a.Hkv) * kD;
+    const uint16_t* qh = kFused ? a.qkv + (int64_t)b * F + ((int64_t)kh * a.G + gc) * kD
+                                : a.q + ((int64_t)b * a.Hq + (int64_t)kh * a.G + gc) * kD;
+    u32x4 qraw[4];
+    for (int s = 0; s < 4; ++s) qraw[s] = ld16(qh + 8 * (4 * s + c));
     if (first < tile1) load_tile(first, kc, vc);
+    bf16x8 qop[4];
+    if (!kFused) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      for (int s = 0; s < 4; ++s) qop[s] = as_bf16x8(g < a.G ? qraw[s] : z);
+    } else {
+      // q = rope(norm(q_raw)) of this head, from the fused qkv row; the 64 RoPE
+      // angles of this sequence's offset are formed once per piece into LDS
+      const int off = a.off[b];
+      if (tid < kD / 2 && !(a.flags & EMA_PRE_NO_ROPE)) {
+        const float inv_freq = exp2f(-((float)tid / (float)(kD / 2)) * a.log2_theta);
+        float sn, cs;
+        sincosf((float)off * inv_freq, &sn, &cs);
+        rope_cs[tid] = make_float2(cs, sn);
+      }
+      __syncthreads();
+      float x[32];
+      for (int s = 0; s < 4; ++s)
+        for (int j = 0; j < 8; ++j) x[8 * s + j] = (j & 1) ? bf16_hi(qraw[s][j >> 1]) : bf16_lo(qraw[s][j >> 1]);
+      norm_rope_q(a, x, a.qw, c, rope_cs);
+      for (int s = 0; s < 4; ++s) {
+        u32x4 v;
+        for (int e = 0; e < 4; ++e) v[e] = g < a.G ? pack_bf16x2(x[8 * s + 2 * e], x[8 * s + 2 * e + 1]) : 0u;
+        qop[s] = as_bf16x8(v);
+      }
+      // The workgroup whose slice ends the segment owns the new row (position L - 1 =
+      // offset): it forms k = rope(norm(k_raw)) and v, writes both into the cache and
+      // uses them for its last tile from LDS. No other workgroup reads that row.
+      const bool in_cap = off >= 0 && off < a.cap;
+      if (tile1 == nb) {
+        if (wave == 0) {
+          const uint16_t* kr = a.qkv + (int64_t)b * F + ((int64_t)a.Hq + kh) * kD;
+          const uint16_t* vr = kr + (int64_t)a.Hkv * kD;
+          float k1 = bf16_to_f32(kr[lane]), k2 = bf16_to_f32(kr[lane + 64]);
+          if (!(a.flags & EMA_PRE_NO_NORM)) {
+            float ss = k1 * k1 + k2 * k2;
+            for (int mm = 32; mm >= 1; mm >>= 1) ss += __shfl_xor(ss, mm, 64);
+            const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
+            k1 = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32((uint16_t)f32_to_bf16_bits(k1 * inv)) *
+                                                       bf16_to_f32(a.kw[lane])));
+            k2 = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32((uint16_t)f32_to_bf16_bits(k2 * inv)) *
+                                                       bf16_to_f32(a.kw[lane + 64])));
+          }
+          if (!(a.flags & EMA_PRE_NO_ROPE)) {
+            const float cs = rope_cs[lane].x, sn = rope_cs[lane].y;
+            const float r1 = k1 * cs - k2 * sn, r2 = k1 * sn + k2 * cs;
+            k1 = r1;
+            k2 = r2;
+          }
+          const uint16_t kb1 = (uint16_t)f32_to_bf16_bits(k1), kb2 = (uint16_t)f32_to_bf16_bits(k2);
+          new_kv[0][lane] = kb1;
+          new_kv[0][lane + 64] = kb2;
+          new_kv[1][lane] = vr[lane];
+          new_kv[1][lane + 64] = vr[lane + 64];
+          if (in_cap) {
+            uint16_t* kd = (uint16_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+            uint16_t* vd = (uint16_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+            kd[lane] = kb1;
+            kd[lane + 64] = kb2;
+            vd[lane] = vr[lane];
+            vd[lane + 64] = vr[lane + 64];
+          }
+        }
+        __syncthreads();
+      }
+    }
+
     for (int tile = first; tile < tile1; tile += kWaves) {
       const bool more = tile + kWaves < tile1;
       if (more) load_tile(tile + kWaves, kn, vn);
       const int p0 = tile * kTile;
+      if (kFused && tile == nb - 1 && a.off[b] == L - 1) {
+        // rows clamped to L - 1 = the new token: take its k, v from LDS
+        for (int r = 0; r < 2; ++r)
+          if (p0 + krow0 + 4 * r >= L - 1)
+            for (int s = 0; s < 4; ++s) kc[r][s] = *(const u32x4*)&new_kv[0][8 * (4 * s + c)];
+        for (int kk = 0; kk < 8; ++kk)
+          if (p0 + 8 * c + kk >= L - 1) vc[kk] = *(const u32x4*)&new_kv[1][8 * m];
+      }
 
       f32x4 sc[2];
       for (int r = 0; r < 2; ++r) {
@@ -274,7 +400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
 
     // combine the four waves; thread e covers (head e / 128, dim e % 128)
-    const bool single = worker_of(seg_first, total, a.W) == worker_of(seg_end - 1, total, a.W);
+    const bool single = worker_of(seg_first, total, W) == worker_of(seg_end - 1, total, W);
     const int64_t s = (int64_t)b * a.Hkv + kh;
     for (int e = tid; e < a.G * kD; e += blockDim.x) {
       const int gg = e / kD, d = e % kD;
@@ -302,77 +428,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
-// One workgroup per segment that spans several workgroups: log-sum-exp merge
-// of its partial slots. The (m, l) pairs of all pieces are staged in LDS by
-// the whole workgroup first, so each output element then streams its piece
-// values with independent loads.
+// Log-sum-exp merge of the segments that span several workgroups, one thread per
+// (segment, head, dim). Every piece's (m, l, o[dim]) is loaded independently, so a
+// thread's loads are in flight together (one memory round trip per 8 pieces).
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-  __shared__ int32_t pre[kMaxB + 1];
-  __shared__ float sm[kMaxWorkers * 2];  // per (piece, head): m, then l in the second half
-  build_prefix(a, pre);
-  const int64_t total = pre[a.B];
-  const int64_t s = blockIdx.x;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_seg = a.G * kD;
+  const int64_t s = e / per_seg;
+  if (s >= (int64_t)a.B * a.Hkv) return;
+  const int gg = (int)(e % per_seg) / kD, d = (int)(e % kD);
   const int b = (int)(s / a.Hkv), kh = (int)(s % a.Hkv);
-  const int L = clamp_len(a.len[b], a.cap);
+  const int L = seq_len(a, b);
+  const int64_t total = a.hdr[a.B];  // tile prefix published by decode_kernel
   if (L == 0 || total == 0) return;
+  const int W = (int)(total < a.W ? total : a.W);
   const int nb = (L + kTile - 1) / kTile;
-  const int64_t seg_first = pre[b] + (int64_t)kh * nb;
-  const int64_t seg_end = seg_first + nb;
-  const int w0 = (int)worker_of(seg_first, total, a.W);
-  const int w1 = (int)worker_of(seg_end - 1, total, a.W);
+  const int64_t seg_first = a.hdr[b] + (int64_t)kh * nb;
+  const int64_t w0 = worker_of(seg_first, total, W);
+  const int64_t w1 = worker_of(seg_first + nb - 1, total, W);
   if (w0 == w1) return;  // written directly by decode_kernel
-  const int P = w1 - w0 + 1;
-  const int G = a.G;
-  // pieces are processed in chunks that fit the staging area
-  const int chunk = kMaxWorkers * 2 / (2 * G);
-  float M_acc[kD * 16 / 256], L_acc[kD * 16 / 256], O_acc[kD * 16 / 256];
-  const int per_thread = (G * kD + blockDim.x - 1) / blockDim.x;
-  for (int i = 0; i < per_thread; ++i) {
-    M_acc[i] = -INFINITY;
-    L_acc[i] = 0.f;
-    O_acc[i] = 0.f;
-  }
-  for (int c0 = 0; c0 < P; c0 += chunk) {
-    const int n = P - c0 < chunk ? P - c0 : chunk;
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < n * G; idx += blockDim.x) {
-      const int w = w0 + c0 + idx / G, gg = idx % G;
-      float m = -INFINITY, l = 0.f;
-      if (worker_nonempty(w, total, a.W)) {  // empty workers wrote nothing this call
-        const float* Pp = a.part + (((int64_t)w + s) * G + gg) * kPieceStride;
-        m = Pp[0];
-        l = Pp[1];
-      }
-      sm[idx] = m;
-      sm[kMaxWorkers + idx] = l;
+  float M = -INFINITY, Lsum = 0.f, acc = 0.f;
+  for (int64_t c0 = w0; c0 <= w1; c0 += 8) {
+    float m[8], l[8], v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t w = c0 + i <= w1 ? c0 + i : w1;  // clamped: duplicates get weight 0 below
+      const float* P = a.part + ((w + s) * a.G + gg) * kPieceStride;
+      m[i] = P[0];
+      l[i] = P[1];
+      v[i] = P[4 + d];
     }
-    __syncthreads();
-    for (int i = 0; i < per_thread; ++i) {
-      const int e = threadIdx.x + i * blockDim.x;
-      if (e >= G * kD) break;
-      const int gg = e / kD, d = e % kD;
-      float Mc = M_acc[i];
-      for (int p = 0; p < n; ++p) Mc = fmaxf(Mc, sm[p * G + gg]);
-      const float r = __builtin_amdgcn_exp2f(M_acc[i] - Mc);
-      float lsum = L_acc[i] * r, acc = O_acc[i] * r;
-#pragma unroll 8
-      for (int p = 0; p < n; ++p) {
-        const float sc = __builtin_amdgcn_exp2f(sm[p * G + gg] - Mc);  // empty pieces: 0
-        lsum += sc * sm[kMaxWorkers + p * G + gg];
-        const float v = a.part[(((int64_t)w0 + c0 + p + s) * G + gg) * kPieceStride + 4 + d];
-        acc += sc == 0.f ? 0.f : sc * v;  // stale slots of empty pieces never leak in
+    float Mc = M;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c0 + i <= w1) Mc = fmaxf(Mc, m[i]);
+    const float r = __builtin_amdgcn_exp2f(M - Mc);
+    Lsum *= r;
+    acc *= r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c0 + i <= w1) {
+        const float sc = __builtin_amdgcn_exp2f(m[i] - Mc);
+        Lsum += sc * l[i];
+        acc += sc * v[i];
       }
-      M_acc[i] = Mc;
-      L_acc[i] = lsum;
-      O_acc[i] = acc;
-    }
+    M = Mc;
   }
-  for (int i = 0; i < per_thread; ++i) {
-    const int e = threadIdx.x + i * blockDim.x;
-    if (e >= G * kD) break;
-    const int gg = e / kD, d = e % kD;
-    a.out[((int64_t)b * a.Hq + (int64_t)kh * G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(O_acc[i] / L_acc[i]);
-  }
+  a.out[((int64_t)b * a.Hq + (int64_t)kh * a.G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(acc / Lsum);
 }
 
 int max_workers() {
@@ -400,10 +502,12 @@ DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len) {
   return p;
 }
 
-uint64_t decode_workspace_bytes(const DecodePlan& p) { return p.part_bytes; }
+constexpr uint64_t kHeaderBytes = ((kMaxB + 1) * sizeof(int32_t) + 255) & ~(uint64_t)255;
+
+uint64_t decode_workspace_bytes(const DecodePlan& p) { return kHeaderBytes + p.part_bytes; }
 
 int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, const int32_t* len,
-                      int Hq, float scale, void* out, void* ws, const DecodePlan& plan) {
+                      int Hq, float scale, void* out, void* ws, const DecodePlan& plan, const FusedPre* fused) {
   if (c.head_dim != kD)
     return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: head_dim %d not supported (128)", c.head_dim);
   if (c.batch > kMaxB)
@@ -417,7 +521,8 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.v = (const uint16_t*)c.v;
   a.len = len;
   a.out = (uint16_t*)out;
-  a.part = (float*)ws;
+  a.hdr = (int32_t*)ws;
+  a.part = (float*)((char*)ws + kHeaderBytes);
   a.sb = c.stride_batch;
   a.sh = c.stride_head;
   a.sp = c.stride_pos;
@@ -428,11 +533,23 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.G = G;
   a.cap = c.capacity;
   a.W = plan.workers;
-  hipLaunchKernelGGL(decode_kernel, dim3(plan.workers), dim3(kWaves * 64), 0, s, a);
+  a.fused = fused != nullptr;
+  a.qkv = fused ? (const uint16_t*)fused->qkv : nullptr;
+  a.qw = fused ? (const uint16_t*)fused->q_norm_w : nullptr;
+  a.kw = fused ? (const uint16_t*)fused->k_norm_w : nullptr;
+  a.off = fused ? fused->offsets : nullptr;
+  a.eps = fused ? fused->eps : 0.f;
+  a.log2_theta = fused ? log2f(fused->theta) : 0.f;
+  a.flags = fused ? fused->flags : 0u;
+  if (a.fused)
+    hipLaunchKernelGGL(decode_kernel<true>, dim3(plan.workers), dim3(kWaves * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL(decode_kernel<false>, dim3(plan.workers), dim3(kWaves * 64), 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");
   if (rc) return rc;
   if (plan.workers > 1) {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(plan.segments), dim3(256), 0, s, a);
+    const int64_t threads = (int64_t)plan.segments * G * kD;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
     rc = check_hip(hipGetLastError(), "ema_decode_attention merge launch");
   }
   return rc;

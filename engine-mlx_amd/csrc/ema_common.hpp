@@ -82,8 +82,19 @@ struct DecodePlan {
 };
 DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len);
 uint64_t decode_workspace_bytes(const DecodePlan& plan);
+// Pre-attention inputs of the fused decode step (ema_decode_step).
+struct FusedPre {
+  const void* qkv;
+  const void* q_norm_w;
+  const void* k_norm_w;
+  const int32_t* offsets;
+  float eps;
+  float theta;
+  uint32_t flags;
+};
 int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, const int32_t* len,
-                      int Hq, float scale, void* out, void* ws, const DecodePlan& plan);
+                      int Hq, float scale, void* out, void* ws, const DecodePlan& plan,
+                      const FusedPre* fused = nullptr);
 
 int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
                        const int32_t* q_off, int T, int Hq, float scale, uint32_t flags,

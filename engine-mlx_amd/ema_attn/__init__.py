@@ -35,7 +35,7 @@ EMA_PREFILL_CHUNK_ONLY = 2
 EXPORTED = (
     "ema_last_error", "ema_version", "ema_kvcache_init", "ema_kvcache_alloc", "ema_kvcache_free",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
-    "ema_decode_attention", "ema_prefill_attention",
+    "ema_decode_attention", "ema_decode_step", "ema_prefill_attention",
 )
 
 
@@ -78,6 +78,7 @@ def lib() -> ctypes.CDLL:
             "ema_pre_attention": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, i32, i32, i32, u32, vp, D]),
             "ema_decode_workspace_size": (i32, [i32, i32, i32, i32, i32, ctypes.POINTER(u64)]),
             "ema_decode_attention": (i32, [vp, vp, D, vp, i32, i32, f32, vp, vp, u64]),
+            "ema_decode_step": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, u32, f32, D, vp, vp, u64]),
             "ema_prefill_attention": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp]),
         }
         for name, (res, args) in sig.items():
@@ -199,6 +200,27 @@ def decode_attention(q, cache: StaticCache, lengths, max_len, scale=None, out=No
         workspace = decode_workspace(B, Hq, cache.desc.n_kv_heads, D, max_len, device=q.device, stream=stream)
     _check(lib().ema_decode_attention(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(lengths), max_len, Hq,
                                       scale, _ptr(out), _ptr(workspace), workspace.numel()), "ema_decode_attention")
+    return out
+
+
+def decode_step(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: StaticCache, max_len, scale=None,
+                flags=0, out=None, workspace=None, stream=None):
+    """Fused pre-attention (one token per sequence) + decode attention.
+
+    qkv [B,(Hq+2Hkv)*D] (or [B,1,...]) bf16; offsets int32 device [B]. Returns out [B, Hq*D]."""
+    import torch
+
+    B = qkv.shape[0]
+    D = cache.desc.head_dim
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty((B, n_heads * D), dtype=torch.bfloat16, device=qkv.device)
+    if workspace is None:
+        workspace = decode_workspace(B, n_heads, cache.desc.n_kv_heads, D, max_len, device=qkv.device)
+    _check(lib().ema_decode_step(_stream(stream), _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), eps, theta,
+                                 _ptr(offsets), max_len, n_heads, flags, scale, ctypes.byref(cache.desc), _ptr(out),
+                                 _ptr(workspace), workspace.numel()), "ema_decode_step")
     return out
 
 

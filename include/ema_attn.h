@@ -140,6 +140,23 @@ EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const e
                              const int32_t* lengths, int32_t max_len, int32_t n_heads,
                              float scale, void* out, void* workspace, uint64_t workspace_bytes);
 
+/* One fused decode step for `batch` sequences of one new token each: the
+ * pre-attention of ema_pre_attention with n_tokens = 1 (q/k RMSNorm, RoPE, k and v
+ * written into cache row offsets[b]) followed by ema_decode_attention over
+ * offsets[b] + 1 positions, in one kernel pass plus the split merge. q stays in
+ * registers (not written out). Replaces the per-layer attention slice of the
+ * compiled decode step, crates/serve/src/compiled.rs:134-163.
+ *   qkv      [batch, (n_heads + 2*n_kv_heads) * head_dim] bf16, order q|k|v
+ *   offsets  device int32 [batch]; an offset outside [0, capacity) writes nothing
+ *   max_len  host upper bound of offsets[b] + 1 (sizes the split; <= capacity)
+ *   out      [batch, n_heads * head_dim] bf16
+ * The workspace is the one ema_decode_workspace_size gives for max_len. */
+EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w,
+                                const void* k_norm_w, float eps, float theta,
+                                const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                                uint32_t flags, float scale, const ema_kvcache_desc* cache,
+                                void* out, void* workspace, uint64_t workspace_bytes);
+
 /* Prefill / chunked-prefill attention over the static cache
  * (MlxCtx::sdpa(causal), blas.rs:82-101 via forward_qwen3.rs:150 and
  * attend_and_project, crates/ops/src/attention.rs:162-177).

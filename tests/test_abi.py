@@ -123,6 +123,20 @@ def test_pre_attention_argument_errors(ema):
     assert rc == ema.EMA_ERR_INVALID_ARG
 
 
+def test_decode_step_argument_errors(ema):
+    L = ema.lib()
+    _, d = _desc(ema)
+    g = 0x40000
+    rc = L.ema_decode_step(None, g, None, None, 1e-6, 1e6, g, 64, 16, 0, 0.088, ctypes.byref(d), g, g, 1 << 30)
+    assert rc == ema.EMA_ERR_INVALID_ARG and "norm" in ema.last_error()
+    rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 65, 16, 0, 0.088, ctypes.byref(d), g, g, 1 << 30)
+    assert rc == ema.EMA_ERR_CAPACITY
+    rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 64, 16, 0, 0.088, ctypes.byref(d), g, g, 8)
+    assert rc == ema.EMA_ERR_WORKSPACE
+    rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 64, 12, 0, 0.088, ctypes.byref(d), g, g, 1 << 30)
+    assert rc == ema.EMA_ERR_SHAPE
+
+
 def test_prefill_argument_errors(ema):
     L = ema.lib()
     _, d = _desc(ema)

@@ -396,3 +396,87 @@ def test_graph_replay_matches_eager(ema, ora):
         assert np.array_equal(host(out), eager), f"replay {i}"
         step()  # eager work between replays
         torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------ fused step
+def _fused_case(ema, ora, B, Hq, Hkv, D, cap, off, seed, flags=0):
+    import torch
+
+    qkv = ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=seed)
+    qw = ora.normal_bf16(D, seed=seed + 1, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=seed + 2, mean=1.0, std=0.02)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 3)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 4)
+    off = np.asarray(off, np.int32)
+    # oracle: write (where it fits), then attend over clamp(off + 1)
+    kr, vr = kc.copy(), vc.copy()
+    q_ref = np.zeros((B, Hq, 1, D), np.uint16)
+    for bb in range(B):
+        if 0 <= off[bb] < cap:
+            kb, vb = kr[bb:bb + 1].copy(), vr[bb:bb + 1].copy()
+            q_ref[bb:bb + 1] = ora.pre_attention(qkv[bb:bb + 1, None].copy(), qw, kw, 1e-6, 1e6, off[bb:bb + 1],
+                                                 Hq, Hkv, kb, vb, flags=flags)
+            kr[bb], vr[bb] = kb[0], vb[0]
+        else:  # nothing is written; q is still normalised and rotated at the offset
+            x = qkv[bb, :Hq * D].reshape(Hq, D).copy()
+            if not flags & 1:
+                x = ora.rms_norm(x, qw, 1e-6)
+            if not flags & 2:
+                x = ora.rope(x, np.full(Hq, off[bb], np.int32), 1e6)
+            q_ref[bb] = x.reshape(Hq, 1, D)
+    L = np.clip(off + 1, 0, cap).astype(np.int32)
+    ref = ora.sdpa(q_ref, kr, vr, L, scale_of(D), False)
+    cache = make_cache(ema, kc, vc)
+    out = ema.decode_step(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, cache, cap, flags=flags)
+    torch.cuda.synchronize()
+    return host(out), ref, host(cache.k), host(cache.v), kr, vr, kc
+
+
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+def test_decode_step_fused_small(ema, ora, flags):
+    B, Hq, Hkv, D, cap = 6, 16, 4, 128, 200
+    off = [0, 31, 32, 100, 199, 63]
+    say(f"fused decode step flags={flags} offsets={off}")
+    got, ref, kg, vg, kr, vr, _ = _fused_case(ema, ora, B, Hq, Hkv, D, cap, off, seed=600 + flags, flags=flags)
+    assert np.array_equal(vg, vr), "V rows: bit copy at the offset, untouched elsewhere"
+    assert_close(kg, kr, "fused k cache")
+    assert_close(got, ref, "fused decode step")
+
+
+def test_decode_step_fused_out_of_capacity(ema, ora):
+    """An offset at or past the capacity writes nothing and attends the (stale) full cache."""
+    B, Hq, Hkv, D, cap = 3, 8, 2, 128, 64
+    got, ref, kg, vg, kr, vr, kc = _fused_case(ema, ora, B, Hq, Hkv, D, cap, [64, 10, 200], seed=620, flags=3)
+    assert np.array_equal(kg[0], kc[0]) and np.array_equal(kg[2], kc[2])
+    assert_close(got, ref, "fused out of capacity")
+
+
+def test_decode_step_fused_matches_unfused_pair(ema, ora):
+    """Fused step == ema_pre_attention(T=1) + ema_decode_attention on the same inputs."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 8, 32, 8, 128, 4096
+    rng = np.random.default_rng(9)
+    off = rng.integers(0, cap, size=B).astype(np.int32)
+    qkv = ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=630)
+    qw = ora.normal_bf16(D, seed=631, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=632, mean=1.0, std=0.02)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=633)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=634)
+    c1, c2 = make_cache(ema, kc, vc), make_cache(ema, kc, vc)
+    fused = ema.decode_step(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c1, cap)
+    q = ema.pre_attention(dev(qkv.reshape(B, 1, -1)), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c2)
+    pair = ema.decode_attention(q, c2, dev(off + 1), cap)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(c1.v), host(c2.v))
+    assert_close(host(c1.k), host(c2.k), "k cache fused vs pair", max_abs=2e-2, mean_abs=1e-5)
+    assert_close(host(fused), host(pair), "fused vs pair", max_abs=1e-2, mean_abs=1e-4)
+
+
+def test_decode_step_fused_qwen3_8b_batched(ema, ora):
+    """The benchmark step: batch 32, 32q/8kv, cap 8192, lengths U[512, 8192]."""
+    L = np.random.default_rng(1234).integers(512, 8193, size=32)
+    say("fused decode step B32 32q/8kv cap 8192")
+    got, ref, kg, vg, kr, vr, _ = _fused_case(ema, ora, 32, 32, 8, 128, 8192, L - 1, seed=640)
+    assert np.array_equal(vg, vr)
+    assert_close(got, ref, "fused 8B batched step")
