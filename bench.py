@@ -266,6 +266,19 @@ def bench_pre(ctx, ema, name, T, Hq, Hkv, D, cap, steps=20):
     return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
 
 
+def profiled_traffic():
+    """HBM bytes per ema_decode_step call measured by the FETCH_SIZE / WRITE_SIZE
+    counter runs recorded in profiles/decode_step_b32_qwen3_8b.md (None if absent)."""
+    path = os.path.join(ROOT, "profiles", "decode_step_b32_qwen3_8b.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -329,7 +342,8 @@ def main():
         "roofline": {
             "bound": "hbm", "kernel": "ema_decode_step (decode_kernel<fused> + decode_merge_kernel)",
             "achieved": round(res["call_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(res["call_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(res["call_gbs"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
+            "traffic_source": "FETCH_SIZE/WRITE_SIZE runs, profiles/decode_step_b32_qwen3_8b.md",
             "call_us": round(res["call_ms"] * 1e3, 2), "call_bytes": res["step_bytes"],
         },
         "cpu_baseline": cpu,
