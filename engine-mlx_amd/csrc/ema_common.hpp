@@ -35,6 +35,12 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// c + a.lo*b.lo + a.hi*b.hi over bf16 pairs, f32 accumulate (v_dot2_f32_bf16). Takes the
+// pairs by value: clang's __builtin_bit_cast of a vector-element lvalue reads element 0.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
 // 16x16x32 bf16 MFMA, f32 accumulate. Lane layout (checked on gfx950):
 //   A[16 x 32]: lane l holds row l%16, k = 8*(l/16) .. +7
 //   B[32 x 16]: lane l holds col l%16, k = 8*(l/16) .. +7

@@ -7,21 +7,28 @@
 // to the end of the key range: query i of a chunk that starts at cache
 // position q_off sees keys j <= q_off + i.
 //
-// Tiling: a workgroup of 4 waves owns 128 query rows of one head (32 per
-// wave) and streams 64-key blocks of K and V through double-buffered LDS.
-// Both contractions run on MFMA 32x32x16 (bf16 in, f32 accumulate), in the
-// transposed form that keeps the softmax lane-local:
+// Work split: one workgroup of 8 waves per CU owns 128 query rows of one head. Its key
+// range is cut in two halves at a 64-key block boundary; wave group 0 (waves 0-3)
+// attends over the first half and group 1 (waves 4-7) over the second, each wave over
+// 32 rows, each group streaming its own 64-key K/V blocks through its own
+// double-buffered LDS. The two partial (o, m, l) states of a row meet in LDS at the end.
+// Halving the key range halves the longest causal work item, and workgroups are
+// dispatched heaviest first, so the short ones fill in behind the long ones.
+//
+// Both contractions run on MFMA 32x32x16 (bf16 in, f32 accumulate), in the transposed
+// form that keeps the softmax lane-local:
 //   S^T[key, q] = K[key, :] . Q^T[:, q]   A = K rows (ds_read_b128), B = Q^T in registers
 //   O^T[d, q]  += V^T[d, key] P^T[key, q] A = V^T via ds_read_b64_tr_b16 (transposing
 //                                          LDS read), B = P^T (the S^T accumulators
 //                                          after exp, unmoved)
-// Each lane therefore owns one query row's scores, running max, row sum and
-// 64 output accumulators; the row max needs one xor-32 exchange per block.
+// Each lane owns one query row's scores, row-sum share and 64 output accumulators.
 //
-// Two workgroups share a CU (2 waves per SIMD). The MFMA sections run at raised
-// wave priority (s_setprio 1) and the softmax at normal priority, so when both
-// waves of a SIMD are ready the arbiter issues the matrix work first and the
-// other wave's softmax VALU fills the gaps (ping-pong between the two waves).
+// Ping-pong: the two waves on each SIMD belong to different groups, and the groups run
+// half a block out of phase, separated by workgroup barriers. In one phase group 0 issues
+// its matrix step (PV of block j-1 and QK of block j, 32 MFMAs) while group 1 runs the
+// softmax of its block and its K/V staging (VALU, exp, LDS stores, global loads); in the
+// next phase the roles swap. The matrix pipe and the vector pipe of a SIMD are fed by
+// different waves throughout.
 #include "ema_common.hpp"
 
 namespace ema {
@@ -30,11 +37,16 @@ namespace {
 constexpr int kD = 128;
 constexpr int kBM = 128;          // query rows per workgroup
 constexpr int kBN = 64;           // keys per block
-constexpr int kKStride = kD + 8;  // LDS row stride (elements) of the K tile: conflict-free b128 reads
-constexpr int kVStride = kD + 32; // LDS row stride of the V tile: conflict-free transposed reads
-constexpr int kKTile = kBN * kKStride;
-constexpr int kVTile = kBN * kVStride;
-constexpr int kLdsBytes = 2 * (kKTile + kVTile) * 2;
+constexpr int kGroupThreads = 256;  // 4 waves per key-range group
+constexpr int kThreads = 2 * kGroupThreads;
+// LDS tiles hold 64 unpadded 256-byte rows. The 16-byte chunks of a row are XOR-swizzled
+// so that the MFMA operand reads hit distinct banks: chunk p of K row r holds column
+// chunk p ^ (r & 15) (the b128 reads of 16 rows at one chunk spread over all banks), and
+// chunk p of V row r holds column chunk p ^ 4(r & 3) (the 4 rows of a transposed read
+// land in 4 different 64-byte bank groups).
+constexpr int kTile = kBN * kD;                    // elements of one K or V tile (16 KB)
+constexpr int kGroupElems = 4 * kTile;              // one group: K0 K1 V0 V1
+constexpr int kLdsBytes = 2 * kGroupElems * 2;      // 131072 B: one workgroup per CU
 constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dispatched round-robin
 
 struct PrefillArgs {
@@ -44,38 +56,53 @@ struct PrefillArgs {
   const int32_t* q_off;
   uint16_t* out;
   int64_t sb, sh, sp;
-  float qk_scale;  // scale * log2(e)
+  float qk_scale;  // scale * log2(e), applied to Q
   int B, Hq, Hkv, G, T, cap, nqb;
   uint32_t flags;
 };
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *(const u32x4*)p; }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
+// Raw buffer resource (V#) over `bytes` bytes from `base`: stride 0, gfx9 dword3 with a
+// 32-bit data format. Loads at offsets at or past `bytes` return zeros.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t addr = (uint64_t)base;
+  return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// 16 bytes per lane from buffer offset `voff` straight into LDS at lds_addr + 16 * lane
+// (buffer_load_dwordx4 ... lds; the LDS base goes through M0). Issued as asm so the
+// compiler does not track it: the caller orders it with explicit vmcnt waits before the
+// barrier that publishes the tile, instead of the compiler draining every load in flight
+// at each barrier and before each LDS read.
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  uint16_t* const Ks = lds;               // K tiles: buffer i at Ks + i * kKTile
-  uint16_t* const Vs = lds + 2 * kKTile;  // V tiles: buffer i at Vs + i * kVTile
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int g = wave >> 2;         // key-range group
+  const int wq = wave & 3;         // row tile of the wave inside the workgroup
   // Grid mapping. Workgroups are dispatched round-robin over the 8 XCDs (x % 8), each
   // with its own L2. When the (batch, kv head) groups divide evenly over the XCDs, all
   // query heads of a group run on the group's XCD, so its K/V stream is read from HBM
   // once and served from that L2 to every workgroup that attends over it. Inside an XCD
-  // (or over the whole grid otherwise) work items are ranked heaviest first (a later
-  // query block sees more keys) and the second half of the local index range takes the
-  // ranks in reverse, so the two workgroups that share a CU (local indices i and
-  // i + n/2 when they are resident together) carry complementary causal work.
+  // (or over the whole grid otherwise) work items are ranked heaviest first: a later
+  // query block sees more keys.
   const int groups = a.B * a.Hkv;
   const bool by_xcd = groups % kXcds == 0 && gridDim.x % kXcds == 0;
   const int64_t x = blockIdx.x;
-  const int64_t n_local = by_xcd ? gridDim.x / kXcds : gridDim.x;
-  const int64_t li = by_xcd ? x / kXcds : x;
-  const int64_t half = (n_local + 1) / 2;
-  const int64_t rank = li < half ? li : n_local - 1 - (li - half);
+  const int64_t rank = by_xcd ? x / kXcds : x;
   const int groups_local = by_xcd ? groups / kXcds : groups;
   const int per_qb = groups_local * a.G;
   const int qb = a.nqb - 1 - (int)(rank / per_qb);
@@ -101,141 +128,113 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   const int blk_begin = kv_begin / kBN;
   const int blk_end = (wg_end + kBN - 1) / kBN;
+  const int nblk = blk_end > blk_begin ? blk_end - blk_begin : 0;
+  const int n0 = (nblk + 1) / 2;                  // group 0: the first half of the blocks
+  const int gb0 = blk_begin + (g ? n0 : 0);       // this group's first block
+  const int ng = g ? nblk - n0 : n0;              // and its block count
 
   // this lane's query row
-  const int qr = row0 + 32 * wave + (lane & 31);
+  const int qr = row0 + 32 * wq + (lane & 31);
   const int qr_c = qr < a.T ? qr : a.T - 1;
   const int q_abs = q_off + qr;                   // causal limit: key <= q_abs
-  const int wave_first_abs = q_off + row0 + 32 * wave;
+  const int wave_first_abs = q_off + row0 + 32 * wq;
   const int wave_last_abs = wave_first_abs + 31;
   const int hh = lane >> 5;                       // which half of the k slots
 
-  // Q^T as B operand: step s covers dims 16s + 8*hh .. +7
+  uint16_t* const Ks = lds + g * kGroupElems;     // this group's K tiles: buffer i at Ks + i * kTile
+  uint16_t* const Vs = Ks + 2 * kTile;            // and V tiles
+
+  // Q^T as B operand: step s covers dims 16s + 8*hh .. +7. Q is scaled by
+  // scale*log2(e) and rounded to bf16 here, so the scores come out of the MFMA in
+  // the log2 domain and the softmax needs no multiply per score.
   bf16x8 qop[8];
   {
     const uint16_t* qp = a.q + (((int64_t)b * a.Hq + h) * a.T + qr_c) * kD + 8 * hh;
-    for (int s = 0; s < 8; ++s) qop[s] = as_bf16x8(ld16(qp + 16 * s));
+    u32x4 raw[8];
+    for (int s = 0; s < 8; ++s) raw[s] = ld16(qp + 16 * s);
     wait_vmem();
+    for (int s = 0; s < 8; ++s) {
+      u32x4 w;
+      for (int e = 0; e < 4; ++e)
+        w[e] = pack_bf16x2(bf16_lo(raw[s][e]) * a.qk_scale, bf16_hi(raw[s][e]) * a.qk_scale);
+      qop[s] = as_bf16x8(w);
+    }
   }
 
+  // K/V of this (batch, kv head) through buffer loads: the resource of a block starts at
+  // the block's first row and covers only the rows below kv_len, so rows past the valid
+  // length read as zeros (finite, and masked out) without per-lane clamping.
   const char* Kg = (const char*)(a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh);
   const char* Vg = (const char*)(a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh);
-  const int64_t blk_bytes = (int64_t)kBN * a.sp * 2;
+  const uint32_t row_bytes = (uint32_t)a.sp * 2;
 
-  // global -> register staging: the thread owns rows rr + 16i (i < 4) of a block at
-  // 16-byte column cc, for K and for V
-  const int rr = tid >> 4, cc = (tid & 15) * 8;
-  uint32_t toff[4];
-  for (int i = 0; i < 4; ++i) toff[i] = (uint32_t)(((int64_t)(rr + 16 * i) * a.sp + cc) * 2);
-  u32x4 kst[4], vst[4];
-  auto gload = [&](int blk) {
-    const int base = blk * kBN;
-    if (base + kBN <= kv_len) {  // whole block valid: uniform block base + 32-bit offsets
-      const char* kp = Kg + (int64_t)blk * blk_bytes;
-      const char* vp = Vg + (int64_t)blk * blk_bytes;
-      for (int i = 0; i < 4; ++i) {
-        kst[i] = *(const u32x4*)(kp + toff[i]);
-        vst[i] = *(const u32x4*)(vp + toff[i]);
-      }
-    } else {  // tail block: clamp rows to the last valid one (masked later)
-      for (int i = 0; i < 4; ++i) {
-        int r = base + rr + 16 * i;
-        r = r < kv_len ? r : kv_len - 1;
-        kst[i] = *(const u32x4*)(Kg + ((int64_t)r * a.sp + cc) * 2);
-        vst[i] = *(const u32x4*)(Vg + ((int64_t)r * a.sp + cc) * 2);
-      }
-    }
+  // Global -> LDS without registers (buffer_load_dwordx4 ... lds): one instruction moves
+  // 1 KB, lane l's 16 bytes landing at byte 16l of the destination, i.e. 4 tile rows.
+  // Wave wq of the group moves rows 16wq .. 16wq+15 (4 instructions per tile); the
+  // per-lane source offsets below apply the swizzle and stay the same for every block.
+  const int r4 = lane >> 4, p16 = lane & 15;  // row within the 4, chunk position in the row
+  uint32_t koff[4], voff[4];
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t row = (uint32_t)(16 * wq + 4 * i + r4);
+    koff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * i + r4)) * 16);
+    voff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * r4)) * 16);
+  }
+  auto dma = [&](const char* src, int blk, const uint32_t* off, uint16_t* tile) {
+    const int base = blk * kBN;  // < kv_len for every block of the range
+    const uint32_t valid = (uint32_t)(kv_len - base) * row_bytes;
+    const u32x4 r = buffer_rsrc(src + (int64_t)base * row_bytes, valid);
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
+    for (int i = 0; i < 4; ++i) dma16(r, off[i], dst + 4 * i * kD * 2);
   };
-  auto sstore = [&](int buf) {
-    for (int i = 0; i < 4; ++i) {
-      *(u32x4*)(Ks + buf * kKTile + (rr + 16 * i) * kKStride + cc) = kst[i];
-      *(u32x4*)(Vs + buf * kVTile + (rr + 16 * i) * kVStride + cc) = vst[i];
-    }
-  };
+  auto load_k = [&](int j) { dma(Kg, gb0 + j, koff, Ks + (j & 1) * kTile); };
+  auto load_v = [&](int j) { dma(Vg, gb0 + j, voff, Vs + (j & 1) * kTile); };
 
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x16 o[4];
+  // Online softmax state of this lane's row, in the log2 domain. The accumulators hold
+  // o and l relative to the base m_use (p = 2^(s - m_use)); m_use only changes on the
+  // slow path of the softmax step.
+  float m_use = 0.f, l_run = 0.f;
+  bool seen = false;      // m_use is this row's running max (some score was finite)
+  bool all_seen = false;  // wave-uniform: every row of the wave is seen
+  bool rescale = false;   // wave-uniform: o is to be scaled by o_scale before the next PV
+  float o_scale = 1.f;
+  f32x16 o[4], sc[2];
   for (int dt = 0; dt < 4; ++dt)
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  for (int kt = 0; kt < 2; ++kt)
+    for (int i = 0; i < 16; ++i) sc[kt][i] = 0.f;
+  u32x4 pw[4] = {};  // P^T of the last softmax step as bf16 pairs, for the next PV
+  const uint32_t ones = 0x3F803F80u;  // bf16 pair (1, 1)
 
-  if (blk_begin < blk_end) {
-    gload(blk_begin);
-    sstore(0);
-  }
-  __syncthreads();
-
-  // transposed-read addressing (per 16-lane group)
+  // K operand reads: row (lane & 31) (+32 for sub-tile 1), column chunk 2s + hh, stored
+  // at chunk (2s + hh) ^ (lane & 15)
+  const int k_lane = (lane & 31) * kD + 8 * (hh ^ (lane & 1));
+  const int k_x = 16 * ((lane & 15) >> 1);            // element offset, xored with 16s
+  // V^T operand reads (per 16-lane group): rows tr_row + 16*st_half + 8u + 32*kt,
+  // columns 4(s16 & 3) + 16(grp & 1) + 32dt, stored at column chunk ^ 4(s16 >> 2)
   const int grp = lane >> 4, s16 = lane & 15;
-  const int tr_row = 4 * (grp >> 1) + (s16 >> 2);     // + 16*st_half + 8u + 32*kt
-  const int tr_col = 16 * (grp & 1) + 4 * (s16 & 3);  // + 32*dt
+  const int tr_row = 4 * (grp >> 1) + (s16 >> 2);
+  int v_col[4];
+  for (int dt = 0; dt < 4; ++dt) v_col[dt] = tr_row * kD + 16 * (grp & 1) + 4 * (s16 & 3) + 32 * (dt ^ (s16 >> 2));
 
-  for (int blk = blk_begin; blk < blk_end; ++blk) {
-    const int buf = (blk - blk_begin) & 1;
-    const bool more = blk + 1 < blk_end;
-    if (more) gload(blk + 1);
-    const int kbase = blk * kBN;
-    const bool active = kbase <= wave_last_abs || !causal;
-    if (active) {
-      const uint16_t* Kt = Ks + buf * kKTile;
-      const uint16_t* Vt = Vs + buf * kVTile;
-      // two independent accumulation chains (sub-tiles kt = 0, 1), interleaved
-      f32x16 sc[2];
-      for (int kt = 0; kt < 2; ++kt)
-        for (int i = 0; i < 16; ++i) sc[kt][i] = 0.f;
-      const uint16_t* kp = Kt + (lane & 31) * kKStride + 8 * hh;
-      __builtin_amdgcn_s_setprio(1);
-      for (int s = 0; s < 8; ++s)
-        for (int kt = 0; kt < 2; ++kt)
-          sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(kp + kt * 32 * kKStride + 16 * s)), qop[s], sc[kt]);
-      __builtin_amdgcn_s_setprio(0);
-      // mask on raw scores; key of slot i in sub-tile kt: kbase + 32kt + (i%4) + 8(i/4) + 4hh
-      const bool need_mask = kbase < kv_begin || kbase + kBN > kv_len ||
-                             (causal && kbase + kBN - 1 > wave_first_abs);
-      if (need_mask) {
-        for (int kt = 0; kt < 2; ++kt)
-          for (int i = 0; i < 16; ++i) {
-            const int key = kbase + 32 * kt + (i & 3) + 8 * (i >> 2) + 4 * hh;
-            const bool ok = key >= kv_begin && key < kv_len && (!causal || key <= q_abs);
-            sc[kt][i] = ok ? sc[kt][i] : -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-      for (int kt = 0; kt < 2; ++kt)
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[kt][i]);
-      mx = wave_max_xor(mx, 32) * a.qk_scale;  // scale > 0: max commutes with it
-      // Lazy rescale: the running max (log2 domain) moves only when a row's max
-      // grows by more than 8, so p = 2^(s - m) stays <= 256 and the O/l rescale
-      // is skipped for most blocks. Any m gives the same normalised result.
-      if (__any(mx > m_run + 8.f)) {
-        const float m_new = mx > m_run + 8.f ? mx : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf -> 0
-        l_run *= alpha;
-        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-        m_run = m_new;
-      }
-      // rows with nothing visible yet keep m = -inf: use 0 as the base (all p = 0)
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      float psum = 0.f;
-      for (int kt = 0; kt < 2; ++kt)
-        for (int i = 0; i < 16; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][i], a.qk_scale, -m_use));
-          sc[kt][i] = p;
-          psum += p;
-        }
-      l_run += psum;
+  auto active = [&](int j) { return !causal || (gb0 + j) * kBN <= wave_last_abs; };
 
-      // PV: step st covers S^T slots 8*(st&1) .. +7 of sub-tile st>>1
-      __builtin_amdgcn_s_setprio(1);
+  // Matrix step j: O += V^T P^T for block j-1, then S^T = K Q^T for block j. A base
+  // change of the softmax step before is applied to o first.
+  auto mstep = [&](int j) {
+    if (rescale) {
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= o_scale;
+      rescale = false;
+    }
+    __builtin_amdgcn_s_setprio(1);
+    if (j >= 1 && j - 1 < ng && active(j - 1)) {
+      const uint16_t* Vt = Vs + ((j - 1) & 1) * kTile;
       for (int st = 0; st < 4; ++st) {
         const int kt = st >> 1, q2 = st & 1;
-        u32x4 pw;
-        for (int e = 0; e < 4; ++e)
-          pw[e] = pack_bf16x2(sc[kt][8 * q2 + 2 * e], sc[kt][8 * q2 + 2 * e + 1]);
-        const bf16x8 pop = as_bf16x8(pw);
-        const int rbase = 32 * kt + 16 * q2 + tr_row;
+        const bf16x8 pop = as_bf16x8(pw[st]);
+        const int rbase = (32 * kt + 16 * q2) * kD;
         for (int dt = 0; dt < 4; ++dt) {
-          const uint16_t* p0 = Vt + rbase * kVStride + 32 * dt + tr_col;
-          const uint16_t* p1 = p0 + 8 * kVStride;
+          const uint16_t* p0 = Vt + rbase + v_col[dt];
+          const uint16_t* p1 = p0 + 8 * kD;
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
           typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -244,12 +243,156 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+    if (j < ng && active(j)) {
+      const uint16_t* kp = Ks + (j & 1) * kTile + k_lane;
+      // two independent accumulation chains (sub-tiles kt = 0, 1), interleaved
+      for (int s = 0; s < 8; ++s) {
+        const uint16_t* ks = kp + (k_x ^ (16 * s));
+        for (int kt = 0; kt < 2; ++kt)
+          sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(ks + kt * 32 * kD)), qop[s], s == 0 ? f32x16{} : sc[kt]);
+      }
+    }
     __builtin_amdgcn_s_setprio(0);
-    if (more) sstore(buf ^ 1);
-    __syncthreads();
+  };
+
+  // Softmax step j: P for block j (into pw), then the loads of K for block j+2 (its
+  // buffer held K of block j, last read by the matrix step just before) and of V for
+  // block j+1 (its buffer held V of block j-1, last read by that same matrix step).
+  auto vstep = [&](int j) {
+    if (j < 0 || j >= ng) return;
+    if (active(j)) {
+      const int kbase = (gb0 + j) * kBN;
+      // key of slot i in sub-tile kt: kbase + 32kt + (i%4) + 8(i/4) + 4hh
+      const bool need_mask = kbase < kv_begin || kbase + kBN > kv_len ||
+                             (causal && kbase + kBN - 1 > wave_first_abs);
+      if (need_mask) {
+        int hi = causal && q_abs < kv_len - 1 ? q_abs : kv_len - 1;
+        hi -= kbase + 4 * hh;
+        const int lo = kv_begin - kbase - 4 * hh;
+        for (int kt = 0; kt < 2; ++kt)
+          for (int i = 0; i < 16; ++i) {
+            const int koff = 32 * kt + (i & 3) + 8 * (i >> 2);
+            sc[kt][i] = koff <= hi && koff >= lo ? sc[kt][i] : -INFINITY;
+          }
+      }
+      // P^T as bf16 pairs for the PV steps (step st: slots 8*(st&1) .. +7 of sub-tile
+      // st>>1) and this lane's share of the block row sum, taken over the rounded
+      // values the PV product uses.
+      float ps0 = 0.f, ps1 = 0.f;
+      // Fast path: p = 2^(s - m_use) as is. It is kept when every lane's sum is at most
+      // 256, which bounds every p by 256 (as a lazy rescale with threshold 8 would), so
+      // neither the max nor a rescale is needed.
+      bool fast = all_seen;
+      if (fast) {
+        for (int st = 0; st < 4; ++st)
+          for (int e = 0; e < 4; ++e) {
+            const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
+            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - m_use),
+                                           __builtin_amdgcn_exp2f(sc[kt][i + 1] - m_use));
+            pw[st][e] = w;
+            if (e & 1) ps1 = dot2_bf16(w, ones, ps1);
+            else ps0 = dot2_bf16(w, ones, ps0);
+          }
+        fast = !__any(!(ps0 + ps1 <= 256.f));  // NaN/inf fall to the slow path too
+      }
+      if (!fast) {
+        // Slow path (first block of a row, or a row max that grew): move the base to
+        // the row's running max and rescale what was accumulated.
+        float bm = -INFINITY;
+        for (int kt = 0; kt < 2; ++kt)
+          for (int i = 0; i < 16; ++i) bm = fmaxf(bm, sc[kt][i]);
+        bm = wave_max_xor(bm, 32) - m_use;
+        const float delta = seen ? fmaxf(bm, 0.f) : (bm == -INFINITY ? 0.f : bm);
+        seen = seen || bm != -INFINITY;
+        const float alpha = __builtin_amdgcn_exp2f(-delta);
+        l_run *= alpha;
+        o_scale = alpha;
+        rescale = true;
+        m_use += delta;
+        ps0 = ps1 = 0.f;
+        for (int st = 0; st < 4; ++st)
+          for (int e = 0; e < 4; ++e) {
+            const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
+            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - m_use),
+                                           __builtin_amdgcn_exp2f(sc[kt][i + 1] - m_use));
+            pw[st][e] = w;
+            if (e & 1) ps1 = dot2_bf16(w, ones, ps1);
+            else ps0 = dot2_bf16(w, ones, ps0);
+          }
+        all_seen = __all(seen);
+      }
+      l_run += ps0 + ps1;
+    }
+    if (j + 2 < ng) load_k(j + 2);
+    if (j + 1 < ng) load_v(j + 1);
+    // the loads of the previous softmax step (K of block j+1, V of block j) are read by
+    // the next matrix step: wait for them, leaving this step's own loads in flight
+    // (loads complete in issue order); step 0's predecessors were waited for up front
+    if (j >= 1) {
+      if (j + 2 < ng) __builtin_amdgcn_s_waitcnt(0x0F78);       // vmcnt(8)
+      else if (j + 1 < ng) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+      else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+    }
+  };
+
+  // LDS starts zeroed, so tile rows that no load writes (past kv_len: the buffer
+  // resources return zeros, but a stale row could otherwise surface) are finite.
+  for (int i = tid; i < 2 * kGroupElems / 8; i += kThreads) ((u32x4*)lds)[i] = u32x4{0, 0, 0, 0};
+  __syncthreads();
+  if (ng > 0) load_k(0);
+  if (ng > 0) load_v(0);
+  if (ng > 1) load_k(1);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+
+  // Phase 2t + half: group 0 runs matrix step t then softmax step t; group 1 runs
+  // softmax step t-1 then matrix step t, so the groups always sit in opposite halves.
+  // Both loops pass the same number of barriers.
+  if (g == 0) {
+    for (int t = 0; t <= n0; ++t) {
+      mstep(t);
+      __syncthreads();
+      vstep(t);
+      __syncthreads();
+    }
+  } else {
+    for (int t = 0; t <= n0; ++t) {
+      vstep(t - 1);
+      __syncthreads();
+      mstep(t);
+      __syncthreads();
+    }
   }
 
-  float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  // Merge: group 1 publishes its (o, m, l) through LDS (the K/V buffers are free now);
+  // group 0 combines them with its own and writes the output rows.
+  float* const xo = (float*)lds;                       // [dt][i4][wq][lane] f32x4
+  float* const xm = xo + 4 * 4 * 4 * 64 * 4;           // [wq][lane] m (or -inf)
+  float* const xl = xm + 4 * 64;                       // [wq][lane] l share
+  if (g == 1) {
+    for (int dt = 0; dt < 4; ++dt)
+      for (int i4 = 0; i4 < 4; ++i4) {
+        f32x4 v = {o[dt][4 * i4], o[dt][4 * i4 + 1], o[dt][4 * i4 + 2], o[dt][4 * i4 + 3]};
+        *(f32x4*)(xo + (((dt * 4 + i4) * 4 + wq) * 64 + lane) * 4) = v;
+      }
+    xm[wq * 64 + lane] = seen ? m_use : -INFINITY;
+    xl[wq * 64 + lane] = l_run;
+  }
+  __syncthreads();
+  if (g == 1) return;
+  const float m1 = xm[wq * 64 + lane];
+  const float l1 = xl[wq * 64 + lane];
+  const float m0 = seen ? m_use : -INFINITY;
+  const float m = fmaxf(m0, m1);
+  const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
+  const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+  for (int dt = 0; dt < 4; ++dt)
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const f32x4 v = *(const f32x4*)(xo + (((dt * 4 + i4) * 4 + wq) * 64 + lane) * 4);
+      for (int e = 0; e < 4; ++e) o[dt][4 * i4 + e] = o[dt][4 * i4 + e] * a0 + v[e] * a1;
+    }
+  const float l_mine = l_run * a0 + l1 * a1;
+  const float l_tot = l_mine + __shfl_xor(l_mine, 32, 64);
   if (qr >= a.T) return;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   // lane holds O[q][32dt + (i%4) + 8(i/4) + 4hh]
@@ -270,6 +413,11 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
                        void* out) {
   if (c.head_dim != kD)
     return set_error(EMA_ERR_UNSUPPORTED, "ema_prefill_attention: head_dim %d not supported (128)", c.head_dim);
+  // K/V rows are addressed through buffer resources with 32-bit byte ranges
+  if ((int64_t)c.capacity * c.stride_pos * 2 >= ((int64_t)1 << 31))
+    return set_error(EMA_ERR_UNSUPPORTED,
+                     "ema_prefill_attention: capacity %d x stride_pos %lld exceeds the 2 GiB per-head range",
+                     c.capacity, (long long)c.stride_pos);
   static bool attr_set = false;
   if (!attr_set) {
     int32_t rc = check_hip(hipFuncSetAttribute((const void*)prefill_kernel,
@@ -298,7 +446,7 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
   a.flags = flags;
   const int64_t blocks = (int64_t)a.nqb * Hq * c.batch;
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_prefill_attention: grid too large");
-  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)blocks), dim3(256), kLdsBytes, s, a);
+  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
   return check_hip(hipGetLastError(), "ema_prefill_attention launch");
 }
 
