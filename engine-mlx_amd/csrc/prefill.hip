@@ -46,7 +46,8 @@ constexpr int kThreads = 2 * kGroupThreads;
 // land in 4 different 64-byte bank groups).
 constexpr int kTile = kBN * kD;                    // elements of one K or V tile (16 KB)
 constexpr int kGroupElems = 4 * kTile;              // one group: K0 K1 V0 V1
-constexpr int kLdsBytes = 2 * kGroupElems * 2;      // 131072 B: one workgroup per CU
+constexpr int kQElems = kBM * kD;                   // the workgroup's Q rows (32 KB)
+constexpr int kLdsBytes = (2 * kGroupElems + kQElems) * 2;  // 163840 B: one workgroup per CU
 constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dispatched round-robin
 
 struct PrefillArgs {
@@ -63,8 +64,6 @@ struct PrefillArgs {
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *(const u32x4*)p; }
 
 // Raw buffer resource (V#) over `bytes` bytes from `base`: stride 0, gfx9 dword3 with a
 // 32-bit data format. Loads at offsets at or past `bytes` return zeros.
@@ -135,7 +134,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   // this lane's query row
   const int qr = row0 + 32 * wq + (lane & 31);
-  const int qr_c = qr < a.T ? qr : a.T - 1;
   const int q_abs = q_off + qr;                   // causal limit: key <= q_abs
   const int wave_first_abs = q_off + row0 + 32 * wq;
   const int wave_last_abs = wave_first_abs + 31;
@@ -143,23 +141,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   uint16_t* const Ks = lds + g * kGroupElems;     // this group's K tiles: buffer i at Ks + i * kTile
   uint16_t* const Vs = Ks + 2 * kTile;            // and V tiles
-
-  // Q^T as B operand: step s covers dims 16s + 8*hh .. +7. Q is scaled by
-  // scale*log2(e) and rounded to bf16 here, so the scores come out of the MFMA in
-  // the log2 domain and the softmax needs no multiply per score.
-  bf16x8 qop[8];
-  {
-    const uint16_t* qp = a.q + (((int64_t)b * a.Hq + h) * a.T + qr_c) * kD + 8 * hh;
-    u32x4 raw[8];
-    for (int s = 0; s < 8; ++s) raw[s] = ld16(qp + 16 * s);
-    wait_vmem();
-    for (int s = 0; s < 8; ++s) {
-      u32x4 w;
-      for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf16x2(bf16_lo(raw[s][e]) * a.qk_scale, bf16_hi(raw[s][e]) * a.qk_scale);
-      qop[s] = as_bf16x8(w);
-    }
-  }
 
   // K/V of this (batch, kv head) through buffer loads: the resource of a block starts at
   // the block's first row and covers only the rows below kv_len, so rows past the valid
@@ -179,30 +160,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     koff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * i + r4)) * 16);
     voff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * r4)) * 16);
   }
-  auto dma = [&](const char* src, int blk, const uint32_t* off, uint16_t* tile) {
+  auto dma = [&](const char* src, int blk, const uint32_t* off, uint16_t* tile) __attribute__((always_inline)) {
     const int base = blk * kBN;  // < kv_len for every block of the range
     const uint32_t valid = (uint32_t)(kv_len - base) * row_bytes;
     const u32x4 r = buffer_rsrc(src + (int64_t)base * row_bytes, valid);
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
     for (int i = 0; i < 4; ++i) dma16(r, off[i], dst + 4 * i * kD * 2);
   };
-  auto load_k = [&](int j) { dma(Kg, gb0 + j, koff, Ks + (j & 1) * kTile); };
-  auto load_v = [&](int j) { dma(Vg, gb0 + j, voff, Vs + (j & 1) * kTile); };
+  auto load_k = [&](int j) __attribute__((always_inline)) { dma(Kg, gb0 + j, koff, Ks + (j & 1) * kTile); };
+  auto load_v = [&](int j) __attribute__((always_inline)) { dma(Vg, gb0 + j, voff, Vs + (j & 1) * kTile); };
+  // one of the 4 instructions of a tile load (spread over the softmax step so the four
+  // waves of a group do not queue 32 KB at the address unit at once)
+  auto dma_part = [&](const char* src, int blk, const uint32_t* off, uint16_t* tile, int i)
+      __attribute__((always_inline)) {
+    const int base = blk * kBN;
+    const uint32_t valid = (uint32_t)(kv_len - base) * row_bytes;
+    const u32x4 r = buffer_rsrc(src + (int64_t)base * row_bytes, valid);
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
+    dma16(r, off[i], dst + 4 * i * kD * 2);
+  };
 
   // Online softmax state of this lane's row, in the log2 domain. The accumulators hold
-  // o and l relative to the base m_use (p = 2^(s - m_use)); m_use only changes on the
-  // slow path of the softmax step.
+  // o and l relative to the base m_use (p = 2^(s - m_use)); the score MFMA starts from
+  // -m_use, so it yields s - m_use directly. m_use only changes on the slow path of the
+  // softmax step.
   float m_use = 0.f, l_run = 0.f;
   bool seen = false;      // m_use is this row's running max (some score was finite)
   bool all_seen = false;  // wave-uniform: every row of the wave is seen
   bool rescale = false;   // wave-uniform: o is to be scaled by o_scale before the next PV
   float o_scale = 1.f;
-  f32x16 o[4], sc[2];
+  f32x16 negm, o[4], sc[2];
+  for (int i = 0; i < 16; ++i) negm[i] = 0.f;
   for (int dt = 0; dt < 4; ++dt)
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
   for (int kt = 0; kt < 2; ++kt)
     for (int i = 0; i < 16; ++i) sc[kt][i] = 0.f;
   u32x4 pw[4] = {};  // P^T of the last softmax step as bf16 pairs, for the next PV
+  bf16x8 qop[8];     // Q^T operand (set after the prologue)
   const uint32_t ones = 0x3F803F80u;  // bf16 pair (1, 1)
 
   // K operand reads: row (lane & 31) (+32 for sub-tile 1), column chunk 2s + hh, stored
@@ -216,49 +210,86 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   int v_col[4];
   for (int dt = 0; dt < 4; ++dt) v_col[dt] = tr_row * kD + 16 * (grp & 1) + 4 * (s16 & 3) + 32 * (dt ^ (s16 >> 2));
 
-  auto active = [&](int j) { return !causal || (gb0 + j) * kBN <= wave_last_abs; };
+  auto active = [&](int j) __attribute__((always_inline)) { return !causal || (gb0 + j) * kBN <= wave_last_abs; };
 
-  // Matrix step j: O += V^T P^T for block j-1, then S^T = K Q^T for block j. A base
+  // Matrix step j: O += V^T P^T for block j-1, then S^T = K Q^T - m_use for block j. A base
   // change of the softmax step before is applied to o first.
-  auto mstep = [&](int j) {
+  auto pv = [&](int jb) __attribute__((always_inline)) {
+    const uint16_t* Vt = Vs + (jb & 1) * kTile;
+    for (int st = 0; st < 4; ++st) {
+      const int kt = st >> 1, q2 = st & 1;
+      const bf16x8 pop = as_bf16x8(pw[st]);
+      const int rbase = (32 * kt + 16 * q2) * kD;
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint16_t* p0 = Vt + rbase + v_col[dt];
+        const uint16_t* p1 = p0 + 8 * kD;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
+        typedef short s16x8 __attribute__((ext_vector_type(8)));
+        const s16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[dt] = mfma32(__builtin_bit_cast(bf16x8, av), pop, o[dt]);
+      }
+    }
+  };
+  auto qk = [&](int jb) __attribute__((always_inline)) {
+    const uint16_t* kp = Ks + (jb & 1) * kTile + k_lane;
+    // two independent accumulation chains (sub-tiles kt = 0, 1), interleaved
+    for (int s = 0; s < 8; ++s) {
+      const uint16_t* ks = kp + (k_x ^ (16 * s));
+      for (int kt = 0; kt < 2; ++kt)
+        sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(ks + kt * 32 * kD)), qop[s], s == 0 ? f32x16{} : sc[kt]);
+    }
+  };
+  // Issue order of the steady-state matrix step (one wave runs it alone on its SIMD, so
+  // it must hide its own LDS latency): operands stay kRA MFMAs ahead of their use, and
+  // the first K reads are issued under the last PV MFMAs.
+  constexpr int kRA = 4;
+  auto pv_qk_schedule = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kRA, 0);  // V^T reads of the first kRA PV MFMAs
+    for (int i = 0; i < 16 - kRA; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // PV MFMA i
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // V^T reads of PV MFMA i + kRA
+    }
+    for (int i = 0; i < kRA; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // PV MFMA 16 - kRA + i
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // K read of QK MFMA i
+    }
+    for (int i = 0; i < 16 - kRA; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // QK MFMA i
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // K read of QK MFMA i + kRA
+    }
+    for (int i = 0; i < kRA; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  };
+  auto apply_rescale = [&]() __attribute__((always_inline)) {
     if (rescale) {
       for (int dt = 0; dt < 4; ++dt) o[dt] *= o_scale;
       rescale = false;
     }
+  };
+  // general matrix step (first and last steps, causal-inactive blocks)
+  auto mstep = [&](int j) __attribute__((always_inline)) {
+    apply_rescale();
+    const bool do_pv = j >= 1 && j - 1 < ng && active(j - 1);
+    const bool do_qk = j < ng && active(j);
     __builtin_amdgcn_s_setprio(1);
-    if (j >= 1 && j - 1 < ng && active(j - 1)) {
-      const uint16_t* Vt = Vs + ((j - 1) & 1) * kTile;
-      for (int st = 0; st < 4; ++st) {
-        const int kt = st >> 1, q2 = st & 1;
-        const bf16x8 pop = as_bf16x8(pw[st]);
-        const int rbase = (32 * kt + 16 * q2) * kD;
-        for (int dt = 0; dt < 4; ++dt) {
-          const uint16_t* p0 = Vt + rbase + v_col[dt];
-          const uint16_t* p1 = p0 + 8 * kD;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
-          typedef short s16x8 __attribute__((ext_vector_type(8)));
-          const s16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          o[dt] = mfma32(__builtin_bit_cast(bf16x8, av), pop, o[dt]);
-        }
-      }
-    }
-    if (j < ng && active(j)) {
-      const uint16_t* kp = Ks + (j & 1) * kTile + k_lane;
-      // two independent accumulation chains (sub-tiles kt = 0, 1), interleaved
-      for (int s = 0; s < 8; ++s) {
-        const uint16_t* ks = kp + (k_x ^ (16 * s));
-        for (int kt = 0; kt < 2; ++kt)
-          sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(ks + kt * 32 * kD)), qop[s], s == 0 ? f32x16{} : sc[kt]);
-      }
-    }
+    if (do_pv) pv(j - 1);
+    if (do_qk) qk(j);
+    __builtin_amdgcn_s_setprio(0);
+  };
+  // steady-state matrix step: both halves run, as one scheduled region
+  auto mstep_full = [&](int j) __attribute__((always_inline)) {
+    apply_rescale();
+    __builtin_amdgcn_s_setprio(1);
+    pv(j - 1);
+    qk(j);
+    pv_qk_schedule();
     __builtin_amdgcn_s_setprio(0);
   };
 
   // Softmax step j: P for block j (into pw), then the loads of K for block j+2 (its
   // buffer held K of block j, last read by the matrix step just before) and of V for
   // block j+1 (its buffer held V of block j-1, last read by that same matrix step).
-  auto vstep = [&](int j) {
+  auto vstep = [&](int j) __attribute__((always_inline)) {
     if (j < 0 || j >= ng) return;
     if (active(j)) {
       const int kbase = (gb0 + j) * kBN;
@@ -284,16 +315,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       // neither the max nor a rescale is needed.
       bool fast = all_seen;
       if (fast) {
-        for (int st = 0; st < 4; ++st)
+        for (int st = 0; st < 4; ++st) {
+          if (j + 2 < ng) dma_part(Kg, gb0 + j + 2, koff, Ks + (j & 1) * kTile, st);
+          if (j + 1 < ng) dma_part(Vg, gb0 + j + 1, voff, Vs + ((j + 1) & 1) * kTile, st);
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
-            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - m_use),
-                                           __builtin_amdgcn_exp2f(sc[kt][i + 1] - m_use));
+            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - m_use), __builtin_amdgcn_exp2f(sc[kt][i + 1] - m_use));
             pw[st][e] = w;
             if (e & 1) ps1 = dot2_bf16(w, ones, ps1);
             else ps0 = dot2_bf16(w, ones, ps0);
           }
+        }
         fast = !__any(!(ps0 + ps1 <= 256.f));  // NaN/inf fall to the slow path too
+      } else {
+        if (j + 2 < ng) load_k(j + 2);
+        if (j + 1 < ng) load_v(j + 1);
       }
       if (!fast) {
         // Slow path (first block of a row, or a row max that grew): move the base to
@@ -322,9 +358,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         all_seen = __all(seen);
       }
       l_run += ps0 + ps1;
+    } else {
+      if (j + 2 < ng) load_k(j + 2);
+      if (j + 1 < ng) load_v(j + 1);
     }
-    if (j + 2 < ng) load_k(j + 2);
-    if (j + 1 < ng) load_v(j + 1);
     // the loads of the previous softmax step (K of block j+1, V of block j) are read by
     // the next matrix step: wait for them, leaving this step's own loads in flight
     // (loads complete in issue order); step 0's predecessors were waited for up front
@@ -335,33 +372,74 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   };
 
-  // LDS starts zeroed, so tile rows that no load writes (past kv_len: the buffer
-  // resources return zeros, but a stale row could otherwise surface) are finite.
-  for (int i = tid; i < 2 * kGroupElems / 8; i += kThreads) ((u32x4*)lds)[i] = u32x4{0, 0, 0, 0};
-  __syncthreads();
+  // Prologue: the workgroup's 128 Q rows (wave w moves rows 16w .. 16w+15, swizzled as
+  // the K tiles) and this group's first tiles go to LDS together, so their memory
+  // latencies overlap; rows past T and past kv_len arrive as zeros (every tile row is
+  // written on every load, so no stale LDS content is ever read).
+  uint16_t* const Qs = lds + 2 * kGroupElems;
+  {
+    const int qrows = a.T - row0 < kBM ? a.T - row0 : kBM;
+    const u32x4 r = buffer_rsrc(a.q + (((int64_t)b * a.Hq + h) * a.T + row0) * kD, (uint32_t)qrows * kD * 2);
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(Qs + 16 * wave * kD);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = (uint32_t)(16 * wave + 4 * i + r4);
+      dma16(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
+    }
+  }
   if (ng > 0) load_k(0);
   if (ng > 0) load_v(0);
   if (ng > 1) load_k(1);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
 
+  // Q^T as B operand: step s covers dims 16s + 8*hh .. +7 of row 32wq + (lane & 31). Q is
+  // scaled by scale*log2(e) and rounded to bf16 here, so the scores come out of the
+  // MFMA in the log2 domain and the softmax needs no multiply per score.
+  {
+    const uint16_t* qp = Qs + 32 * wq * kD + k_lane;
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 raw = *(const u32x4*)(qp + (k_x ^ (16 * s)));
+      u32x4 w;
+      for (int e = 0; e < 4; ++e)
+        w[e] = pack_bf16x2(bf16_lo(raw[e]) * a.qk_scale, bf16_hi(raw[e]) * a.qk_scale);
+      qop[s] = as_bf16x8(w);
+    }
+  }
+
   // Phase 2t + half: group 0 runs matrix step t then softmax step t; group 1 runs
   // softmax step t-1 then matrix step t, so the groups always sit in opposite halves.
-  // Both loops pass the same number of barriers.
+  // Every wave passes the same number of barriers. Matrix steps 1 .. jm-1 of a wave have
+  // both halves active and run in a loop of their own with the scheduled full step.
+  int j_act = ng;  // blocks this wave attends to (causal: up to its last row)
+  if (causal) {
+    const int last = wave_last_abs / kBN - gb0 + 1;
+    j_act = last < 0 ? 0 : (last < ng ? last : ng);
+  }
+  const int jm = j_act;
   if (g == 0) {
-    for (int t = 0; t <= n0; ++t) {
-      mstep(t);
+    auto half0 = [&](int t, bool full) __attribute__((always_inline)) {
+      if (full) mstep_full(t);
+      else mstep(t);
       __syncthreads();
       vstep(t);
       __syncthreads();
-    }
+    };
+    int t = 0;
+    for (; t <= n0 && t < 1; ++t) half0(t, false);
+    for (; t < jm; ++t) half0(t, true);
+    for (; t <= n0; ++t) half0(t, false);
   } else {
-    for (int t = 0; t <= n0; ++t) {
+    auto half1 = [&](int t, bool full) __attribute__((always_inline)) {
       vstep(t - 1);
       __syncthreads();
-      mstep(t);
+      if (full) mstep_full(t);
+      else mstep(t);
       __syncthreads();
-    }
+    };
+    int t = 0;
+    for (; t <= n0 && t < 1; ++t) half1(t, false);
+    for (; t < jm; ++t) half1(t, true);
+    for (; t <= n0; ++t) half1(t, false);
   }
 
   // Merge: group 1 publishes its (o, m, l) through LDS (the K/V buffers are free now);
