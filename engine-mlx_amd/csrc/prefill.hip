@@ -165,7 +165,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t valid = (uint32_t)(kv_len - base) * row_bytes;
     const u32x4 r = buffer_rsrc(src + (int64_t)base * row_bytes, valid);
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
-    for (int i = 0; i < 4; ++i) dma16(r, off[i], dst + 4 * i * kD * 2);
+    if (base < kv_begin) {
+      // first block of a chunk-only window: rows before kv_begin are outside the
+      // attended range; an out-of-range offset makes them arrive as zeros, so whatever
+      // the cache holds there (even NaN) cannot reach the masked products
+      for (int i = 0; i < 4; ++i) {
+        const int row = base + 16 * wq + 4 * i + r4;
+        dma16(r, row < kv_begin ? 0x80000000u : off[i], dst + 4 * i * kD * 2);
+      }
+    } else {
+      for (int i = 0; i < 4; ++i) dma16(r, off[i], dst + 4 * i * kD * 2);
+    }
   };
   auto load_k = [&](int j) __attribute__((always_inline)) { dma(Kg, gb0 + j, koff, Ks + (j & 1) * kTile); };
   auto load_v = [&](int j) __attribute__((always_inline)) { dma(Vg, gb0 + j, voff, Vs + (j & 1) * kTile); };

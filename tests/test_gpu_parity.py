@@ -315,6 +315,40 @@ def test_prefill_chunk_on_existing_cache_sampled_rows(ema, ora):
             assert_close(out[i, h][None], ref.reshape(1, D), f"row {i} head {h}")
 
 
+@pytest.mark.parametrize("causal,chunk,q_off", [(True, True, 100), (True, True, 64), (False, True, 37),
+                                                (True, False, 150), (False, False, 0)])
+def test_prefill_ignores_cache_rows_outside_the_window(ema, ora, causal, chunk, q_off):
+    """NaN in every cache row outside [kv_begin, kv_len) (before a chunk-only window and
+    past the valid length) gives bit-identical output to finite data there: the
+    reference attends over a slice of the cache (crates/serve/src/forward_qwen3.rs:150),
+    so those rows are never read."""
+    import torch
+
+    B, Hq, Hkv, D, cap, T = 1, 4, 2, 128, 512, 120
+    say(f"prefill NaN outside window causal={causal} chunk={chunk} q_off={q_off}")
+    q = ora.normal_bf16((B, Hq, T, D), seed=360)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=361)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=362)
+    kv_len = q_off + T
+    lo = q_off if chunk else 0
+    qo = np.asarray([q_off], np.int32)
+
+    def run(k, v):
+        out = host(ema.prefill_attention(dev(q), make_cache(ema, k, v), dev(qo), causal=causal, chunk_only=chunk))
+        torch.cuda.synchronize()
+        return out
+
+    clean = run(kc, vc)
+    kp, vp = kc.copy(), vc.copy()
+    for a in (kp, vp):  # bf16 quiet NaN bits
+        a[:, :, kv_len:] = 0x7FC0
+        a[:, :, :lo] = 0x7FC0
+    dirty = run(kp, vp)
+    assert np.array_equal(clean, dirty)
+    ref = ora.sdpa(q, kc, vc, np.asarray([kv_len]), scale_of(D), causal, kv_begin=np.asarray([lo]) if chunk else None)
+    assert_close(clean, ref, "prefill window")
+
+
 def test_prefill_rows_match_decode_on_gpu(ema, ora):
     """Causal prefill row i equals decode with len = off + i + 1 on the same cache."""
     import torch
