@@ -242,12 +242,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   };
   auto qk = [&](int jb) __attribute__((always_inline)) {
+    f32x16 neg_m;  // the chains start from -m_use, so the scores come out relative to it
+    for (int i = 0; i < 16; ++i) neg_m[i] = -m_use;
     const uint16_t* kp = Ks + (jb & 1) * kTile + k_lane;
     // two independent accumulation chains (sub-tiles kt = 0, 1), interleaved
     for (int s = 0; s < 8; ++s) {
       const uint16_t* ks = kp + (k_x ^ (16 * s));
       for (int kt = 0; kt < 2; ++kt)
-        sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(ks + kt * 32 * kD)), qop[s], s == 0 ? f32x16{} : sc[kt]);
+        sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(ks + kt * 32 * kD)), qop[s], s == 0 ? neg_m : sc[kt]);
     }
   };
   // Issue order of the steady-state matrix step (one wave runs it alone on its SIMD, so
@@ -330,7 +332,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           if (j + 1 < ng) dma_part(Vg, gb0 + j + 1, voff, Vs + ((j + 1) & 1) * kTile, st);
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
-            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - m_use), __builtin_amdgcn_exp2f(sc[kt][i + 1] - m_use));
+            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i]), __builtin_amdgcn_exp2f(sc[kt][i + 1]));
             pw[st][e] = w;
             if (e & 1) ps1 = dot2_bf16(w, ones, ps1);
             else ps0 = dot2_bf16(w, ones, ps0);
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         float bm = -INFINITY;
         for (int kt = 0; kt < 2; ++kt)
           for (int i = 0; i < 16; ++i) bm = fmaxf(bm, sc[kt][i]);
-        bm = wave_max_xor(bm, 32) - m_use;
+        bm = wave_max_xor(bm, 32);
         const float delta = seen ? fmaxf(bm, 0.f) : (bm == -INFINITY ? 0.f : bm);
         seen = seen || bm != -INFINITY;
         const float alpha = __builtin_amdgcn_exp2f(-delta);
@@ -359,8 +361,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int st = 0; st < 4; ++st)
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
-            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - m_use),
-                                           __builtin_amdgcn_exp2f(sc[kt][i + 1] - m_use));
+            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - delta),
+                                           __builtin_amdgcn_exp2f(sc[kt][i + 1] - delta));
             pw[st][e] = w;
             if (e & 1) ps1 = dot2_bf16(w, ones, ps1);
             else ps0 = dot2_bf16(w, ones, ps0);
