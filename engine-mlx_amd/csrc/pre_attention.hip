@@ -10,11 +10,14 @@
 // normalised value rounded to bf16 before the weight multiply, RoPE angle
 // pos * 2^(-(i/(D/2)) * log2(theta)) formed in f32.
 //
-// Mapping: one 16-lane group per head vector (b, t, h), h over the
-// Hq + 2*Hkv heads of the fused row; lane j holds elements
-// [j*E, j*E+E) and [D/2 + j*E, D/2 + j*E + E) with E = D/32, so each RoPE pair
-// sits in one lane and each half of the row is one contiguous 2*D-byte access
-// per group. HBM-bound: every byte of qkv is read once, q/k/v written once.
+// Mapping: one workgroup per token (b, t). Its first D/2 threads form the
+// token's RoPE table (cos, sin of each frequency) in LDS once; then each group
+// of 8 lanes takes head vectors h of the fused row (h over the Hq + 2*Hkv
+// heads, stride 32). Lane j holds elements [j*E, j*E+E) and
+// [D/2 + j*E, D/2 + j*E + E) with E = D/16 (16-byte accesses at D = 128), so
+// each RoPE pair sits in one lane and each half of the row is one contiguous
+// D-byte access per group.
+// HBM-bound: every byte of qkv is read once, q/k/v written once.
 #include "ema_common.hpp"
 
 namespace ema {
@@ -65,6 +68,18 @@ struct Vec<8> {
   }
 };
 
+template <>
+struct Vec<16> {
+  static __device__ __forceinline__ void load(const uint16_t* p, uint16_t* x) {
+    Vec<8>::load(p, x);
+    Vec<8>::load(p + 8, x + 8);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const uint16_t* x) {
+    Vec<8>::store(p, x);
+    Vec<8>::store(p + 8, x + 8);
+  }
+};
+
 struct PreArgs {
   const uint16_t* qkv;
   const uint16_t* qw;
@@ -74,7 +89,6 @@ struct PreArgs {
   uint16_t* kc;
   uint16_t* vc;
   int64_t sb, sh, sp;
-  int64_t nvec;
   float eps;
   float log2_theta;
   int B, T, Hq, Hkv, cap;
@@ -84,80 +98,86 @@ struct PreArgs {
 template <int D>
 __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
   constexpr int HALF = D / 2;
-  constexpr int E = D / 32;
-  const int lane16 = threadIdx.x & 15;
-  const int64_t vec = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
-  if (vec >= a.nvec) return;  // whole 16-lane groups exit together
-  const int H = a.Hq + 2 * a.Hkv;
-  const int h = (int)(vec % H);
-  const int64_t bt = vec / H;
+  constexpr int E = D / 16;  // elements per lane in each half of the row
+  // one workgroup per token (b, t); its 32 groups of 8 lanes walk the token's head vectors
+  __shared__ float rope_cs[HALF], rope_sn[HALF];
+  const int64_t bt = blockIdx.x;
   const int t = (int)(bt % a.T);
   const int b = (int)(bt / a.T);
   const int off = a.off[b];
   const int pos = off + t;
   const bool in_cap = off >= 0 && (int64_t)off + a.T <= a.cap;
+  const bool rope = !(a.flags & EMA_PRE_NO_ROPE);
+  // RoPE angles of this position, shared by every q and k head of the token
+  if (rope && (int)threadIdx.x < HALF) {
+    const int i = threadIdx.x;
+    const float inv_freq = exp2f(-((float)i / (float)HALF) * a.log2_theta);
+    const float ang = (float)pos * inv_freq;
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    rope_cs[i] = cs;
+    rope_sn[i] = sn;
+  }
+  __syncthreads();
 
-  const uint16_t* src = a.qkv + vec * D;
-  uint16_t x[2 * E];
-  Vec<E>::load(src + lane16 * E, x);
-  Vec<E>::load(src + HALF + lane16 * E, x + E);
+  const int lane8 = threadIdx.x & 7;
+  const int H = a.Hq + 2 * a.Hkv;
+  for (int h = threadIdx.x >> 3; h < H; h += 32) {
+    const uint16_t* src = a.qkv + (bt * H + h) * D;
+    uint16_t x[2 * E];
+    Vec<E>::load(src + lane8 * E, x);
+    Vec<E>::load(src + HALF + lane8 * E, x + E);
 
-  if (h >= a.Hq + a.Hkv) {  // v: bit copy into the cache row
-    if (!in_cap) return;
-    const int kh = h - a.Hq - a.Hkv;
-    uint16_t* dst = a.vc + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)pos * a.sp;
-    Vec<E>::store(dst + lane16 * E, x);
-    Vec<E>::store(dst + HALF + lane16 * E, x + E);
-    return;
-  }
-  const bool is_q = h < a.Hq;
-  float y[2 * E];
-  if (!(a.flags & EMA_PRE_NO_NORM)) {
-    float ss = 0.f;
-    for (int e = 0; e < 2 * E; ++e) {
-      const float f = bf16_to_f32(x[e]);
-      ss += f * f;
+    if (h >= a.Hq + a.Hkv) {  // v: bit copy into the cache row
+      if (!in_cap) continue;
+      const int kh = h - a.Hq - a.Hkv;
+      uint16_t* dst = a.vc + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)pos * a.sp;
+      Vec<E>::store(dst + lane8 * E, x);
+      Vec<E>::store(dst + HALF + lane8 * E, x + E);
+      continue;
     }
-    ss += __shfl_xor(ss, 8, 16);
-    ss += __shfl_xor(ss, 4, 16);
-    ss += __shfl_xor(ss, 2, 16);
-    ss += __shfl_xor(ss, 1, 16);
-    const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
-    const uint16_t* w = is_q ? a.qw : a.kw;
-    uint16_t wv[2 * E];
-    Vec<E>::load(w + lane16 * E, wv);
-    Vec<E>::load(w + HALF + lane16 * E, wv + E);
-    for (int e = 0; e < 2 * E; ++e) {
-      const float n = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32(x[e]) * inv));
-      y[e] = bf16_to_f32((uint16_t)f32_to_bf16_bits(n * bf16_to_f32(wv[e])));
+    const bool is_q = h < a.Hq;
+    if (!is_q && !in_cap) continue;
+    float y[2 * E];
+    if (!(a.flags & EMA_PRE_NO_NORM)) {
+      float ss = 0.f;
+      for (int e = 0; e < 2 * E; ++e) {
+        const float f = bf16_to_f32(x[e]);
+        ss += f * f;
+      }
+      ss += __shfl_xor(ss, 4, 8);
+      ss += __shfl_xor(ss, 2, 8);
+      ss += __shfl_xor(ss, 1, 8);
+      const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+      const uint16_t* w = is_q ? a.qw : a.kw;
+      uint16_t wv[2 * E];
+      Vec<E>::load(w + lane8 * E, wv);
+      Vec<E>::load(w + HALF + lane8 * E, wv + E);
+      for (int e = 0; e < 2 * E; ++e) {
+        const float n = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32(x[e]) * inv));
+        y[e] = bf16_to_f32((uint16_t)f32_to_bf16_bits(n * bf16_to_f32(wv[e])));
+      }
+    } else {
+      for (int e = 0; e < 2 * E; ++e) y[e] = bf16_to_f32(x[e]);
     }
-  } else {
-    for (int e = 0; e < 2 * E; ++e) y[e] = bf16_to_f32(x[e]);
-  }
-  uint16_t o[2 * E];
-  if (!(a.flags & EMA_PRE_NO_ROPE)) {
-    for (int e = 0; e < E; ++e) {
-      const int i = lane16 * E + e;
-      const float inv_freq = exp2f(-((float)i / (float)HALF) * a.log2_theta);
-      const float ang = (float)pos * inv_freq;
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
-      const float x1 = y[e], x2 = y[E + e];
-      o[e] = (uint16_t)f32_to_bf16_bits(x1 * cs - x2 * sn);
-      o[E + e] = (uint16_t)f32_to_bf16_bits(x1 * sn + x2 * cs);
+    uint16_t o[2 * E];
+    if (rope) {
+      for (int e = 0; e < E; ++e) {
+        const int i = lane8 * E + e;
+        const float cs = rope_cs[i], sn = rope_sn[i];
+        const float x1 = y[e], x2 = y[E + e];
+        o[e] = (uint16_t)f32_to_bf16_bits(x1 * cs - x2 * sn);
+        o[E + e] = (uint16_t)f32_to_bf16_bits(x1 * sn + x2 * cs);
+      }
+    } else {
+      for (int e = 0; e < 2 * E; ++e) o[e] = (uint16_t)f32_to_bf16_bits(y[e]);
     }
-  } else {
-    for (int e = 0; e < 2 * E; ++e) o[e] = (uint16_t)f32_to_bf16_bits(y[e]);
+    uint16_t* dst;
+    if (is_q) dst = a.q_out + (((int64_t)b * a.Hq + h) * a.T + t) * D;
+    else dst = a.kc + (int64_t)b * a.sb + (int64_t)(h - a.Hq) * a.sh + (int64_t)pos * a.sp;
+    Vec<E>::store(dst + lane8 * E, o);
+    Vec<E>::store(dst + HALF + lane8 * E, o + E);
   }
-  uint16_t* dst;
-  if (is_q) {
-    dst = a.q_out + (((int64_t)b * a.Hq + h) * a.T + t) * D;
-  } else {
-    if (!in_cap) return;
-    dst = a.kc + (int64_t)b * a.sb + (int64_t)(h - a.Hq) * a.sh + (int64_t)pos * a.sp;
-  }
-  Vec<E>::store(dst + lane16 * E, o);
-  Vec<E>::store(dst + HALF + lane16 * E, o + E);
 }
 
 }  // namespace
@@ -177,7 +197,6 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   a.sb = c.stride_batch;
   a.sh = c.stride_head;
   a.sp = c.stride_pos;
-  a.nvec = (int64_t)B * T * (Hq + 2 * Hkv);
   a.eps = eps;
   a.log2_theta = log2f(theta);
   a.B = B;
@@ -187,8 +206,8 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   a.cap = c.capacity;
   a.flags = flags;
   const int threads = 256;
-  const int64_t blocks = (a.nvec + 15) / 16;
-  if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many head vectors");
+  const int64_t blocks = (int64_t)B * T;  // one workgroup per token
+  if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many tokens");
   switch (D) {
     case 64:
       hipLaunchKernelGGL(pre_attention_kernel<64>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
