@@ -59,6 +59,7 @@ struct PrefillArgs {
   int64_t sb, sh, sp;
   float qk_scale;  // scale * log2(e), applied to Q
   int B, Hq, Hkv, G, T, cap, nqb;
+  int paired;  // each workgroup runs query blocks qb and nqb-1-qb of one head, in turn
   uint32_t flags;
 };
 
@@ -97,14 +98,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // query heads of a group run on the group's XCD, so its K/V stream is read from HBM
   // once and served from that L2 to every workgroup that attends over it. Inside an XCD
   // (or over the whole grid otherwise) work items are ranked heaviest first: a later
-  // query block sees more keys.
+  // query block sees more keys. With two workgroups' worth of query blocks or more per
+  // CU, a workgroup takes a pair instead -- the heavy query block nqb-1-p, then the light
+  // one p of the same head -- which balances the causal work per workgroup and pays the
+  // launch of one workgroup per pair.
   const int groups = a.B * a.Hkv;
   const bool by_xcd = groups % kXcds == 0 && gridDim.x % kXcds == 0;
   const int64_t x = blockIdx.x;
   const int64_t rank = by_xcd ? x / kXcds : x;
   const int groups_local = by_xcd ? groups / kXcds : groups;
   const int per_qb = groups_local * a.G;
-  const int qb = a.nqb - 1 - (int)(rank / per_qb);
+  const int qb_first = a.nqb - 1 - (int)(rank / per_qb);
+  const int qb_second = a.paired ? a.nqb - 1 - qb_first : qb_first;  // == qb_first: no second
   const int rest = (int)(rank % per_qb);
   const int grp_id = by_xcd ? (rest / a.G) * kXcds + (int)(x % kXcds) : rest / a.G;
   const int b = grp_id / a.Hkv;
@@ -113,6 +118,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   int q_off = a.q_off[b];
   q_off = q_off < 0 ? 0 : q_off;
+  auto run_block = [&](const int qb) __attribute__((always_inline)) {
   int kv_len = q_off + a.T;
   kv_len = kv_len > a.cap ? a.cap : kv_len;
   const bool causal = a.flags & EMA_PREFILL_CAUSAL;
@@ -469,7 +475,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     xl[wq * 64 + lane] = l_run;
   }
   __syncthreads();
-  if (g == 1) return;
+  if (g == 0) {
   const float m1 = xm[wq * 64 + lane];
   const float l1 = xl[wq * 64 + lane];
   const float m0 = seen ? m_use : -INFINITY;
@@ -483,17 +489,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   const float l_mine = l_run * a0 + l1 * a1;
   const float l_tot = l_mine + __shfl_xor(l_mine, 32, 64);
-  if (qr >= a.T) return;
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  // lane holds O[q][32dt + (i%4) + 8(i/4) + 4hh]
-  uint16_t* dst = a.out + (((int64_t)b * a.T + qr) * a.Hq + h) * kD + 4 * hh;
-  for (int dt = 0; dt < 4; ++dt)
-    for (int qq = 0; qq < 4; ++qq) {
-      u32x2 wv;
-      wv[0] = pack_bf16x2(o[dt][4 * qq] * inv, o[dt][4 * qq + 1] * inv);
-      wv[1] = pack_bf16x2(o[dt][4 * qq + 2] * inv, o[dt][4 * qq + 3] * inv);
-      *(u32x2*)(dst + 32 * dt + 8 * qq) = wv;
-    }
+  if (qr < a.T) {
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    // lane holds O[q][32dt + (i%4) + 8(i/4) + 4hh]
+    uint16_t* dst = a.out + (((int64_t)b * a.T + qr) * a.Hq + h) * kD + 4 * hh;
+    for (int dt = 0; dt < 4; ++dt)
+      for (int qq = 0; qq < 4; ++qq) {
+        u32x2 wv;
+        wv[0] = pack_bf16x2(o[dt][4 * qq] * inv, o[dt][4 * qq + 1] * inv);
+        wv[1] = pack_bf16x2(o[dt][4 * qq + 2] * inv, o[dt][4 * qq + 3] * inv);
+        *(u32x2*)(dst + 32 * dt + 8 * qq) = wv;
+      }
+  }
+  }
+  };
+
+  run_block(qb_first);
+  if (qb_second != qb_first) {
+    __syncthreads();  // the merge area is read before the next block's tiles land there
+    run_block(qb_second);
+  }
 }
 
 }  // namespace
@@ -534,7 +549,17 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
   a.cap = c.capacity;
   a.nqb = (T + kBM - 1) / kBM;
   a.flags = flags;
-  const int64_t blocks = (int64_t)a.nqb * Hq * c.batch;
+  // pair the query blocks when there are at least two workgroups' worth per CU
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  const int64_t items = (int64_t)a.nqb * Hq * c.batch;
+  a.paired = a.nqb >= 2 && items >= 2 * (int64_t)cus;
+  const int64_t blocks = a.paired ? (int64_t)((a.nqb + 1) / 2) * Hq * c.batch : items;
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_prefill_attention: grid too large");
   hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
   return check_hip(hipGetLastError(), "ema_prefill_attention launch");
