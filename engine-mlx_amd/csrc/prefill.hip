@@ -13,7 +13,8 @@
 // 32 rows, each group streaming its own 64-key K/V blocks through its own
 // double-buffered LDS. The two partial (o, m, l) states of a row meet in LDS at the end.
 // Halving the key range halves the longest causal work item, and workgroups are
-// dispatched heaviest first, so the short ones fill in behind the long ones.
+// dispatched heaviest first, so the short ones fill in behind the long ones (or, with
+// two or more query blocks per CU, each workgroup runs a heavy and a light block).
 //
 // Both contractions run on MFMA 32x32x16 (bf16 in, f32 accumulate), in the transposed
 // form that keeps the softmax lane-local:
@@ -26,9 +27,9 @@
 // Ping-pong: the two waves on each SIMD belong to different groups, and the groups run
 // half a block out of phase, separated by workgroup barriers. In one phase group 0 issues
 // its matrix step (PV of block j-1 and QK of block j, 32 MFMAs) while group 1 runs the
-// softmax of its block and its K/V staging (VALU, exp, LDS stores, global loads); in the
-// next phase the roles swap. The matrix pipe and the vector pipe of a SIMD are fed by
-// different waves throughout.
+// softmax of its block (VALU, exp) and issues the global-to-LDS loads of its next tiles;
+// in the next phase the roles swap. The matrix pipe and the vector pipe of a SIMD are fed
+// by different waves throughout.
 #include "ema_common.hpp"
 
 namespace ema {
@@ -205,8 +206,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   bool all_seen = false;  // wave-uniform: every row of the wave is seen
   bool rescale = false;   // wave-uniform: o is to be scaled by o_scale before the next PV
   float o_scale = 1.f;
-  f32x16 negm, o[4], sc[2];
-  for (int i = 0; i < 16; ++i) negm[i] = 0.f;
+  f32x16 o[4], sc[2];
   for (int dt = 0; dt < 4; ++dt)
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
   for (int kt = 0; kt < 2; ++kt)
