@@ -69,9 +69,9 @@ class Ctx:
 
 
 def time_calls(torch, fn, steps, warmup):
-    """Average ms per call of fn(): `steps` calls captured in one HIP graph and
-    replayed, timed with HIP events on the replay stream, so host launch cost
-    is not in the figure."""
+    """Average ms per call of fn(): `steps` calls captured in one HIP graph; after
+    three warm replays, five replays are timed with HIP events on the replay stream
+    and the median is returned, so host launch cost is not in the figure."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -83,14 +83,19 @@ def time_calls(torch, fn, steps, warmup):
             for _ in range(steps):
                 fn()
     torch.cuda.synchronize()
+    times = []
     with torch.cuda.stream(stream):
-        graph.replay()  # warm replay
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        graph.replay()
-        e1.record(stream)
+        for _ in range(3):
+            graph.replay()  # warm replays (clocks settle under sustained load)
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) / steps)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    return sorted(times)[len(times) // 2]  # median of 5 timed replays
 
 
 # ---------------------------------------------------------------- decode
