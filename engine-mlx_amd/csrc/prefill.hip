@@ -460,53 +460,77 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (; t <= n0; ++t) half1(t, false);
   }
 
-  // Merge: group 1 publishes its (o, m, l) through LDS (the K/V buffers are free now);
-  // group 0 combines them with its own and writes the output rows.
-  float* const xo = (float*)lds;                       // [dt][i4][wq][lane] f32x4
-  float* const xm = xo + 4 * 4 * 4 * 64 * 4;           // [wq][lane] m (or -inf)
-  float* const xl = xm + 4 * 64;                       // [wq][lane] l share
-  if (g == 1) {
-    for (int dt = 0; dt < 4; ++dt)
-      for (int i4 = 0; i4 < 4; ++i4) {
-        f32x4 v = {o[dt][4 * i4], o[dt][4 * i4 + 1], o[dt][4 * i4 + 2], o[dt][4 * i4 + 3]};
-        *(f32x4*)(xo + (((dt * 4 + i4) * 4 + wq) * 64 + lane) * 4) = v;
-      }
-    xm[wq * 64 + lane] = seen ? m_use : -INFINITY;
-    xl[wq * 64 + lane] = l_run;
+  // Merge. Each group finishes half of the head dims: group g keeps dims 64g .. 64g+63
+  // (accumulators dt = 2g, 2g+1) and hands the other half to the other group through LDS
+  // (the tiles are dead now), together with its (m, l). The normalised bf16 rows go to a
+  // staging tile in the Q area (Q is in registers since the prologue), from which all
+  // eight waves store whole 256-byte rows with 16-byte stores.
+  //   xo[g]: [d][i4][wq][lane] f32x4, the dims of group g that the other group finishes
+  //   xm[g], xl[g]: [wq][lane] this group's m (or -inf) and l share of the row
+  float* const xo = (float*)lds;
+  float* const xm = xo + 2 * 2 * 4 * 4 * 64 * 4;
+  float* const xl = xm + 2 * 4 * 64;
+  const int rr = 32 * wq + (lane & 31);  // row inside the workgroup
+  {
+    float* const mx = xo + g * (2 * 4 * 4 * 64 * 4);
+    auto publish = [&](const int dt0) __attribute__((always_inline)) {
+      for (int d = 0; d < 2; ++d)
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const f32x16& od = o[dt0 + d];
+          const f32x4 v = {od[4 * i4], od[4 * i4 + 1], od[4 * i4 + 2], od[4 * i4 + 3]};
+          *(f32x4*)(mx + (((d * 4 + i4) * 4 + wq) * 64 + lane) * 4) = v;
+        }
+    };
+    if (g == 0) publish(2);
+    else publish(0);
+    xm[(g * 4 + wq) * 64 + lane] = seen ? m_use : -INFINITY;
+    xl[(g * 4 + wq) * 64 + lane] = l_run;
   }
   __syncthreads();
-  if (g == 0) {
-  const float m1 = xm[wq * 64 + lane];
-  const float l1 = xl[wq * 64 + lane];
-  const float m0 = seen ? m_use : -INFINITY;
-  const float m = fmaxf(m0, m1);
-  const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
-  const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-  for (int dt = 0; dt < 4; ++dt)
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const f32x4 v = *(const f32x4*)(xo + (((dt * 4 + i4) * 4 + wq) * 64 + lane) * 4);
-      for (int e = 0; e < 4; ++e) o[dt][4 * i4 + e] = o[dt][4 * i4 + e] * a0 + v[e] * a1;
-    }
-  const float l_mine = l_run * a0 + l1 * a1;
-  const float l_tot = l_mine + __shfl_xor(l_mine, 32, 64);
-  if (qr < a.T) {
+  {
+    const float m0 = xm[wq * 64 + lane], m1 = xm[(4 + wq) * 64 + lane];
+    const float l0 = xl[wq * 64 + lane], l1 = xl[(4 + wq) * 64 + lane];
+    const float m = fmaxf(m0, m1);
+    const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
+    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+    const float l_half = l0 * a0 + l1 * a1;
+    const float l_tot = l_half + __shfl_xor(l_half, 32, 64);
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    // lane holds O[q][32dt + (i%4) + 8(i/4) + 4hh]
-    uint16_t* dst = a.out + (((int64_t)b * a.T + qr) * a.Hq + h) * kD + 4 * hh;
-    for (int dt = 0; dt < 4; ++dt)
-      for (int qq = 0; qq < 4; ++qq) {
-        u32x2 wv;
-        wv[0] = pack_bf16x2(o[dt][4 * qq] * inv, o[dt][4 * qq + 1] * inv);
-        wv[1] = pack_bf16x2(o[dt][4 * qq + 2] * inv, o[dt][4 * qq + 3] * inv);
-        *(u32x2*)(dst + 32 * dt + 8 * qq) = wv;
-      }
+    const float a_mine = g ? a1 : a0, a_other = g ? a0 : a1;
+    const float* const ox = xo + (1 - g) * (2 * 4 * 4 * 64 * 4);
+    uint16_t* const St = Qs;  // bf16 [128 rows][128 dims], 16-byte chunk c of row r at c ^ (r & 15)
+    auto finish = [&](const int dt0) __attribute__((always_inline)) {
+      for (int d = 0; d < 2; ++d)
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const f32x4 v = *(const f32x4*)(ox + (((d * 4 + i4) * 4 + wq) * 64 + lane) * 4);
+          float r[4];
+          for (int e = 0; e < 4; ++e) r[e] = (o[dt0 + d][4 * i4 + e] * a_mine + v[e] * a_other) * inv;
+          // lane holds O[rr][32dt + (i%4) + 8(i/4) + 4hh]: chunk 4dt + i4, half hh
+          u32x2 wv;
+          wv[0] = pack_bf16x2(r[0], r[1]);
+          wv[1] = pack_bf16x2(r[2], r[3]);
+          const int c = 4 * (dt0 + d) + i4;
+          *(u32x2*)(St + rr * kD + 8 * (c ^ (rr & 15)) + 4 * hh) = wv;
+        }
+    };
+    if (g == 0) finish(0);
+    else finish(2);
   }
+  __syncthreads();
+  {
+    // 128 rows x 16 chunks over 512 threads: a wave stores 4 whole rows per instruction
+    for (int it = 0; it < 4; ++it) {
+      const int n = it * kThreads + tid;
+      const int r = n >> 4, c = n & 15;
+      const u32x4 v = *(const u32x4*)(Qs + r * kD + 8 * (c ^ (r & 15)));
+      if (row0 + r < a.T) *(u32x4*)(a.out + (((int64_t)b * a.T + row0 + r) * a.Hq + h) * kD + 8 * c) = v;
+    }
   }
   };
 
   run_block(qb_first);
   if (qb_second != qb_first) {
-    __syncthreads();  // the merge area is read before the next block's tiles land there
+    __syncthreads();  // the staging tile is read before the next block's Q lands there
     run_block(qb_second);
   }
 }
