@@ -69,9 +69,11 @@ class Ctx:
 
 
 def time_calls(torch, fn, steps, warmup):
-    """Average ms per call of fn(): `steps` calls captured in one HIP graph; after
-    three warm replays, five replays are timed with HIP events on the replay stream
-    and the median is returned, so host launch cost is not in the figure."""
+    """Average ms per call of fn(): `steps` calls captured in one HIP graph; the graph is
+    replayed for about half a second first (so the clocks reach the level they hold
+    under sustained load of this kernel), then five replays are timed with HIP events on
+    the replay stream and the median is returned, so host launch cost is not in the
+    figure."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -85,8 +87,12 @@ def time_calls(torch, fn, steps, warmup):
     torch.cuda.synchronize()
     times = []
     with torch.cuda.stream(stream):
-        for _ in range(3):
+        t_warm = time.perf_counter() + 0.5
+        n_warm = 0
+        while n_warm < 3 or time.perf_counter() < t_warm:
             graph.replay()  # warm replays (clocks settle under sustained load)
+            stream.synchronize()
+            n_warm += 1
         for _ in range(5):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
@@ -130,6 +136,13 @@ def primary(ctx, ema, args):
         ema.decode_step(qkv2d, qw, kw, 1e-6, 1e6, off_d, Hq, cache, cap, scale, out=out, workspace=ws)
 
     qkv2d = qkv.reshape(B, -1)
+    # untimed: about half a second of steps (clocks settle under sustained load), then the
+    # W warmup steps
+    t_warm = time.perf_counter() + 0.5
+    while time.perf_counter() < t_warm:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
