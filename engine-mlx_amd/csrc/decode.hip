@@ -132,11 +132,12 @@ struct Combine {
 // RMSNorm + split-half RoPE of the head vector whose dims 8*(4s + c) + j (s < 4, j < 8)
 // this lane holds in x[8s + j] (c = lane / 16; the four lanes of one head together
 // hold all 128 dims, and dims d, d + 64 -- a RoPE pair -- sit in one lane as s, s + 2).
-// Same arithmetic as the pre-attention kernel: f32 statistics, normalised value
-// rounded to bf16 before the weight multiply; cs_tab[i] = (cos, sin) of the angle
-// pos * 2^(-(i/64) log2 theta) formed in f32.
-__device__ __forceinline__ void norm_rope_q(const DecodeArgs& a, float (&x)[32], const uint16_t* w, int c,
-                                            const float2* cs_tab) {
+// wv[s] holds the norm weights of the same dims. Same arithmetic as the pre-attention
+// kernel: f32 statistics, normalised value rounded to bf16 before the weight multiply;
+// cs_tab[i] = (cos, sin) of the angle pos * 2^(-(i/64) log2 theta) formed in f32.
+__device__ __forceinline__ void norm_rope(const DecodeArgs& a, float (&x)[32], const u32x4 (&wv)[4],
+                                          const float2* cs_tab) {
+  const int c = (threadIdx.x & 63) >> 4;
   if (!(a.flags & EMA_PRE_NO_NORM)) {
     float ss = 0.f;
     for (int e = 0; e < 32; ++e) ss += x[e] * x[e];
@@ -144,10 +145,9 @@ __device__ __forceinline__ void norm_rope_q(const DecodeArgs& a, float (&x)[32],
     ss += __shfl_xor(ss, 32, 64);
     const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
     for (int s2 = 0; s2 < 4; ++s2) {
-      const u32x4 wv = ld16(w + 8 * (4 * s2 + c));
       for (int j = 0; j < 8; ++j) {
         const float n = bf16_to_f32((uint16_t)f32_to_bf16_bits(x[8 * s2 + j] * inv));
-        const float wj = (j & 1) ? bf16_hi(wv[j >> 1]) : bf16_lo(wv[j >> 1]);
+        const float wj = (j & 1) ? bf16_hi(wv[s2][j >> 1]) : bf16_lo(wv[s2][j >> 1]);
         x[8 * s2 + j] = bf16_to_f32((uint16_t)f32_to_bf16_bits(n * wj));
       }
     }
@@ -164,12 +164,18 @@ __device__ __forceinline__ void norm_rope_q(const DecodeArgs& a, float (&x)[32],
   }
 }
 
+// bf16 pairs of the 4 chunks a lane holds -> f32 x[8s + j]
+__device__ __forceinline__ void unpack32(const u32x4 (&r)[4], float (&x)[32]) {
+  for (int s = 0; s < 4; ++s)
+    for (int j = 0; j < 8; ++j) x[8 * s + j] = (j & 1) ? bf16_hi(r[s][j >> 1]) : bf16_lo(r[s][j >> 1]);
+}
+
 template <bool kFused>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
-  __shared__ __attribute__((aligned(16))) uint16_t new_kv[2][kD];  // fused: the new token's k, v
-  __shared__ float2 rope_cs[kD / 2];                                 // fused: RoPE (cos, sin) at the offset
+  __shared__ float2 rope_cs[kWaves][kD / 2];  // fused: each wave's RoPE (cos, sin) table at the offset
+  __shared__ __attribute__((aligned(16))) uint16_t new_kv[2][kD];  // fused: the new row, for its owner wave
   build_prefix(a, pre);
   if (blockIdx.x == 0)
     for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.hdr[i] = pre[i];
@@ -249,72 +255,85 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int F = (a.Hq + 2 * a.Hkv) * kD;
     const uint16_t* qh = kFused ? a.qkv + (int64_t)b * F + ((int64_t)kh * a.G + gc) * kD
                                 : a.q + ((int64_t)b * a.Hq + (int64_t)kh * a.G + gc) * kD;
-    u32x4 qraw[4];
+    u32x4 qraw[4], qwv[4];
+    uint16_t kr1 = 0, kr2 = 0, kw1 = 0, kw2 = 0, vr1 = 0, vr2 = 0;
     for (int s = 0; s < 4; ++s) qraw[s] = ld16(qh + 8 * (4 * s + c));
+    // fused: the wave that will run the segment's last tile (position L - 1 = offset) forms
+    // the new k, v row; its inputs are loaded now, with the q row and the norm weights
+    const bool owner = kFused && tile1 == nb && wave == (nb - 1 - tile0) % kWaves;
+    if (kFused) {
+      for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + 8 * (4 * s + c));
+      if (owner) {  // lane i: dims i and i + 64 (a RoPE pair)
+        const uint16_t* kr = a.qkv + (int64_t)b * F + ((int64_t)a.Hq + kh) * kD;
+        const uint16_t* vr = kr + (int64_t)a.Hkv * kD;
+        kr1 = kr[lane];
+        kr2 = kr[lane + 64];
+        kw1 = a.kw[lane];
+        kw2 = a.kw[lane + 64];
+        vr1 = vr[lane];
+        vr2 = vr[lane + 64];
+      }
+    }
     if (first < tile1) load_tile(first, kc, vc);
     bf16x8 qop[4];
+    const float2* const cs_tab = rope_cs[wave];
     if (!kFused) {
       const u32x4 z = {0u, 0u, 0u, 0u};
       for (int s = 0; s < 4; ++s) qop[s] = as_bf16x8(g < a.G ? qraw[s] : z);
     } else {
-      // q = rope(norm(q_raw)) of this head, from the fused qkv row; the 64 RoPE
-      // angles of this sequence's offset are formed once per piece into LDS
+      // q = rope(norm(q_raw)) of this head, from the fused qkv row. Each wave forms the 64
+      // RoPE angles of this sequence's offset into its own table (lane i: angle i), so no
+      // workgroup barrier is needed.
       const int off = a.off[b];
-      if (tid < kD / 2 && !(a.flags & EMA_PRE_NO_ROPE)) {
-        const float inv_freq = exp2f(-((float)tid / (float)(kD / 2)) * a.log2_theta);
+      if (!(a.flags & EMA_PRE_NO_ROPE)) {
+        const float inv_freq = exp2f(-((float)lane / (float)(kD / 2)) * a.log2_theta);
         float sn, cs;
         sincosf((float)off * inv_freq, &sn, &cs);
-        rope_cs[tid] = make_float2(cs, sn);
+        rope_cs[wave][lane] = make_float2(cs, sn);
       }
-      __syncthreads();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float x[32];
-      for (int s = 0; s < 4; ++s)
-        for (int j = 0; j < 8; ++j) x[8 * s + j] = (j & 1) ? bf16_hi(qraw[s][j >> 1]) : bf16_lo(qraw[s][j >> 1]);
-      norm_rope_q(a, x, a.qw, c, rope_cs);
+      unpack32(qraw, x);
+      norm_rope(a, x, qwv, cs_tab);
       for (int s = 0; s < 4; ++s) {
         u32x4 v;
         for (int e = 0; e < 4; ++e) v[e] = g < a.G ? pack_bf16x2(x[8 * s + 2 * e], x[8 * s + 2 * e + 1]) : 0u;
         qop[s] = as_bf16x8(v);
       }
-      // The workgroup whose slice ends the segment owns the new row (position L - 1 =
-      // offset): it forms k = rope(norm(k_raw)) and v, writes both into the cache and
-      // uses them for its last tile from LDS. No other workgroup reads that row.
-      const bool in_cap = off >= 0 && off < a.cap;
-      if (tile1 == nb) {
-        if (wave == 0) {
-          const uint16_t* kr = a.qkv + (int64_t)b * F + ((int64_t)a.Hq + kh) * kD;
-          const uint16_t* vr = kr + (int64_t)a.Hkv * kD;
-          float k1 = bf16_to_f32(kr[lane]), k2 = bf16_to_f32(kr[lane + 64]);
-          if (!(a.flags & EMA_PRE_NO_NORM)) {
-            float ss = k1 * k1 + k2 * k2;
-            for (int mm = 32; mm >= 1; mm >>= 1) ss += __shfl_xor(ss, mm, 64);
-            const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
-            k1 = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32((uint16_t)f32_to_bf16_bits(k1 * inv)) *
-                                                       bf16_to_f32(a.kw[lane])));
-            k2 = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32((uint16_t)f32_to_bf16_bits(k2 * inv)) *
-                                                       bf16_to_f32(a.kw[lane + 64])));
-          }
-          if (!(a.flags & EMA_PRE_NO_ROPE)) {
-            const float cs = rope_cs[lane].x, sn = rope_cs[lane].y;
-            const float r1 = k1 * cs - k2 * sn, r2 = k1 * sn + k2 * cs;
-            k1 = r1;
-            k2 = r2;
-          }
-          const uint16_t kb1 = (uint16_t)f32_to_bf16_bits(k1), kb2 = (uint16_t)f32_to_bf16_bits(k2);
-          new_kv[0][lane] = kb1;
-          new_kv[0][lane + 64] = kb2;
-          new_kv[1][lane] = vr[lane];
-          new_kv[1][lane + 64] = vr[lane + 64];
-          if (in_cap) {
-            uint16_t* kd = (uint16_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
-            uint16_t* vd = (uint16_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
-            kd[lane] = kb1;
-            kd[lane + 64] = kb2;
-            vd[lane] = vr[lane];
-            vd[lane + 64] = vr[lane + 64];
-          }
+      if (owner && off == L - 1) {
+        // the new row (lane i: dims i, i + 64): k = rope(norm(k_raw)), v a bit copy; it
+        // goes to the cache at the offset and to LDS, from where this same wave patches
+        // its last tile (rows clamped to L - 1 = the new token)
+        float k1 = bf16_to_f32(kr1), k2 = bf16_to_f32(kr2);
+        if (!(a.flags & EMA_PRE_NO_NORM)) {
+          float ss = k1 * k1 + k2 * k2;
+          for (int mm = 32; mm >= 1; mm >>= 1) ss += __shfl_xor(ss, mm, 64);
+          const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
+          k1 = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32((uint16_t)f32_to_bf16_bits(k1 * inv)) * bf16_to_f32(kw1)));
+          k2 = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32((uint16_t)f32_to_bf16_bits(k2 * inv)) * bf16_to_f32(kw2)));
         }
-        __syncthreads();
+        if (!(a.flags & EMA_PRE_NO_ROPE)) {
+          const float cs = cs_tab[lane].x, sn = cs_tab[lane].y;
+          const float r1 = k1 * cs - k2 * sn, r2 = k1 * sn + k2 * cs;
+          k1 = r1;
+          k2 = r2;
+        }
+        const uint16_t kb1 = (uint16_t)f32_to_bf16_bits(k1), kb2 = (uint16_t)f32_to_bf16_bits(k2);
+        new_kv[0][lane] = kb1;
+        new_kv[0][lane + 64] = kb2;
+        new_kv[1][lane] = vr1;
+        new_kv[1][lane + 64] = vr2;
+        uint16_t* const kd = (uint16_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+        uint16_t* const vd = (uint16_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+        kd[lane] = kb1;
+        kd[lane + 64] = kb2;
+        vd[lane] = vr1;
+        vd[lane + 64] = vr2;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
     }
 
@@ -322,8 +341,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const bool more = tile + kWaves < tile1;
       if (more) load_tile(tile + kWaves, kn, vn);
       const int p0 = tile * kTile;
-      if (kFused && tile == nb - 1 && a.off[b] == L - 1) {
-        // rows clamped to L - 1 = the new token: take its k, v from LDS
+      if (kFused && owner && tile == nb - 1 && a.off[b] == L - 1) {
         for (int r = 0; r < 2; ++r)
           if (p0 + krow0 + 4 * r >= L - 1)
             for (int s = 0; s < 4; ++s) kc[r][s] = *(const u32x4*)&new_kv[0][8 * (4 * s + c)];
