@@ -40,7 +40,15 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
   if (!c) return set_error(EMA_ERR_INVALID_ARG, "%s: cache descriptor is null", op);
   if (!c->k || !c->v) return set_error(EMA_ERR_INVALID_ARG, "%s: KV cache is empty (null K/V buffer)", op);
-  if (c->dtype != EMA_DTYPE_BF16) return set_error(EMA_ERR_INVALID_ARG, "%s: cache dtype must be bf16", op);
+  if (c->dtype != EMA_DTYPE_BF16 && c->dtype != EMA_DTYPE_FP8_E4M3)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: cache dtype %d is neither bf16 nor fp8 e4m3", op, c->dtype);
+  if (c->dtype == EMA_DTYPE_FP8_E4M3) {
+    if (!c->k_exp || !c->v_exp) return set_error(EMA_ERR_INVALID_ARG, "%s: fp8 cache without block exponents", op);
+    if (c->head_dim != 128)
+      return set_error(EMA_ERR_UNSUPPORTED, "%s: fp8 cache with head_dim %d not supported (128)", op, c->head_dim);
+    if (c->stride_pos % 16 || c->stride_head % 16 || c->stride_batch % 16)
+      return set_error(EMA_ERR_SHAPE, "%s: fp8 cache strides must be multiples of 16 bytes", op);
+  }
   if (c->batch <= 0 || c->n_kv_heads <= 0 || c->capacity <= 0 || c->head_dim <= 0)
     return set_error(EMA_ERR_SHAPE, "%s: cache dims must be positive (batch=%d n_kv_heads=%d capacity=%d head_dim=%d)",
                      op, c->batch, c->n_kv_heads, c->capacity, c->head_dim);
@@ -109,14 +117,60 @@ int32_t ema_kvcache_alloc(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_hea
   return ema_kvcache_init(out, k, v, batch, n_kv_heads, capacity, head_dim);
 }
 
+int32_t ema_kvcache_init_fp8(ema_kvcache_desc* d, void* k, void* v, void* k_exp, void* v_exp, int32_t batch,
+                             int32_t n_kv_heads, int32_t capacity, int32_t head_dim) {
+  if (!d) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_init_fp8: descriptor is null");
+  memset(d, 0, sizeof(*d));
+  d->k = k;
+  d->v = v;
+  d->k_exp = k_exp;
+  d->v_exp = v_exp;
+  d->batch = batch;
+  d->n_kv_heads = n_kv_heads;
+  d->capacity = capacity;
+  d->head_dim = head_dim;
+  d->stride_pos = head_dim;
+  d->stride_head = (int64_t)capacity * head_dim;
+  d->stride_batch = (int64_t)n_kv_heads * capacity * head_dim;
+  d->dtype = EMA_DTYPE_FP8_E4M3;
+  return check_cache("ema_kvcache_init_fp8", d);
+}
+
+int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads, int32_t capacity,
+                              int32_t head_dim) {
+  const char* op = "ema_kvcache_alloc_fp8";
+  if (!out) return set_error(EMA_ERR_INVALID_ARG, "%s: descriptor is null", op);
+  memset(out, 0, sizeof(*out));
+  if (batch <= 0 || n_kv_heads <= 0 || capacity <= 0 || head_dim != 128)
+    return set_error(head_dim != 128 && head_dim > 0 ? EMA_ERR_UNSUPPORTED : EMA_ERR_SHAPE,
+                     "%s: bad dims (batch=%d n_kv_heads=%d capacity=%d head_dim=%d; fp8 needs head_dim 128)", op,
+                     batch, n_kv_heads, capacity, head_dim);
+  const size_t rows = (size_t)batch * n_kv_heads * capacity;
+  const size_t code_bytes = rows * head_dim, exp_bytes = rows * (head_dim / 64);
+  void* p[4] = {nullptr, nullptr, nullptr, nullptr};
+  const size_t sz[4] = {code_bytes, code_bytes, exp_bytes, exp_bytes};
+  int32_t rc = EMA_OK;
+  for (int i = 0; i < 4 && !rc; ++i) {
+    rc = check_hip(hipMalloc(&p[i], sz[i]), "ema_kvcache_alloc_fp8: hipMalloc");
+    if (!rc) rc = check_hip(hipMemset(p[i], 0, sz[i]), "ema_kvcache_alloc_fp8: zero");
+  }
+  if (rc) {
+    for (int i = 0; i < 4; ++i)
+      if (p[i]) (void)hipFree(p[i]);
+    return rc;
+  }
+  return ema_kvcache_init_fp8(out, p[0], p[1], p[2], p[3], batch, n_kv_heads, capacity, head_dim);
+}
+
 int32_t ema_kvcache_free(ema_kvcache_desc* d) {
   if (!d) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_free: descriptor is null");
   int32_t rc = EMA_OK;
-  if (d->k) rc = check_hip(hipFree(d->k), "ema_kvcache_free: K");
-  if (d->v) {
-    int32_t r2 = check_hip(hipFree(d->v), "ema_kvcache_free: V");
-    rc = rc ? rc : r2;
-  }
+  void* const bufs[4] = {d->k, d->v, d->k_exp, d->v_exp};
+  for (int i = 0; i < 4; ++i)
+    if (bufs[i]) {
+      const int32_t r2 = check_hip(hipFree(bufs[i]), "ema_kvcache_free");
+      rc = rc ? rc : r2;
+    }
   memset(d, 0, sizeof(*d));
   return rc;
 }
@@ -125,7 +179,8 @@ int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* d, uint64_t* bytes) {
   if (!bytes) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_memory_bytes: output is null");
   int32_t rc = check_cache("ema_kvcache_memory_bytes", d);
   if (rc) return rc;
-  *bytes = 2ull * d->batch * d->n_kv_heads * d->capacity * d->head_dim * 2ull;
+  const uint64_t rows = 2ull * d->batch * d->n_kv_heads * d->capacity;  // K and V
+  *bytes = d->dtype == EMA_DTYPE_FP8_E4M3 ? rows * (d->head_dim + d->head_dim / 64) : rows * d->head_dim * 2ull;
   return EMA_OK;
 }
 
@@ -228,6 +283,8 @@ int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvca
     return set_error(EMA_ERR_CAPACITY, "%s: %d tokens exceed capacity %d", op, n_tokens, cache->capacity);
   if (!(scale > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: scale must be > 0", op);
   if (!aligned16(q) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: q/out must be 16-byte aligned", op);
+  if (cache->dtype != EMA_DTYPE_BF16)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over an fp8 cache is not supported (bf16 only)", op);
   return launch_prefill((hipStream_t)stream, q, *cache, q_offsets, n_tokens, n_heads, scale, flags, out);
 }
 

@@ -33,6 +33,11 @@
 // also holds it in the B-operand slot of P^T, so P never crosses lanes; the
 // only cross-lane traffic per tile is the max over the four 16-lane groups.
 // All softmax state is f32; P is rounded to bf16 for the PV MFMA.
+//
+// FP8 E4M3FN cache: a lane loads the same row pieces as 8 codes (8 bytes) instead of
+// 8 bf16 values, plus the row's two block exponents, and turns them into the same bf16
+// operands just before use (code value times 2^exp is exact in bf16). Half the bytes,
+// identical arithmetic after the decode step.
 #include <cstdlib>
 
 #include "ema_common.hpp"
@@ -66,6 +71,9 @@ struct DecodeArgs {
   float eps, log2_theta;
   uint32_t flags;
   int fused;
+  // fp8 cache: block exponents [B, Hkv, cap, 2] (k, v then hold E4M3FN codes)
+  const int8_t* kexp;
+  const int8_t* vexp;
 };
 
 __device__ __forceinline__ int64_t worker_of(int64_t t, int64_t total, int W) {
@@ -121,6 +129,37 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *(const u32x4*
 __device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
   return __builtin_nontemporal_load((const u32x4*)p);
 }
+__device__ __forceinline__ u32x2 ld8_stream(const uint8_t* p) { return __builtin_nontemporal_load((const u32x2*)p); }
+
+// 8 E4M3FN codes -> 8 bf16 values code * 2^e (exact), in the bf16 operand layout
+__device__ __forceinline__ u32x4 fp8_decode8(u32x2 w, int e) {
+  const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  u32x4 o;
+  o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], sc, false));
+  o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], sc, true));
+  o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], sc, false));
+  o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], sc, true));
+  return o;
+}
+
+// Quantisation of one 64-value block held one value per lane (the fused step's new row):
+// exponent ceil(log2(amax / 448)), amax = max(1e-4, max |x|) over the wave (logarithm in
+// double, rounded to f32: an f32 log2 rounded to nearest), code = E4M3FN(x * 2^-e) with
+// +-448 saturation (NaN -> +448) and -0 stored as +0. Returns the code; *xq gets the
+// decoded bf16 bits.
+__device__ __forceinline__ uint32_t fp8_quant_lane(float x, int* e_out, uint16_t* xq) {
+  float amax = fmaxf(fabsf(x), 1.0e-4f);
+  for (int mm = 32; mm >= 1; mm >>= 1) amax = fmaxf(amax, __shfl_xor(amax, mm, 64));
+  const int e = (int)ceilf((float)log2((double)(amax / 448.0f)));
+  float y = x * ldexpf(1.0f, -e);
+  y = y != y ? 448.0f : fminf(fmaxf(y, -448.0f), 448.0f);
+  const uint32_t code = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y + 0.0f, 0.0f, 0, false) & 0xffu;
+  const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
+  *xq = (uint16_t)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)code, sc, false));
+  *e_out = e;
+  return code;
+}
 
 // LDS used to combine the four waves' states at the end of a piece.
 struct Combine {
@@ -170,7 +209,7 @@ __device__ __forceinline__ void unpack32(const u32x4 (&r)[4], float (&x)[32]) {
     for (int j = 0; j < 8; ++j) x[8 * s + j] = (j & 1) ? bf16_hi(r[s][j >> 1]) : bf16_lo(r[s][j >> 1]);
 }
 
-template <bool kFused>
+template <bool kFused, bool kFp8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
@@ -231,7 +270,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f32x4 o[8];
     for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // fp8: codes and exponents of the tile in flight, decoded into kc/vc before use
+    const uint8_t* const Kb8 = (const uint8_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh;
+    const uint8_t* const Vb8 = (const uint8_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh;
+    const int64_t erow = ((int64_t)b * a.Hkv + kh) * a.cap;  // exponent row of position 0
+    const uint16_t* const Ke = kFp8 ? (const uint16_t*)a.kexp + erow : nullptr;
+    const uint16_t* const Ve = kFp8 ? (const uint16_t*)a.vexp + erow : nullptr;
+    u32x2 k8[2][4], v8[8], k8n[2][4], v8n[8];
+    uint32_t ke[2], ve[8], ken[2], ven[8];
+    auto load_tile8 = [&](int tile, u32x2 (&kr)[2][4], u32x2 (&vr)[8], uint32_t (&kx)[2], uint32_t (&vx)[8]) {
+      const int p0 = tile * kTile;
+      for (int r = 0; r < 2; ++r) {
+        int p = p0 + krow0 + 4 * r;
+        p = p < L ? p : L - 1;
+        const uint8_t* row = Kb8 + (int64_t)p * a.sp;
+        for (int s = 0; s < 4; ++s) kr[r][s] = ld8_stream(row + 8 * (4 * s + c));
+        kx[r] = Ke[p];
+      }
+      for (int kk = 0; kk < 8; ++kk) {
+        int p = p0 + 8 * c + kk;
+        p = p < L ? p : L - 1;
+        vr[kk] = ld8_stream(Vb8 + (int64_t)p * a.sp + 8 * m);
+        vx[kk] = Ve[p];
+      }
+    };
     u32x4 kc[2][4], vc[8], kn[2][4], vn[8];
+    auto decode_tile8 = [&]() {
+      for (int r = 0; r < 2; ++r)
+        for (int s = 0; s < 4; ++s) kc[r][s] = fp8_decode8(k8[r][s], (int)(int8_t)(ke[r] >> (s >= 2 ? 8 : 0)));
+      for (int kk = 0; kk < 8; ++kk) vc[kk] = fp8_decode8(v8[kk], (int)(int8_t)(ve[kk] >> (m >= 8 ? 8 : 0)));
+    };
     auto load_tile = [&](int tile, u32x4 (&kr)[2][4], u32x4 (&vr)[8]) {
       const int p0 = tile * kTile;
       for (int r = 0; r < 2; ++r) {
@@ -274,7 +342,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         vr2 = vr[lane + 64];
       }
     }
-    if (first < tile1) load_tile(first, kc, vc);
+    if (first < tile1) {
+      if (kFp8) load_tile8(first, k8, v8, ke, ve);
+      else load_tile(first, kc, vc);
+    }
     bf16x8 qop[4];
     const float2* const cs_tab = rope_cs[wave];
     if (!kFused) {
@@ -321,16 +392,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           k2 = r2;
         }
         const uint16_t kb1 = (uint16_t)f32_to_bf16_bits(k1), kb2 = (uint16_t)f32_to_bf16_bits(k2);
-        new_kv[0][lane] = kb1;
-        new_kv[0][lane + 64] = kb2;
-        new_kv[1][lane] = vr1;
-        new_kv[1][lane + 64] = vr2;
-        uint16_t* const kd = (uint16_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
-        uint16_t* const vd = (uint16_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
-        kd[lane] = kb1;
-        kd[lane + 64] = kb2;
-        vd[lane] = vr1;
-        vd[lane + 64] = vr2;
+        if (kFp8) {
+          // the row is stored as E4M3FN codes and attended in its decoded form
+          uint16_t d[4];
+          int e[4];
+          const uint32_t c0 = fp8_quant_lane(bf16_to_f32(kb1), &e[0], &d[0]);
+          const uint32_t c1 = fp8_quant_lane(bf16_to_f32(kb2), &e[1], &d[1]);
+          const uint32_t c2 = fp8_quant_lane(bf16_to_f32(vr1), &e[2], &d[2]);
+          const uint32_t c3 = fp8_quant_lane(bf16_to_f32(vr2), &e[3], &d[3]);
+          new_kv[0][lane] = d[0];
+          new_kv[0][lane + 64] = d[1];
+          new_kv[1][lane] = d[2];
+          new_kv[1][lane + 64] = d[3];
+          uint8_t* const kd = (uint8_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+          uint8_t* const vd = (uint8_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+          kd[lane] = (uint8_t)c0;
+          kd[lane + 64] = (uint8_t)c1;
+          vd[lane] = (uint8_t)c2;
+          vd[lane + 64] = (uint8_t)c3;
+          if (lane == 0) {
+            ((uint16_t*)a.kexp)[erow + off] = (uint16_t)((uint8_t)e[0] | ((uint32_t)(uint8_t)e[1] << 8));
+            ((uint16_t*)a.vexp)[erow + off] = (uint16_t)((uint8_t)e[2] | ((uint32_t)(uint8_t)e[3] << 8));
+          }
+        } else {
+          new_kv[0][lane] = kb1;
+          new_kv[0][lane + 64] = kb2;
+          new_kv[1][lane] = vr1;
+          new_kv[1][lane + 64] = vr2;
+          uint16_t* const kd = (uint16_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+          uint16_t* const vd = (uint16_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+          kd[lane] = kb1;
+          kd[lane + 64] = kb2;
+          vd[lane] = vr1;
+          vd[lane + 64] = vr2;
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -339,7 +434,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     for (int tile = first; tile < tile1; tile += kWaves) {
       const bool more = tile + kWaves < tile1;
-      if (more) load_tile(tile + kWaves, kn, vn);
+      if (kFp8) {
+        if (more) load_tile8(tile + kWaves, k8n, v8n, ken, ven);
+        decode_tile8();
+      } else if (more) {
+        load_tile(tile + kWaves, kn, vn);
+      }
       const int p0 = tile * kTile;
       if (kFused && owner && tile == nb - 1 && a.off[b] == L - 1) {
         for (int r = 0; r < 2; ++r)
@@ -396,9 +496,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         o[j] = mfma16(as_bf16x8(av), pop, o[j]);
       }
       if (more) {
-        for (int r = 0; r < 2; ++r)
-          for (int s = 0; s < 4; ++s) kc[r][s] = kn[r][s];
-        for (int kk = 0; kk < 8; ++kk) vc[kk] = vn[kk];
+        if (kFp8) {
+          for (int r = 0; r < 2; ++r) {
+            for (int s = 0; s < 4; ++s) k8[r][s] = k8n[r][s];
+            ke[r] = ken[r];
+          }
+          for (int kk = 0; kk < 8; ++kk) {
+            v8[kk] = v8n[kk];
+            ve[kk] = ven[kk];
+          }
+        } else {
+          for (int r = 0; r < 2; ++r)
+            for (int s = 0; s < 4; ++s) kc[r][s] = kn[r][s];
+          for (int kk = 0; kk < 8; ++kk) vc[kk] = vn[kk];
+        }
       }
     }
 
@@ -559,10 +670,14 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.eps = fused ? fused->eps : 0.f;
   a.log2_theta = fused ? log2f(fused->theta) : 0.f;
   a.flags = fused ? fused->flags : 0u;
-  if (a.fused)
-    hipLaunchKernelGGL(decode_kernel<true>, dim3(plan.workers), dim3(kWaves * 64), 0, s, a);
-  else
-    hipLaunchKernelGGL(decode_kernel<false>, dim3(plan.workers), dim3(kWaves * 64), 0, s, a);
+  a.kexp = (const int8_t*)c.k_exp;
+  a.vexp = (const int8_t*)c.v_exp;
+  const bool fp8 = c.dtype == EMA_DTYPE_FP8_E4M3;
+  const dim3 grid(plan.workers), block(kWaves * 64);
+  if (a.fused && fp8) hipLaunchKernelGGL((decode_kernel<true, true>), grid, block, 0, s, a);
+  else if (a.fused) hipLaunchKernelGGL((decode_kernel<true, false>), grid, block, 0, s, a);
+  else if (fp8) hipLaunchKernelGGL((decode_kernel<false, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((decode_kernel<false, false>), grid, block, 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");
   if (rc) return rc;
   if (plan.workers > 1) {

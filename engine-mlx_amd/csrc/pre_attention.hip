@@ -18,6 +18,11 @@
 // each RoPE pair sits in one lane and each half of the row is one contiguous
 // D-byte access per group.
 // HBM-bound: every byte of qkv is read once, q/k/v written once.
+//
+// FP8 E4M3FN cache (D = 128): the two halves of a row that the 8 lanes of a head hold
+// are exactly its two 64-element blocks; each block's scale exponent comes from an
+// 8-lane max, and the lane writes its 2 x 8 codes (the quantisation of
+// crates/ops/src/fp8.rs:71-92, applied to the bf16 row as Fp8Cache::append does).
 #include "ema_common.hpp"
 
 namespace ema {
@@ -88,6 +93,8 @@ struct PreArgs {
   uint16_t* q_out;
   uint16_t* kc;
   uint16_t* vc;
+  int8_t* kexp;  // fp8 cache: block exponents [B, Hkv, cap, D/64]
+  int8_t* vexp;
   int64_t sb, sh, sp;
   float eps;
   float log2_theta;
@@ -95,7 +102,38 @@ struct PreArgs {
   uint32_t flags;
 };
 
-template <int D>
+// Scale exponent of one 64-element block from this lane's share (amax over the 8 lanes
+// of the head): ceil(log2(amax / 448)) with amax = max(1e-4, max |x|). The logarithm is
+// taken in double and rounded to f32 before the ceiling, which reproduces an f32 log2
+// rounded to nearest (the reference's f32::log2) also just above powers of two.
+__device__ __forceinline__ int fp8_block_exp(float amax_lane) {
+  float amax = fmaxf(amax_lane, 1.0e-4f);
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+  return (int)ceilf((float)log2((double)(amax / 448.0f)));
+}
+
+// 8 values (bf16 bits) -> 8 E4M3FN codes of v * 2^-e: clamp to +-448 (NaN -> +448, as
+// the reference's f32::min does), round to nearest even; -0 is stored as +0.
+__device__ __forceinline__ u32x2 fp8_encode8(const uint16_t* x, int e) {
+  const float inv = ldexpf(1.0f, -e);
+  float y[8];
+  for (int i = 0; i < 8; ++i) {
+    float t = bf16_to_f32(x[i]) * inv;
+    t = t != t ? 448.0f : fminf(fmaxf(t, -448.0f), 448.0f);
+    y[i] = t + 0.0f;
+  }
+  u32x2 w;
+  for (int h = 0; h < 2; ++h) {
+    int d = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h], y[4 * h + 1], 0, false);
+    d = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h + 2], y[4 * h + 3], d, true);
+    w[h] = (uint32_t)d;
+  }
+  return w;
+}
+
+template <int D, bool kFp8>
 __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
   constexpr int HALF = D / 2;
   constexpr int E = D / 16;  // elements per lane in each half of the row
@@ -122,6 +160,22 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
 
   const int lane8 = threadIdx.x & 7;
   const int H = a.Hq + 2 * a.Hkv;
+  // fp8 cache row (b, kh, pos) from the bf16 values x[0..2E) of this lane (E = 8)
+  auto store_fp8 = [&](const uint16_t* x, uint16_t* codes16, int8_t* exps, int b_, int kh, int p_) {
+    float m0 = 0.f, m1 = 0.f;
+    for (int e = 0; e < E; ++e) {
+      m0 = fmaxf(m0, fabsf(bf16_to_f32(x[e])));
+      m1 = fmaxf(m1, fabsf(bf16_to_f32(x[E + e])));
+    }
+    const int e0 = fp8_block_exp(m0), e1 = fp8_block_exp(m1);
+    uint8_t* row = (uint8_t*)codes16 + (int64_t)b_ * a.sb + (int64_t)kh * a.sh + (int64_t)p_ * a.sp;
+    *(u32x2*)(row + lane8 * E) = fp8_encode8(x, e0);
+    *(u32x2*)(row + HALF + lane8 * E) = fp8_encode8(x + E, e1);
+    if (lane8 == 0) {
+      const int64_t r = ((int64_t)b_ * a.Hkv + kh) * a.cap + p_;
+      *(uint16_t*)(exps + 2 * r) = (uint16_t)((uint8_t)e0 | ((uint32_t)(uint8_t)e1 << 8));
+    }
+  };
   for (int h = threadIdx.x >> 3; h < H; h += 32) {
     const uint16_t* src = a.qkv + (bt * H + h) * D;
     uint16_t x[2 * E];
@@ -131,6 +185,10 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
     if (h >= a.Hq + a.Hkv) {  // v: bit copy into the cache row
       if (!in_cap) continue;
       const int kh = h - a.Hq - a.Hkv;
+      if (kFp8) {
+        store_fp8(x, a.vc, a.vexp, b, kh, pos);
+        continue;
+      }
       uint16_t* dst = a.vc + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)pos * a.sp;
       Vec<E>::store(dst + lane8 * E, x);
       Vec<E>::store(dst + HALF + lane8 * E, x + E);
@@ -172,6 +230,10 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
     } else {
       for (int e = 0; e < 2 * E; ++e) o[e] = (uint16_t)f32_to_bf16_bits(y[e]);
     }
+    if (kFp8 && !is_q) {
+      store_fp8(o, a.kc, a.kexp, b, h - a.Hq, pos);
+      continue;
+    }
     uint16_t* dst;
     if (is_q) dst = a.q_out + (((int64_t)b * a.Hq + h) * a.T + t) * D;
     else dst = a.kc + (int64_t)b * a.sb + (int64_t)(h - a.Hq) * a.sh + (int64_t)pos * a.sp;
@@ -194,6 +256,8 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   a.q_out = (uint16_t*)q_out;
   a.kc = (uint16_t*)c.k;
   a.vc = (uint16_t*)c.v;
+  a.kexp = (int8_t*)c.k_exp;
+  a.vexp = (int8_t*)c.v_exp;
   a.sb = c.stride_batch;
   a.sh = c.stride_head;
   a.sp = c.stride_pos;
@@ -208,15 +272,19 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   const int threads = 256;
   const int64_t blocks = (int64_t)B * T;  // one workgroup per token
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many tokens");
+  if (c.dtype == EMA_DTYPE_FP8_E4M3) {  // head_dim 128 (checked with the descriptor)
+    hipLaunchKernelGGL((pre_attention_kernel<128, true>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
+    return check_hip(hipGetLastError(), "ema_pre_attention launch");
+  }
   switch (D) {
     case 64:
-      hipLaunchKernelGGL(pre_attention_kernel<64>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      hipLaunchKernelGGL((pre_attention_kernel<64, false>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
       break;
     case 128:
-      hipLaunchKernelGGL(pre_attention_kernel<128>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      hipLaunchKernelGGL((pre_attention_kernel<128, false>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
       break;
     case 256:
-      hipLaunchKernelGGL(pre_attention_kernel<256>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      hipLaunchKernelGGL((pre_attention_kernel<256, false>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
       break;
     default:
       return set_error(EMA_ERR_UNSUPPORTED, "ema_pre_attention: head_dim %d not supported (64/128/256)", D);

@@ -27,6 +27,7 @@ EMA_ERR_UNSUPPORTED = -5
 EMA_ERR_HIP = -6
 
 EMA_DTYPE_BF16 = 1
+EMA_DTYPE_FP8_E4M3 = 2
 EMA_PRE_NO_NORM = 1
 EMA_PRE_NO_ROPE = 2
 EMA_PREFILL_CAUSAL = 1
@@ -34,6 +35,7 @@ EMA_PREFILL_CHUNK_ONLY = 2
 
 EXPORTED = (
     "ema_last_error", "ema_version", "ema_kvcache_init", "ema_kvcache_alloc", "ema_kvcache_free",
+    "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
     "ema_decode_attention", "ema_decode_step", "ema_prefill_attention",
 )
@@ -54,6 +56,7 @@ class KvCacheDesc(ctypes.Structure):
         ("capacity", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("stride_batch", ctypes.c_int64), ("stride_head", ctypes.c_int64),
         ("stride_pos", ctypes.c_int64), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("k_exp", ctypes.c_void_p), ("v_exp", ctypes.c_void_p),
     ]
 
 
@@ -73,6 +76,8 @@ def lib() -> ctypes.CDLL:
             "ema_version": (ctypes.c_char_p, []),
             "ema_kvcache_init": (i32, [D, vp, vp, i32, i32, i32, i32]),
             "ema_kvcache_alloc": (i32, [D, i32, i32, i32, i32]),
+            "ema_kvcache_init_fp8": (i32, [D, vp, vp, vp, vp, i32, i32, i32, i32]),
+            "ema_kvcache_alloc_fp8": (i32, [D, i32, i32, i32, i32]),
             "ema_kvcache_free": (i32, [D]),
             "ema_kvcache_memory_bytes": (i32, [D, ctypes.POINTER(u64)]),
             "ema_pre_attention": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, i32, i32, i32, u32, vp, D]),
@@ -115,25 +120,44 @@ def _stream(stream) -> int | None:
 
 
 class StaticCache:
-    """Static pre-allocated bf16 KV cache of one layer, [B, Hkv, cap, D].
+    """Static pre-allocated KV cache of one layer, [B, Hkv, cap, D], bf16 or FP8.
 
     Mirrors the reference's static KV state (crates/serve/src/engine.rs:31-42,
     alloc_kv_static at crates/serve/src/engine_ext.rs:266-306) behind the
     KvCache trait surface (crates/kvcache/src/lib.rs:52-76): ``len`` is the
     number of valid positions per sequence, ``reset`` only rewinds the offsets
     (stale rows stay and are excluded by length, engine_ext.rs:218-228).
+
+    ``dtype="fp8"``: the stored form of the reference's Fp8Cache
+    (crates/kvcache/src/fp8.rs): ``k``/``v`` are uint8 E4M3FN codes and
+    ``k_exp``/``v_exp`` int8 [B, Hkv, cap, D/64] block exponents
+    (value = code * 2^exp); head_dim 128.
     """
 
     def __init__(self, batch: int, n_kv_heads: int, capacity: int, head_dim: int, device="cuda",
-                 k=None, v=None):
+                 k=None, v=None, dtype="bf16", k_exp=None, v_exp=None):
         import torch
 
         shape = (batch, n_kv_heads, capacity, head_dim)
-        self.k = k if k is not None else torch.zeros(shape, dtype=torch.bfloat16, device=device)
-        self.v = v if v is not None else torch.zeros(shape, dtype=torch.bfloat16, device=device)
         self.desc = KvCacheDesc()
-        _check(lib().ema_kvcache_init(ctypes.byref(self.desc), _ptr(self.k), _ptr(self.v), batch, n_kv_heads,
-                                      capacity, head_dim), "ema_kvcache_init")
+        self.dtype = dtype
+        if dtype == "bf16":
+            self.k = k if k is not None else torch.zeros(shape, dtype=torch.bfloat16, device=device)
+            self.v = v if v is not None else torch.zeros(shape, dtype=torch.bfloat16, device=device)
+            self.k_exp = self.v_exp = None
+            _check(lib().ema_kvcache_init(ctypes.byref(self.desc), _ptr(self.k), _ptr(self.v), batch, n_kv_heads,
+                                          capacity, head_dim), "ema_kvcache_init")
+        elif dtype == "fp8":
+            eshape = (batch, n_kv_heads, capacity, head_dim // 64)
+            self.k = k if k is not None else torch.zeros(shape, dtype=torch.uint8, device=device)
+            self.v = v if v is not None else torch.zeros(shape, dtype=torch.uint8, device=device)
+            self.k_exp = k_exp if k_exp is not None else torch.zeros(eshape, dtype=torch.int8, device=device)
+            self.v_exp = v_exp if v_exp is not None else torch.zeros(eshape, dtype=torch.int8, device=device)
+            _check(lib().ema_kvcache_init_fp8(ctypes.byref(self.desc), _ptr(self.k), _ptr(self.v), _ptr(self.k_exp),
+                                              _ptr(self.v_exp), batch, n_kv_heads, capacity, head_dim),
+                   "ema_kvcache_init_fp8")
+        else:
+            raise ValueError(f"unknown cache dtype {dtype!r} (bf16 or fp8)")
         self.offsets = [0] * batch
 
     @property

@@ -16,6 +16,10 @@
  *   MlxCtx::sdpa(causal=true)  blas.rs:82-101                   ema_prefill_attention
  *   static KV buffers  crates/serve/src/engine_ext.rs:266-306   ema_kvcache_*
  *   KvCache::memory_bytes  crates/kvcache/src/lib.rs:75         ema_kvcache_memory_bytes
+ *   Fp8Cache (E4M3FN round trip per 64-value block)
+ *              crates/kvcache/src/fp8.rs:47-68, crates/ops/src/fp8.rs:71-92
+ *                                                               ema_kvcache_init_fp8 / _alloc_fp8
+ *                                                               (stored, not simulated)
  *
  * Conventions
  *   - Every entry point returns int32_t: EMA_OK (0) or a negative EMA_ERR_*.
@@ -52,6 +56,13 @@ extern "C" {
 #define EMA_ERR_HIP (-6)         /* HIP runtime error (launch, malloc)       */
 
 #define EMA_DTYPE_BF16 1
+/* FP8 E4M3FN codes (one byte per element) plus one int8 exponent per 64-element block
+ * of a row: element = e4m3(code) * 2^exp. Written with the quantisation of the
+ * reference's FP8 cache (crates/ops/src/fp8.rs:71-92: exp = ceil(log2(amax / 448)),
+ * amax = max(1e-4, max |x|) over the block, round to nearest even, saturate at 448; the
+ * whole head is quantised, i.e. n_rot = 0). Decoded exactly to bf16 by the readers.
+ * head_dim 128 only. Values must be finite. */
+#define EMA_DTYPE_FP8_E4M3 2
 
 /* ema_pre_attention flags */
 #define EMA_PRE_NO_NORM 1u /* q_norm/k_norm are None: crates/ops/src/attention.rs:57-76 */
@@ -72,9 +83,12 @@ typedef void* ema_stream_t; /* hipStream_t */
 #endif
 
 /* Static KV cache of one layer: K and V of logical shape
- * [batch, n_kv_heads, capacity, head_dim], bf16, head_dim contiguous.
+ * [batch, n_kv_heads, capacity, head_dim], head_dim contiguous, bf16 or FP8 E4M3FN.
  * Owned by the caller (the reference allocates these once at MAX_CAP,
- * crates/serve/src/engine_ext.rs:266-306, and reuses them across requests). */
+ * crates/serve/src/engine_ext.rs:266-306, and reuses them across requests).
+ * FP8: k/v hold the codes (strides in elements = bytes, multiples of 16) and
+ * k_exp/v_exp the block exponents, int8 [batch, n_kv_heads, capacity, head_dim / 64],
+ * contiguous. */
 typedef struct ema_kvcache_desc {
   void* k;
   void* v;
@@ -85,8 +99,10 @@ typedef struct ema_kvcache_desc {
   int64_t stride_batch; /* in elements */
   int64_t stride_head;  /* in elements */
   int64_t stride_pos;   /* in elements, >= head_dim */
-  int32_t dtype;        /* EMA_DTYPE_BF16 */
+  int32_t dtype;        /* EMA_DTYPE_BF16 or EMA_DTYPE_FP8_E4M3 */
   int32_t reserved;
+  void* k_exp;          /* EMA_DTYPE_FP8_E4M3: block exponents of K and V (else NULL) */
+  void* v_exp;
 } ema_kvcache_desc;
 
 /* Thread-local message of the last failed call on this thread ("" if none). */
@@ -101,9 +117,16 @@ EMA_API int32_t ema_kvcache_init(ema_kvcache_desc* desc, void* k, void* v, int32
  * crates/serve/src/engine_ext.rs:273-278). Not for the hot path. */
 EMA_API int32_t ema_kvcache_alloc(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads,
                           int32_t capacity, int32_t head_dim);
-/* Free buffers obtained from ema_kvcache_alloc and clear the descriptor. */
+/* FP8 E4M3FN cache over caller-owned codes [batch, n_kv_heads, capacity, head_dim] (uint8)
+ * and exponents [batch, n_kv_heads, capacity, head_dim / 64] (int8), all contiguous. */
+EMA_API int32_t ema_kvcache_init_fp8(ema_kvcache_desc* desc, void* k, void* v, void* k_exp, void* v_exp,
+                                     int32_t batch, int32_t n_kv_heads, int32_t capacity, int32_t head_dim);
+/* Allocate a zeroed FP8 cache (codes and exponents). Not for the hot path. */
+EMA_API int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads,
+                                      int32_t capacity, int32_t head_dim);
+/* Free buffers obtained from ema_kvcache_alloc or ema_kvcache_alloc_fp8 and clear the descriptor. */
 EMA_API int32_t ema_kvcache_free(ema_kvcache_desc* desc);
-/* Bytes held by K and V (KvCache::memory_bytes, crates/kvcache/src/lib.rs:75). */
+/* Bytes held by K and V, exponents included (KvCache::memory_bytes, crates/kvcache/src/lib.rs:75). */
 EMA_API int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* desc, uint64_t* bytes);
 
 /* Fused Qwen3 pre-attention for `batch` sequences of `n_tokens` new tokens.
@@ -116,7 +139,9 @@ EMA_API int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* desc, uint64_t*
  * (base theta), then K and V are written into cache rows [offsets[b], offsets[b]+n_tokens).
  * Replaces forward_qwen3.rs:56-68,124-142 and compiled.rs:134-161.
  * Offsets are read on the device; offsets[b] + n_tokens > capacity writes nothing
- * for that sequence (callers guard on the host as decode_compiled.rs:18-20 does). */
+ * for that sequence (callers guard on the host as decode_compiled.rs:18-20 does).
+ * FP8 cache: each written K and V row is quantised per 64-element block (the bf16 k
+ * after norm and RoPE, v as given), as Fp8Cache::append does (crates/kvcache/src/fp8.rs:47-68). */
 EMA_API int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_norm_w,
                           const void* k_norm_w, float eps, float theta, const int32_t* offsets,
                           int32_t batch, int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads,
@@ -135,7 +160,9 @@ EMA_API int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_
  *            clamped to [0, capacity]; a sequence with 0 valid positions yields zeros
  *   max_len  host upper bound of lengths (sizes the split; <= capacity)
  *   out      [batch, n_heads * head_dim] bf16 (the o_proj input layout)
- * GQA: q head h reads kv head h / (n_heads / n_kv_heads). */
+ * GQA: q head h reads kv head h / (n_heads / n_kv_heads).
+ * FP8 cache: K/V rows are decoded exactly to bf16 (code value times 2^exp) and attended
+ * as a bf16 cache holding those values would be. */
 EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                              const int32_t* lengths, int32_t max_len, int32_t n_heads,
                              float scale, void* out, void* workspace, uint64_t workspace_bytes);
@@ -150,7 +177,9 @@ EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const e
  *   offsets  device int32 [batch]; an offset outside [0, capacity) writes nothing
  *   max_len  host upper bound of offsets[b] + 1 (sizes the split; <= capacity)
  *   out      [batch, n_heads * head_dim] bf16
- * The workspace is the one ema_decode_workspace_size gives for max_len. */
+ * The workspace is the one ema_decode_workspace_size gives for max_len.
+ * FP8 cache: the new k/v row is quantised as in ema_pre_attention and attended in
+ * its decoded form, like every other row. */
 EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w,
                                 const void* k_norm_w, float eps, float theta,
                                 const int32_t* offsets, int32_t max_len, int32_t n_heads,
@@ -164,7 +193,8 @@ EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void
  *   q_offsets  device int32 [batch]: cache position of the first query; keys
  *              [0, q_offsets[b] + n_tokens) (or [q_offsets[b], ...) with CHUNK_ONLY)
  *   out        [batch, n_tokens, n_heads * head_dim] bf16
- * With EMA_PREFILL_CAUSAL, query i sees key j iff j <= q_offsets[b] + i. */
+ * With EMA_PREFILL_CAUSAL, query i sees key j iff j <= q_offsets[b] + i.
+ * bf16 caches only (EMA_ERR_UNSUPPORTED for FP8). */
 EMA_API int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                               const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads,
                               float scale, uint32_t flags, void* out);

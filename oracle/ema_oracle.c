@@ -365,3 +365,111 @@ int ora_num_threads(void) {
   return 1;
 #endif
 }
+
+/* ---------------------------------------------------------------- FP8 E4M3FN
+ * Restatement of crates/ops/src/fp8.rs (the FP8 cache of crates/kvcache/src/fp8.rs
+ * quantises through it). Magnitude codes 0..126 enumerate the finite non-negative
+ * E4M3FN values in increasing order, so "even code" is "even mantissa". */
+
+/* fp8.rs:20-29: exponent field e = code >> 3, mantissa m = code & 7 */
+static float e4m3_mag(unsigned i) {
+  const unsigned e = (i >> 3) & 15u, m = i & 7u;
+  if (e == 0) return (float)m * 0.001953125f; /* m * 2^-9 */
+  return (1.0f + (float)m * 0.125f) * ldexpf(1.0f, (int)e - 7);
+}
+
+float ora_e4m3_value(uint8_t code) {
+  const unsigned mag = code & 0x7Fu;
+  if (mag == 0x7Fu) return NAN;
+  const float v = e4m3_mag(mag);
+  return (code & 0x80u) ? -v : v;
+}
+
+/* fp8.rs:36-64 */
+float ora_e4m3fn_round(float x, uint8_t* code) {
+  const int neg = x < 0.0f;
+  const float ax = fminf(fabsf(x), 448.0f); /* NaN -> 448, as f32::min */
+  int lo = 0, hi = 126; /* largest code with value <= ax */
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (e4m3_mag((unsigned)mid) <= ax) lo = mid;
+    else hi = mid - 1;
+  }
+  unsigned best = (unsigned)lo;
+  if (best < 126) {
+    const float d0 = fabsf(ax - e4m3_mag(best)), d1 = fabsf(ax - e4m3_mag(best + 1));
+    if (d1 < d0 || (d1 == d0 && ((best + 1) & 1u) == 0 && (best & 1u) != 0)) best += 1;
+  }
+  if (code) *code = (uint8_t)((neg ? 0x80u : 0u) | best);
+  const float v = e4m3_mag(best);
+  return neg ? -v : v;
+}
+
+int ora_fp8_exp_of(float r, int ref) {
+  if (ref) return (int)ceilf(log2f(r));
+  return (int)ceilf((float)log2((double)r));
+}
+
+/* fp8.rs:80-84: amax folds from 1e-4 with f32::max (NaN operands ignored) */
+static float fp8_amax(const float* x, int n) {
+  float amax = 1.0e-4f;
+  for (int i = 0; i < n; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  return amax;
+}
+
+int ora_fp8_block_exp(const float* x, int n) { return ora_fp8_exp_of(fp8_amax(x, n) / 448.0f, 1); }
+
+int64_t ora_fp8_exp_mismatches(int kmin, int kmax, int nulps) {
+  int64_t bad = 0;
+  for (int k = kmin; k <= kmax; ++k) {
+    const float p = ldexpf(1.0f, k);
+    float up = p, down = p;
+    for (int n = 0; n < nulps; ++n) {
+      bad += ora_fp8_exp_of(up, 1) != ora_fp8_exp_of(up, 0);
+      bad += ora_fp8_exp_of(down, 1) != ora_fp8_exp_of(down, 0);
+      up = nextafterf(up, INFINITY);
+      down = nextafterf(down, 0.0f);
+    }
+  }
+  return bad;
+}
+
+/* one 64-value block: fp8.rs:80-89 */
+static void fp8_block(float* v, int n, uint8_t* codes, int8_t* exp_out) {
+  const int e = ora_fp8_block_exp(v, n);
+  const float scale = powf(2.0f, (float)e);
+  const float inv_scale = 1.0f / scale;
+  for (int i = 0; i < n; ++i) {
+    float y = v[i] * inv_scale;
+    if (!isnan(y)) y = y < -448.0f ? -448.0f : (y > 448.0f ? 448.0f : y); /* f32::clamp keeps NaN */
+    uint8_t c;
+    const float q = ora_e4m3fn_round(y, &c);
+    if (codes) codes[i] = c;
+    v[i] = q * scale;
+  }
+  if (exp_out) *exp_out = (int8_t)e;
+}
+
+void ora_fp8_round_trip(float* x, int64_t rows, int D, int n_rot) {
+  const int n_nope = D - n_rot;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int off = 0; off < n_nope; off += 64) {
+      const int end = off + 64 < n_nope ? off + 64 : n_nope;
+      fp8_block(x + r * D + off, end - off, NULL, NULL);
+    }
+}
+
+void ora_fp8_quantize_rows(const float* x, int64_t rows, int D, uint8_t* codes, int8_t* exps) {
+  float blk[64];
+  for (int64_t r = 0; r < rows; ++r)
+    for (int b = 0; b < D / 64; ++b) {
+      memcpy(blk, x + r * D + 64 * b, sizeof(blk));
+      fp8_block(blk, 64, codes + r * D + 64 * b, exps + r * (D / 64) + b);
+    }
+}
+
+void ora_fp8_dequantize_rows(const uint8_t* codes, const int8_t* exps, int64_t rows, int D, float* out) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int i = 0; i < D; ++i)
+      out[r * D + i] = ldexpf(ora_e4m3_value(codes[r * D + i]), exps[r * (D / 64) + i / 64]);
+}

@@ -102,6 +102,37 @@ void ora_lse_merge(const double* m, const double* l, const double* acc, int P, i
 /* Number of OpenMP threads ora_sdpa(precision=1) uses. */
 int ora_num_threads(void);
 
+/* ---- FP8 E4M3FN KV format: crates/ops/src/fp8.rs (used by crates/kvcache/src/fp8.rs) ----
+ * E4M3FN (OCP): sign, 4 exponent bits (bias 7), 3 mantissa bits; exponent field 0 is
+ * subnormal (mant * 2^-9); no infinities; codes 0x7F / 0xFF are NaN; largest finite 448. */
+
+/* Value of an E4M3FN code (e4m3fn_value, fp8.rs:20-29, plus the sign bit). */
+float ora_e4m3_value(uint8_t code);
+/* e4m3fn_dequant (fp8.rs:36-64): the E4M3FN value nearest to x, ties to the even code,
+ * |x| saturated at 448; NaN gives +448 (f32::min returns the non-NaN operand). The sign is
+ * that of x < 0 as in the reference (so -0.0 gives +0). *code receives the byte. */
+float ora_e4m3fn_round(float x, uint8_t* code);
+/* The reference's block scale exponent, ceil(log2(amax / 448)) with
+ * amax = max(1e-4, max_i |x_i|) (NaN ignored): fp8.rs:80-84 and :123-126, in f32 with the C
+ * library's log2f and ceilf, as Rust's f32::log2 / f32::ceil do on Linux. */
+int ora_fp8_block_exp(const float* x, int n);
+/* Exponent of the reference formula for a given amax / 448 = r: ceilf(log2f(r)) (ref = 1) or
+ * ceilf((float)log2((double)r)) (ref = 0, the device kernels' form). */
+int ora_fp8_exp_of(float r, int ref);
+/* Count of r = 2^k * (1 + n * 2^-23), k in [kmin, kmax], |n| < nulps, for which the two forms
+ * of ora_fp8_exp_of differ. */
+int64_t ora_fp8_exp_mismatches(int kmin, int kmax, int nulps);
+/* fp8_round_trip_slice (fp8.rs:71-92), in place on rows of D values: values [0, D - n_rot) in
+ * 64-value blocks are replaced by e4m3fn_dequant(clamp(v / s, -448, 448)) * s with
+ * s = 2^ora_fp8_block_exp(block); the RoPE tail [D - n_rot, D) passes through. */
+void ora_fp8_round_trip(float* x, int64_t rows, int D, int n_rot);
+/* The stored form of the same quantisation (n_rot = 0, D a multiple of 64): codes[i] = the
+ * E4M3FN byte of row value i, exps[r * D/64 + b] = exponent of block b of row r, so that
+ * value = e4m3(code) * 2^exp. */
+void ora_fp8_quantize_rows(const float* x, int64_t rows, int D, uint8_t* codes, int8_t* exps);
+/* value = e4m3(code) * 2^exp, exact in f32. */
+void ora_fp8_dequantize_rows(const uint8_t* codes, const int8_t* exps, int64_t rows, int D, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,8 @@ _u16p = ctypes.POINTER(ctypes.c_uint16)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i8p = ctypes.POINTER(ctypes.c_int8)
 
 
 def build() -> None:
@@ -63,6 +65,19 @@ def lib():
         L.ora_sdpa_partial.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f64p, _f64p, _f64p]
         L.ora_lse_merge.argtypes = [_f64p, _f64p, _f64p, ctypes.c_int, ctypes.c_int, _f64p]
         L.ora_num_threads.restype = ctypes.c_int
+        L.ora_e4m3_value.restype = ctypes.c_float
+        L.ora_e4m3_value.argtypes = [ctypes.c_uint8]
+        L.ora_e4m3fn_round.restype = ctypes.c_float
+        L.ora_e4m3fn_round.argtypes = [ctypes.c_float, ctypes.POINTER(ctypes.c_uint8)]
+        L.ora_fp8_block_exp.restype = ctypes.c_int
+        L.ora_fp8_block_exp.argtypes = [_f32p, ctypes.c_int]
+        L.ora_fp8_exp_of.restype = ctypes.c_int
+        L.ora_fp8_exp_of.argtypes = [ctypes.c_float, ctypes.c_int]
+        L.ora_fp8_exp_mismatches.restype = ctypes.c_int64
+        L.ora_fp8_exp_mismatches.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.ora_fp8_round_trip.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int]
+        L.ora_fp8_quantize_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _u8p, _i8p]
+        L.ora_fp8_dequantize_rows.argtypes = [_u8p, _i8p, ctypes.c_int64, ctypes.c_int, _f32p]
         _lib = L
     return _lib
 
@@ -195,3 +210,54 @@ def lse_merge(ms, ls, accs) -> np.ndarray:
 
 def num_threads() -> int:
     return int(lib().ora_num_threads())
+
+
+# ------------------------------------------------------------------ FP8 E4M3FN (crates/ops/src/fp8.rs)
+def e4m3_value(code: int) -> float:
+    return float(lib().ora_e4m3_value(code))
+
+
+def e4m3fn_round(x: float):
+    """e4m3fn_dequant (fp8.rs:36-64): returns (value, code)."""
+    c = ctypes.c_uint8()
+    v = lib().ora_e4m3fn_round(float(x), ctypes.byref(c))
+    return float(v), int(c.value)
+
+
+def e4m3fn_round_array(x) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32).ravel()
+    return np.array([lib().ora_e4m3fn_round(float(v), None) for v in x], dtype=np.float32)
+
+
+def fp8_exp_of(r: float, ref: bool = True) -> int:
+    return int(lib().ora_fp8_exp_of(float(r), 1 if ref else 0))
+
+
+def fp8_exp_mismatches(kmin: int, kmax: int, nulps: int) -> int:
+    return int(lib().ora_fp8_exp_mismatches(kmin, kmax, nulps))
+
+
+def fp8_round_trip(x, D: int, n_rot: int = 0) -> np.ndarray:
+    """fp8_round_trip_slice (fp8.rs:71-92) on rows of D f32 values; returns a new array."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().ora_fp8_round_trip(_p(x, _f32p), x.size // D, D, n_rot)
+    return x
+
+
+def fp8_quantize(x):
+    """Rows of D (multiple of 64) f32 values -> (codes uint8 [..., D], exps int8 [..., D/64])."""
+    x = _c(np.asarray(x, dtype=np.float32), np.float32)
+    D = x.shape[-1]
+    codes = np.empty(x.shape, dtype=np.uint8)
+    exps = np.empty(x.shape[:-1] + (D // 64,), dtype=np.int8)
+    lib().ora_fp8_quantize_rows(_p(x, _f32p), x.size // D, D, _p(codes, _u8p), _p(exps, _i8p))
+    return codes, exps
+
+
+def fp8_dequantize(codes, exps) -> np.ndarray:
+    codes = _c(np.asarray(codes), np.uint8)
+    exps = _c(np.asarray(exps), np.int8)
+    D = codes.shape[-1]
+    out = np.empty(codes.shape, dtype=np.float32)
+    lib().ora_fp8_dequantize_rows(_p(codes, _u8p), _p(exps, _i8p), codes.size // D, D, _p(out, _f32p))
+    return out

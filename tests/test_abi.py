@@ -167,3 +167,35 @@ def test_errors_are_thread_local(ema):
     t.start()
     t.join()
     assert main_msg and seen["msg"] == ""
+
+
+def test_fp8_descriptor_and_memory_bytes(ema):
+    L = ema.lib()
+    d = ema.KvCacheDesc()
+    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128)
+    assert rc == ema.EMA_OK
+    assert d.dtype == ema.EMA_DTYPE_FP8_E4M3 and (d.stride_pos, d.stride_head) == (128, 64 * 128)
+    n = ctypes.c_uint64()
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 8 * 64 * (128 + 2)  # codes + one exponent byte per 64 values
+    # exponents are required; head_dim 128 only
+    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, None, 0x40000, 2, 8, 64, 128)
+    assert rc == ema.EMA_ERR_INVALID_ARG and "exponent" in ema.last_error()
+    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 64)
+    assert rc == ema.EMA_ERR_UNSUPPORTED
+
+
+def test_fp8_prefill_is_unsupported(ema):
+    L = ema.lib()
+    d = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128) == 0
+    g = 0x40000
+    rc = L.ema_prefill_attention(None, g, ctypes.byref(d), g, 8, 16, 0.088, 1, g)
+    assert rc == ema.EMA_ERR_UNSUPPORTED and "fp8" in ema.last_error()
+
+
+def test_unknown_dtype_is_rejected(ema):
+    rc, d = _desc(ema)
+    d.dtype = 7
+    n = ctypes.c_uint64()
+    assert ema.lib().ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == ema.EMA_ERR_INVALID_ARG

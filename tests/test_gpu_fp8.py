@@ -1,0 +1,211 @@
+"""GPU parity of the FP8 E4M3FN KV cache (the stored form of the reference's
+Fp8Cache, crates/kvcache/src/fp8.rs over crates/ops/src/fp8.rs), through the C ABI.
+
+Bars:
+  - written rows: codes and block exponents bit-exact against the oracle's
+    quantisation of the same bf16 row (every finite bf16 value is exercised);
+  - decode over an FP8 cache is bit-identical to decode over a bf16 cache that
+    holds the decoded values (the decoder is exact), and within the bf16
+    tolerance (max-abs 2e-2, mean-abs 2e-3) of the f64 oracle;
+  - the fused step writes the same codes as the oracle and attends within the
+    same tolerance.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import assert_close, dev, host, say, scale_of
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ema():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import ema_attn
+
+    ema_attn.lib()
+    return ema_attn
+
+
+def fp8_cache(ema, codes_k, exps_k, codes_v, exps_v):
+    B, Hkv, cap, D = codes_k.shape
+    return ema.StaticCache(B, Hkv, cap, D, dtype="fp8", k=dev(codes_k), v=dev(codes_v), k_exp=dev(exps_k),
+                           v_exp=dev(exps_v))
+
+
+def quantized_pair(ora, shape, seed, outliers=False):
+    """Random bf16 K/V rows quantised by the oracle: (codes, exps, decoded bf16) for K and V."""
+    out = []
+    for i in range(2):
+        x = ora.normal_f32(shape, seed=seed + i)
+        if outliers and i == 0:  # 1% of K entries x8
+            sel = np.random.default_rng(seed).random(shape, dtype=np.float32) < 0.01
+            x[sel] *= 8.0
+        x = ora.f32_from_bf16(ora.bf16_from_f32(x))
+        codes, exps = ora.fp8_quantize(x)
+        deq = ora.bf16_from_f32(ora.fp8_dequantize(codes, exps))
+        out.append((codes, exps, deq))
+    return out
+
+
+def random_fp8_pair(ora, shape, seed):
+    """Random finite E4M3FN codes with block exponents in {-8, -7} (values of N(0,1) size):
+    (codes, exps, decoded bf16) for K and V, decoded through the oracle's code table."""
+    rng = np.random.default_rng(seed)
+    table = np.array([ora.e4m3_value(c) for c in range(256)], np.float32)
+    out = []
+    for _ in range(2):
+        codes = rng.integers(0, 254, size=shape, dtype=np.uint8)
+        codes = codes + (codes >= 0x7F)  # skip the NaN code 0x7F (and 0xFF: max 254 + 1)
+        exps = rng.integers(-8, -6, size=shape[:-1] + (shape[-1] // 64,), dtype=np.int8)
+        vals = table[codes] * np.ldexp(np.float32(1), np.repeat(exps, 64, axis=-1).astype(np.int32))
+        out.append((codes, exps, ora.bf16_from_f32(vals)))
+    return out
+
+
+def canon(codes):
+    """-0 (0x80) and +0 (0x00) are the same value."""
+    c = np.asarray(codes).copy()
+    c[c == 0x80] = 0
+    return c
+
+
+# ------------------------------------------------------------------ writes
+def test_fp8_write_every_bf16_value(ema, ora):
+    """pre_attention without norm/RoPE writes k, v as given: their codes must be the
+    oracle's for all 65536 bf16 bit patterns (non-finite ones replaced by 0)."""
+    import torch
+
+    B, T, Hq, Hkv, D, cap = 1, 64, 8, 8, 128, 80
+    say("fp8 write: every bf16 pattern")
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = (pats.astype(np.uint32) << 16).view(np.float32)
+    pats[~np.isfinite(f)] = 0
+    k = pats.reshape(T, Hkv, D)
+    v = pats[::-1].copy().reshape(T, Hkv, D)  # other block compositions
+    qkv = np.zeros((B, T, (Hq + 2 * Hkv) * D), np.uint16)
+    qkv[0, :, Hq * D:(Hq + Hkv) * D] = k.reshape(T, -1)
+    qkv[0, :, (Hq + Hkv) * D:] = v.reshape(T, -1)
+    off = np.array([9], np.int32)
+    cache = ema.StaticCache(B, Hkv, cap, D, dtype="fp8")
+    ema.pre_attention(dev(qkv), None, None, 1e-6, 1e6, dev(off), Hq, cache, flags=3)
+    torch.cuda.synchronize()
+    for name, src, codes, exps in (("k", k, cache.k, cache.k_exp), ("v", v, cache.v, cache.v_exp)):
+        rows = ora.f32_from_bf16(np.ascontiguousarray(src.transpose(1, 0, 2)))  # [Hkv, T, D]
+        rc, re = ora.fp8_quantize(rows)
+        gc, ge = host(codes)[0], host(exps)[0]
+        assert np.array_equal(canon(gc[:, 9:9 + T]), canon(rc)), f"{name} codes"
+        assert np.array_equal(ge[:, 9:9 + T], re), f"{name} exponents"
+        assert np.all(gc[:, :9] == 0) and np.all(gc[:, 9 + T:] == 0) and np.all(ge[:, :9] == 0)
+
+
+@pytest.mark.parametrize("flags", [0, 2])
+def test_fp8_write_after_norm_rope(ema, ora, flags):
+    """With norm and RoPE the written codes are the oracle's quantisation of the bf16 k
+    the same kernel writes into a bf16 cache (which the bf16 tests hold to the oracle)."""
+    import torch
+
+    B, T, Hq, Hkv, D, cap = 2, 7, 16, 8, 128, 64
+    say(f"fp8 write after norm/rope flags={flags}")
+    qkv = ora.normal_bf16((B, T, (Hq + 2 * Hkv) * D), seed=700 + flags)
+    qw = ora.normal_bf16(D, seed=701, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=702, mean=1.0, std=0.02)
+    off = np.array([0, 40], np.int32)
+    c16 = ema.StaticCache(B, Hkv, cap, D)
+    c8 = ema.StaticCache(B, Hkv, cap, D, dtype="fp8")
+    q16 = ema.pre_attention(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c16, flags=flags)
+    q8 = ema.pre_attention(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c8, flags=flags)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q16), host(q8)), "q does not depend on the cache format"
+    for src, codes, exps in ((c16.k, c8.k, c8.k_exp), (c16.v, c8.v, c8.v_exp)):
+        rows = ora.f32_from_bf16(host(src))
+        rc, re = ora.fp8_quantize(rows)
+        for b in range(B):
+            sl = slice(off[b], off[b] + T)
+            assert np.array_equal(canon(host(codes)[b][:, sl]), canon(rc[b][:, sl]))
+            assert np.array_equal(host(exps)[b][:, sl], re[b][:, sl])
+
+
+# ------------------------------------------------------------------ decode
+@pytest.mark.parametrize("G,lengths,cap", [
+    (4, [1, 31, 32, 33, 100, 1000, 1024], 1024),
+    (8, [4096, 17, 2500], 4096),
+    (1, [64, 65, 3], 96),
+])
+def test_fp8_decode_equals_bf16_decode_of_decoded_cache(ema, ora, G, lengths, cap):
+    import torch
+
+    Hkv, D = 4, 128
+    B, Hq = len(lengths), 4 * G
+    say(f"fp8 decode == bf16 decode G={G} lengths={lengths}")
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, cap, D), seed=710 + G, outliers=True)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=715)
+    L = np.asarray(lengths, np.int32)
+    c8 = fp8_cache(ema, kc, ke, vc, ve)
+    c16 = ema.StaticCache(B, Hkv, cap, D, k=dev(kd), v=dev(vd))
+    o8 = ema.decode_attention(dev(q), c8, dev(L), int(L.max()))
+    o16 = ema.decode_attention(dev(q), c16, dev(L), int(L.max()))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(o8), host(o16)), "the fp8 decoder is exact"
+    assert_close(host(o8), ora.sdpa(q, kd, vd, L, scale_of(D), False), "fp8 decode vs oracle")
+
+
+def test_fp8_decode_qwen3_8b_batched_shape(ema, ora):
+    """Batch 32, 32q/8kv, cap 8192, lengths U[512, 8192] (the benchmark workload)."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 32, 32, 8, 128, 8192
+    L = np.random.default_rng(1234).integers(512, 8193, size=B).astype(np.int32)
+    say("fp8 decode B32 32q/8kv cap 8192")
+    (kc, ke, kd), (vc, ve, vd) = random_fp8_pair(ora, (B, Hkv, cap, D), seed=720)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=722)
+    c8 = fp8_cache(ema, kc, ke, vc, ve)
+    del kc, vc
+    o8 = ema.decode_attention(dev(q), c8, dev(L), cap)
+    torch.cuda.synchronize()
+    assert_close(host(o8), ora.sdpa(q, kd, vd, L, scale_of(D), False), "fp8 decode 8B batched")
+
+
+# ------------------------------------------------------------------ fused step
+@pytest.mark.parametrize("flags", [0, 3])
+def test_fp8_fused_step(ema, ora, flags):
+    """decode_step on an fp8 cache: the new row is quantised like pre_attention's and
+    attended in its decoded form; rows elsewhere stay untouched."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 6, 16, 4, 128, 200
+    off = np.array([0, 31, 32, 100, 199, 63], np.int32)
+    say(f"fp8 fused step flags={flags}")
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, cap, D), seed=730)
+    qkv = ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=733)
+    qw = ora.normal_bf16(D, seed=734, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=735, mean=1.0, std=0.02)
+    # the same step through the separate kernels (pre_attention writes the row)
+    c_pair = fp8_cache(ema, kc, ke, vc, ve)
+    q = ema.pre_attention(dev(qkv.reshape(B, 1, -1)), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c_pair,
+                          flags=flags)
+    pair = ema.decode_attention(q, c_pair, dev(off + 1), cap)
+    c_f = fp8_cache(ema, kc, ke, vc, ve)
+    fused = ema.decode_step(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c_f, cap, flags=flags)
+    torch.cuda.synchronize()
+    gk, gke, gv, gve = host(c_f.k), host(c_f.k_exp), host(c_f.v), host(c_f.v_exp)
+    pk, pke = host(c_pair.k), host(c_pair.k_exp)
+    assert np.array_equal(canon(gv), canon(host(c_pair.v))) and np.array_equal(gve, host(c_pair.v_exp))
+    for b in range(B):
+        others = np.r_[0:off[b], off[b] + 1:cap]
+        assert np.array_equal(gk[b][:, others], kc[b][:, others]) and np.array_equal(gke[b][:, others],
+                                                                                     ke[b][:, others])
+    # k rows: same quantisation of a bf16 k that may differ from pre_attention's by the last
+    # bit (f32 sum order), so compare the decoded rows
+    dk_f = ora.bf16_from_f32(ora.fp8_dequantize(gk, gke))
+    dk_p = ora.bf16_from_f32(ora.fp8_dequantize(pk, pke))
+    assert_close(dk_f, dk_p, "fused vs pair decoded k rows", max_abs=2e-2, mean_abs=1e-5)
+    assert_close(host(fused), host(pair), "fp8 fused vs pair", max_abs=1e-2, mean_abs=1e-4)
+    # oracle: attend the decoded cache the fused step left behind
+    q_ref = host(q)
+    L = np.clip(off + 1, 0, cap).astype(np.int32)
+    dv = ora.bf16_from_f32(ora.fp8_dequantize(gv, gve))
+    assert_close(host(fused), ora.sdpa(q_ref, dk_f, dv, L, scale_of(D), False), "fp8 fused vs oracle")
