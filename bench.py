@@ -44,7 +44,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk"], default="all")
+    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk", "fp8"],
+                   default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--calibrate-copy", action="store_true")
@@ -267,6 +268,64 @@ def bench_decode_pair(ctx, ema, name, steps=20):
             "attn_gbs": by / (ms_attn * 1e-3) / 1e9, "frac_of_peak": by / (ms_attn * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def fp8_cache(ctx, ema, B, Hkv, cap, D):
+    """FP8 cache of random finite E4M3FN codes with block exponents in {-8, -7} (values of
+    N(0,1) size)."""
+    torch = ctx.torch
+
+    def codes():
+        c = torch.randint(0, 254, (B, Hkv, cap, D), generator=ctx.gen, device=ctx.dev, dtype=torch.int32)
+        return (c + (c >= 0x7F).to(torch.int32)).to(torch.uint8)  # no NaN codes
+
+    def exps():
+        return torch.randint(-8, -6, (B, Hkv, cap, D // 64), generator=ctx.gen, device=ctx.dev,
+                             dtype=torch.int32).to(torch.int8)
+
+    return ema.StaticCache(B, Hkv, cap, D, dtype="fp8", k=codes(), v=codes(), k_exp=exps(), v_exp=exps())
+
+
+def fp8_decode_bytes(lengths, Hq, Hkv, D):
+    """K and V codes + block exponents of the valid rows, q in, out."""
+    B = len(lengths)
+    return sum(2 * Hkv * int(L) * (D + D // 64) for L in lengths) + 2 * B * Hq * D * 2
+
+
+def bench_fp8_step(ctx, ema, name, steps=20):
+    """The batch-32 Qwen3-8B-shape decode step (fused ema_decode_step) over an FP8 cache."""
+    import numpy as np
+
+    torch = ctx.torch
+    B, Hq, Hkv, D, cap = 32, 32, 8, 128, 8192
+    lengths = np.random.default_rng(1234).integers(512, 8193, size=B)
+    cache = fp8_cache(ctx, ema, B, Hkv, cap, D)
+    qkv = ctx.randn((B, (Hq + 2 * Hkv) * D))
+    qw, kw = ctx.randn((D,), 1.0, 0.02), ctx.randn((D,), 1.0, 0.02)
+    off_d = ctx.i32(lengths - 1)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+    ms = time_calls(torch, lambda: ema.decode_step(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, cap, out=out,
+                                                   workspace=ws), steps, 5)
+    by = fp8_decode_bytes(lengths, Hq, Hkv, D) + B * (Hq + 2 * Hkv) * D * 2 + B * Hkv * 2 * (D + D // 64)
+    gbs = by / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: step {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM)")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
+
+
+def bench_fp8_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
+    torch = ctx.torch
+    cache = fp8_cache(ctx, ema, B, Hkv, cap, D)
+    q = ctx.randn((B, Hq, D))
+    ld = ctx.i32(lengths)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+    ms = time_calls(torch, lambda: ema.decode_attention(q, cache, ld, int(max(lengths)), out=out, workspace=ws),
+                    steps, 5)
+    by = fp8_decode_bytes(lengths, Hq, Hkv, D)
+    gbs = by / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM)")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
+
+
 def bench_pre(ctx, ema, name, T, Hq, Hkv, D, cap, steps=20):
     torch = ctx.torch
     cache = ema.StaticCache(1, Hkv, cap, D)
@@ -334,6 +393,10 @@ def main():
     if args.only in ("all", "prefill_chunk"):
         secondary.append(bench_prefill(ctx, ema, "prefill_chunk_off14336_T2048_64q8kv", 1, 64, 8, 128, 16384, 2048,
                                        14336, steps=10))
+    if args.only in ("all", "fp8"):
+        secondary.append(bench_fp8_step(ctx, ema, "decode_step_B32_32q8kv_fp8_cache"))
+        secondary.append(bench_fp8_decode(ctx, ema, "decode_B8_32q4kv_L32768_fp8_cache", 8, 32, 4, 128, 32768,
+                                          [32768] * 8))
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle f32 SDPA on the host)")

@@ -168,12 +168,24 @@ struct Combine {
   float o[kWaves][16][kD];
 };
 
-// RMSNorm + split-half RoPE of the head vector whose dims 8*(4s + c) + j (s < 4, j < 8)
+// Head dims lane group c feeds to the QK MFMA of step s (8 of them, d .. d+7). bf16
+// cache: d = 8(4s + c), so that the four lanes of a K row read 64 contiguous bytes per
+// step. fp8 cache: d = 64(s/2) + 16c + 8(s%2), so that a lane's two steps s = 2i, 2i+1
+// are one 16-byte load and the four lanes of a row read 64 contiguous bytes per load.
+// Any order works as long as q uses the same one; in both, dims d and d + 64 (a RoPE
+// pair) sit in one lane as steps s and s + 2.
+template <bool kFp8>
+__device__ __forceinline__ int kdim(int s, int c) {
+  return kFp8 ? 64 * (s >> 1) + 16 * c + 8 * (s & 1) : 8 * (4 * s + c);
+}
+
+// RMSNorm + split-half RoPE of the head vector whose dims kdim(s, c) + j (s < 4, j < 8)
 // this lane holds in x[8s + j] (c = lane / 16; the four lanes of one head together
-// hold all 128 dims, and dims d, d + 64 -- a RoPE pair -- sit in one lane as s, s + 2).
+// hold all 128 dims).
 // wv[s] holds the norm weights of the same dims. Same arithmetic as the pre-attention
 // kernel: f32 statistics, normalised value rounded to bf16 before the weight multiply;
 // cs_tab[i] = (cos, sin) of the angle pos * 2^(-(i/64) log2 theta) formed in f32.
+template <bool kFp8>
 __device__ __forceinline__ void norm_rope(const DecodeArgs& a, float (&x)[32], const u32x4 (&wv)[4],
                                           const float2* cs_tab) {
   const int c = (threadIdx.x & 63) >> 4;
@@ -194,7 +206,7 @@ __device__ __forceinline__ void norm_rope(const DecodeArgs& a, float (&x)[32], c
   if (!(a.flags & EMA_PRE_NO_ROPE)) {
     for (int s2 = 0; s2 < 2; ++s2)
       for (int j = 0; j < 8; ++j) {
-        const int i = 8 * (4 * s2 + c) + j;  // < 64; partner i + 64 is slot s2 + 2
+        const int i = kdim<kFp8>(s2, c) + j;  // < 64; partner i + 64 is slot s2 + 2
         const float cs = cs_tab[i].x, sn = cs_tab[i].y;
         const float x1 = x[8 * s2 + j], x2 = x[8 * (s2 + 2) + j];
         x[8 * s2 + j] = x1 * cs - x2 * sn;
@@ -284,7 +296,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         int p = p0 + krow0 + 4 * r;
         p = p < L ? p : L - 1;
         const uint8_t* row = Kb8 + (int64_t)p * a.sp;
-        for (int s = 0; s < 4; ++s) kr[r][s] = ld8_stream(row + 8 * (4 * s + c));
+        for (int i = 0; i < 2; ++i) {  // steps 2i, 2i+1: one 16-byte load
+          const u32x4 w = __builtin_nontemporal_load((const u32x4*)(row + kdim<true>(2 * i, c)));
+          kr[r][2 * i] = u32x2{w[0], w[1]};
+          kr[r][2 * i + 1] = u32x2{w[2], w[3]};
+        }
         kx[r] = Ke[p];
       }
       for (int kk = 0; kk < 8; ++kk) {
@@ -316,7 +332,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
 
     // q loads, then this wave's first tile loads, then the q work: the work below
-    // runs while the tile is in flight. B operand Q^T: step s <-> dims 8*(4s + c) .. +7;
+    // runs while the tile is in flight. B operand Q^T: step s <-> dims kdim(s, c) .. +7;
     // columns g >= G are zero padding (their clamped, in-bounds loads are discarded).
     const int first = tile0 + wave;
     const int gc = g < a.G ? g : 0;
@@ -325,12 +341,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                 : a.q + ((int64_t)b * a.Hq + (int64_t)kh * a.G + gc) * kD;
     u32x4 qraw[4], qwv[4];
     uint16_t kr1 = 0, kr2 = 0, kw1 = 0, kw2 = 0, vr1 = 0, vr2 = 0;
-    for (int s = 0; s < 4; ++s) qraw[s] = ld16(qh + 8 * (4 * s + c));
+    for (int s = 0; s < 4; ++s) qraw[s] = ld16(qh + kdim<kFp8>(s, c));
     // fused: the wave that will run the segment's last tile (position L - 1 = offset) forms
     // the new k, v row; its inputs are loaded now, with the q row and the norm weights
     const bool owner = kFused && tile1 == nb && wave == (nb - 1 - tile0) % kWaves;
     if (kFused) {
-      for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + 8 * (4 * s + c));
+      for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + kdim<kFp8>(s, c));
       if (owner) {  // lane i: dims i and i + 64 (a RoPE pair)
         const uint16_t* kr = a.qkv + (int64_t)b * F + ((int64_t)a.Hq + kh) * kD;
         const uint16_t* vr = kr + (int64_t)a.Hkv * kD;
@@ -367,7 +383,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float x[32];
       unpack32(qraw, x);
-      norm_rope(a, x, qwv, cs_tab);
+      norm_rope<kFp8>(a, x, qwv, cs_tab);
       for (int s = 0; s < 4; ++s) {
         u32x4 v;
         for (int e = 0; e < 4; ++e) v[e] = g < a.G ? pack_bf16x2(x[8 * s + 2 * e], x[8 * s + 2 * e + 1]) : 0u;
@@ -444,7 +460,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (kFused && owner && tile == nb - 1 && a.off[b] == L - 1) {
         for (int r = 0; r < 2; ++r)
           if (p0 + krow0 + 4 * r >= L - 1)
-            for (int s = 0; s < 4; ++s) kc[r][s] = *(const u32x4*)&new_kv[0][8 * (4 * s + c)];
+            for (int s = 0; s < 4; ++s) kc[r][s] = *(const u32x4*)&new_kv[0][kdim<kFp8>(s, c)];
         for (int kk = 0; kk < 8; ++kk)
           if (p0 + 8 * c + kk >= L - 1) vc[kk] = *(const u32x4*)&new_kv[1][8 * m];
       }
