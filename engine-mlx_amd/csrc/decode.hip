@@ -346,14 +346,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // the new k, v row; its inputs are loaded now, with the q row and the norm weights
     const bool owner = kFused && tile1 == nb && wave == (nb - 1 - tile0) % kWaves;
     if (kFused) {
-      for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + kdim<kFp8>(s, c));
+      // the norm weights may be null with EMA_PRE_NO_NORM: read only when used
+      const bool norm = !(a.flags & EMA_PRE_NO_NORM);
+      if (norm)
+        for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + kdim<kFp8>(s, c));
       if (owner) {  // lane i: dims i and i + 64 (a RoPE pair)
         const uint16_t* kr = a.qkv + (int64_t)b * F + ((int64_t)a.Hq + kh) * kD;
         const uint16_t* vr = kr + (int64_t)a.Hkv * kD;
         kr1 = kr[lane];
         kr2 = kr[lane + 64];
-        kw1 = a.kw[lane];
-        kw2 = a.kw[lane + 64];
+        if (norm) {
+          kw1 = a.kw[lane];
+          kw2 = a.kw[lane + 64];
+        }
         vr1 = vr[lane];
         vr2 = vr[lane + 64];
       }

@@ -213,3 +213,81 @@ def test_fp8_fused_step(ema, ora, flags):
     L = np.clip(off + 1, 0, cap).astype(np.int32)
     dv = ora.bf16_from_f32(ora.fp8_dequantize(gv, gve))
     assert_close(host(fused), ora.sdpa(q_ref, dk_f, dv, L, scale_of(D), False), "fp8 fused vs oracle")
+
+
+def test_fp8_fused_step_out_of_capacity(ema, ora):
+    """An offset at or past the capacity writes nothing and attends the full (stale) cache."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 3, 8, 2, 128, 64
+    off = np.array([64, 10, 200], np.int32)
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, cap, D), seed=740)
+    qkv = ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=742)
+    cache = fp8_cache(ema, kc, ke, vc, ve)
+    out = ema.decode_step(dev(qkv), None, None, 1e-6, 1e6, dev(off), Hq, cache, cap, flags=3)
+    torch.cuda.synchronize()
+    for b in (0, 2):
+        assert np.array_equal(host(cache.k)[b], kc[b]) and np.array_equal(host(cache.k_exp)[b], ke[b])
+        assert np.array_equal(host(cache.v)[b], vc[b]) and np.array_equal(host(cache.v_exp)[b], ve[b])
+    # flags 3: q is the raw q row; sequence 1 also wrote row 10 (checked by the fused tests)
+    q = qkv[:, :Hq * D].reshape(B, Hq, 1, D).copy()
+    L = np.clip(off + 1, 0, cap).astype(np.int32)
+    dk = ora.bf16_from_f32(ora.fp8_dequantize(host(cache.k), host(cache.k_exp)))
+    dv = ora.bf16_from_f32(ora.fp8_dequantize(host(cache.v), host(cache.v_exp)))
+    assert_close(host(out), ora.sdpa(q, dk, dv, L, scale_of(D), False), "fp8 fused out of capacity")
+
+
+@pytest.mark.parametrize("B,G,L,max_len", [(1, 4, [1024], 4096), (2, 16, [777, 1], 2048), (3, 2, [5, 300, 64], 300)])
+def test_fp8_decode_shapes(ema, ora, B, G, L, max_len):
+    """Batch 1, 16 query heads per kv head, a split sized for more rows than are valid."""
+    import torch
+
+    Hkv, D, cap = 2, 128, 4096
+    Hq = G * Hkv
+    say(f"fp8 decode B={B} G={G} L={L} max_len={max_len}")
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, cap, D), seed=750 + G)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=753)
+    L = np.asarray(L, np.int32)
+    out = ema.decode_attention(dev(q), fp8_cache(ema, kc, ke, vc, ve), dev(L), max_len)
+    torch.cuda.synchronize()
+    assert_close(host(out), ora.sdpa(q, kd, vd, L, scale_of(D), False), "fp8 decode shapes")
+
+
+def test_fp8_graph_replay_matches_eager(ema, ora):
+    """The fused fp8 step captured in a HIP graph: every replay, with eager work and
+    synchronisation in between, equals the eager result (and rewrites the same row)."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 4, 16, 8, 128, 1024
+    off = np.array([100, 1023, 0, 512], np.int32)
+    (kc, ke, _), (vc, ve, _) = quantized_pair(ora, (B, Hkv, cap, D), seed=760)
+    qkv = dev(ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=762))
+    qw = dev(ora.normal_bf16(D, seed=763, mean=1.0, std=0.02))
+    kw = dev(ora.normal_bf16(D, seed=764, mean=1.0, std=0.02))
+    cache = fp8_cache(ema, kc, ke, vc, ve)
+    off_d = dev(off)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device="cuda")
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+
+    def step():
+        ema.decode_step(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, cap, out=out, workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    eager, k_eager = host(out).copy(), host(cache.k).copy()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), eager), f"replay {i}"
+        assert np.array_equal(host(cache.k), k_eager)
+        step()
+        torch.cuda.synchronize()

@@ -485,6 +485,25 @@ def test_decode_step_fused_out_of_capacity(ema, ora):
     assert_close(got, ref, "fused out of capacity")
 
 
+@pytest.mark.parametrize("flags", [1, 3])
+def test_decode_step_fused_null_norm_weights(ema, ora, flags):
+    """With EMA_PRE_NO_NORM the norm weights may be null (they are never read): the result
+    equals the call that passes (unused) weights, bit for bit."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 4, 16, 4, 128, 256
+    off = np.array([0, 100, 255, 300], np.int32)
+    qkv = dev(ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=660))
+    w = dev(ora.normal_bf16(D, seed=661, mean=1.0, std=0.02))
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=662)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=663)
+    c1, c2 = make_cache(ema, kc, vc), make_cache(ema, kc, vc)
+    o1 = ema.decode_step(qkv, None, None, 1e-6, 1e6, dev(off), Hq, c1, cap, flags=flags)
+    o2 = ema.decode_step(qkv, w, w, 1e-6, 1e6, dev(off), Hq, c2, cap, flags=flags)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(o1), host(o2)) and np.array_equal(host(c1.k), host(c2.k))
+
+
 def test_decode_step_fused_matches_unfused_pair(ema, ora):
     """Fused step == ema_pre_attention(T=1) + ema_decode_attention on the same inputs."""
     import torch
