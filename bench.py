@@ -326,6 +326,24 @@ def bench_fp8_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
     return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
 
 
+def bench_fp8_prefill(ctx, ema, name, B, Hq, Hkv, D, cap, T, off, steps=20):
+    """Prefill over an FP8 cache: decode of the attended rows into the bf16 workspace + the
+    bf16 prefill, per call."""
+    torch = ctx.torch
+    cache = fp8_cache(ctx, ema, B, Hkv, cap, D)
+    q = ctx.randn((B, Hq, T, D))
+    qo = ctx.i32([off] * B)
+    out = torch.empty((B, T, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    kv = off + T
+    ws = torch.empty(ema.prefill_workspace_size(cache, kv), dtype=torch.uint8, device=ctx.dev)
+    ms = time_calls(torch, lambda: ema.prefill_attention(q, cache, qo, causal=True, out=out, max_kv_len=kv,
+                                                         workspace=ws), steps, 5)
+    fl = B * prefill_flops(Hq, D, T, off)
+    tf = fl / (ms * 1e-3) / 1e12
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s ({tf/BF16_PEAK_TFLOPS:.1%} of bf16 peak)")
+    return {"workload": name, "us": ms * 1e3, "tflops": tf, "frac_of_peak": tf / BF16_PEAK_TFLOPS, "flops": fl}
+
+
 def bench_pre(ctx, ema, name, T, Hq, Hkv, D, cap, steps=20):
     torch = ctx.torch
     cache = ema.StaticCache(1, Hkv, cap, D)
@@ -397,6 +415,8 @@ def main():
         secondary.append(bench_fp8_step(ctx, ema, "decode_step_B32_32q8kv_fp8_cache"))
         secondary.append(bench_fp8_decode(ctx, ema, "decode_B8_32q4kv_L32768_fp8_cache", 8, 32, 4, 128, 32768,
                                           [32768] * 8))
+        secondary.append(bench_fp8_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_fp8_cache", 1, 32, 8, 128, 4096,
+                                           2048, 0))
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle f32 SDPA on the host)")

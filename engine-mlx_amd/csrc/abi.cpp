@@ -268,6 +268,76 @@ int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm
   return launch_decode((hipStream_t)stream, nullptr, *cache, nullptr, n_heads, scale, out, workspace, p, &f);
 }
 
+static int32_t check_prefill(const char* op, const void* q, const ema_kvcache_desc* cache,
+                             const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads, float scale,
+                             uint32_t flags, void* out) {
+  int32_t rc = check_cache(op, cache);
+  if (rc) return rc;
+  if (!q || !out || !q_offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null q/out/q_offsets", op);
+  if (flags & ~(EMA_PREFILL_CAUSAL | EMA_PREFILL_CHUNK_ONLY))
+    return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
+  if ((rc = check_heads(op, n_heads, cache->n_kv_heads))) return rc;
+  if (n_tokens <= 0) return set_error(EMA_ERR_SHAPE, "%s: n_tokens %d must be positive", op, n_tokens);
+  if (n_tokens > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: %d tokens exceed capacity %d", op, n_tokens, cache->capacity);
+  if (!(scale > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: scale must be > 0", op);
+  if (!aligned16(q) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: q/out must be 16-byte aligned", op);
+  return EMA_OK;
+}
+
+static uint64_t prefill_ws_bytes(const ema_kvcache_desc* c, int32_t max_kv_len) {
+  if (c->dtype != EMA_DTYPE_FP8_E4M3) return 0;
+  return 2ull * (uint64_t)c->batch * c->n_kv_heads * (uint64_t)max_kv_len * c->head_dim * 2ull;
+}
+
+int32_t ema_prefill_workspace_size(const ema_kvcache_desc* cache, int32_t max_kv_len, uint64_t* bytes) {
+  const char* op = "ema_prefill_workspace_size";
+  if (!bytes) return set_error(EMA_ERR_INVALID_ARG, "%s: output is null", op);
+  int32_t rc = check_cache(op, cache);
+  if (rc) return rc;
+  if (max_kv_len <= 0 || max_kv_len > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: max_kv_len %d outside (0, capacity %d]", op, max_kv_len, cache->capacity);
+  *bytes = prefill_ws_bytes(cache, max_kv_len);
+  return EMA_OK;
+}
+
+int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
+                                 const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads, float scale,
+                                 uint32_t flags, void* out, int32_t max_kv_len, void* workspace,
+                                 uint64_t workspace_bytes) {
+  const char* op = "ema_prefill_attention_ws";
+  int32_t rc = check_prefill(op, q, cache, q_offsets, n_tokens, n_heads, scale, flags, out);
+  if (rc) return rc;
+  if (max_kv_len < n_tokens || max_kv_len > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: max_kv_len %d outside [n_tokens %d, capacity %d]", op, max_kv_len,
+                     n_tokens, cache->capacity);
+  if (cache->dtype == EMA_DTYPE_BF16)
+    return launch_prefill((hipStream_t)stream, q, *cache, q_offsets, n_tokens, n_heads, scale, flags, out);
+  const uint64_t need = prefill_ws_bytes(cache, max_kv_len);
+  if (!workspace || workspace_bytes < need)
+    return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes needed, %llu given", op,
+                     (unsigned long long)need, (unsigned long long)(workspace ? workspace_bytes : 0));
+  if (!aligned16(workspace)) return set_error(EMA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", op);
+  if ((int64_t)cache->batch * cache->n_kv_heads > 65535)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: batch * n_kv_heads exceeds 65535", op);
+  rc = launch_fp8_to_bf16((hipStream_t)stream, *cache, q_offsets, n_tokens, flags, max_kv_len, workspace);
+  if (rc) return rc;
+  // the bf16 copy: [B, Hkv, max_kv_len, D] K then V
+  ema_kvcache_desc w{};
+  const int64_t per = (int64_t)cache->batch * cache->n_kv_heads * max_kv_len * cache->head_dim;
+  w.k = workspace;
+  w.v = (uint16_t*)workspace + per;
+  w.batch = cache->batch;
+  w.n_kv_heads = cache->n_kv_heads;
+  w.capacity = max_kv_len;
+  w.head_dim = cache->head_dim;
+  w.stride_pos = cache->head_dim;
+  w.stride_head = (int64_t)max_kv_len * cache->head_dim;
+  w.stride_batch = (int64_t)cache->n_kv_heads * max_kv_len * cache->head_dim;
+  w.dtype = EMA_DTYPE_BF16;
+  return launch_prefill((hipStream_t)stream, q, w, q_offsets, n_tokens, n_heads, scale, flags, out);
+}
+
 int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                               const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads, float scale,
                               uint32_t flags, void* out) {

@@ -37,7 +37,8 @@ EXPORTED = (
     "ema_last_error", "ema_version", "ema_kvcache_init", "ema_kvcache_alloc", "ema_kvcache_free",
     "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
-    "ema_decode_attention", "ema_decode_step", "ema_prefill_attention",
+    "ema_decode_attention", "ema_decode_step", "ema_prefill_attention", "ema_prefill_workspace_size",
+    "ema_prefill_attention_ws",
 )
 
 
@@ -85,6 +86,8 @@ def lib() -> ctypes.CDLL:
             "ema_decode_attention": (i32, [vp, vp, D, vp, i32, i32, f32, vp, vp, u64]),
             "ema_decode_step": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, u32, f32, D, vp, vp, u64]),
             "ema_prefill_attention": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp]),
+            "ema_prefill_workspace_size": (i32, [D, i32, ctypes.POINTER(u64)]),
+            "ema_prefill_attention_ws": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp, i32, vp, u64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -248,9 +251,19 @@ def decode_step(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: St
     return out
 
 
+def prefill_workspace_size(cache: StaticCache, max_kv_len: int) -> int:
+    out = ctypes.c_uint64()
+    _check(lib().ema_prefill_workspace_size(ctypes.byref(cache.desc), max_kv_len, ctypes.byref(out)),
+           "ema_prefill_workspace_size")
+    return out.value
+
+
 def prefill_attention(q, cache: StaticCache, q_offsets, scale=None, causal=True, chunk_only=False, out=None,
-                      stream=None):
-    """q [B,Hq,T,D] bf16; q_offsets int32 device [B]. Returns out [B,T,Hq*D]."""
+                      stream=None, max_kv_len=None, workspace=None):
+    """q [B,Hq,T,D] bf16; q_offsets int32 device [B]. Returns out [B,T,Hq*D].
+
+    An FP8 cache goes through ema_prefill_attention_ws: its attended rows (at most
+    max_kv_len per sequence, default the capacity) are decoded into a bf16 workspace."""
     import torch
 
     B, Hq, T, D = q.shape
@@ -259,6 +272,16 @@ def prefill_attention(q, cache: StaticCache, q_offsets, scale=None, causal=True,
     if out is None:
         out = torch.empty((B, T, Hq * D), dtype=torch.bfloat16, device=q.device)
     flags = (EMA_PREFILL_CAUSAL if causal else 0) | (EMA_PREFILL_CHUNK_ONLY if chunk_only else 0)
-    _check(lib().ema_prefill_attention(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(q_offsets), T, Hq,
-                                       scale, flags, _ptr(out)), "ema_prefill_attention")
+    if cache.dtype == "bf16" and workspace is None:
+        _check(lib().ema_prefill_attention(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(q_offsets), T,
+                                           Hq, scale, flags, _ptr(out)), "ema_prefill_attention")
+        return out
+    if max_kv_len is None:
+        max_kv_len = cache.capacity
+    if workspace is None:
+        workspace = torch.empty(max(prefill_workspace_size(cache, max_kv_len), 16), dtype=torch.uint8,
+                                device=q.device)
+    _check(lib().ema_prefill_attention_ws(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(q_offsets), T,
+                                          Hq, scale, flags, _ptr(out), max_kv_len, _ptr(workspace),
+                                          workspace.numel()), "ema_prefill_attention_ws")
     return out

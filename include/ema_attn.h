@@ -194,10 +194,26 @@ EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void
  *              [0, q_offsets[b] + n_tokens) (or [q_offsets[b], ...) with CHUNK_ONLY)
  *   out        [batch, n_tokens, n_heads * head_dim] bf16
  * With EMA_PREFILL_CAUSAL, query i sees key j iff j <= q_offsets[b] + i.
- * bf16 caches only (EMA_ERR_UNSUPPORTED for FP8). */
+ * bf16 caches only (EMA_ERR_UNSUPPORTED for FP8: use ema_prefill_attention_ws). */
 EMA_API int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                               const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads,
                               float scale, uint32_t flags, void* out);
+
+/* Workspace (bytes) ema_prefill_attention_ws needs: 0 for a bf16 cache; for an FP8 cache
+ * a bf16 copy of the attended rows, 2 * batch * n_kv_heads * max_kv_len * head_dim * 2. */
+EMA_API int32_t ema_prefill_workspace_size(const ema_kvcache_desc* cache, int32_t max_kv_len,
+                                           uint64_t* bytes);
+/* ema_prefill_attention for either cache format (the prefill over the reference's FP8
+ * cache, whose SDPA sees the round-tripped values: crates/kvcache/src/fp8.rs:60-68). An
+ * FP8 cache's attended rows are decoded exactly into bf16 in the workspace, and the bf16
+ * prefill runs over that copy, so the result equals that of a bf16 cache holding the
+ * decoded values. max_kv_len: host upper bound of q_offsets[b] + n_tokens (<= capacity;
+ * rows at or past it are not attended). The workspace needs no initialisation; calls that
+ * share one must not overlap. */
+EMA_API int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
+                                         const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads,
+                                         float scale, uint32_t flags, void* out, int32_t max_kv_len,
+                                         void* workspace, uint64_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -199,3 +199,21 @@ def test_unknown_dtype_is_rejected(ema):
     d.dtype = 7
     n = ctypes.c_uint64()
     assert ema.lib().ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == ema.EMA_ERR_INVALID_ARG
+
+
+def test_prefill_workspace_size_and_errors(ema):
+    L = ema.lib()
+    n = ctypes.c_uint64()
+    _, d16 = _desc(ema)
+    assert L.ema_prefill_workspace_size(ctypes.byref(d16), 64, ctypes.byref(n)) == 0 and n.value == 0
+    d8 = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d8), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128) == 0
+    assert L.ema_prefill_workspace_size(ctypes.byref(d8), 48, ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 8 * 48 * 128 * 2  # bf16 K and V copies of 48 rows
+    assert L.ema_prefill_workspace_size(ctypes.byref(d8), 65, ctypes.byref(n)) == ema.EMA_ERR_CAPACITY
+    g = 0x40000
+    # workspace too small, max_kv_len below n_tokens
+    rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d8), g, 8, 16, 0.088, 1, g, 48, g, 16)
+    assert rc == ema.EMA_ERR_WORKSPACE and "workspace" in ema.last_error()
+    rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d8), g, 8, 16, 0.088, 1, g, 4, g, 1 << 30)
+    assert rc == ema.EMA_ERR_CAPACITY

@@ -291,3 +291,34 @@ def test_fp8_graph_replay_matches_eager(ema, ora):
         assert np.array_equal(host(cache.k), k_eager)
         step()
         torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ prefill
+@pytest.mark.parametrize("T,q_off,causal,chunk,G,max_kv", [
+    (300, 0, True, False, 4, None),
+    (257, 1000, True, True, 8, 1500),
+    (128, 700, True, False, 2, None),
+    (64, 33, False, False, 1, 97),
+])
+def test_fp8_prefill_equals_bf16_prefill_of_decoded_cache(ema, ora, T, q_off, causal, chunk, G, max_kv):
+    """Prefill over an FP8 cache (ema_prefill_attention_ws) is the bf16 prefill over the
+    decoded rows: bit-identical to a bf16 cache holding them, and within the bf16
+    tolerance of the f64 oracle."""
+    import torch
+
+    B, Hkv, D, cap = 2, 2, 128, 2048
+    Hq = G * Hkv
+    say(f"fp8 prefill T={T} q_off={q_off} causal={causal} chunk={chunk} G={G} max_kv={max_kv}")
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, cap, D), seed=770 + G)
+    q = ora.normal_bf16((B, Hq, T, D), seed=773)
+    qo = np.array([q_off, q_off // 2], np.int32)
+    c8 = fp8_cache(ema, kc, ke, vc, ve)
+    c16 = ema.StaticCache(B, Hkv, cap, D, k=dev(kd), v=dev(vd))
+    o8 = ema.prefill_attention(dev(q), c8, dev(qo), causal=causal, chunk_only=chunk, max_kv_len=max_kv)
+    o16 = ema.prefill_attention(dev(q), c16, dev(qo), causal=causal, chunk_only=chunk)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(o8), host(o16)), "decoded fp8 rows == the bf16 cache"
+    kv_len = np.minimum(qo + T, cap).astype(np.int32)
+    kb = qo if chunk else None
+    ref = ora.sdpa(q, kd, vd, kv_len, scale_of(D), causal, kv_begin=kb)
+    assert_close(host(o8), ref, "fp8 prefill vs oracle")
