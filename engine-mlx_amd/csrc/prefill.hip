@@ -65,6 +65,9 @@ struct PrefillArgs {
 };
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+// compile-time choice of the softmax step's masking code
+struct MaskOn { static constexpr bool value = true; };
+struct MaskOff { static constexpr bool value = false; };
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Raw buffer resource (V#) over `bytes` bytes from `base`: stride 0, gfx9 dword3 with a
@@ -74,17 +77,22 @@ __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu, bytes, 0x00020000u};
 }
 
-// 16 bytes per lane from buffer offset `voff` straight into LDS at lds_addr + 16 * lane
-// (buffer_load_dwordx4 ... lds; the LDS base goes through M0). Issued as asm so the
+// 16 bytes per lane from buffer offset `voff` + 1024 * I straight into LDS at lds_addr +
+// 1024 * I + 16 * lane (buffer_load_dwordx4 ... lds; the LDS base goes through M0, and the
+// instruction offset moves the memory and the LDS address alike). Issued as asm so the
 // compiler does not track it: the caller orders it with explicit vmcnt waits before the
 // barrier that publishes the tile, instead of the compiler draining every load in flight
 // at each barrier and before each LDS read.
+template <int I>
 __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen offset:%3 lds"
                :
-               : "v"(voff), "s"(rsrc), "s"(lds_addr)
+               : "v"(voff), "s"(rsrc), "s"(lds_addr), "i"(1024 * I)
                : "memory", "m0");
 }
+// Block offset that no buffer range reaches (ranges stay below 2^31 bytes, and a per-lane
+// offset added to it stays below 2^32): the load returns zeros and touches no memory.
+constexpr uint32_t kNoRow = 0xF0000000u;
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -149,53 +157,67 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   uint16_t* const Ks = lds + g * kGroupElems;     // this group's K tiles: buffer i at Ks + i * kTile
   uint16_t* const Vs = Ks + 2 * kTile;            // and V tiles
 
-  // K/V of this (batch, kv head) through buffer loads: the resource of a block starts at
-  // the block's first row and covers only the rows below kv_len, so rows past the valid
-  // length read as zeros (finite, and masked out) without per-lane clamping.
+  // K/V of this (batch, kv head) through buffer loads. One resource per tensor covers the
+  // rows below kv_len, so rows past the valid length read as zeros (finite, and masked
+  // out) without per-lane clamping; a block is addressed by adding its byte offset to the
+  // per-lane offsets.
   const char* Kg = (const char*)(a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh);
   const char* Vg = (const char*)(a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh);
   const uint32_t row_bytes = (uint32_t)a.sp * 2;
+  const u32x4 k_rsrc = buffer_rsrc(Kg, (uint32_t)kv_len * row_bytes);
+  const u32x4 v_rsrc = buffer_rsrc(Vg, (uint32_t)kv_len * row_bytes);
 
   // Global -> LDS without registers (buffer_load_dwordx4 ... lds): one instruction moves
   // 1 KB, lane l's 16 bytes landing at byte 16l of the destination, i.e. 4 tile rows.
-  // Wave wq of the group moves rows 16wq .. 16wq+15 (4 instructions per tile); the
-  // per-lane source offsets below apply the swizzle and stay the same for every block.
+  // Wave wq of the group moves rows 16wq .. 16wq+15 (4 instructions per tile, the i-th
+  // at instruction offset 1024 i); the per-lane source offsets below apply the swizzle,
+  // have that instruction offset taken out (row >= 4i and row_bytes >= 256 keep them
+  // non-negative) and stay the same for every block.
   const int r4 = lane >> 4, p16 = lane & 15;  // row within the 4, chunk position in the row
   uint32_t koff[4], voff[4];
   for (int i = 0; i < 4; ++i) {
     const uint32_t row = (uint32_t)(16 * wq + 4 * i + r4);
-    koff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * i + r4)) * 16);
-    voff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * r4)) * 16);
+    koff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * i + r4)) * 16) - 1024u * i;
+    voff[i] = row * row_bytes + (uint32_t)((p16 ^ (4 * r4)) * 16) - 1024u * i;
   }
-  auto dma = [&](const char* src, int blk, const uint32_t* off, uint16_t* tile) __attribute__((always_inline)) {
-    const int base = blk * kBN;  // < kv_len for every block of the range
-    const uint32_t valid = (uint32_t)(kv_len - base) * row_bytes;
-    const u32x4 r = buffer_rsrc(src + (int64_t)base * row_bytes, valid);
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
-    if (base < kv_begin) {
+  // byte offset of block j of this group, or kNoRow past the group's range (its loads
+  // then fill the tile with zeros that nothing reads, which keeps the issue count of a
+  // step fixed)
+  auto blk_off = [&](int j) __attribute__((always_inline)) {
+    return j < ng ? (uint32_t)((gb0 + j) * kBN) * row_bytes : kNoRow;
+  };
+  auto tile_dst = [&](const uint16_t* tile) __attribute__((always_inline)) {
+    return (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
+  };
+  // one of the 4 instructions of a tile load (spread over the softmax step so the four
+  // waves of a group do not queue 32 KB at the address unit at once)
+  auto dma_part = [&](const u32x4 r, uint32_t off_blk, const uint32_t* off, uint32_t dst, int i)
+      __attribute__((always_inline)) {
+    const uint32_t o = off[i] + off_blk;
+    switch (i) {
+      case 0: dma16<0>(r, o, dst); break;
+      case 1: dma16<1>(r, o, dst); break;
+      case 2: dma16<2>(r, o, dst); break;
+      default: dma16<3>(r, o, dst); break;
+    }
+  };
+  auto dma = [&](const u32x4 r, int j, const uint32_t* off, const uint16_t* tile) __attribute__((always_inline)) {
+    const uint32_t ob = blk_off(j), dst = tile_dst(tile);
+    const int base = (gb0 + j) * kBN;
+    if (j < ng && base < kv_begin) {
       // first block of a chunk-only window: rows before kv_begin are outside the
       // attended range; an out-of-range offset makes them arrive as zeros, so whatever
       // the cache holds there (even NaN) cannot reach the masked products
       for (int i = 0; i < 4; ++i) {
         const int row = base + 16 * wq + 4 * i + r4;
-        dma16(r, row < kv_begin ? 0x80000000u : off[i], dst + 4 * i * kD * 2);
+        dma_part(r, row < kv_begin ? kNoRow : ob, off, dst, i);
       }
     } else {
-      for (int i = 0; i < 4; ++i) dma16(r, off[i], dst + 4 * i * kD * 2);
+      for (int i = 0; i < 4; ++i) dma_part(r, ob, off, dst, i);
     }
   };
-  auto load_k = [&](int j) __attribute__((always_inline)) { dma(Kg, gb0 + j, koff, Ks + (j & 1) * kTile); };
-  auto load_v = [&](int j) __attribute__((always_inline)) { dma(Vg, gb0 + j, voff, Vs + (j & 1) * kTile); };
-  // one of the 4 instructions of a tile load (spread over the softmax step so the four
-  // waves of a group do not queue 32 KB at the address unit at once)
-  auto dma_part = [&](const char* src, int blk, const uint32_t* off, uint16_t* tile, int i)
-      __attribute__((always_inline)) {
-    const int base = blk * kBN;
-    const uint32_t valid = (uint32_t)(kv_len - base) * row_bytes;
-    const u32x4 r = buffer_rsrc(src + (int64_t)base * row_bytes, valid);
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
-    dma16(r, off[i], dst + 4 * i * kD * 2);
-  };
+  auto load_k = [&](int j) __attribute__((always_inline)) { dma(k_rsrc, j, koff, Ks + (j & 1) * kTile); };
+  auto load_v = [&](int j) __attribute__((always_inline)) { dma(v_rsrc, j, voff, Vs + (j & 1) * kTile); };
 
   // Online softmax state of this lane's row, in the log2 domain. The accumulators hold
   // o and l relative to the base m_use (p = 2^(s - m_use)); the score MFMA starts from
@@ -227,6 +249,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   for (int dt = 0; dt < 4; ++dt) v_col[dt] = tr_row * kD + 16 * (grp & 1) + 4 * (s16 & 3) + 32 * (dt ^ (s16 >> 2));
 
   auto active = [&](int j) __attribute__((always_inline)) { return !causal || (gb0 + j) * kBN <= wave_last_abs; };
+  // Block j holds keys outside [kv_begin, kv_len) or above the causal limit of some row
+  // of this wave. For j >= 1 this holds exactly from block j_mask on.
+  auto need_mask = [&](int j) __attribute__((always_inline)) {
+    const int kbase = (gb0 + j) * kBN;
+    return kbase < kv_begin || kbase + kBN > kv_len || (causal && kbase + kBN - 1 > wave_first_abs);
+  };
+  int j_mask = kv_len / kBN - gb0;  // first block reaching past kv_len
+  if (causal) {
+    const int jc = (wave_first_abs + 1) / kBN - gb0;  // first block reaching past row 0's limit
+    j_mask = jc < j_mask ? jc : j_mask;
+  }
+  j_mask = j_mask < 1 ? 1 : j_mask;
 
   // Matrix step j: O += V^T P^T for block j-1, then S^T = K Q^T - m_use for block j. A base
   // change of the softmax step before is applied to o first.
@@ -307,14 +341,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // Softmax step j: P for block j (into pw), then the loads of K for block j+2 (its
   // buffer held K of block j, last read by the matrix step just before) and of V for
   // block j+1 (its buffer held V of block j-1, last read by that same matrix step).
-  auto vstep = [&](int j) __attribute__((always_inline)) {
+  // With kMask false the block is known to need no mask (the steady-state loop).
+  auto vstep = [&](int j, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool kMask = decltype(mask_tag)::value;
     if (j < 0 || j >= ng) return;
     if (active(j)) {
       const int kbase = (gb0 + j) * kBN;
       // key of slot i in sub-tile kt: kbase + 32kt + (i%4) + 8(i/4) + 4hh
-      const bool need_mask = kbase < kv_begin || kbase + kBN > kv_len ||
-                             (causal && kbase + kBN - 1 > wave_first_abs);
-      if (need_mask) {
+      if (kMask && need_mask(j)) {
         int hi = causal && q_abs < kv_len - 1 ? q_abs : kv_len - 1;
         hi -= kbase + 4 * hh;
         const int lo = kv_begin - kbase - 4 * hh;
@@ -333,9 +367,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       // neither the max nor a rescale is needed.
       bool fast = all_seen;
       if (fast) {
+        const uint32_t kob = blk_off(j + 2), vob = blk_off(j + 1);
+        const uint32_t kdst = tile_dst(Ks + (j & 1) * kTile), vdst = tile_dst(Vs + ((j + 1) & 1) * kTile);
         for (int st = 0; st < 4; ++st) {
-          if (j + 2 < ng) dma_part(Kg, gb0 + j + 2, koff, Ks + (j & 1) * kTile, st);
-          if (j + 1 < ng) dma_part(Vg, gb0 + j + 1, voff, Vs + ((j + 1) & 1) * kTile, st);
+          dma_part(k_rsrc, kob, koff, kdst, st);
+          dma_part(v_rsrc, vob, voff, vdst, st);
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
             const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i]), __builtin_amdgcn_exp2f(sc[kt][i + 1]));
@@ -346,8 +382,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
         fast = !__any(!(ps0 + ps1 <= 256.f));  // NaN/inf fall to the slow path too
       } else {
-        if (j + 2 < ng) load_k(j + 2);
-        if (j + 1 < ng) load_v(j + 1);
+        load_k(j + 2);
+        load_v(j + 1);
       }
       if (!fast) {
         // Slow path (first block of a row, or a row max that grew): move the base to
@@ -377,17 +413,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
       l_run += ps0 + ps1;
     } else {
-      if (j + 2 < ng) load_k(j + 2);
-      if (j + 1 < ng) load_v(j + 1);
+      load_k(j + 2);
+      load_v(j + 1);
     }
     // the loads of the previous softmax step (K of block j+1, V of block j) are read by
-    // the next matrix step: wait for them, leaving this step's own loads in flight
+    // the next matrix step: wait for them, leaving this step's own 8 loads in flight
     // (loads complete in issue order); step 0's predecessors were waited for up front
-    if (j >= 1) {
-      if (j + 2 < ng) __builtin_amdgcn_s_waitcnt(0x0F78);       // vmcnt(8)
-      else if (j + 1 < ng) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
-      else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
-    }
+    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
   };
 
   // Prologue: the workgroup's 128 Q rows (wave w moves rows 16w .. 16w+15, swizzled as
@@ -401,12 +433,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(Qs + 16 * wave * kD);
     for (int i = 0; i < 4; ++i) {
       const uint32_t row = (uint32_t)(16 * wave + 4 * i + r4);
-      dma16(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
+      dma16<0>(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
     }
   }
-  if (ng > 0) load_k(0);
-  if (ng > 0) load_v(0);
-  if (ng > 1) load_k(1);
+  if (ng > 0) {
+    load_k(0);
+    load_v(0);
+    load_k(1);
+  }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
 
@@ -433,32 +467,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int last = wave_last_abs / kBN - gb0 + 1;
     j_act = last < 0 ? 0 : (last < ng ? last : ng);
   }
+  // The steady-state loop also runs only over softmax steps of blocks that need no mask
+  // (blocks 1 .. j_mask-1), so its softmax step carries no masking code.
   const int jm = j_act;
+  const MaskOn mask_on;
+  const MaskOff mask_off;
   if (g == 0) {
-    auto half0 = [&](int t, bool full) __attribute__((always_inline)) {
+    auto half0 = [&](int t, bool full, auto mask_tag) __attribute__((always_inline)) {
       if (full) mstep_full(t);
       else mstep(t);
       __syncthreads();
-      vstep(t);
+      vstep(t, mask_tag);
       __syncthreads();
     };
+    const int t_full = jm < j_mask ? jm : j_mask;
     int t = 0;
-    for (; t <= n0 && t < 1; ++t) half0(t, false);
-    for (; t < jm; ++t) half0(t, true);
-    for (; t <= n0; ++t) half0(t, false);
+    for (; t <= n0 && t < 1; ++t) half0(t, false, mask_on);
+    for (; t < t_full; ++t) half0(t, true, mask_off);
+    for (; t <= n0; ++t) half0(t, false, mask_on);
   } else {
-    auto half1 = [&](int t, bool full) __attribute__((always_inline)) {
-      vstep(t - 1);
+    auto half1 = [&](int t, bool full, auto mask_tag) __attribute__((always_inline)) {
+      vstep(t - 1, mask_tag);
       __syncthreads();
       if (full) mstep_full(t);
       else mstep(t);
       __syncthreads();
     };
+    const int t_full = jm < j_mask + 1 ? jm : j_mask + 1;
     int t = 0;
-    for (; t <= n0 && t < 1; ++t) half1(t, false);
-    for (; t < jm; ++t) half1(t, true);
-    for (; t <= n0; ++t) half1(t, false);
+    for (; t <= n0 && t < 2; ++t) half1(t, false, mask_on);
+    for (; t < t_full; ++t) half1(t, true, mask_off);
+    for (; t <= n0; ++t) half1(t, false, mask_on);
   }
+
+  // the last softmax steps' loads (zero fills past the range) land before the merge
+  // reuses the tiles
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
 
   // Merge. Each group finishes half of the head dims: group g keeps dims 64g .. 64g+63
   // (accumulators dt = 2g, 2g+1) and hands the other half to the other group through LDS
