@@ -44,7 +44,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk", "fp8"],
+    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk", "fp8", "gdn", "gdn_step"],
                    default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -344,6 +344,32 @@ def bench_fp8_prefill(ctx, ema, name, B, Hq, Hkv, D, cap, T, off, steps=20):
     return {"workload": name, "us": ms * 1e3, "tflops": tf, "frac_of_peak": tf / BF16_PEAK_TFLOPS, "flops": fl}
 
 
+def gdn_bytes(B, T, Hk, Hv, Dk, Dv, act=2):
+    """State read + write, q/k/v in, y out, g/beta in."""
+    return 8 * B * Hv * Dv * Dk + act * B * T * (2 * Hk * Dk + 2 * Hv * Dv) + 8 * B * T * Hv
+
+
+def bench_gdn(ctx, ema, name, B, T, Hk, Hv, Dk, Dv, steps=20):
+    """Gated DeltaNet scan (ema_gdn_scan), bf16 activations, f32 state updated in place
+    (bounded: unit keys, g and beta in (0, 1))."""
+    torch = ctx.torch
+    q = ctx.randn((B, T, Hk, Dk), 0.0, 1.0 / Dk)
+    k = ctx.randn((B, T, Hk, Dk), 0.0, 1.0)
+    k = (k.float() / k.float().norm(dim=-1, keepdim=True)).to(torch.bfloat16).contiguous()
+    v = ctx.randn((B, T, Hv, Dv))
+    g = torch.rand((B, T, Hv), device=ctx.dev) * 0.5 + 0.5
+    beta = torch.rand((B, T, Hv), device=ctx.dev)
+    S = torch.randn((B, Hv, Dv, Dk), device=ctx.dev) * 0.5
+    y = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=ctx.dev)
+    ms = time_calls(torch, lambda: ema.gdn_scan(q, k, v, g, beta, S, y=y), steps, 5)
+    by = gdn_bytes(B, T, Hk, Hv, Dk, Dv)
+    gbs = by / (ms * 1e-3) / 1e9
+    tok = B * T / (ms * 1e-3)
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM), {tok:.3g} tokens/s")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by,
+            "tokens_per_s": tok}
+
+
 def bench_pre(ctx, ema, name, T, Hq, Hkv, D, cap, steps=20):
     torch = ctx.torch
     cache = ema.StaticCache(1, Hkv, cap, D)
@@ -417,6 +443,12 @@ def main():
                                           [32768] * 8))
         secondary.append(bench_fp8_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_fp8_cache", 1, 32, 8, 128, 4096,
                                            2048, 0))
+    if args.only in ("all", "gdn", "gdn_step"):
+        # Gated DeltaNet layer of Qwen3-Next shape: 16 key / 32 value heads, head dims 128
+        secondary.append(bench_gdn(ctx, ema, "gdn_decode_step_B32_16k32v_dk128_dv128", 32, 1, 16, 32, 128, 128))
+    if args.only in ("all", "gdn"):
+        secondary.append(bench_gdn(ctx, ema, "gdn_scan_T2048_B1_16k32v_dk128_dv128", 1, 2048, 16, 32, 128, 128,
+                                   steps=5))
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle f32 SDPA on the host)")

@@ -359,3 +359,26 @@ int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvca
 }
 
 }  // extern "C"
+
+int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, const void* v, const float* g,
+                     const float* beta, float* state, void* y, int32_t batch, int32_t n_tokens, int32_t hk,
+                     int32_t hv, int32_t dk, int32_t dv, int32_t dtype) {
+  const char* op = "ema_gdn_scan";
+  if (!q || !k || !v || !g || !beta || !state || !y)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: null q/k/v/g/beta/state/y", op);
+  if (dtype != EMA_DTYPE_BF16 && dtype != EMA_DTYPE_F16 && dtype != EMA_DTYPE_F32)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: dtype %d is not bf16, f16 or f32", op, dtype);
+  if (batch <= 0 || n_tokens <= 0 || hk <= 0 || hv <= 0 || dk <= 0 || dv <= 0)
+    return set_error(EMA_ERR_SHAPE, "%s: dims must be positive (batch=%d n_tokens=%d hk=%d hv=%d dk=%d dv=%d)", op,
+                     batch, n_tokens, hk, hv, dk, dv);
+  if (hv % hk) return set_error(EMA_ERR_SHAPE, "%s: hv %d is not a multiple of hk %d", op, hv, hk);
+  if (dk != 64 && dk != 128) return set_error(EMA_ERR_UNSUPPORTED, "%s: dk %d not supported (64, 128)", op, dk);
+  if (dv % 16) return set_error(EMA_ERR_SHAPE, "%s: dv %d is not a multiple of 16", op, dv);
+  const uintptr_t el_align = dtype == EMA_DTYPE_F32 ? 3u : 1u;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(state) || ((uintptr_t)v | (uintptr_t)y) & el_align ||
+      ((uintptr_t)g | (uintptr_t)beta) & 3u)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: misaligned buffer (q, k and state 16-byte aligned)", op);
+  if ((int64_t)batch * n_tokens * hv * dv >= ((int64_t)1 << 31) || (int64_t)batch * hv * dv * dk >= ((int64_t)1 << 40))
+    return set_error(EMA_ERR_SHAPE, "%s: tensors too large", op);
+  return launch_gdn_scan((hipStream_t)stream, q, k, v, g, beta, state, y, batch, n_tokens, hk, hv, dk, dv, dtype);
+}

@@ -28,6 +28,8 @@ EMA_ERR_HIP = -6
 
 EMA_DTYPE_BF16 = 1
 EMA_DTYPE_FP8_E4M3 = 2
+EMA_DTYPE_F16 = 3
+EMA_DTYPE_F32 = 4
 EMA_PRE_NO_NORM = 1
 EMA_PRE_NO_ROPE = 2
 EMA_PREFILL_CAUSAL = 1
@@ -38,7 +40,7 @@ EXPORTED = (
     "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
     "ema_decode_attention", "ema_decode_step", "ema_prefill_attention", "ema_prefill_workspace_size",
-    "ema_prefill_attention_ws",
+    "ema_prefill_attention_ws", "ema_gdn_scan",
 )
 
 
@@ -88,6 +90,7 @@ def lib() -> ctypes.CDLL:
             "ema_prefill_attention": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp]),
             "ema_prefill_workspace_size": (i32, [D, i32, ctypes.POINTER(u64)]),
             "ema_prefill_attention_ws": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp, i32, vp, u64]),
+            "ema_gdn_scan": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -285,3 +288,21 @@ def prefill_attention(q, cache: StaticCache, q_offsets, scale=None, causal=True,
                                           Hq, scale, flags, _ptr(out), max_kv_len, _ptr(workspace),
                                           workspace.numel()), "ema_prefill_attention_ws")
     return out
+
+
+def gdn_scan(q, k, v, g, beta, state, y=None, stream=None):
+    """Gated DeltaNet recurrent scan (ema_gdn_scan): q, k [B,T,Hk,Dk], v [B,T,Hv,Dv] in bf16,
+    f16 or f32; g, beta [B,T,Hv] f32; state [B,Hv,Dv,Dk] f32, updated in place. Returns
+    y [B,T,Hv,Dv] in the activation dtype."""
+    import torch
+
+    dtypes = {torch.bfloat16: EMA_DTYPE_BF16, torch.float16: EMA_DTYPE_F16, torch.float32: EMA_DTYPE_F32}
+    if q.dtype not in dtypes:
+        raise EmaError(EMA_ERR_INVALID_ARG, "ema_gdn_scan", f"unsupported activation dtype {q.dtype}")
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    if y is None:
+        y = torch.empty((B, T, Hv, Dv), dtype=q.dtype, device=q.device)
+    _check(lib().ema_gdn_scan(_stream(stream), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state),
+                              _ptr(y), B, T, Hk, Hv, Dk, Dv, dtypes[q.dtype]), "ema_gdn_scan")
+    return y

@@ -20,6 +20,9 @@
  *              crates/kvcache/src/fp8.rs:47-68, crates/ops/src/fp8.rs:71-92
  *                                                               ema_kvcache_init_fp8 / _alloc_fp8
  *                                                               (stored, not simulated)
+ *   gdn_step / gdn_step_metal and the per-token scan of gdn_forward
+ *              crates/ops/src/gdn.rs:83-150, gdn_metal.rs:56-88, gdn_forward.rs:173-192
+ *                                                               ema_gdn_scan
  *
  * Conventions
  *   - Every entry point returns int32_t: EMA_OK (0) or a negative EMA_ERR_*.
@@ -63,6 +66,9 @@ extern "C" {
  * whole head is quantised, i.e. n_rot = 0). Decoded exactly to bf16 by the readers.
  * head_dim 128 only. Values must be finite. */
 #define EMA_DTYPE_FP8_E4M3 2
+/* activation types of ema_gdn_scan (besides EMA_DTYPE_BF16) */
+#define EMA_DTYPE_F16 3
+#define EMA_DTYPE_F32 4
 
 /* ema_pre_attention flags */
 #define EMA_PRE_NO_NORM 1u /* q_norm/k_norm are None: crates/ops/src/attention.rs:57-76 */
@@ -214,6 +220,29 @@ EMA_API int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, con
                                          const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads,
                                          float scale, uint32_t flags, void* out, int32_t max_kv_len,
                                          void* workspace, uint64_t workspace_bytes);
+
+/* Gated DeltaNet recurrent scan over n_tokens tokens (n_tokens = 1: the decode step of
+ * gdn_step / gdn_step_metal, crates/ops/src/gdn.rs:83-150 and gdn_metal.rs:56-88; n_tokens
+ * > 1: the token loop of gdn_forward, crates/ops/src/gdn_forward.rs:173-192). For each
+ * token t and value head h, with key head h / (hv / hk):
+ *   S = g S;  kv = S k;  delta = (v - kv) beta;  S = S + delta k^T;  y = S q
+ * where S = state[b, h] is [dv, dk] f32.
+ *   q, k:    [batch, n_tokens, hk, dk]  in `dtype`
+ *   v:       [batch, n_tokens, hv, dv]  in `dtype`
+ *   g, beta: [batch, n_tokens, hv] f32  the decay exp(-exp(A_log) softplus(a + dt_bias))
+ *            and sigmoid(b), computed by the caller as in both reference paths
+ *   state:   [batch, hv, dv, dk] f32, read and updated in place (zeros for a new sequence,
+ *            as GdnState initialises it: gdn_forward.rs:166-170)
+ *   y:       [batch, n_tokens, hv, dv] in `dtype` (gdn_step returns y cast to the
+ *            activation type; pass EMA_DTYPE_F32 activations for the f32 y of
+ *            gdn_step_metal)
+ * dtype: EMA_DTYPE_BF16, EMA_DTYPE_F16 or EMA_DTYPE_F32. dk: 64 or 128; dv a multiple of
+ * 16; hv a multiple of hk. q, k and state 16-byte aligned; v, y, g, beta element-aligned.
+ * Calls that update the same state must not overlap. */
+EMA_API int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, const void* v,
+                             const float* g, const float* beta, float* state, void* y,
+                             int32_t batch, int32_t n_tokens, int32_t hk, int32_t hv, int32_t dk,
+                             int32_t dv, int32_t dtype);
 
 #ifdef __cplusplus
 }

@@ -473,3 +473,38 @@ void ora_fp8_dequantize_rows(const uint8_t* codes, const int8_t* exps, int64_t r
     for (int i = 0; i < D; ++i)
       out[r * D + i] = ldexpf(ora_e4m3_value(codes[r * D + i]), exps[r * (D / 64) + i / 64]);
 }
+
+/* ------------------------------------------------------ gated deltanet */
+
+void ora_gdn_scan(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                  double* state, double* y, int B, int T, int hk, int hv, int dk, int dv) {
+  const int rep = hv / hk;
+  for (int b = 0; b < B; ++b)
+    for (int t = 0; t < T; ++t)
+      for (int h = 0; h < hv; ++h) {
+        const int kh = h / rep;
+        const float* kt = k + (((int64_t)b * T + t) * hk + kh) * dk;
+        const float* qt = q + (((int64_t)b * T + t) * hk + kh) * dk;
+        const float* vt = v + (((int64_t)b * T + t) * hv + h) * dv;
+        const double gg = g[((int64_t)b * T + t) * hv + h];
+        const double bb = beta[((int64_t)b * T + t) * hv + h];
+        double* S = state + ((int64_t)b * hv + h) * dv * dk;
+        double* yt = y + (((int64_t)b * T + t) * hv + h) * dv;
+        for (int r = 0; r < dv; ++r) {
+          double* Sr = S + (int64_t)r * dk;
+          double kv = 0.0;
+          for (int d = 0; d < dk; ++d) {
+            Sr[d] *= gg;
+            kv += Sr[d] * kt[d];
+          }
+          const double delta = (vt[r] - kv) * bb;
+          double acc = 0.0;
+          for (int d = 0; d < dk; ++d) {
+            Sr[d] += kt[d] * delta;
+            acc += Sr[d] * qt[d];
+          }
+          yt[r] = acc;
+        }
+      }
+}
+

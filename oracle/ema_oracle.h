@@ -16,6 +16,8 @@
  *                                 crates/mlx-ffi/src/ops/real/blas.rs:82-101 ("causal")
  *   - op order norm -> transpose -> rope -> write -> sdpa
  *                                 crates/serve/src/forward_qwen3.rs:52-152
+ *   - FP8 KV format               crates/ops/src/fp8.rs, crates/kvcache/src/fp8.rs
+ *   - Gated DeltaNet step/scan    crates/ops/src/gdn.rs:83-150, gdn_forward.rs:173-192
  *
  * bf16 tensors are passed as uint16_t bit patterns (IEEE bfloat16, RNE).
  *
@@ -132,6 +134,19 @@ void ora_fp8_round_trip(float* x, int64_t rows, int D, int n_rot);
 void ora_fp8_quantize_rows(const float* x, int64_t rows, int D, uint8_t* codes, int8_t* exps);
 /* value = e4m3(code) * 2^exp, exact in f32. */
 void ora_fp8_dequantize_rows(const uint8_t* codes, const int8_t* exps, int64_t rows, int D, float* out);
+
+/* ---- Gated DeltaNet recurrent scan ----
+ * gdn_step (crates/ops/src/gdn.rs:83-150; the fused kernel body gdn_metal.rs:16-50 does the
+ * same arithmetic) applied token by token as gdn_forward does (gdn_forward.rs:173-192), in
+ * double. For each token t and value head h, with key head h / (hv / hk) (the tile-based
+ * expansion of gdn.rs:100-110):
+ *   S = g S (gdn.rs:97-99);  kv = S k (:112-115);  delta = (v - kv) beta (:117-121);
+ *   S = S + delta k^T (:123-126);  y = S q (:138-141)
+ * with S = state[b, h] of shape [dv, dk].
+ *   q, k [B, T, hk, dk]; v [B, T, hv, dv]; g, beta [B, T, hv]  (f32 inputs)
+ *   state [B, hv, dv, dk] double, updated in place; y [B, T, hv, dv] double. */
+void ora_gdn_scan(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                  double* state, double* y, int B, int T, int hk, int hv, int dk, int dv);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,7 @@ def lib():
         L.ora_fp8_round_trip.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int]
         L.ora_fp8_quantize_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _u8p, _i8p]
         L.ora_fp8_dequantize_rows.argtypes = [_u8p, _i8p, ctypes.c_int64, ctypes.c_int, _f32p]
+        L.ora_gdn_scan.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f64p, _f64p] + [ctypes.c_int] * 6
         _lib = L
     return _lib
 
@@ -261,3 +262,24 @@ def fp8_dequantize(codes, exps) -> np.ndarray:
     out = np.empty(codes.shape, dtype=np.float32)
     lib().ora_fp8_dequantize_rows(_p(codes, _u8p), _p(exps, _i8p), codes.size // D, D, _p(out, _f32p))
     return out
+
+
+def gdn_scan(q, k, v, g, beta, state):
+    """Gated DeltaNet scan (gdn.rs:83-150 per token, gdn_forward.rs:173-192): q, k [B,T,Hk,Dk],
+    v [B,T,Hv,Dv], g, beta [B,T,Hv] (f32 values), state [B,Hv,Dv,Dk]. Returns (y [B,T,Hv,Dv],
+    new state), both float64; the input state is not modified."""
+    q = _c(np.asarray(q, dtype=np.float32), np.float32)
+    k = _c(np.asarray(k, dtype=np.float32), np.float32)
+    v = _c(np.asarray(v, dtype=np.float32), np.float32)
+    g = _c(np.asarray(g, dtype=np.float32), np.float32)
+    beta = _c(np.asarray(beta, dtype=np.float32), np.float32)
+    S = np.array(state, dtype=np.float64, copy=True)
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    assert k.shape == q.shape and v.shape[:2] == (B, T) and g.shape == (B, T, Hv) == beta.shape
+    assert S.shape == (B, Hv, Dv, Dk) and Hv % Hk == 0
+    y = np.empty((B, T, Hv, Dv), dtype=np.float64)
+    lib().ora_gdn_scan(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), _p(g, _f32p), _p(beta, _f32p), _p(S, _f64p),
+                       _p(y, _f64p), B, T, Hk, Hv, Dk, Dv)
+    return y, S
+

@@ -217,3 +217,21 @@ def test_prefill_workspace_size_and_errors(ema):
     assert rc == ema.EMA_ERR_WORKSPACE and "workspace" in ema.last_error()
     rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d8), g, 8, 16, 0.088, 1, g, 4, g, 1 << 30)
     assert rc == ema.EMA_ERR_CAPACITY
+
+
+def test_gdn_scan_argument_errors(ema):
+    L = ema.lib()
+    p = 0x40000  # 16-byte aligned stand-in; every call below fails validation before any HIP call
+
+    def call(q=p, k=p, v=p, g=p, beta=p, state=p, y=p, B=2, T=3, hk=2, hv=4, dk=128, dv=32, dtype=ema.EMA_DTYPE_BF16):
+        return L.ema_gdn_scan(None, q, k, v, g, beta, state, y, B, T, hk, hv, dk, dv, dtype)
+
+    assert call(state=None) == ema.EMA_ERR_INVALID_ARG and "null" in ema.last_error()
+    assert call(dtype=ema.EMA_DTYPE_FP8_E4M3) == ema.EMA_ERR_INVALID_ARG
+    assert call(T=0) == ema.EMA_ERR_SHAPE
+    assert call(hv=6, hk=4) == ema.EMA_ERR_SHAPE and "multiple of hk" in ema.last_error()
+    assert call(dk=96) == ema.EMA_ERR_UNSUPPORTED
+    assert call(dv=24) == ema.EMA_ERR_SHAPE
+    assert call(state=p + 4) == ema.EMA_ERR_INVALID_ARG and "misaligned" in ema.last_error()
+    assert call(q=p + 8) == ema.EMA_ERR_INVALID_ARG
+    assert call(v=p + 2, dtype=ema.EMA_DTYPE_F32) == ema.EMA_ERR_INVALID_ARG
