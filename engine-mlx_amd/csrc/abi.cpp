@@ -49,6 +49,7 @@ int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
     if (c->stride_pos % 16 || c->stride_head % 16 || c->stride_batch % 16)
       return set_error(EMA_ERR_SHAPE, "%s: fp8 cache strides must be multiples of 16 bytes", op);
   }
+  if (c->flags & ~EMA_KV_ROTATING) return set_error(EMA_ERR_INVALID_ARG, "%s: unknown cache flags 0x%x", op, c->flags);
   if (c->batch <= 0 || c->n_kv_heads <= 0 || c->capacity <= 0 || c->head_dim <= 0)
     return set_error(EMA_ERR_SHAPE, "%s: cache dims must be positive (batch=%d n_kv_heads=%d capacity=%d head_dim=%d)",
                      op, c->batch, c->n_kv_heads, c->capacity, c->head_dim);
@@ -200,7 +201,7 @@ int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_no
   if (batch != cache->batch || n_kv_heads != cache->n_kv_heads || head_dim != cache->head_dim)
     return set_error(EMA_ERR_SHAPE, "%s: shape (batch=%d n_kv_heads=%d head_dim=%d) does not match the cache (%d, %d, %d)",
                      op, batch, n_kv_heads, head_dim, cache->batch, cache->n_kv_heads, cache->head_dim);
-  if (n_tokens > cache->capacity)
+  if (n_tokens > cache->capacity && !(cache->flags & EMA_KV_ROTATING))  // a ring keeps the last capacity
     return set_error(EMA_ERR_CAPACITY, "%s: static KV overflow: %d tokens exceed capacity %d", op, n_tokens, cache->capacity);
   if (!(eps >= 0.f) || !(theta > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: eps must be >= 0 and theta > 0", op);
   if (!aligned16(qkv) || !aligned16(q_out)) return set_error(EMA_ERR_INVALID_ARG, "%s: qkv/q_out must be 16-byte aligned", op);
@@ -313,6 +314,8 @@ int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_k
                      n_tokens, cache->capacity);
   if (cache->dtype == EMA_DTYPE_BF16)
     return launch_prefill((hipStream_t)stream, q, *cache, q_offsets, n_tokens, n_heads, scale, flags, out);
+  if (cache->flags & EMA_KV_ROTATING)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over a rotating fp8 cache is not supported", op);
   const uint64_t need = prefill_ws_bytes(cache, max_kv_len);
   if (!workspace || workspace_bytes < need)
     return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes needed, %llu given", op,

@@ -71,6 +71,7 @@ struct DecodeArgs {
   float eps, log2_theta;
   uint32_t flags;
   int fused;
+  int rot;  // rotating cache: the fused step's new row is row off % cap
   // fp8 cache: block exponents [B, Hkv, cap, 2] (k, v then hold E4M3FN codes)
   const int8_t* kexp;
   const int8_t* vexp;
@@ -341,9 +342,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     u32x4 qraw[4], qwv[4];
     uint16_t kr1 = 0, kr2 = 0, kw1 = 0, kw2 = 0, vr1 = 0, vr2 = 0;
     for (int s = 0; s < 4; ++s) qraw[s] = ld16(qh + kdim<kFp8>(s, c));
-    // fused: the wave that will run the segment's last tile (position L - 1 = offset) forms
-    // the new k, v row; its inputs are loaded now, with the q row and the norm weights
-    const bool owner = kFused && tile1 == nb && wave == (nb - 1 - tile0) % kWaves;
+    // fused: the new k, v row goes to row w of the cache (the offset; offset % cap for a
+    // rotating cache) when it is written at all (a static cache skips an offset past the
+    // capacity). The wave that will run the tile holding row w forms the row; its inputs
+    // are loaded now, with the q row and the norm weights.
+    int w_row = -1;
+    if (kFused) {
+      const int off_b = a.off[b];
+      if (a.rot) w_row = off_b >= 0 ? off_b % a.cap : -1;
+      else w_row = off_b == L - 1 ? off_b : -1;
+    }
+    const int w_tile = w_row >= 0 ? w_row / kTile : -1;
+    const bool owner = kFused && w_row >= 0 && tile0 <= w_tile && w_tile < tile1 && wave == (w_tile - tile0) % kWaves;
     if (kFused) {
       // the norm weights may be null with EMA_PRE_NO_NORM: read only when used
       const bool norm = !(a.flags & EMA_PRE_NO_NORM);
@@ -393,10 +403,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int e = 0; e < 4; ++e) v[e] = g < a.G ? pack_bf16x2(x[8 * s + 2 * e], x[8 * s + 2 * e + 1]) : 0u;
         qop[s] = as_bf16x8(v);
       }
-      if (owner && off == L - 1) {
+      if (owner) {
         // the new row (lane i: dims i, i + 64): k = rope(norm(k_raw)), v a bit copy; it
-        // goes to the cache at the offset and to LDS, from where this same wave patches
-        // its last tile (rows clamped to L - 1 = the new token)
+        // goes to cache row w and to LDS, from where this same wave patches the rows of its
+        // tile that load row w (with a static cache, also the rows past L - 1 = w, which
+        // the loads clamp to it)
         float k1 = bf16_to_f32(kr1), k2 = bf16_to_f32(kr2);
         if (!(a.flags & EMA_PRE_NO_NORM)) {
           float ss = k1 * k1 + k2 * k2;
@@ -424,23 +435,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           new_kv[0][lane + 64] = d[1];
           new_kv[1][lane] = d[2];
           new_kv[1][lane + 64] = d[3];
-          uint8_t* const kd = (uint8_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
-          uint8_t* const vd = (uint8_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+          uint8_t* const kd = (uint8_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)w_row * a.sp;
+          uint8_t* const vd = (uint8_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)w_row * a.sp;
           kd[lane] = (uint8_t)c0;
           kd[lane + 64] = (uint8_t)c1;
           vd[lane] = (uint8_t)c2;
           vd[lane + 64] = (uint8_t)c3;
           if (lane == 0) {
-            ((uint16_t*)a.kexp)[erow + off] = (uint16_t)((uint8_t)e[0] | ((uint32_t)(uint8_t)e[1] << 8));
-            ((uint16_t*)a.vexp)[erow + off] = (uint16_t)((uint8_t)e[2] | ((uint32_t)(uint8_t)e[3] << 8));
+            ((uint16_t*)a.kexp)[erow + w_row] = (uint16_t)((uint8_t)e[0] | ((uint32_t)(uint8_t)e[1] << 8));
+            ((uint16_t*)a.vexp)[erow + w_row] = (uint16_t)((uint8_t)e[2] | ((uint32_t)(uint8_t)e[3] << 8));
           }
         } else {
           new_kv[0][lane] = kb1;
           new_kv[0][lane + 64] = kb2;
           new_kv[1][lane] = vr1;
           new_kv[1][lane + 64] = vr2;
-          uint16_t* const kd = (uint16_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
-          uint16_t* const vd = (uint16_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)off * a.sp;
+          uint16_t* const kd = (uint16_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)w_row * a.sp;
+          uint16_t* const vd = (uint16_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)w_row * a.sp;
           kd[lane] = kb1;
           kd[lane + 64] = kb2;
           vd[lane] = vr1;
@@ -461,12 +472,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         load_tile(tile + kWaves, kn, vn);
       }
       const int p0 = tile * kTile;
-      if (kFused && owner && tile == nb - 1 && a.off[b] == L - 1) {
-        for (int r = 0; r < 2; ++r)
-          if (p0 + krow0 + 4 * r >= L - 1)
+      if (kFused && owner && tile == w_tile) {
+        // rows whose (clamped) load position is w
+        for (int r = 0; r < 2; ++r) {
+          const int p = p0 + krow0 + 4 * r;
+          if ((p < L ? p : L - 1) == w_row)
             for (int s = 0; s < 4; ++s) kc[r][s] = *(const u32x4*)&new_kv[0][kdim<kFp8>(s, c)];
-        for (int kk = 0; kk < 8; ++kk)
-          if (p0 + 8 * c + kk >= L - 1) vc[kk] = *(const u32x4*)&new_kv[1][8 * m];
+        }
+        for (int kk = 0; kk < 8; ++kk) {
+          const int p = p0 + 8 * c + kk;
+          if ((p < L ? p : L - 1) == w_row) vc[kk] = *(const u32x4*)&new_kv[1][8 * m];
+        }
       }
 
       f32x4 sc[2];
@@ -683,6 +699,7 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.cap = c.capacity;
   a.W = plan.workers;
   a.fused = fused != nullptr;
+  a.rot = (c.flags & EMA_KV_ROTATING) != 0;
   a.qkv = fused ? (const uint16_t*)fused->qkv : nullptr;
   a.qw = fused ? (const uint16_t*)fused->q_norm_w : nullptr;
   a.kw = fused ? (const uint16_t*)fused->k_norm_w : nullptr;

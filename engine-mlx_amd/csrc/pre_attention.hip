@@ -100,6 +100,7 @@ struct PreArgs {
   float log2_theta;
   int B, T, Hq, Hkv, cap;
   uint32_t flags;
+  int rot;  // rotating cache: position p lives in row p % cap
 };
 
 // Scale exponent of one 64-element block from this lane's share (amax over the 8 lanes
@@ -144,7 +145,11 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
   const int b = (int)(bt / a.T);
   const int off = a.off[b];
   const int pos = off + t;
-  const bool in_cap = off >= 0 && (int64_t)off + a.T <= a.cap;
+  // the cache row of this token, and whether it is written: a static cache takes the
+  // call's rows only when all fit; a rotating one keeps the last cap tokens of the call
+  // (earlier ones would be overwritten within it)
+  const int row = a.rot ? pos % a.cap : pos;
+  const bool in_cap = a.rot ? off >= 0 && a.T - t <= a.cap : off >= 0 && (int64_t)off + a.T <= a.cap;
   const bool rope = !(a.flags & EMA_PRE_NO_ROPE);
   // RoPE angles of this position, shared by every q and k head of the token
   if (rope && (int)threadIdx.x < HALF) {
@@ -186,10 +191,10 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       if (!in_cap) continue;
       const int kh = h - a.Hq - a.Hkv;
       if (kFp8) {
-        store_fp8(x, a.vc, a.vexp, b, kh, pos);
+        store_fp8(x, a.vc, a.vexp, b, kh, row);
         continue;
       }
-      uint16_t* dst = a.vc + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)pos * a.sp;
+      uint16_t* dst = a.vc + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)row * a.sp;
       Vec<E>::store(dst + lane8 * E, x);
       Vec<E>::store(dst + HALF + lane8 * E, x + E);
       continue;
@@ -231,12 +236,12 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       for (int e = 0; e < 2 * E; ++e) o[e] = (uint16_t)f32_to_bf16_bits(y[e]);
     }
     if (kFp8 && !is_q) {
-      store_fp8(o, a.kc, a.kexp, b, h - a.Hq, pos);
+      store_fp8(o, a.kc, a.kexp, b, h - a.Hq, row);
       continue;
     }
     uint16_t* dst;
     if (is_q) dst = a.q_out + (((int64_t)b * a.Hq + h) * a.T + t) * D;
-    else dst = a.kc + (int64_t)b * a.sb + (int64_t)(h - a.Hq) * a.sh + (int64_t)pos * a.sp;
+    else dst = a.kc + (int64_t)b * a.sb + (int64_t)(h - a.Hq) * a.sh + (int64_t)row * a.sp;
     Vec<E>::store(dst + lane8 * E, o);
     Vec<E>::store(dst + HALF + lane8 * E, o + E);
   }
@@ -269,6 +274,7 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   a.Hkv = Hkv;
   a.cap = c.capacity;
   a.flags = flags;
+  a.rot = (c.flags & EMA_KV_ROTATING) != 0;
   const int threads = 256;
   const int64_t blocks = (int64_t)B * T;  // one workgroup per token
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many tokens");

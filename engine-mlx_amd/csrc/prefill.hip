@@ -94,6 +94,11 @@ __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_ad
 // offset added to it stays below 2^32): the load returns zeros and touches no memory.
 constexpr uint32_t kNoRow = 0xF0000000u;
 
+// kRot: rotating cache (EMA_KV_ROTATING). The keys of a sequence are the positions
+// [base, q_off + T) with base = max(0, q_off + T - cap), position p in row p % cap; the
+// kernel works on key indices c = p - base (q_off is taken relative to base), so all its
+// causal and range logic is that of a static cache, and only the loads map c to its row.
+template <bool kRot>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
 
@@ -127,6 +132,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   int q_off = a.q_off[b];
   q_off = q_off < 0 ? 0 : q_off;
+  int key_base = 0;  // absolute position of key index 0 (rotating cache; n_tokens <= cap)
+  if (kRot) {
+    key_base = q_off + a.T - a.cap;
+    key_base = key_base < 0 ? 0 : key_base;
+    q_off -= key_base;
+  }
   auto run_block = [&](const int qb) __attribute__((always_inline)) {
   int kv_len = q_off + a.T;
   kv_len = kv_len > a.cap ? a.cap : kv_len;
@@ -182,17 +193,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   // byte offset of block j of this group, or kNoRow past the group's range (its loads
   // then fill the tile with zeros that nothing reads, which keeps the issue count of a
-  // step fixed)
+  // step fixed). Rotating cache: the row of the block's first key, and wrap_rows, the
+  // number of its rows before the ring's end (rows past it are cap rows back).
   auto blk_off = [&](int j) __attribute__((always_inline)) {
-    return j < ng ? (uint32_t)((gb0 + j) * kBN) * row_bytes : kNoRow;
+    if (j >= ng) return kNoRow;
+    if (kRot) return (uint32_t)((key_base + (gb0 + j) * kBN) % a.cap) * row_bytes;
+    return (uint32_t)((gb0 + j) * kBN) * row_bytes;
   };
+  auto wrap_rows = [&](int j) __attribute__((always_inline)) {
+    return kRot && j < ng ? a.cap - (key_base + (gb0 + j) * kBN) % a.cap : kBN;
+  };
+  const uint32_t ring_bytes = (uint32_t)a.cap * row_bytes;
   auto tile_dst = [&](const uint16_t* tile) __attribute__((always_inline)) {
     return (uint32_t)(uintptr_t)(lds_void*)(tile + 16 * wq * kD);
   };
   // one of the 4 instructions of a tile load (spread over the softmax step so the four
   // waves of a group do not queue 32 KB at the address unit at once)
-  auto dma_part = [&](const u32x4 r, uint32_t off_blk, const uint32_t* off, uint32_t dst, int i)
+  auto dma_part = [&](const u32x4 r, uint32_t off_blk, const uint32_t* off, uint32_t dst, int i, int wrap)
       __attribute__((always_inline)) {
+    if (kRot) {
+      // true offsets (the instruction offset unused, the LDS address moved through M0), so
+      // a row past the ring's end, moved cap rows back, never goes below zero
+      uint32_t o = off[i] + 1024u * i + off_blk;
+      if (16 * wq + 4 * i + r4 >= wrap) o -= ring_bytes;
+      dma16<0>(r, o, dst + 1024u * i);
+      return;
+    }
     const uint32_t o = off[i] + off_blk;
     switch (i) {
       case 0: dma16<0>(r, o, dst); break;
@@ -203,6 +229,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
   auto dma = [&](const u32x4 r, int j, const uint32_t* off, const uint16_t* tile) __attribute__((always_inline)) {
     const uint32_t ob = blk_off(j), dst = tile_dst(tile);
+    const int wrap = wrap_rows(j);
     const int base = (gb0 + j) * kBN;
     if (j < ng && base < kv_begin) {
       // first block of a chunk-only window: rows before kv_begin are outside the
@@ -210,10 +237,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       // the cache holds there (even NaN) cannot reach the masked products
       for (int i = 0; i < 4; ++i) {
         const int row = base + 16 * wq + 4 * i + r4;
-        dma_part(r, row < kv_begin ? kNoRow : ob, off, dst, i);
+        dma_part(r, row < kv_begin ? kNoRow : ob, off, dst, i, row < kv_begin ? kBN : wrap);
       }
     } else {
-      for (int i = 0; i < 4; ++i) dma_part(r, ob, off, dst, i);
+      for (int i = 0; i < 4; ++i) dma_part(r, ob, off, dst, i, wrap);
     }
   };
   auto load_k = [&](int j) __attribute__((always_inline)) { dma(k_rsrc, j, koff, Ks + (j & 1) * kTile); };
@@ -368,10 +395,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       bool fast = all_seen;
       if (fast) {
         const uint32_t kob = blk_off(j + 2), vob = blk_off(j + 1);
+        const int kwrap = wrap_rows(j + 2), vwrap = wrap_rows(j + 1);
         const uint32_t kdst = tile_dst(Ks + (j & 1) * kTile), vdst = tile_dst(Vs + ((j + 1) & 1) * kTile);
         for (int st = 0; st < 4; ++st) {
-          dma_part(k_rsrc, kob, koff, kdst, st);
-          dma_part(v_rsrc, vob, voff, vdst, st);
+          dma_part(k_rsrc, kob, koff, kdst, st, kwrap);
+          dma_part(v_rsrc, vob, voff, vdst, st, vwrap);
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
             const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i]), __builtin_amdgcn_exp2f(sc[kt][i + 1]));
@@ -594,9 +622,13 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
                      c.capacity, (long long)c.stride_pos);
   static bool attr_set = false;
   if (!attr_set) {
-    int32_t rc = check_hip(hipFuncSetAttribute((const void*)prefill_kernel,
+    int32_t rc = check_hip(hipFuncSetAttribute((const void*)prefill_kernel<false>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
                            "ema_prefill_attention: LDS attribute");
+    if (rc) return rc;
+    rc = check_hip(hipFuncSetAttribute((const void*)prefill_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       kLdsBytes),
+                   "ema_prefill_attention: LDS attribute");
     if (rc) return rc;
     attr_set = true;
   }
@@ -630,7 +662,10 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
   a.paired = a.nqb >= 2 && items >= 2 * (int64_t)cus;
   const int64_t blocks = a.paired ? (int64_t)((a.nqb + 1) / 2) * Hq * c.batch : items;
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_prefill_attention: grid too large");
-  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
+  if (c.flags & EMA_KV_ROTATING)
+    hipLaunchKernelGGL(prefill_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
+  else
+    hipLaunchKernelGGL(prefill_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
   return check_hip(hipGetLastError(), "ema_prefill_attention launch");
 }
 

@@ -32,6 +32,7 @@ EMA_DTYPE_F16 = 3
 EMA_DTYPE_F32 = 4
 EMA_PRE_NO_NORM = 1
 EMA_PRE_NO_ROPE = 2
+EMA_KV_ROTATING = 1
 EMA_PREFILL_CAUSAL = 1
 EMA_PREFILL_CHUNK_ONLY = 2
 
@@ -58,7 +59,7 @@ class KvCacheDesc(ctypes.Structure):
         ("batch", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32),
         ("capacity", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("stride_batch", ctypes.c_int64), ("stride_head", ctypes.c_int64),
-        ("stride_pos", ctypes.c_int64), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("stride_pos", ctypes.c_int64), ("dtype", ctypes.c_int32), ("flags", ctypes.c_int32),
         ("k_exp", ctypes.c_void_p), ("v_exp", ctypes.c_void_p),
     ]
 
@@ -138,10 +139,14 @@ class StaticCache:
     (crates/kvcache/src/fp8.rs): ``k``/``v`` are uint8 E4M3FN codes and
     ``k_exp``/``v_exp`` int8 [B, Hkv, cap, D/64] block exponents
     (value = code * 2^exp); head_dim 128.
+
+    ``rotating=True``: the reference's RotatingCache (crates/kvcache/src/rotating.rs) as a
+    ring of ``capacity`` rows (EMA_KV_ROTATING): position p lives in row p % capacity and
+    attention covers the last ``capacity`` tokens; ``len`` is then min(tokens, capacity).
     """
 
     def __init__(self, batch: int, n_kv_heads: int, capacity: int, head_dim: int, device="cuda",
-                 k=None, v=None, dtype="bf16", k_exp=None, v_exp=None):
+                 k=None, v=None, dtype="bf16", k_exp=None, v_exp=None, rotating=False):
         import torch
 
         shape = (batch, n_kv_heads, capacity, head_dim)
@@ -164,6 +169,9 @@ class StaticCache:
                    "ema_kvcache_init_fp8")
         else:
             raise ValueError(f"unknown cache dtype {dtype!r} (bf16 or fp8)")
+        self.rotating = bool(rotating)
+        if self.rotating:
+            self.desc.flags = EMA_KV_ROTATING
         self.offsets = [0] * batch
 
     @property
@@ -171,7 +179,8 @@ class StaticCache:
         return self.desc.capacity
 
     def len(self) -> int:
-        return max(self.offsets) if self.offsets else 0
+        n = max(self.offsets) if self.offsets else 0
+        return min(n, self.capacity) if self.rotating else n
 
     def is_empty(self) -> bool:
         return self.len() == 0

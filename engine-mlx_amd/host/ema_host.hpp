@@ -7,6 +7,7 @@
 //   static KV state + alloc  crates/serve/src/engine.rs:31-42,
 //                            crates/serve/src/engine_ext.rs:266-306
 //                                                            class StaticCache
+//   struct RotatingCache     crates/kvcache/src/rotating.rs:22-122  class RotatingCache (a ring)
 //   struct GqaConfig         crates/attention/src/gqa.rs:27-42  struct GqaConfig
 //   struct GqaWeights        crates/attention/src/gqa.rs:45-53  struct GqaWeights (q/k norm only)
 //   fn gqa_attention         crates/attention/src/gqa.rs:62-107 gqa_attention
@@ -115,6 +116,58 @@ class EMA_HOST_API StaticCache final : public KvCache {
   uint64_t ws_bytes_ = 0;
 };
 
+// Rotating (sliding-window) bf16 cache of one layer: the reference's RotatingCache
+// (crates/kvcache/src/rotating.rs:22-122), which keeps the last window_size tokens, held
+// as a ring [1, Hkv, window_size, head_dim] (EMA_KV_ROTATING): the token at position p
+// lives in row p % window_size, so an append writes rows in place instead of
+// concatenating and slicing. len() = min(tokens seen, window_size) (rotating.rs:108-110).
+class EMA_HOST_API RotatingCache final : public KvCache {
+ public:
+  RotatingCache(int32_t window_size, int32_t n_kv_heads, int32_t head_dim);
+  ~RotatingCache() override;
+  RotatingCache(const RotatingCache&) = delete;
+  RotatingCache& operator=(const RotatingCache&) = delete;
+
+  // Appends at positions [total, total + T); with T > window_size only the last
+  // window_size tokens are kept (rotating.rs:81-92).
+  void append(const Ctx& ctx, const Array& k, const Array& v) override;
+  // The held tokens in order, [1, Hkv, len, head_dim]: the ring itself until it wraps,
+  // then a rotated copy in cache-owned scratch (valid until the next call).
+  std::pair<Array, Array> get(const Ctx& ctx) const override;
+  size_t len() const override { return total_ < (int64_t)desc_.capacity ? (size_t)total_ : (size_t)desc_.capacity; }
+  void reset() override { total_ = 0; }
+  size_t memory_bytes() const override;
+
+  int32_t window_size() const { return desc_.capacity; }
+  int32_t n_kv_heads() const { return desc_.n_kv_heads; }
+  int32_t head_dim() const { return desc_.head_dim; }
+  int64_t total_len() const { return total_; }
+  const ema_kvcache_desc& desc() const { return desc_; }
+  // Device pointer to the int32 value p (any p >= 0 below 2^31; the table grows on
+  // demand, outside the steady state).
+  const int32_t* device_position(int64_t p);
+  // Record that the tokens [total, total + n) were written in place.
+  void advance(int32_t n) { total_ += n; }
+
+  void* q_scratch(size_t bytes);
+  void* out_scratch(size_t bytes);
+  void* decode_workspace(int32_t n_heads, uint64_t* bytes);
+
+ private:
+  ema_kvcache_desc desc_{};
+  int64_t total_ = 0;
+  int32_t* positions_ = nullptr;
+  int64_t n_positions_ = 0;
+  void* q_buf_ = nullptr;
+  size_t q_bytes_ = 0;
+  void* o_buf_ = nullptr;
+  size_t o_bytes_ = 0;
+  void* ws_ = nullptr;
+  uint64_t ws_bytes_ = 0;
+  mutable void* get_buf_ = nullptr;
+  mutable size_t get_bytes_ = 0;
+};
+
 struct GqaConfig {
   int32_t n_heads = 0;
   int32_t n_kv_heads = 0;
@@ -146,5 +199,13 @@ EMA_HOST_API Array gqa_attention(const Ctx& ctx, const Array& qkv, const GqaWeig
 
 EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights,
                                             StaticCache& cache, const SlidingWindowConfig& config, int32_t offset);
+
+// The same over a RotatingCache, which enforces the window (config.window_size must
+// equal the cache's): K/V of positions [offset, offset + T) go to their ring rows; T > 1
+// attends causally over the window the cache holds after the append (keys
+// [max(0, offset + T - window), p] for query position p), T == 1 over the last window
+// tokens. T must not exceed the window.
+EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights,
+                                            RotatingCache& cache, const SlidingWindowConfig& config, int32_t offset);
 
 }  // namespace ema

@@ -70,6 +70,18 @@ extern "C" {
 #define EMA_DTYPE_F16 3
 #define EMA_DTYPE_F32 4
 
+/* ema_kvcache_desc.flags */
+/* Rotating (sliding-window) cache of the last `capacity` tokens, the reference's
+ * RotatingCache (crates/kvcache/src/rotating.rs:56-122) as a ring: the token at absolute
+ * position p lives in row p % capacity. Writes (ema_pre_attention, ema_decode_step) go to
+ * that row, RoPE still uses p; a call writing n_tokens > capacity rows keeps the last
+ * capacity of them. Decode attends min(length, capacity) rows (the window; attention does
+ * not depend on the rows' order). Prefill attends, for query position p of a chunk that
+ * ends at L = q_offset + n_tokens, the keys at positions [max(0, L - capacity), p]: the
+ * window the reference's cache holds after the chunk's append (rotating.rs:86-97), with
+ * MLX's end-aligned causal mask over it. */
+#define EMA_KV_ROTATING 1
+
 /* ema_pre_attention flags */
 #define EMA_PRE_NO_NORM 1u /* q_norm/k_norm are None: crates/ops/src/attention.rs:57-76 */
 #define EMA_PRE_NO_ROPE 2u /* NoPE layer (use_rope=false): crates/ops/src/rope.rs:38-40  */
@@ -106,7 +118,7 @@ typedef struct ema_kvcache_desc {
   int64_t stride_head;  /* in elements */
   int64_t stride_pos;   /* in elements, >= head_dim */
   int32_t dtype;        /* EMA_DTYPE_BF16 or EMA_DTYPE_FP8_E4M3 */
-  int32_t reserved;
+  int32_t flags;        /* 0 or EMA_KV_ROTATING (set by the caller after init/alloc) */
   void* k_exp;          /* EMA_DTYPE_FP8_E4M3: block exponents of K and V (else NULL) */
   void* v_exp;
 } ema_kvcache_desc;

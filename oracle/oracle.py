@@ -283,3 +283,28 @@ def gdn_scan(q, k, v, g, beta, state):
                        _p(y, _f64p), B, T, Hk, Hv, Dk, Dv)
     return y, S
 
+
+
+def rotating_append(kept, n_new, window):
+    """One RotatingCache::append (crates/kvcache/src/rotating.rs:56-97) on the list of
+    absolute positions the cache holds, in its order: the first call with n_new <= window
+    stores the chunk as is (:60-67); otherwise the chunk is concatenated (:70-77) and, past
+    the window, only the last `window` positions are kept (:81-92). Returns the new list."""
+    total = kept[-1] + 1 if kept else 0
+    new = list(range(total, total + n_new))
+    if not kept and n_new <= window:
+        return new
+    full = list(kept) + new
+    return full[-window:] if len(full) > window else full
+
+
+def rotating_window(total, window):
+    """Positions a rotating cache of `window` rows holds after `total` tokens: [lo, total)."""
+    return max(0, total - window), total
+
+
+def ring_rows(total, window):
+    """Ring layout of the rotating cache here (EMA_KV_ROTATING): row r holds the position
+    p in rotating_window(total, window) with p % window == r; returns {row: position}."""
+    lo, hi = rotating_window(total, window)
+    return {p % window: p for p in range(lo, hi)}

@@ -8,6 +8,7 @@
 // usage: test_host_api cpu|gpu   (exit status 0 = all passed)
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -195,6 +196,97 @@ static void gpu_tests() {
     // reset keeps the buffers, rewinds the length (crates/serve/src/engine_ext.rs:10-36)
     c.reset();
     EXPECT(c.is_empty() && c.memory_bytes() == (size_t)2 * Hkv * cap * D * 2);
+    (void)hipFree(dqw);
+    (void)hipFree(dkw);
+  });
+  // ---- RotatingCache (crates/kvcache/src/rotating.rs; tests in crates/kvcache/tests/rotating.rs)
+  run("rotating_cache_new_is_empty", [&] {
+    RotatingCache c(128, 2, 64);
+    EXPECT(c.len() == 0 && c.is_empty());
+    EXPECT(c.memory_bytes() == (size_t)2 * 2 * 128 * 64 * 2);
+    EXPECT(error_of([&] { c.get(Ctx{}); }).find("empty") != std::string::npos);
+    c.reset();
+    EXPECT(c.is_empty());
+  });
+  run("rotating_cache_keeps_the_last_window_in_order", [&] {
+    const int W = 8, H = 2;
+    RotatingCache c(W, H, D);
+    std::vector<std::vector<uint16_t>> seq;  // token t of the whole sequence: [H][D]
+    auto push = [&](int T, uint64_t seed) {
+      auto k = normal((size_t)H * T * D, seed);
+      void* dk = upload(k);
+      c.append(Ctx{}, Array{dk, {1, H, T, D}, {}}, Array{dk, {1, H, T, D}, {}});
+      (void)hipDeviceSynchronize();
+      for (int t = 0; t < T; ++t) {
+        std::vector<uint16_t> tok((size_t)H * D);
+        for (int h = 0; h < H; ++h)
+          for (int d = 0; d < D; ++d) tok[(size_t)h * D + d] = k[((size_t)h * T + t) * D + d];
+        seq.push_back(tok);
+      }
+      (void)hipFree(dk);
+    };
+    for (auto [T, seed] : std::vector<std::pair<int, uint64_t>>{{5, 1}, {6, 2}, {1, 3}, {20, 4}, {3, 5}}) {
+      push(T, seed);
+      const size_t n = std::min<size_t>(seq.size(), W);
+      EXPECT(c.len() == n);
+      auto kv = c.get(Ctx{});
+      (void)hipDeviceSynchronize();
+      EXPECT(kv.first.shape[2] == (int64_t)n);
+      const int64_t sh = kv.first.strides.empty() ? (int64_t)n * D : kv.first.strides[1];
+      const int64_t sp = kv.first.strides.empty() ? D : kv.first.strides[2];
+      auto all = download(kv.first.data, (size_t)H * (size_t)sh);
+      bool ok = true;
+      for (size_t i = 0; i < n; ++i)  // i-th held token = position seq.size() - n + i
+        for (int h = 0; h < H; ++h)
+          for (int d = 0; d < D; ++d)
+            ok &= all[(size_t)h * sh + i * sp + d] == seq[seq.size() - n + i][(size_t)h * D + d];
+      EXPECT(ok);
+    }
+  });
+  run("sliding_window_attention_matches_oracle", [&] {
+    const int W = 48, cap_ref = 256;
+    RotatingCache c(W, Hkv, D);
+    GqaConfig cfg{Hq, Hkv, D, 1e6f, 1e-6f, true};
+    SlidingWindowConfig sw{cfg, (size_t)W};
+    const int F = (Hq + 2 * Hkv) * D;
+    auto qw = normal(D, 20, 1.f, 0.02f), kw = normal(D, 21, 1.f, 0.02f);
+    void *dqw = upload(qw), *dkw = upload(kw);
+    GqaWeights w{Array{dqw, {D}, {}}, Array{dkw, {D}, {}}};
+    std::vector<uint16_t> kref((size_t)Hkv * cap_ref * D, 0), vref((size_t)Hkv * cap_ref * D, 0);
+    const float scale = 1.0f / std::sqrt((float)D);
+    // prefill 40, 20 decode steps (the ring wraps), then a 30-token chunk that wraps within it
+    std::vector<std::pair<int, int>> calls{{0, 40}};
+    for (int i = 0; i < 20; ++i) calls.push_back({40 + i, 1});
+    calls.push_back({60, 30});
+    int step = 0;
+    for (auto [off, t] : calls) {
+      auto qkv = normal((size_t)t * F, 300 + step);
+      void* dqkv = upload(qkv);
+      Array out = sliding_window_attention(Ctx{}, Array{dqkv, {1, t, F}, {}}, w, c, sw, off);
+      (void)hipDeviceSynchronize();
+      EXPECT(c.len() == (size_t)std::min(off + t, W) && c.total_len() == off + t);
+      std::vector<uint16_t> q((size_t)Hq * t * D), ref((size_t)t * Hq * D);
+      int32_t o32 = off, len = off + t, begin = std::max(0, off + t - W);
+      EXPECT(ora_pre_attention(qkv.data(), qw.data(), kw.data(), 1e-6f, 1e6f, &o32, 1, t, Hq, Hkv, D, 0, q.data(),
+                               kref.data(), vref.data(), cap_ref) == 0);
+      ora_sdpa(q.data(), kref.data(), vref.data(), &len, &begin, 1, Hq, Hkv, t, D, cap_ref, scale, t > 1 ? 1 : 0, 0,
+               ref.data());
+      if (step == 0 || step == 20 || step == 21)
+        expect_close(download(out.data, ref.size()), ref, t > 1 ? "window prefill" : "window decode");
+      else {
+        double mx = 0;
+        auto got = download(out.data, ref.size());
+        for (size_t i = 0; i < got.size(); ++i)
+          mx = std::max(mx, std::fabs((double)ora_bf16_to_f32(got[i]) - (double)ora_bf16_to_f32(ref[i])));
+        EXPECT(mx <= 2e-2);
+      }
+      (void)hipFree(dqkv);
+      ++step;
+    }
+    SlidingWindowConfig bad{cfg, (size_t)W + 1};
+    Array ok{(void*)0x1000, {1, 1, (int64_t)F}, {}};
+    EXPECT(error_of([&] { sliding_window_attention(Ctx{}, ok, w, c, bad, 90); }).find("window_size") !=
+           std::string::npos);
     (void)hipFree(dqw);
     (void)hipFree(dkw);
   });

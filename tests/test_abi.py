@@ -235,3 +235,20 @@ def test_gdn_scan_argument_errors(ema):
     assert call(state=p + 4) == ema.EMA_ERR_INVALID_ARG and "misaligned" in ema.last_error()
     assert call(q=p + 8) == ema.EMA_ERR_INVALID_ARG
     assert call(v=p + 2, dtype=ema.EMA_DTYPE_F32) == ema.EMA_ERR_INVALID_ARG
+
+
+def test_rotating_flag_is_validated(ema):
+    L = ema.lib()
+    rc, d = _desc(ema)
+    d.flags = 2  # unknown flag
+    n = ctypes.c_uint64()
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == ema.EMA_ERR_INVALID_ARG
+    assert "flags" in ema.last_error()
+    d.flags = ema.EMA_KV_ROTATING
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    d8 = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d8), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128) == 0
+    d8.flags = ema.EMA_KV_ROTATING
+    g = 0x40000
+    rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d8), g, 8, 16, 0.088, 1, g, 48, g, 1 << 30)
+    assert rc == ema.EMA_ERR_UNSUPPORTED and "rotating" in ema.last_error()
