@@ -44,7 +44,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk", "fp8", "gdn", "gdn_step"],
+    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk", "fp8", "gdn", "gdn_step",
+                                       "qmm"],
                    default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -349,6 +350,45 @@ def gdn_bytes(B, T, Hk, Hv, Dk, Dv, act=2):
     return 8 * B * Hv * Dv * Dk + act * B * T * (2 * Hk * Dk + 2 * Hv * Dv) + 8 * B * T * Hv
 
 
+def qmm_bytes(M, N, K, gs, bits, act=2):
+    """Packed weights, scales and biases, x in, y out: each read or written once."""
+    return N * K * bits // 8 + 2 * act * N * (K // gs) + act * M * K + act * M * N
+
+
+def bench_qmm(ctx, ema, name, M, N, K, gs=64, bits=4, steps=48, min_set_bytes=300 << 20):
+    """Affine-quantised projection (ema_quantized_matmul) y[M, N] = x W^T, bf16 activations.
+    As in a decode step, each call reads another layer's weights: the calls cycle over
+    enough distinct weight sets (over 300 MB, more than the 256 MB last-level cache)
+    that every call streams its weights from HBM."""
+    torch = ctx.torch
+    per = N * K * bits // 8 + 4 * N * (K // gs)
+    L = max(1, min(steps, -(-min_set_bytes // per)))
+    words = K * bits // 32
+    sets = []
+    for _ in range(L):
+        w = torch.randint(-2**31, 2**31 - 1, (N, words), dtype=torch.int32, device=ctx.dev, generator=ctx.gen)
+        sc = (torch.rand((N, K // gs), device=ctx.dev, generator=ctx.gen) * 0.004 + 0.001).to(torch.bfloat16)
+        bi = (torch.rand((N, K // gs), device=ctx.dev, generator=ctx.gen) * 0.04 - 0.02).to(torch.bfloat16)
+        sets.append((w, sc, bi))
+    x = ctx.randn((M, K))
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=ctx.dev)
+    it = [0]
+
+    def call():
+        w, sc, bi = sets[it[0] % L]
+        it[0] += 1
+        ema.quantized_matmul(x, w, sc, bi, group_size=gs, bits=bits, out=y)
+
+    ms = time_calls(torch, call, steps, 2 * L)
+    by = qmm_bytes(M, N, K, gs, bits)
+    gbs = by / (ms * 1e-3) / 1e9
+    tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    log(f"[bench] {name}: {ms*1e3:.2f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM), {tf:.1f} TFLOP/s "
+        f"({L} weight sets)")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by,
+            "tflops": tf, "weight_sets": L}
+
+
 def bench_gdn(ctx, ema, name, B, T, Hk, Hv, Dk, Dv, steps=20):
     """Gated DeltaNet scan (ema_gdn_scan), bf16 activations, f32 state updated in place
     (bounded: unit keys, g and beta in (0, 1))."""
@@ -449,6 +489,15 @@ def main():
     if args.only in ("all", "gdn"):
         secondary.append(bench_gdn(ctx, ema, "gdn_scan_T2048_B1_16k32v_dk128_dv128", 1, 2048, 16, 32, 128, 128,
                                    steps=5))
+    if args.only in ("all", "qmm"):
+        # affine-quantised projections around the attention path (MLX 4-bit, group 64):
+        # Qwen3-8B q|k|v (4096 -> 6144) and o_proj (4096 -> 4096) per decode step
+        secondary.append(bench_qmm(ctx, ema, "qmatmul_qkv_M32_K4096_N6144_4bit_g64", 32, 6144, 4096))
+        secondary.append(bench_qmm(ctx, ema, "qmatmul_qkv_M1_K4096_N6144_4bit_g64", 1, 6144, 4096))
+        secondary.append(bench_qmm(ctx, ema, "qmatmul_o_proj_M32_K4096_N4096_4bit_g64", 32, 4096, 4096))
+        secondary.append(bench_qmm(ctx, ema, "qmatmul_qkv_M32_K4096_N6144_8bit_g64", 32, 6144, 4096, bits=8))
+        secondary.append(bench_qmm(ctx, ema, "qmatmul_qkv_prefill_M2048_K2048_N4096_4bit_g64", 2048, 4096, 2048,
+                                   steps=8))
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle f32 SDPA on the host)")

@@ -385,3 +385,30 @@ int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, const vo
     return set_error(EMA_ERR_SHAPE, "%s: tensors too large", op);
   return launch_gdn_scan((hipStream_t)stream, q, k, v, g, beta, state, y, batch, n_tokens, hk, hv, dk, dv, dtype);
 }
+
+int32_t ema_quantized_matmul(ema_stream_t stream, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                             const void* biases, void* y, int64_t ldy, int32_t M, int32_t N, int32_t K,
+                             int32_t group_size, int32_t bits, int32_t dtype) {
+  const char* op = "ema_quantized_matmul";
+  if (M < 0 || N <= 0 || K <= 0)
+    return set_error(EMA_ERR_SHAPE, "%s: need M >= 0 and positive N, K (M=%d N=%d K=%d)", op, M, N, K);
+  if (M == 0) return EMA_OK;
+  if (!x || !w || !scales || !biases || !y) return set_error(EMA_ERR_INVALID_ARG, "%s: null x/w/scales/biases/y", op);
+  if (dtype != EMA_DTYPE_BF16 && dtype != EMA_DTYPE_F16)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: dtype %d is not bf16 or f16", op, dtype);
+  if (bits != 4 && bits != 8) return set_error(EMA_ERR_UNSUPPORTED, "%s: bits %d not supported (4, 8)", op, bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: group_size %d not supported (32, 64, 128)", op, group_size);
+  if (K % group_size) return set_error(EMA_ERR_SHAPE, "%s: K %d is not a multiple of group_size %d", op, K, group_size);
+  if (ldx < K || ldy < N) return set_error(EMA_ERR_SHAPE, "%s: ldx %lld < K %d or ldy %lld < N %d", op, (long long)ldx, K,
+                                           (long long)ldy, N);
+  if (!aligned16(x) || !aligned16(w) || (ldx & 7) || ((uintptr_t)scales | (uintptr_t)biases | (uintptr_t)y) & 1u)
+    return set_error(EMA_ERR_INVALID_ARG,
+                     "%s: misaligned buffer (x and w 16-byte aligned, ldx a multiple of 8, scales/biases/y 2-byte)",
+                     op);
+  // 32-bit buffer offsets inside one 32 x 32 tile
+  if (K > (1 << 20) || 31 * ldx + K >= ((int64_t)1 << 30) ||
+      ((int64_t)(N + 31) / 32) * ((M + 31) / 32) >= ((int64_t)1 << 31))
+    return set_error(EMA_ERR_SHAPE, "%s: tensors too large (K <= 2^20, 31 * ldx + K < 2^30)", op);
+  return launch_qmatmul((hipStream_t)stream, x, ldx, w, scales, biases, y, ldy, M, N, K, group_size, bits, dtype);
+}

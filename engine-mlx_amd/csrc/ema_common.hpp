@@ -109,6 +109,10 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
 int32_t launch_gdn_scan(hipStream_t s, const void* q, const void* k, const void* v, const float* g,
                         const float* beta, float* state, void* y, int B, int T, int hk, int hv, int dk,
                         int dv, int dtype);
+// Affine-quantised matmul y = x W^T over MLX-packed W (arguments validated by the caller).
+int32_t launch_qmatmul(hipStream_t s, const void* x, int64_t ldx, const void* w, const void* scales,
+                       const void* biases, void* y, int64_t ldy, int M, int N, int K, int gs, int bits,
+                       int dtype);
 // Decode the fp8 rows a prefill call attends to into bf16 [B, Hkv, R, D] K then V at ws.
 int32_t launch_fp8_to_bf16(hipStream_t s, const ema_kvcache_desc& c, const int32_t* q_off, int T,
                            uint32_t flags, int R, void* ws);

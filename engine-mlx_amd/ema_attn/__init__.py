@@ -41,7 +41,7 @@ EXPORTED = (
     "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
     "ema_decode_attention", "ema_decode_step", "ema_prefill_attention", "ema_prefill_workspace_size",
-    "ema_prefill_attention_ws", "ema_gdn_scan",
+    "ema_prefill_attention_ws", "ema_gdn_scan", "ema_quantized_matmul",
 )
 
 
@@ -74,6 +74,7 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(f"ema_attn HIP library not built: {LIB_PATH} (run __graft_entry__.build())")
         L = ctypes.CDLL(LIB_PATH)
         vp, i32, u32, f32, u64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float, ctypes.c_uint64
+        i64 = ctypes.c_int64
         D = ctypes.POINTER(KvCacheDesc)
         sig = {
             "ema_last_error": (ctypes.c_char_p, []),
@@ -92,6 +93,7 @@ def lib() -> ctypes.CDLL:
             "ema_prefill_workspace_size": (i32, [D, i32, ctypes.POINTER(u64)]),
             "ema_prefill_attention_ws": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp, i32, vp, u64]),
             "ema_gdn_scan": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32]),
+            "ema_quantized_matmul": (i32, [vp, vp, i64, vp, vp, vp, vp, i64, i32, i32, i32, i32, i32, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -315,3 +317,32 @@ def gdn_scan(q, k, v, g, beta, state, y=None, stream=None):
     _check(lib().ema_gdn_scan(_stream(stream), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state),
                               _ptr(y), B, T, Hk, Hv, Dk, Dv, dtypes[q.dtype]), "ema_gdn_scan")
     return y
+
+
+def quantized_matmul(x, w, scales, biases, group_size=64, bits=4, out=None, stream=None):
+    """MLX quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits, "affine")
+    (ema_quantized_matmul; the reference's qmatmul, crates/ops/src/quant.rs:57-76): x [..., K]
+    bf16 or f16 with a contiguous last axis; w [N, K*bits/32] int32/uint32 words of MLX's
+    packing; scales, biases [N, K/group_size] in x's dtype. Returns y [..., N] in x's dtype.
+    `out` may be a 2-D view whose rows are wider than N (e.g. the q, k or v columns of a
+    q|k|v buffer)."""
+    import torch
+
+    dtypes = {torch.bfloat16: EMA_DTYPE_BF16, torch.float16: EMA_DTYPE_F16}
+    if x.dtype not in dtypes:
+        raise EmaError(EMA_ERR_INVALID_ARG, "ema_quantized_matmul", f"unsupported activation dtype {x.dtype}")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M, N = x2.shape[0], w.shape[0]
+    if w.shape[1] * 32 // bits != K:
+        raise EmaError(EMA_ERR_SHAPE, "ema_quantized_matmul", f"w {tuple(w.shape)} does not pack K={K} at {bits} bits")
+    if out is None:
+        y2 = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    else:
+        y2 = out
+        if y2.dim() != 2 or y2.shape[0] != M or y2.shape[1] != N or y2.stride(1) != 1:
+            raise EmaError(EMA_ERR_SHAPE, "ema_quantized_matmul", "out must be a [M, N] view with unit column stride")
+    _check(lib().ema_quantized_matmul(_stream(stream), _ptr(x2), x2.stride(0), _ptr(w), _ptr(scales), _ptr(biases),
+                                      _ptr(y2), y2.stride(0), M, N, K, group_size, bits, dtypes[x.dtype]),
+           "ema_quantized_matmul")
+    return y2.reshape(x.shape[:-1] + (N,)) if out is None else y2

@@ -23,6 +23,10 @@
  *   gdn_step / gdn_step_metal and the per-token scan of gdn_forward
  *              crates/ops/src/gdn.rs:83-150, gdn_metal.rs:56-88, gdn_forward.rs:173-192
  *                                                               ema_gdn_scan
+ *   MlxCtx::quantized_matmul (affine, transpose=true)
+ *              crates/mlx-ffi/src/ops/real/transform.rs:77-88, via qmatmul
+ *              (crates/ops/src/quant.rs:57-76) and run_qkv / o_proj
+ *              (crates/serve/src/forward/projection.rs:105-152)  ema_quantized_matmul
  *
  * Conventions
  *   - Every entry point returns int32_t: EMA_OK (0) or a negative EMA_ERR_*.
@@ -255,6 +259,26 @@ EMA_API int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, 
                              const float* g, const float* beta, float* state, void* y,
                              int32_t batch, int32_t n_tokens, int32_t hk, int32_t hv, int32_t dk,
                              int32_t dv, int32_t dtype);
+
+/* y = x W^T over an affine-quantised W in MLX's packing: MLX quantized_matmul(x, w,
+ * scales, biases, transpose=true, group_size, bits, "affine"), the call behind the
+ * reference's qmatmul (crates/ops/src/quant.rs:57-76) for the q|k|v and o projections:
+ *   y[m, n] = sum_k x[m, k] * (scales[n, k / group_size] * q[n, k] + biases[n, k / group_size])
+ *   x:      [M, ldx] in `dtype` (row m's first K values are used)
+ *   w:      [N, K * bits / 32] uint32; field k of row n is bits (k % (32 / bits)) * bits ..
+ *           + bits - 1 of word k / (32 / bits) (lowest bits first)
+ *   scales, biases: [N, K / group_size] in `dtype`
+ *   y:      [M, ldy] in `dtype`; columns [0, N) of each row written, the rest untouched
+ *           (ldy > N writes one piece of a wider row: the separate q, k and v projections
+ *           of run_qkv land in one q|k|v row without a concatenation)
+ * Products are exact and accumulate in f32; y is rounded once (RNE) to `dtype`.
+ * dtype: EMA_DTYPE_BF16 or EMA_DTYPE_F16. bits: 4 or 8; group_size: 32, 64 or 128; K a
+ * multiple of group_size; ldx >= K, ldy >= N. x and w 16-byte aligned, ldx a multiple
+ * of 8; scales, biases and y element-aligned. M = 0 is a no-op. */
+EMA_API int32_t ema_quantized_matmul(ema_stream_t stream, const void* x, int64_t ldx, const uint32_t* w,
+                                     const void* scales, const void* biases, void* y, int64_t ldy,
+                                     int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t bits,
+                                     int32_t dtype);
 
 #ifdef __cplusplus
 }

@@ -508,3 +508,39 @@ void ora_gdn_scan(const float* q, const float* k, const float* v, const float* g
       }
 }
 
+
+/* ------------------------------------------------------------ affine quantized matmul */
+
+static inline uint32_t qfield(const uint32_t* row, int k, int bits) {
+  const int per = 32 / bits;
+  return (row[k / per] >> ((k % per) * bits)) & ((1u << bits) - 1u);
+}
+
+void ora_dequantize(const uint32_t* wq, const float* scales, const float* biases, int N, int K,
+                    int gs, int bits, double* w) {
+  const int G = K / gs;
+  const int64_t words = (int64_t)K * bits / 32;
+  for (int n = 0; n < N; ++n)
+    for (int k = 0; k < K; ++k)
+      w[(int64_t)n * K + k] = (double)scales[(int64_t)n * G + k / gs] * qfield(wq + n * words, k, bits) +
+                              (double)biases[(int64_t)n * G + k / gs];
+}
+
+void ora_qmatmul(const float* x, const uint32_t* wq, const float* scales, const float* biases,
+                 int M, int N, int K, int gs, int bits, double* y) {
+  const int G = K / gs;
+  const int64_t words = (int64_t)K * bits / 32;
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n) {
+    const uint32_t* row = wq + n * words;
+    for (int m = 0; m < M; ++m) {
+      const float* xm = x + (int64_t)m * K;
+      double acc = 0.0;
+      for (int g = 0; g < G; ++g) {
+        const double s = scales[(int64_t)n * G + g], b = biases[(int64_t)n * G + g];
+        for (int k = g * gs; k < (g + 1) * gs; ++k) acc += (double)xm[k] * (s * qfield(row, k, bits) + b);
+      }
+      y[(int64_t)m * N + n] = acc;
+    }
+  }
+}

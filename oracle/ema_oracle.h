@@ -18,6 +18,8 @@
  *                                 crates/serve/src/forward_qwen3.rs:52-152
  *   - FP8 KV format               crates/ops/src/fp8.rs, crates/kvcache/src/fp8.rs
  *   - Gated DeltaNet step/scan    crates/ops/src/gdn.rs:83-150, gdn_forward.rs:173-192
+ *   - affine quantized_matmul     crates/mlx-ffi/src/ops/real/transform.rs:77-88 via
+ *                                 crates/ops/src/quant.rs:57-76 (transpose = true)
  *
  * bf16 tensors are passed as uint16_t bit patterns (IEEE bfloat16, RNE).
  *
@@ -147,6 +149,22 @@ void ora_fp8_dequantize_rows(const uint8_t* codes, const int8_t* exps, int64_t r
  *   state [B, hv, dv, dk] double, updated in place; y [B, T, hv, dv] double. */
 void ora_gdn_scan(const float* q, const float* k, const float* v, const float* g, const float* beta,
                   double* state, double* y, int B, int T, int hk, int hv, int dk, int dv);
+
+/* MLX affine quantized_matmul(x, w, scales, biases, transpose=true, group_size, bits)
+ * (transform.rs:77-88, called by qmatmul, quant.rs:57-76, and the fused / separate
+ * projections, crates/serve/src/forward/projection.rs:105-152), in double:
+ *   y[m, n] = sum_k x[m, k] * (scales[n, k / gs] * q[n, k] + biases[n, k / gs])
+ * with q[n, k] the bits-wide field (k % (32 / bits)) * bits .. +bits of word
+ * wq[n, k / (32 / bits)] (lowest bits first: MLX's affine packing for widths that divide
+ * 32). Weight row n is output column n (transpose = true: y = x W^T, W [N, K]).
+ *   x [M, K] f32 (the bf16/f16 activations as f32); wq [N, K * bits / 32] uint32;
+ *   scales, biases [N, K / gs] f32; y [M, N] double. bits in {2, 4, 8}; K % gs == 0. */
+void ora_qmatmul(const float* x, const uint32_t* wq, const float* scales, const float* biases,
+                 int M, int N, int K, int gs, int bits, double* y);
+/* The dequantised weight W [N, K] = scales * q + biases (MLX dequantize, affine mode,
+ * transform.rs:45-58), in double. */
+void ora_dequantize(const uint32_t* wq, const float* scales, const float* biases, int N, int K,
+                    int gs, int bits, double* w);
 
 #ifdef __cplusplus
 }

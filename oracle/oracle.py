@@ -25,6 +25,7 @@ _i32p = ctypes.POINTER(ctypes.c_int32)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
 _i8p = ctypes.POINTER(ctypes.c_int8)
 
 
@@ -79,6 +80,8 @@ def lib():
         L.ora_fp8_quantize_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _u8p, _i8p]
         L.ora_fp8_dequantize_rows.argtypes = [_u8p, _i8p, ctypes.c_int64, ctypes.c_int, _f32p]
         L.ora_gdn_scan.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f64p, _f64p] + [ctypes.c_int] * 6
+        L.ora_qmatmul.argtypes = [_f32p, _u32p, _f32p, _f32p] + [ctypes.c_int] * 5 + [_f64p]
+        L.ora_dequantize.argtypes = [_u32p, _f32p, _f32p] + [ctypes.c_int] * 4 + [_f64p]
         _lib = L
     return _lib
 
@@ -283,6 +286,78 @@ def gdn_scan(q, k, v, g, beta, state):
                        _p(y, _f64p), B, T, Hk, Hv, Dk, Dv)
     return y, S
 
+
+
+def pack_bits(q, bits: int) -> np.ndarray:
+    """Packs integer fields q [..., K] (0 <= q < 2**bits) into uint32 words [..., K*bits/32],
+    field k at bits (k % (32/bits))*bits of word k // (32/bits), lowest bits first (MLX's
+    affine packing for widths that divide 32)."""
+    q = np.asarray(q, dtype=np.uint32)
+    per = 32 // bits
+    assert 32 % bits == 0 and q.shape[-1] % per == 0 and int(q.max(initial=0)) < (1 << bits)
+    f = q.reshape(q.shape[:-1] + (q.shape[-1] // per, per))
+    shifts = (np.arange(per, dtype=np.uint32) * bits).astype(np.uint32)
+    return np.bitwise_or.reduce(f << shifts, axis=-1).astype(np.uint32)
+
+
+def unpack_bits(wq, bits: int) -> np.ndarray:
+    """Inverse of pack_bits: uint32 words [..., W] -> fields [..., W*32/bits]."""
+    wq = np.asarray(wq, dtype=np.uint32)
+    per = 32 // bits
+    shifts = (np.arange(per, dtype=np.uint32) * bits).astype(np.uint32)
+    f = (wq[..., None] >> shifts) & np.uint32((1 << bits) - 1)
+    return f.reshape(wq.shape[:-1] + (wq.shape[-1] * per,))
+
+
+def minmax_quantize(w, gs: int, bits: int):
+    """Test-data generator: min-max affine quantisation of w [N, K] in groups of gs along K
+    (scale = (max - min) / (2**bits - 1), bias = min, q = round((w - bias) / scale)), with
+    scale and bias rounded to bf16 first. Returns (wq uint32, scales bf16 bits, biases bf16
+    bits). Not MLX's quantiser (which also moves the edge onto the grid); the kernels here
+    consume stored (wq, scales, biases) and never quantise."""
+    w = np.asarray(w, dtype=np.float32)
+    N, K = w.shape
+    g = w.reshape(N, K // gs, gs)
+    lo, hi = g.min(-1), g.max(-1)
+    s = bf16_from_f32(np.maximum((hi - lo) / ((1 << bits) - 1), 1e-7).astype(np.float32))
+    b = bf16_from_f32(lo)
+    sf, bf = f32_from_bf16(s), f32_from_bf16(b)
+    q = np.clip(np.rint((g - bf[..., None]) / sf[..., None]), 0, (1 << bits) - 1).astype(np.uint32)
+    return pack_bits(q.reshape(N, K), bits), s, b
+
+
+def dequantize(wq, scales, biases, gs: int, bits: int) -> np.ndarray:
+    """W [N, K] = scales * q + biases in float64 (MLX affine dequantize, transform.rs:45-58);
+    scales and biases as f32 values [N, K/gs]."""
+    wq = _c(np.asarray(wq), np.uint32)
+    s = _c(np.asarray(scales, dtype=np.float32), np.float32)
+    b = _c(np.asarray(biases, dtype=np.float32), np.float32)
+    N = wq.shape[0]
+    K = wq.shape[1] * 32 // bits
+    assert s.shape == (N, K // gs) == b.shape
+    out = np.empty((N, K), dtype=np.float64)
+    lib().ora_dequantize(_p(wq, _u32p), _p(s, _f32p), _p(b, _f32p), N, K, gs, bits, _p(out, _f64p))
+    return out
+
+
+def qmatmul(x, wq, scales, biases, gs: int, bits: int) -> np.ndarray:
+    """MLX quantized_matmul(x, w, scales, biases, transpose=true, gs, bits, "affine")
+    (transform.rs:77-88; qmatmul, crates/ops/src/quant.rs:57-76) in float64: x [..., K]
+    (activation values as f32), wq [N, K*bits/32], scales/biases [N, K/gs] (f32 values).
+    Returns y [..., N]."""
+    x = np.asarray(x, dtype=np.float32)
+    lead = x.shape[:-1]
+    K = x.shape[-1]
+    x2 = _c(x.reshape(-1, K), np.float32)
+    wq = _c(np.asarray(wq), np.uint32)
+    s = _c(np.asarray(scales, dtype=np.float32), np.float32)
+    b = _c(np.asarray(biases, dtype=np.float32), np.float32)
+    N = wq.shape[0]
+    assert wq.shape[1] * 32 // bits == K and K % gs == 0 and s.shape == (N, K // gs) == b.shape
+    y = np.empty((x2.shape[0], N), dtype=np.float64)
+    lib().ora_qmatmul(_p(x2, _f32p), _p(wq, _u32p), _p(s, _f32p), _p(b, _f32p), x2.shape[0], N, K, gs, bits,
+                      _p(y, _f64p))
+    return y.reshape(lead + (N,))
 
 
 def rotating_append(kept, n_new, window):

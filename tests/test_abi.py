@@ -252,3 +252,27 @@ def test_rotating_flag_is_validated(ema):
     g = 0x40000
     rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d8), g, 8, 16, 0.088, 1, g, 48, g, 1 << 30)
     assert rc == ema.EMA_ERR_UNSUPPORTED and "rotating" in ema.last_error()
+
+
+def test_quantized_matmul_argument_errors(ema):
+    L = ema.lib()
+    p = 0x40000  # 16-byte aligned stand-in; every failing call below stops before any HIP call
+
+    def call(x=p, ldx=4096, w=p, s=p, b=p, y=p, ldy=6144, M=4, N=6144, K=4096, gs=64, bits=4,
+             dtype=ema.EMA_DTYPE_BF16):
+        return L.ema_quantized_matmul(None, x, ldx, w, s, b, y, ldy, M, N, K, gs, bits, dtype)
+
+    assert call(M=0, x=None, w=None) == ema.EMA_OK  # empty batch: no-op
+    assert call(w=None) == ema.EMA_ERR_INVALID_ARG and "null" in ema.last_error()
+    assert call(M=-1) == ema.EMA_ERR_SHAPE
+    assert call(N=0) == ema.EMA_ERR_SHAPE
+    assert call(dtype=ema.EMA_DTYPE_F32) == ema.EMA_ERR_INVALID_ARG
+    assert call(bits=3) == ema.EMA_ERR_UNSUPPORTED and "bits" in ema.last_error()
+    assert call(gs=16) == ema.EMA_ERR_UNSUPPORTED and "group_size" in ema.last_error()
+    assert call(K=4000) == ema.EMA_ERR_SHAPE and "multiple" in ema.last_error()
+    assert call(ldx=2048) == ema.EMA_ERR_SHAPE
+    assert call(ldy=100) == ema.EMA_ERR_SHAPE
+    assert call(x=p + 8) == ema.EMA_ERR_INVALID_ARG and "misaligned" in ema.last_error()
+    assert call(ldx=4100) == ema.EMA_ERR_INVALID_ARG
+    assert call(s=p + 1) == ema.EMA_ERR_INVALID_ARG
+    assert call(K=1 << 21, ldx=1 << 21) == ema.EMA_ERR_SHAPE and "too large" in ema.last_error()

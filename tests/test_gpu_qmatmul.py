@@ -1,0 +1,156 @@
+"""GPU parity of the affine quantized matmul (ema_quantized_matmul, MLX quantized_matmul
+with transpose=true as called by crates/ops/src/quant.rs:57-76) against the oracle's f64
+restatement (oracle.qmatmul), through the C ABI.
+
+Bars. The kernel multiplies exactly and accumulates in f32, so every output is within
+one rounding of the exact sum: |y - ref| <= 2^-8 |ref| (bf16; 2^-10 for f16) plus
+4e-5 * sum_k |x_k w_k| for the f32 accumulation; at the Qwen3-8B decode shape also the
+bf16 bar of the other parity tests (max-abs 2e-2, mean-abs 2e-3). Separate q, k and v
+calls into one q|k|v row (ldy > N) equal the fused call bit for bit, the property the
+reference checks at 1e-3 (crates/serve/tests/forward_separate.rs:80-91).
+"""
+import numpy as np
+import pytest
+
+from gpu_util import MAX_ABS, MEAN_ABS, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ema():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import ema_attn
+
+    ema_attn.lib()
+    return ema_attn
+
+
+def make(ora, seed, M, N, K, gs, bits, dtype="bf16", wstd=0.02):
+    """Host inputs: x [M, K] (activation values as f32), packed w, scales/biases as f32
+    values of the activation type, and the matching device tensors."""
+    import torch
+
+    td = torch.bfloat16 if dtype == "bf16" else torch.float16
+    rng = np.random.default_rng(seed)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(td)
+    w = (rng.standard_normal((N, K)) * wstd).astype(np.float32)
+    wq, sb, bb = ora.minmax_quantize(w, gs, bits)
+    s = torch.from_numpy(ora.f32_from_bf16(sb)).to(td)  # bf16 values, exact in f16 at this range
+    b = torch.from_numpy(ora.f32_from_bf16(bb)).to(td)
+    hx, hs, hb = x.float().numpy(), s.float().numpy(), b.float().numpy()
+    d = (x.cuda(), torch.from_numpy(wq.view(np.int32)).cuda(), s.cuda(), b.cuda())
+    return d, (hx, wq, hs, hb)
+
+
+def check(ora, y, h, gs, bits, what, dtype="bf16", bar=False):
+    hx, wq, hs, hb = h
+    ref = ora.qmatmul(hx, wq, hs, hb, gs, bits)
+    W = ora.dequantize(wq, hs, hb, gs, bits)
+    mag = np.abs(hx).astype(np.float64) @ np.abs(W).T
+    got = y.float().cpu().numpy().astype(np.float64)
+    assert got.shape == ref.shape and np.all(np.isfinite(got)), what
+    rel = 2.0**-8 if dtype == "bf16" else 2.0**-10
+    err = np.abs(got - ref)
+    over = err - (rel * np.abs(ref) + 4e-5 * mag)
+    say(f"  {what}: max_abs={err.max():.3e} mean_abs={err.mean():.3e} worst margin={over.max():.3e} "
+        f"(|y| max {np.abs(ref).max():.2f})")
+    assert np.all(over <= 0), f"{what}: {int((over > 0).sum())} outputs beyond one rounding"
+    if bar:
+        assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, what
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_qmatmul_matches_oracle(ema, ora, dtype, bits, gs):
+    for M, N, K in ((1, 96, 512), (5, 100, 1024), (16, 48, 256), (17, 64, 768), (32, 80, 2048)):
+        say(f"qmatmul {dtype} bits={bits} gs={gs} M={M} N={N} K={K}")
+        d, h = make(ora, M * 7 + N + K + gs + bits, M, N, K, gs, bits, dtype)
+        y = ema.quantized_matmul(*d, group_size=gs, bits=bits)
+        check(ora, y, h, gs, bits, f"M={M} N={N} K={K}", dtype)
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_qmatmul_qwen3_8b_qkv_decode_shape(ema, ora, M):
+    # x [M, 4096] -> q|k|v [M, 6144], 4-bit, group 64 (MLX's default quantisation); M <= 8
+    # runs the LDS-staged kernel, M = 32 the streaming one
+    N, K, gs, bits = 6144, 4096, 64, 4
+    say(f"qmatmul Qwen3-8B qkv M={M} N={N} K={K}")
+    d, h = make(ora, 1, M, N, K, gs, bits)
+    y = ema.quantized_matmul(*d, group_size=gs, bits=bits)
+    check(ora, y, h, gs, bits, "8B qkv", bar=True)
+
+
+@pytest.mark.parametrize("M", [64, 300])
+def test_qmatmul_prefill_rows(ema, ora, M):
+    # several 32-row tiles of x per weight tile (grid remapped per XCD when divisible)
+    N, K, gs, bits = 256, 1024, 64, 4
+    say(f"qmatmul prefill rows M={M}")
+    d, h = make(ora, M, M, N, K, gs, bits)
+    y = ema.quantized_matmul(*d, group_size=gs, bits=bits)
+    check(ora, y, h, gs, bits, f"M={M}")
+
+
+def test_qmatmul_separate_pieces_equal_fused(ema, ora):
+    # run_qkv's separate branch (projection.rs:119-125) writing its three pieces straight
+    # into one q|k|v row (ldy = 6144) equals the fused call; columns of other pieces untouched
+    import torch
+
+    M, K, gs, bits = 8, 4096, 64, 4
+    sizes = (4096, 1024, 1024)
+    say(f"qmatmul separate vs fused M={M} pieces={sizes}")
+    parts = [make(ora, 50 + i, M, n, K, gs, bits)[0] for i, n in enumerate(sizes)]
+    x = parts[0][0]
+    fused = ema.quantized_matmul(x, torch.cat([p[1] for p in parts]), torch.cat([p[2] for p in parts]),
+                                 torch.cat([p[3] for p in parts]), group_size=gs, bits=bits)
+    qkv = torch.full((M, sum(sizes)), 7.0, dtype=torch.bfloat16, device="cuda")
+    col = 0
+    for (_, w, s, b), n in zip(parts, sizes):
+        if col == 0:
+            assert torch.all(qkv[:, n:] == 7.0)
+        ema.quantized_matmul(x, w, s, b, group_size=gs, bits=bits, out=qkv[:, col:col + n])
+        if col + n < qkv.shape[1]:
+            assert torch.all(qkv[:, col + n:] == 7.0), "wrote past its piece"
+        col += n
+    torch.cuda.synchronize()
+    assert torch.equal(qkv.view(torch.int16), fused.view(torch.int16))
+
+
+def test_qmatmul_strided_rows_and_determinism(ema, ora):
+    import torch
+
+    M, N, K, gs, bits = 9, 128, 1024, 64, 8
+    say("qmatmul strided x rows, repeat determinism")
+    d, h = make(ora, 3, M, N, K, gs, bits)
+    x, w, s, b = d
+    wide = torch.zeros((M, K + 64), dtype=x.dtype, device="cuda")
+    wide[:, :K] = x
+    y1 = ema.quantized_matmul(wide[:, :K], w, s, b, group_size=gs, bits=bits)
+    y2 = ema.quantized_matmul(x, w, s, b, group_size=gs, bits=bits)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    check(ora, y1, h, gs, bits, "strided")
+
+
+def test_qmatmul_extreme_fields_and_groups(ema, ora):
+    # all-zero and all-max fields, zero and negative scales, large biases: the C + q
+    # offset and the bias term cancel exactly
+    import torch
+
+    M, N, K, gs = 4, 32, 512, 64
+    for bits in (4, 8):
+        say(f"qmatmul extreme fields bits={bits}")
+        rng = np.random.default_rng(bits)
+        q = np.where(rng.random((N, K)) < 0.5, 0, (1 << bits) - 1).astype(np.uint32)
+        wq = ora.pack_bits(q, bits)
+        s = rng.choice([0.0, -0.015625, 0.03125, 1.0], (N, K // gs)).astype(np.float32)
+        b = rng.choice([0.0, -3.0, 2.5, 100.0], (N, K // gs)).astype(np.float32)
+        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16)
+        args = (x.cuda(), torch.from_numpy(wq.view(np.int32)).cuda(), torch.from_numpy(s).to(torch.bfloat16).cuda(),
+                torch.from_numpy(b).to(torch.bfloat16).cuda())
+        y = ema.quantized_matmul(*args, group_size=gs, bits=bits)
+        check(ora, y, (x.float().numpy(), wq, s, b), gs, bits, f"extreme bits={bits}")
