@@ -287,183 +287,276 @@ __device__ __forceinline__ u32x4 rsrc4(const void* base, uint32_t bytes) {
 }
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Staged layout of one workgroup (16 weight rows, the MX rows of x, all of K), in 16-byte
+// Staged kernel for up to 32 rows of x. A workgroup owns 16 NT weight rows (NT column
+// tiles of 16) and all of K, walked in NC chunks of KCH. All of its weights, scales and
+// biases are staged in LDS by DMA issued up front in chunk order (the HBM stream that
+// bounds the call, kept in flight from the start); the rows of x, read from L2, pass
+// through a ring of NB slots, the DMA of chunk c + NB issued once chunk c is multiplied
+// (NB = NC when x fits, so then everything is in flight at once). LDS layout, in 16-byte
 // units, chosen so both the DMA (64 consecutive units per instruction, whole 128-byte
-// lines of the source) and the MFMA-layout reads (consecutive lanes on consecutive
-// units) run without bank conflicts:
-//   weights  row block rb = c / 8 (two, 128 bytes of padding apart), then unit u of the
-//            row, then row c % 8:   unit (rb, u, c % 8) <- row c, bytes [16 u, 16 u + 16)
-//   x        unit u, then row r:   unit (u, r) <- x row r, bytes [16 u, 16 u + 16)
-//   scales   8 groups, then row c: unit (g / 8, c) <- scales row c, groups [g, g + 8)
-//   biases   likewise
-struct QmvLayout {
-  uint32_t U;        // 16-byte units per weight row
-  uint32_t rb_bytes; // one row block plus padding
-  uint32_t x_off, s_off, b_off, bytes;
-  uint32_t nW, nX, nS;  // DMA instructions per region
-  __host__ __device__ QmvLayout(int K, int bits, int gs, int mx) {
-    const uint32_t G = K / gs;
-    U = (uint32_t)K * bits / 128;
-    rb_bytes = U * 128 + 128;
-    nW = U / 4;  // 16 U units, 64 per instruction
-    nX = ((uint32_t)mx * K / 8 + 63) / 64;
-    nS = (16 * ((G + 7) / 8) + 63) / 64;
-    x_off = (2 * rb_bytes + 1023) & ~1023u;
-    s_off = x_off + 1024 * nX;
-    b_off = s_off + 1024 * nS;
-    bytes = b_off + 1024 * nS;
-  }
+// lines of the source) and the MFMA-layout reads (consecutive lanes on consecutive units)
+// run without bank conflicts:
+//   weights  row block rb = row / 8 (2 NT of them, 128 bytes of padding apart), then
+//            unit u of the row, then row % 8:  unit (rb, u, row % 8) <- row, bytes [16 u, +16)
+//   x slot   unit u of the chunk, then row r:  unit (u, r) <- x row r, chunk bytes [16 u, +16)
+//   scales   unit (g / 8, row) <- row, groups [g, g + 8); biases likewise
+constexpr uint32_t kQmvMaxLds = 150 * 1024;
+
+struct QmvPlan {
+  int NT, KCH, NC, NB;
+  uint32_t U;         // weight units per row (all of K)
+  uint32_t Uc;        // weight units per row per chunk
+  uint32_t rb_bytes;  // one row block plus padding
+  uint32_t x_off;     // first x slot
+  uint32_t x_slot;    // bytes per x slot
+  uint32_t nW, nX;    // DMA instructions per chunk (weights, x)
+  uint32_t nS;        // DMA instructions for all scales (and again for the biases)
+  uint32_t s_off, b_off, z_off, bytes;
 };
 
-template <int BITS, int GS, bool F16, int MX>
-__global__ __launch_bounds__(64 * kMaxWaves) void qmv_kernel(QmmArgs a) {
-  using F = Fields<BITS, F16>;
-  constexpr int kSteps = GS / 32;
-  constexpr int kWDw = GS * BITS / 128;
-  constexpr uint32_t kWBytes = GS * BITS / 8;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const QmvLayout L(a.K, BITS, GS, MX);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
-
-  const int n0 = blockIdx.x * 16;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = blockDim.x >> 6;
-  const int rows_n = min(16, a.N - n0), rows_m = min(MX, a.M);
-  const uint32_t wrow = (uint32_t)a.K * BITS / 8;
-  const uint32_t G2 = (uint32_t)a.G * 2;
-
-  // ---- stage: every DMA instruction of the three regions, spread over the waves
-  {
-    const u32x4 W = rsrc4(a.w + (int64_t)n0 * wrow, rows_n * wrow);
-    const u32x4 X = rsrc4(a.x, (rows_m - 1) * (uint32_t)a.ldx * 2 + (uint32_t)a.K * 2);
-    const u32x4 S = rsrc4(a.s + (int64_t)n0 * G2, rows_n * G2);
-    const u32x4 B = rsrc4(a.b + (int64_t)n0 * G2, rows_n * G2);
-    const uint32_t total = L.nW + L.nX + 2 * L.nS;
-    for (uint32_t i = wave; i < total; i += nw) {
-      if (i < L.nW) {
-        // the instruction's 64 units lie in one row block (8 U is a multiple of 64)
-        const uint32_t rb = (64 * i) / (8 * L.U), rem = 64 * i - rb * 8 * L.U + lane;
-        const uint32_t c = rb * 8 + (rem & 7), u = rem >> 3;
-        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + rb * L.rb_bytes + 16 * (64 * i - rb * 8 * L.U));
-        dma16(W, c < (uint32_t)rows_n ? c * wrow + 16 * u : kOffRow, dst);
-      } else if (i < L.nW + L.nX) {
-        const uint32_t j = i - L.nW, q = 64 * j + lane, u = q / MX, r = q % MX;
-        const bool ok = r < (uint32_t)rows_m && u < (uint32_t)a.K / 8;
-        dma16(X, ok ? r * (uint32_t)a.ldx * 2 + 16 * u : kOffRow,
-              __builtin_amdgcn_readfirstlane(lds0 + L.x_off + 1024 * j));
-      } else {
-        const uint32_t j = i - L.nW - L.nX, jj = j % L.nS, q = 64 * jj + lane, g8 = q >> 4, c = q & 15;
-        const bool ok = c < (uint32_t)rows_n && 8 * g8 < (uint32_t)a.G;
-        dma16(j < L.nS ? S : B, ok ? c * G2 + 16 * g8 : kOffRow,
-              __builtin_amdgcn_readfirstlane(lds0 + (j < L.nS ? L.s_off : L.b_off) + 1024 * jj));
-      }
-    }
-  }
-  wait_vmem();
-  __syncthreads();
-
-  // ---- compute: wave w takes groups [g0, g1)
-  const int c = lane & 15, j = lane >> 4;
-  const int g0 = (wave * a.G) / nw, g1 = ((wave + 1) * a.G) / nw;
-  const uint8_t* wbase = smem + (c >> 3) * L.rb_bytes + 16 * (c & 7);
-  const uint8_t* xbase = smem + L.x_off + 16 * (c < MX ? c : 0);
-  const uint8_t* sbase = smem + L.s_off + 16 * c;
-  const uint8_t* bbase = smem + L.b_off + 16 * c;
-  const u32x4 ones = {F::kOnes, F::kOnes, F::kOnes, F::kOnes};
-  f32x4 tot = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-  for (int g = g0; g < g1; ++g) {
-    uint32_t wd[kWDw];
-    {
-      const uint32_t bo = g * kWBytes + j * (kWBytes / 4);  // byte of row c this lane reads
-      if constexpr (kWDw <= 4) {
-        const uint8_t* p = wbase + 128 * (bo >> 4) + (bo & 15);
-#pragma unroll
-        for (int e = 0; e < kWDw; ++e) wd[e] = reinterpret_cast<const uint32_t*>(p)[e];
-      } else {
-        const uint8_t* p = wbase + 128 * (bo >> 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wd[e] = reinterpret_cast<const uint32_t*>(p)[e];
-#pragma unroll
-        for (int e = 0; e < kWDw - 4; ++e) wd[4 + e] = reinterpret_cast<const uint32_t*>(p + 128)[e];
-      }
-    }
-    const uint32_t sb = *reinterpret_cast<const uint16_t*>(sbase + 256 * (g >> 3) + 2 * (g & 7));
-    const uint32_t bb = *reinterpret_cast<const uint16_t*>(bbase + 256 * (g >> 3) + 2 * (g & 7));
-    const float sc = act_to_f32<F16>(sb);
-    const float bc = act_to_f32<F16>(bb) - F::kOff * sc;
-    f32x4 aq = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-      const uint32_t u = (g * GS + j * (GS / 4) + 8 * st) >> 3;  // x unit of this step
-      u32x4 xv = {0u, 0u, 0u, 0u};
-      if (c < MX) xv = *reinterpret_cast<const u32x4*>(xbase + 16 * MX * u);
-      uint32_t xd[4] = {xv[0], xv[1], xv[2], xv[3]};
-      const u32x4 A = F::acts(xd);
-      aq = mma<F16>(A, F::weights(wd, st), aq);
-      a1 = mma<F16>(A, ones, a1);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) tot[q] = fmaf(sc, aq[q], fmaf(bc, a1[q], tot[q]));
-  }
-
-  // ---- sum the waves' partial tiles (the staging area is free again after the barrier)
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(smem);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) red[wave * 256 + (4 * j + q) * 16 + c] = tot[q];
-  __syncthreads();
-  for (int e = threadIdx.x; e < 256; e += blockDim.x) {  // a workgroup may have one wave only
-    const int r = e >> 4, col = e & 15;
-    float v = 0.0f;
-    for (int w = 0; w < nw; ++w) v += red[w * 256 + e];
-    if (r < rows_m && col < rows_n)
-      reinterpret_cast<uint16_t*>(a.y)[(int64_t)r * a.ldy + n0 + col] = f32_to_act<F16>(v);
+// 0..31 outstanding vector-memory operations; larger counts wait for 31 (a longer wait).
+__device__ __forceinline__ void wait_vmcnt(uint32_t n) {
+  switch (n) {
+#define EMA_VM(i) case i: __builtin_amdgcn_s_waitcnt(0x0F70 | ((i) & 15) | (((i) >> 4) << 14)); break;
+    EMA_VM(0) EMA_VM(1) EMA_VM(2) EMA_VM(3) EMA_VM(4) EMA_VM(5) EMA_VM(6) EMA_VM(7)
+    EMA_VM(8) EMA_VM(9) EMA_VM(10) EMA_VM(11) EMA_VM(12) EMA_VM(13) EMA_VM(14) EMA_VM(15)
+    EMA_VM(16) EMA_VM(17) EMA_VM(18) EMA_VM(19) EMA_VM(20) EMA_VM(21) EMA_VM(22) EMA_VM(23)
+    EMA_VM(24) EMA_VM(25) EMA_VM(26) EMA_VM(27) EMA_VM(28) EMA_VM(29) EMA_VM(30)
+#undef EMA_VM
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15 | (1 << 14)); break;
   }
 }
 
-// The staged kernel for up to 8 rows of x when the workgroup's tile fits in LDS: K in
-// multiples of 256 (4-bit) / 128 (8-bit), so each weight row block is whole DMA blocks,
-// and K / gs a multiple of 8, so each 16-byte scale load ends inside its row.
-constexpr uint32_t kQmvMaxLds = 96 * 1024;
+template <int BITS, int GS, bool F16, int MX, int NT>
+__global__ __launch_bounds__(64 * kMaxWaves) void qmv_kernel(QmmArgs a, QmvPlan p) {
+  using F = Fields<BITS, F16>;
+  constexpr int MR = MX > 16 ? 2 : 1;       // row tiles of 16
+  constexpr int kSteps = GS / 32;
+  constexpr int kWDw = GS * BITS / 128;
+  constexpr uint32_t kWBytes = GS * BITS / 8;
+  constexpr int kRows = 16 * NT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
 
-template <int BITS, int GS, bool F16, int MX>
-int32_t launch_qmv(hipStream_t st, const QmmArgs& a, int nw) {
-  const QmvLayout L(a.K, BITS, GS, MX);
-  static bool attr_set = false;  // every instantiation needs the LDS above 64 KB allowed once
+  const int n0 = blockIdx.x * kRows;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = kMaxWaves;
+  const int rows_n = min(kRows, a.N - n0), rows_m = min(MX, a.M);
+  const uint32_t wrow = (uint32_t)a.K * BITS / 8;
+  const uint32_t G2 = (uint32_t)a.G * 2;
+  const u32x4 W = rsrc4(a.w + (int64_t)n0 * wrow, rows_n * wrow);
+  const u32x4 X = rsrc4(a.x, (rows_m - 1) * (uint32_t)a.ldx * 2 + (uint32_t)a.K * 2);
+  const u32x4 S = rsrc4(a.s + (int64_t)n0 * G2, rows_n * G2);
+  const u32x4 B = rsrc4(a.b + (int64_t)n0 * G2, rows_n * G2);
+
+  // Each wave issues instructions wave, wave + nw, ... of every list, so it issues the
+  // same number of each kind per chunk (cw weights, cx x).
+  auto mine = [&](uint32_t n) -> uint32_t { return n > (uint32_t)wave ? (n - wave + nw - 1) / nw : 0; };
+  const uint32_t cw = mine(p.nW), cx = mine(p.nX);
+  auto issue_w = [&](int c) {
+    for (uint32_t i = wave; i < p.nW; i += nw) {
+      // 64 units of chunk c's part of one row block (8 Uc is a multiple of 64)
+      const uint32_t per_rb = 8 * p.Uc, rb = (64 * i) / per_rb, first = 64 * i - rb * per_rb, rem = first + lane;
+      const uint32_t row = rb * 8 + (rem & 7), u = (uint32_t)c * p.Uc + (rem >> 3);
+      dma16(W, row < (uint32_t)rows_n ? row * wrow + 16 * u : kOffRow,
+            __builtin_amdgcn_readfirstlane(lds0 + rb * p.rb_bytes + 16 * (8 * (uint32_t)c * p.Uc + first)));
+    }
+  };
+  auto issue_x = [&](int c) {
+    const uint32_t kb = (uint32_t)c * p.KCH;
+    for (uint32_t i = wave; i < p.nX; i += nw) {
+      const uint32_t q = 64 * i + lane, u = q / MX, r = q % MX;
+      const bool ok = r < (uint32_t)rows_m && u < (uint32_t)p.KCH / 8;
+      dma16(X, ok ? r * (uint32_t)a.ldx * 2 + 2 * kb + 16 * u : kOffRow,
+            __builtin_amdgcn_readfirstlane(lds0 + p.x_off + (uint32_t)(c % p.NB) * p.x_slot + 1024 * i));
+    }
+  };
+  if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(smem + p.z_off)[threadIdx.x] = 0u;
+  // scales and biases first (needed from chunk 0 on), then weights and x chunk by chunk
+  for (uint32_t i = wave; i < 2 * p.nS; i += nw) {
+    const uint32_t jj = i % p.nS, q = 64 * jj + lane, g8 = q / kRows, row = q % kRows;
+    const bool ok = row < (uint32_t)rows_n && 8 * g8 < (uint32_t)a.G;
+    dma16(i < p.nS ? S : B, ok ? row * G2 + 16 * g8 : kOffRow,
+          __builtin_amdgcn_readfirstlane(lds0 + (i < p.nS ? p.s_off : p.b_off) + 1024 * jj));
+  }
+  for (int c = 0; c < p.NC; ++c) {
+    issue_w(c);
+    if (c < p.NB) issue_x(c);
+  }
+
+  // wave -> column tile t, and its share of each chunk's groups
+  const int per_t = nw / NT, t = wave / per_t, wt = wave % per_t;
+  const int GC = p.KCH / GS;
+  const int gb = (wt * GC) / per_t, ge = ((wt + 1) * GC) / per_t;
+  const int c16 = lane & 15, j = lane >> 4;
+  const int row = 16 * t + c16;  // weight row (output column) of this lane
+  const uint8_t* wbase = smem + (row >> 3) * p.rb_bytes + 16 * (row & 7);
+  const u32x4 ones = {F::kOnes, F::kOnes, F::kOnes, F::kOnes};
+  f32x4 tot[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c = 0; c < p.NC; ++c) {
+    // loads issued after chunk c's weights and x may stay in flight
+    const int later = p.NC - 1 - c;
+    const int x_later = p.NB - 1 < later ? p.NB - 1 : later;
+    wait_vmcnt((c < p.NB ? (uint32_t)later * cw : 0u) + (uint32_t)x_later * cx);
+    __syncthreads();
+    const uint8_t* xbase = smem + p.x_off + (uint32_t)(c % p.NB) * p.x_slot;
+#pragma unroll 2
+    for (int g = gb; g < ge; ++g) {
+      const int gg = c * GC + g;  // group index within K
+      uint32_t wd[kWDw];
+      {
+        const uint32_t bo = gg * kWBytes + j * (kWBytes / 4);
+        if constexpr (kWDw <= 4) {
+          const uint8_t* q = wbase + 128 * (bo >> 4) + (bo & 15);
+#pragma unroll
+          for (int e = 0; e < kWDw; ++e) wd[e] = reinterpret_cast<const uint32_t*>(q)[e];
+        } else {
+          const uint8_t* q = wbase + 128 * (bo >> 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wd[e] = reinterpret_cast<const uint32_t*>(q)[e];
+#pragma unroll
+          for (int e = 0; e < kWDw - 4; ++e) wd[4 + e] = reinterpret_cast<const uint32_t*>(q + 128)[e];
+        }
+      }
+      const uint32_t so = 16 * ((gg >> 3) * kRows + row) + 2 * (gg & 7);
+      const float sc = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.s_off + so));
+      const float bc = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.b_off + so)) - F::kOff * sc;
+      f32x4 aq[MR], a1[MR];
+#pragma unroll
+      for (int r = 0; r < MR; ++r) aq[r] = a1[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) {
+        const uint32_t u = (g * GS + j * (GS / 4) + 8 * st) >> 3;  // x unit of this step
+        const u32x4 Bw = F::weights(wd, st);
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          const int xr = 16 * r + c16;
+          // rows past MX read the zero block (one address select instead of four value selects)
+          const u32x4 xv = *reinterpret_cast<const u32x4*>(xr < MX ? xbase + 16 * (u * MX + xr) : smem + p.z_off);
+          const uint32_t xd[4] = {xv[0], xv[1], xv[2], xv[3]};
+          const u32x4 A = F::acts(xd);
+          aq[r] = mma<F16>(A, Bw, aq[r]);
+          a1[r] = mma<F16>(A, ones, a1[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tot[r][q] = fmaf(sc, aq[r][q], fmaf(bc, a1[r][q], tot[r][q]));
+    }
+    if (c + p.NB < p.NC) {
+      __syncthreads();  // every wave is done with the slot before it is refilled
+      issue_x(c + p.NB);
+    }
+  }
+
+  // ---- sum the partial tiles of each column tile's waves (no DMA is in flight now)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[(wave * MR + r) * 256 + (4 * j + q) * 16 + c16] = tot[r][q];
+  __syncthreads();
+  for (int e = threadIdx.x; e < NT * MR * 256; e += 64 * nw) {
+    const int tt = e / (MR * 256), r = (e / 256) % MR, rr = (e >> 4) & 15, col = e & 15;
+    float v = 0.0f;
+    for (int w = 0; w < per_t; ++w) v += red[((tt * per_t + w) * MR + r) * 256 + (e & 255)];
+    const int m = 16 * r + rr, n = 16 * tt + col;
+    if (m < rows_m && n < rows_n)
+      reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.ldy + n0 + n] = f32_to_act<F16>(v);
+  }
+}
+
+
+// Plan of the staged kernel for M <= 32 rows, or NC = 0 when it does not apply: a chunk
+// is whole DMA blocks per weight row block (KCH * bits / 128 a multiple of 8) and whole
+// groups, K is a multiple of it, and K / gs is a multiple of 8 (each 16-byte scale load
+// ends inside its row). Two column tiles share each x chunk from 9 rows of x on, when
+// their weights fit.
+QmvPlan plan_qmv(int K, int gs, int bits, int mx) {
+  QmvPlan none{};
+  none.NC = 0;
+  if ((K / gs) % 8 != 0) return none;
+  const int G = K / gs;
+  for (int nt = mx > 8 ? 2 : 1; nt >= 1; --nt) {
+    const int rows = 16 * nt;
+    for (int kch = 1024; kch >= 256; kch /= 2) {
+      if (K % kch || kch % gs || (kch * bits / 128) % 8) continue;
+      QmvPlan q{};
+      q.NT = nt;
+      q.KCH = kch;
+      q.NC = K / kch;
+      q.U = (uint32_t)K * bits / 128;
+      q.Uc = (uint32_t)kch * bits / 128;
+      q.rb_bytes = q.U * 128 + 128;
+      q.nW = (uint32_t)rows * q.Uc / 64;
+      q.nX = ((uint32_t)mx * kch / 8 + 63) / 64;
+      q.x_slot = 1024 * q.nX;
+      q.nS = ((uint32_t)rows * (G / 8) + 63) / 64;
+      q.x_off = ((2 * nt) * q.rb_bytes + 1023) & ~1023u;
+      const uint32_t fixed = q.x_off + 2 * 1024 * q.nS;
+      // all of x if it fits (then everything is in flight from the start), else the
+      // deepest ring that fits beside the weights
+      int nb = q.NC;
+      while (nb > 2 && fixed + 16 + nb * q.x_slot > kQmvMaxLds) --nb;
+      q.NB = nb;
+      q.s_off = q.x_off + nb * q.x_slot;
+      q.b_off = q.s_off + 1024 * q.nS;
+      q.z_off = q.b_off + 1024 * q.nS;  // 16 zero bytes read by rows of x past M
+      q.bytes = q.z_off + 16;
+      const uint32_t red = (uint32_t)kMaxWaves * (mx > 16 ? 2 : 1) * 1024;
+      if (q.bytes < red) q.bytes = red;
+      // the largest chunk that fits: fewer chunks, fewer barriers (measured faster at
+      // 32 rows than deeper rings of smaller chunks)
+      if (q.bytes <= kQmvMaxLds) return q;
+    }
+  }
+  return none;
+}
+
+template <int BITS, int GS, bool F16, int MX, int NT>
+int32_t launch_qmv(hipStream_t st, const QmmArgs& a, const QmvPlan& p) {
+  static bool attr_set = false;  // each instantiation allows its LDS above 64 KB once
   if (!attr_set) {
-    const int32_t rc = check_hip(hipFuncSetAttribute((const void*)qmv_kernel<BITS, GS, F16, MX>,
+    const int32_t rc = check_hip(hipFuncSetAttribute((const void*)qmv_kernel<BITS, GS, F16, MX, NT>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, kQmvMaxLds),
                                  "quantized_matmul: LDS attribute");
     if (rc) return rc;
     attr_set = true;
   }
-  const uint32_t lds = L.bytes > (uint32_t)nw * 1024 ? L.bytes : (uint32_t)nw * 1024;
-  hipLaunchKernelGGL((qmv_kernel<BITS, GS, F16, MX>), dim3((a.N + 15) / 16), dim3(64 * nw), lds, st, a);
+  hipLaunchKernelGGL((qmv_kernel<BITS, GS, F16, MX, NT>), dim3((a.N + 16 * NT - 1) / (16 * NT)),
+                     dim3(64 * kMaxWaves), p.bytes, st, a, p);
   return check_hip(hipGetLastError(), "quantized_matmul launch");
 }
 
-// Whether the staged kernel takes this call (and with how many rows of x).
-int qmv_rows(int M, int K, int gs, int bits) {
-  if (M > 8 || (K * bits / 128) % 8 != 0 || (K / gs) % 8 != 0) return 0;
-  const int mx = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-  return QmvLayout(K, bits, gs, mx).bytes <= kQmvMaxLds ? mx : 0;
-}
+int qmv_rows(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : 32; }
 
 template <int BITS, int GS, bool F16>
-int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, int nw) {
-  if (mx == 1) return launch_qmv<BITS, GS, F16, 1>(st, a, nw);
-  if (mx == 2) return launch_qmv<BITS, GS, F16, 2>(st, a, nw);
-  if (mx == 4) return launch_qmv<BITS, GS, F16, 4>(st, a, nw);
-  return launch_qmv<BITS, GS, F16, 8>(st, a, nw);
+int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, const QmvPlan& p) {
+  switch (mx) {
+    case 1: return launch_qmv<BITS, GS, F16, 1, 1>(st, a, p);
+    case 2: return launch_qmv<BITS, GS, F16, 2, 1>(st, a, p);
+    case 4: return launch_qmv<BITS, GS, F16, 4, 1>(st, a, p);
+    case 8: return launch_qmv<BITS, GS, F16, 8, 1>(st, a, p);
+    case 16: return launch_qmv<BITS, GS, F16, 16, 2>(st, a, p);
+    default: return launch_qmv<BITS, GS, F16, 32, 2>(st, a, p);
+  }
 }
 
 template <int BITS, int GS, bool F16>
 int32_t launch_t(hipStream_t st, QmmArgs a) {
   int nw = a.G / 8;  // waves per workgroup: about 8 groups each, at most 8 waves
   nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
-  if (const int mx = qmv_rows(a.M, a.K, GS, BITS)) return launch_qmv_rows<BITS, GS, F16>(st, a, mx, nw);
+  if (a.M <= 32) {
+    const int mx = qmv_rows(a.M);
+    const QmvPlan p = plan_qmv(a.K, GS, BITS, mx);
+    if (p.NC > 0) return launch_qmv_rows<BITS, GS, F16>(st, a, mx, p);
+  }
   const int mr = a.M <= 16 ? 1 : 2;
   a.mtiles = (a.M + 16 * mr - 1) / (16 * mr);
   const int64_t tiles = (int64_t)a.mtiles * ((a.N + 15) / 16);
