@@ -548,6 +548,208 @@ int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, const QmvPlan&
   }
 }
 
+// ---------------------------------------------------------------- tiled GEMM (M > 32)
+// A workgroup of four waves computes a 128 x 64 tile of y (128 rows of x, 64 weight rows);
+// wave (wm, wn) = (wave & 1, wave >> 1) owns rows 64 wm .. + 64 (four 16-row tiles) and
+// columns 32 wn .. + 32 (two 16-column tiles), so each unpacked B operand serves four row
+// tiles and each x operand two column tiles. K is walked in chunks of KC (64, or 128 for
+// group 128) through two LDS buffers filled by LDS-DMA, chunk c + 2 issued once chunk c
+// is multiplied; all scales and biases of the 64 rows are staged with chunk 0. Products
+// are exact as in qmv_kernel (C + q in the mantissa, per-group f32 epilogue). LDS layout
+// in 16-byte units:
+//   x        row block rb = row / 8 (16, padded by 128 bytes), unit u of the chunk, row % 8
+//   weights  unit u of the chunk, then row (64): (u, row) <- row, chunk bytes [16 u, +16)
+//   scales   (g / 8, row) <- row, groups [g, g + 8); biases likewise
+struct QgemmPlan {
+  int KC, NC;
+  uint32_t x_rb;               // one x row block plus padding
+  uint32_t buf;                // bytes of one buffer (x then weights)
+  uint32_t w_off;              // weights within a buffer
+  uint32_t nX, nW, nS;         // DMA instructions per chunk (x, weights) and for the scales
+  uint32_t s_off, b_off, bytes;
+  int ntiles;                  // 64-column tiles
+  int remap;
+};
+
+constexpr int kGemmWaves = 4;
+
+template <int BITS, int GS, bool F16>
+__global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, QgemmPlan p) {
+  using F = Fields<BITS, F16>;
+  constexpr int kSteps = GS / 32;
+  constexpr int kWDw = GS * BITS / 128;
+  constexpr uint32_t kWBytes = GS * BITS / 8;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+
+  int tile = blockIdx.x;
+  if (p.remap) tile = (tile % 8) * (gridDim.x / 8) + tile / 8;
+  const int m0 = (tile / p.ntiles) * 128, n0 = (tile % p.ntiles) * 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rows_n = min(64, a.N - n0), rows_m = min(128, a.M - m0);
+  const uint32_t wrow = (uint32_t)a.K * BITS / 8;
+  const uint32_t xrow = (uint32_t)a.ldx * 2;
+  const uint32_t G2 = (uint32_t)a.G * 2;
+  const u32x4 X = rsrc4(a.x + (int64_t)m0 * xrow, (rows_m - 1) * xrow + (uint32_t)a.K * 2);
+  const u32x4 W = rsrc4(a.w + (int64_t)n0 * wrow, rows_n * wrow);
+  const u32x4 S = rsrc4(a.s + (int64_t)n0 * G2, rows_n * G2);
+  const u32x4 B = rsrc4(a.b + (int64_t)n0 * G2, rows_n * G2);
+  const uint32_t ux = (uint32_t)p.KC / 8;             // x units per row per chunk
+  const uint32_t uw = (uint32_t)p.KC * BITS / 128;    // weight units per row per chunk
+
+  auto mine = [&](uint32_t n) -> uint32_t {
+    return n > (uint32_t)wave ? (n - wave + kGemmWaves - 1) / kGemmWaves : 0;
+  };
+  const uint32_t per_chunk = mine(p.nX) + mine(p.nW);
+  auto issue = [&](int c) {
+    const uint32_t bb = lds0 + (uint32_t)(c & 1) * p.buf;
+    const uint32_t kb = (uint32_t)c * p.KC;
+    for (uint32_t i = wave; i < p.nX + p.nW; i += kGemmWaves) {
+      if (i < p.nX) {
+        // 64 units of one x row block: 8 units u of each of its 8 rows (8 ux is a multiple of 64)
+        const uint32_t rb = (64 * i) / (8 * ux), first = 64 * i - rb * 8 * ux, rem = first + lane;
+        const uint32_t row = rb * 8 + (rem & 7), u = rem >> 3;
+        dma16(X, row < (uint32_t)rows_m ? row * xrow + 2 * kb + 16 * u : kOffRow,
+              __builtin_amdgcn_readfirstlane(bb + rb * p.x_rb + 16 * first));
+      } else {
+        const uint32_t j = i - p.nX, q = 64 * j + lane, u = q >> 6, row = q & 63;
+        dma16(W, row < (uint32_t)rows_n && u < uw ? row * wrow + kb * BITS / 8 + 16 * u : kOffRow,
+              __builtin_amdgcn_readfirstlane(bb + p.w_off + 1024 * j));
+      }
+    }
+  };
+  for (uint32_t i = wave; i < 2 * p.nS; i += kGemmWaves) {
+    const uint32_t jj = i % p.nS, q = 64 * jj + lane, g8 = q >> 6, row = q & 63;
+    const bool ok = row < (uint32_t)rows_n && 8 * g8 < (uint32_t)a.G;
+    dma16(i < p.nS ? S : B, ok ? row * G2 + 16 * g8 : kOffRow,
+          __builtin_amdgcn_readfirstlane(lds0 + (i < p.nS ? p.s_off : p.b_off) + 1024 * jj));
+  }
+  issue(0);
+  if (p.NC > 1) issue(1);
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int c16 = lane & 15, j = lane >> 4;
+  const u32x4 ones = {F::kOnes, F::kOnes, F::kOnes, F::kOnes};
+  f32x4 tot[4][2];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) tot[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int GC = p.KC / GS;  // groups per chunk
+
+  for (int c = 0; c < p.NC; ++c) {
+    wait_vmcnt(c + 1 < p.NC ? per_chunk : 0u);
+    __syncthreads();
+    const uint8_t* xb = smem + (uint32_t)(c & 1) * p.buf;
+    const uint8_t* wb = xb + p.w_off;
+    for (int g = 0; g < GC; ++g) {
+      const int gg = c * GC + g;
+      float sc[2], bc[2];
+      uint32_t wd[2][kWDw];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const int row = 32 * wn + 16 * ct + c16;
+        const uint32_t so = 16 * ((gg >> 3) * 64 + row) + 2 * (gg & 7);
+        sc[ct] = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.s_off + so));
+        bc[ct] = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.b_off + so)) - F::kOff * sc[ct];
+        const uint32_t bo = g * kWBytes + j * (kWBytes / 4);  // byte of the row within the chunk
+#pragma unroll
+        for (int e = 0; e < kWDw; ++e) {
+          const uint32_t be = bo + 4 * e;
+          wd[ct][e] = *reinterpret_cast<const uint32_t*>(wb + 16 * ((be >> 4) * 64 + row) + (be & 15));
+        }
+      }
+      f32x4 aq[4][2], a1[4];
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        a1[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) aq[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) {
+        const u32x4 Bw0 = F::weights(wd[0], st), Bw1 = F::weights(wd[1], st);
+        const uint32_t u = (g * GS + j * (GS / 4) + 8 * st) >> 3;  // x unit of this step
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+          const int row = 64 * wm + 16 * rt + c16;
+          const u32x4 xv = *reinterpret_cast<const u32x4*>(xb + (row >> 3) * p.x_rb + 16 * (u * 8 + (row & 7)));
+          const uint32_t xd[4] = {xv[0], xv[1], xv[2], xv[3]};
+          const u32x4 A = F::acts(xd);
+          aq[rt][0] = mma<F16>(A, Bw0, aq[rt][0]);
+          aq[rt][1] = mma<F16>(A, Bw1, aq[rt][1]);
+          a1[rt] = mma<F16>(A, ones, a1[rt]);
+        }
+      }
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            tot[rt][ct][q] = fmaf(sc[ct], aq[rt][ct][q], fmaf(bc[ct], a1[rt][q], tot[rt][ct][q]));
+    }
+    if (c + 2 < p.NC) {
+      __syncthreads();  // every wave is done with the buffer before it is refilled
+      issue(c + 2);
+    }
+  }
+
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = 64 * wm + 16 * rt + 4 * j + q, n = 32 * wn + 16 * ct + c16;
+        if (m < rows_m && n < rows_n)
+          reinterpret_cast<uint16_t*>(a.y)[(int64_t)(m0 + m) * a.ldy + n0 + n] = f32_to_act<F16>(tot[rt][ct][q]);
+      }
+}
+
+// Plan of the tiled GEMM, or NC = 0 when it does not apply (K a multiple of the chunk,
+// K / gs a multiple of 8, everything within the LDS budget).
+QgemmPlan plan_qgemm(int M, int N, int K, int gs, int bits) {
+  QgemmPlan p{};
+  p.NC = 0;
+  const int kc = gs > 64 ? gs : 64;
+  if (K % kc || (K / gs) % 8) return p;
+  const int G = K / gs;
+  p.KC = kc;
+  p.NC = K / kc;
+  p.x_rb = (uint32_t)kc / 8 * 128 + 128;
+  p.nX = 16 * ((uint32_t)kc / 8) * 8 / 64;
+  const uint32_t uw = (uint32_t)kc * bits / 128;
+  p.nW = uw;  // 64 rows x uw units, 64 per instruction
+  p.w_off = 16 * p.x_rb;
+  p.buf = p.w_off + 1024 * p.nW;
+  p.nS = (64u * (G / 8) + 63) / 64;
+  p.s_off = 2 * p.buf;
+  p.b_off = p.s_off + 1024 * p.nS;
+  p.bytes = p.b_off + 1024 * p.nS;
+  p.ntiles = (N + 63) / 64;
+  const int64_t tiles = (int64_t)p.ntiles * ((M + 127) / 128);
+  p.remap = tiles % 8 == 0;
+  if (p.bytes > kQmvMaxLds) p.NC = 0;
+  return p;
+}
+
+template <int BITS, int GS, bool F16>
+int32_t launch_qgemm(hipStream_t st, const QmmArgs& a, const QgemmPlan& p) {
+  static bool attr_set = false;  // each instantiation allows its LDS above 64 KB once
+  if (!attr_set) {
+    const int32_t rc = check_hip(hipFuncSetAttribute((const void*)qgemm_kernel<BITS, GS, F16>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kQmvMaxLds),
+                                 "quantized_matmul: LDS attribute");
+    if (rc) return rc;
+    attr_set = true;
+  }
+  const unsigned tiles = (unsigned)(p.ntiles * ((a.M + 127) / 128));
+  hipLaunchKernelGGL((qgemm_kernel<BITS, GS, F16>), dim3(tiles), dim3(64 * kGemmWaves), p.bytes, st, a, p);
+  return check_hip(hipGetLastError(), "quantized_matmul launch");
+}
+
 template <int BITS, int GS, bool F16>
 int32_t launch_t(hipStream_t st, QmmArgs a) {
   int nw = a.G / 8;  // waves per workgroup: about 8 groups each, at most 8 waves
@@ -556,6 +758,9 @@ int32_t launch_t(hipStream_t st, QmmArgs a) {
     const int mx = qmv_rows(a.M);
     const QmvPlan p = plan_qmv(a.K, GS, BITS, mx);
     if (p.NC > 0) return launch_qmv_rows<BITS, GS, F16>(st, a, mx, p);
+  } else {
+    const QgemmPlan p = plan_qgemm(a.M, a.N, a.K, GS, BITS);
+    if (p.NC > 0) return launch_qgemm<BITS, GS, F16>(st, a, p);
   }
   const int mr = a.M <= 16 ? 1 : 2;
   a.mtiles = (a.M + 16 * mr - 1) / (16 * mr);

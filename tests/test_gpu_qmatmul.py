@@ -85,14 +85,48 @@ def test_qmatmul_qwen3_8b_qkv_decode_shape(ema, ora, M):
     check(ora, y, h, gs, bits, "8B qkv", bar=True)
 
 
-@pytest.mark.parametrize("M", [64, 300])
-def test_qmatmul_prefill_rows(ema, ora, M):
-    # several 32-row tiles of x per weight tile (grid remapped per XCD when divisible)
-    N, K, gs, bits = 256, 1024, 64, 4
-    say(f"qmatmul prefill rows M={M}")
-    d, h = make(ora, M, M, N, K, gs, bits)
+@pytest.mark.parametrize("M,N,K,gs,bits,dtype", [
+    (64, 256, 1024, 64, 4, "bf16"),     # tiled GEMM: one 128-row tile, several column tiles
+    (300, 256, 1024, 64, 4, "bf16"),    # ragged last row tile
+    (130, 100, 2048, 128, 4, "bf16"),   # group 128: 128-wide chunks; ragged columns
+    (500, 70, 1024, 128, 8, "f16"),
+    (96, 80, 512, 32, 8, "bf16"),
+    (2048, 256, 2048, 64, 4, "bf16"),   # a prefill chunk's rows
+    (40, 48, 320, 32, 4, "bf16"),       # K / gs = 10: the streaming kernel
+    (70, 64, 320, 32, 8, "f16"),
+])
+def test_qmatmul_prefill_rows(ema, ora, M, N, K, gs, bits, dtype):
+    say(f"qmatmul prefill rows M={M} N={N} K={K} gs={gs} bits={bits} {dtype}")
+    d, h = make(ora, M + N, M, N, K, gs, bits, dtype)
     y = ema.quantized_matmul(*d, group_size=gs, bits=bits)
-    check(ora, y, h, gs, bits, f"M={M}")
+    check(ora, y, h, gs, bits, f"M={M}", dtype)
+
+
+@pytest.mark.parametrize("M", [1, 32, 256])
+def test_qmatmul_graph_replay(ema, ora, M):
+    # captured in a HIP graph and replayed several times with eager work between the
+    # replays: every replay equals the eager call (no memsets or host state in the call)
+    import torch
+
+    N, K, gs, bits = 192, 1024, 64, 4
+    say(f"qmatmul graph replay M={M}")
+    d, _ = make(ora, 5 + M, M, N, K, gs, bits)
+    y_eager = ema.quantized_matmul(*d, group_size=gs, bits=bits)
+    torch.cuda.synchronize()
+    y = torch.empty_like(y_eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ema.quantized_matmul(*d, group_size=gs, bits=bits, out=y, stream=s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        y.fill_(float(i + 3))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y_eager.view(torch.int16)), f"replay {i}"
 
 
 def test_qmatmul_separate_pieces_equal_fused(ema, ora):
