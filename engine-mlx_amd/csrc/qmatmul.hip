@@ -549,29 +549,30 @@ int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, const QmvPlan&
 }
 
 // ---------------------------------------------------------------- tiled GEMM (M > 32)
-// A workgroup of four waves computes a 128 x 64 tile of y (128 rows of x, 64 weight rows);
-// wave (wm, wn) = (wave & 1, wave >> 1) owns rows 64 wm .. + 64 (four 16-row tiles) and
-// columns 32 wn .. + 32 (two 16-column tiles), so each unpacked B operand serves four row
-// tiles and each x operand two column tiles. K is walked in chunks of KC (64, or 128 for
-// group 128) through two LDS buffers filled by LDS-DMA, chunk c + 2 issued once chunk c
-// is multiplied; all scales and biases of the 64 rows are staged with chunk 0. Products
-// are exact as in qmv_kernel (C + q in the mantissa, per-group f32 epilogue). LDS layout
-// in 16-byte units:
+// A workgroup of eight waves computes a 128 x 128 tile of y (128 rows of x, 128 weight
+// rows); wave (wm, wn) = (wave & 1, wave >> 1) owns rows 64 wm .. + 64 (four 16-row tiles)
+// and columns 32 wn .. + 32 (two 16-column tiles), so each unpacked B operand serves four
+// row tiles and each x tile in LDS four column waves. K is walked in chunks of KC (64, or
+// 128 for group 128) through a ring of NB = 2 LDS buffers filled by LDS-DMA, chunk c + 1
+// issued as chunk c starts (into the buffer chunk c - 1 freed); all scales and biases of
+// the 128 rows are staged first. Products are exact as in qmv_kernel (C + q in the
+// mantissa, per-group f32 epilogue). LDS layout in 16-byte units:
 //   x        row block rb = row / 8 (16, padded by 128 bytes), unit u of the chunk, row % 8
-//   weights  unit u of the chunk, then row (64): (u, row) <- row, chunk bytes [16 u, +16)
+//   weights  unit u of the chunk, then row (128): (u, row) <- row, chunk bytes [16 u, +16)
 //   scales   (g / 8, row) <- row, groups [g, g + 8); biases likewise
 struct QgemmPlan {
-  int KC, NC;
+  int KC, NC, NB;
   uint32_t x_rb;               // one x row block plus padding
   uint32_t buf;                // bytes of one buffer (x then weights)
   uint32_t w_off;              // weights within a buffer
   uint32_t nX, nW, nS;         // DMA instructions per chunk (x, weights) and for the scales
   uint32_t s_off, b_off, bytes;
-  int ntiles;                  // 64-column tiles
+  int ntiles;                  // 128-column tiles
   int remap;
 };
 
-constexpr int kGemmWaves = 4;
+constexpr int kGemmWaves = 8;
+constexpr int kGemmBN = 128;
 
 template <int BITS, int GS, bool F16>
 __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, QgemmPlan p) {
@@ -584,10 +585,10 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, Qgemm
 
   int tile = blockIdx.x;
   if (p.remap) tile = (tile % 8) * (gridDim.x / 8) + tile / 8;
-  const int m0 = (tile / p.ntiles) * 128, n0 = (tile % p.ntiles) * 64;
+  const int m0 = (tile / p.ntiles) * 128, n0 = (tile % p.ntiles) * kGemmBN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rows_n = min(64, a.N - n0), rows_m = min(128, a.M - m0);
+  const int rows_n = min(kGemmBN, a.N - n0), rows_m = min(128, a.M - m0);
   const uint32_t wrow = (uint32_t)a.K * BITS / 8;
   const uint32_t xrow = (uint32_t)a.ldx * 2;
   const uint32_t G2 = (uint32_t)a.G * 2;
@@ -603,7 +604,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, Qgemm
   };
   const uint32_t per_chunk = mine(p.nX) + mine(p.nW);
   auto issue = [&](int c) {
-    const uint32_t bb = lds0 + (uint32_t)(c & 1) * p.buf;
+    const uint32_t bb = lds0 + (uint32_t)(c % p.NB) * p.buf;
     const uint32_t kb = (uint32_t)c * p.KC;
     for (uint32_t i = wave; i < p.nX + p.nW; i += kGemmWaves) {
       if (i < p.nX) {
@@ -613,20 +614,20 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, Qgemm
         dma16(X, row < (uint32_t)rows_m ? row * xrow + 2 * kb + 16 * u : kOffRow,
               __builtin_amdgcn_readfirstlane(bb + rb * p.x_rb + 16 * first));
       } else {
-        const uint32_t j = i - p.nX, q = 64 * j + lane, u = q >> 6, row = q & 63;
+        const uint32_t j = i - p.nX, q = 64 * j + lane, u = q / kGemmBN, row = q % kGemmBN;
         dma16(W, row < (uint32_t)rows_n && u < uw ? row * wrow + kb * BITS / 8 + 16 * u : kOffRow,
               __builtin_amdgcn_readfirstlane(bb + p.w_off + 1024 * j));
       }
     }
   };
   for (uint32_t i = wave; i < 2 * p.nS; i += kGemmWaves) {
-    const uint32_t jj = i % p.nS, q = 64 * jj + lane, g8 = q >> 6, row = q & 63;
+    const uint32_t jj = i % p.nS, q = 64 * jj + lane, g8 = q / kGemmBN, row = q % kGemmBN;
     const bool ok = row < (uint32_t)rows_n && 8 * g8 < (uint32_t)a.G;
     dma16(i < p.nS ? S : B, ok ? row * G2 + 16 * g8 : kOffRow,
           __builtin_amdgcn_readfirstlane(lds0 + (i < p.nS ? p.s_off : p.b_off) + 1024 * jj));
   }
-  issue(0);
-  if (p.NC > 1) issue(1);
+  const int pre = p.NB - 1 < p.NC ? p.NB - 1 : p.NC;
+  for (int c = 0; c < pre; ++c) issue(c);
 
   const int wm = wave & 1, wn = wave >> 1;
   const int c16 = lane & 15, j = lane >> 4;
@@ -639,9 +640,11 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, Qgemm
   const int GC = p.KC / GS;  // groups per chunk
 
   for (int c = 0; c < p.NC; ++c) {
-    wait_vmcnt(c + 1 < p.NC ? per_chunk : 0u);
+    if (c + p.NB - 1 < p.NC) issue(c + p.NB - 1);  // its buffer held chunk c - 1
+    const int later = min(p.NB - 1, p.NC - 1 - c);
+    wait_vmcnt((uint32_t)later * per_chunk);
     __syncthreads();
-    const uint8_t* xb = smem + (uint32_t)(c & 1) * p.buf;
+    const uint8_t* xb = smem + (uint32_t)(c % p.NB) * p.buf;
     const uint8_t* wb = xb + p.w_off;
     for (int g = 0; g < GC; ++g) {
       const int gg = c * GC + g;
@@ -650,14 +653,14 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, Qgemm
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         const int row = 32 * wn + 16 * ct + c16;
-        const uint32_t so = 16 * ((gg >> 3) * 64 + row) + 2 * (gg & 7);
+        const uint32_t so = 16 * ((gg >> 3) * kGemmBN + row) + 2 * (gg & 7);
         sc[ct] = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.s_off + so));
         bc[ct] = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.b_off + so)) - F::kOff * sc[ct];
         const uint32_t bo = g * kWBytes + j * (kWBytes / 4);  // byte of the row within the chunk
 #pragma unroll
         for (int e = 0; e < kWDw; ++e) {
           const uint32_t be = bo + 4 * e;
-          wd[ct][e] = *reinterpret_cast<const uint32_t*>(wb + 16 * ((be >> 4) * 64 + row) + (be & 15));
+          wd[ct][e] = *reinterpret_cast<const uint32_t*>(wb + 16 * ((be >> 4) * kGemmBN + row) + (be & 15));
         }
       }
       f32x4 aq[4][2], a1[4];
@@ -690,10 +693,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, Qgemm
           for (int q = 0; q < 4; ++q)
             tot[rt][ct][q] = fmaf(sc[ct], aq[rt][ct][q], fmaf(bc[ct], a1[rt][q], tot[rt][ct][q]));
     }
-    if (c + 2 < p.NC) {
-      __syncthreads();  // every wave is done with the buffer before it is refilled
-      issue(c + 2);
-    }
+    __syncthreads();  // the buffer is refilled at the next turn
   }
 
 #pragma unroll
@@ -709,7 +709,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, Qgemm
 }
 
 // Plan of the tiled GEMM, or NC = 0 when it does not apply (K a multiple of the chunk,
-// K / gs a multiple of 8, everything within the LDS budget).
+// K / gs a multiple of 8, everything within the LDS budget with at least two buffers).
 QgemmPlan plan_qgemm(int M, int N, int K, int gs, int bits) {
   QgemmPlan p{};
   p.NC = 0;
@@ -717,18 +717,22 @@ QgemmPlan plan_qgemm(int M, int N, int K, int gs, int bits) {
   if (K % kc || (K / gs) % 8) return p;
   const int G = K / gs;
   p.KC = kc;
-  p.NC = K / kc;
   p.x_rb = (uint32_t)kc / 8 * 128 + 128;
   p.nX = 16 * ((uint32_t)kc / 8) * 8 / 64;
   const uint32_t uw = (uint32_t)kc * bits / 128;
-  p.nW = uw;  // 64 rows x uw units, 64 per instruction
+  p.nW = (uint32_t)kGemmBN * uw / 64;
   p.w_off = 16 * p.x_rb;
   p.buf = p.w_off + 1024 * p.nW;
-  p.nS = (64u * (G / 8) + 63) / 64;
-  p.s_off = 2 * p.buf;
+  p.nS = ((uint32_t)kGemmBN * (G / 8) + 63) / 64;
+  // two buffers: at most ~75 KB, so two workgroups (four waves per SIMD) share a CU,
+  // which hides the LDS and DMA latency better than a deeper ring at one workgroup
+  const int nb = 2;
+  p.NC = K / kc;
+  p.NB = nb < p.NC ? nb : (p.NC < 2 ? 2 : p.NC);
+  p.s_off = p.NB * p.buf;
   p.b_off = p.s_off + 1024 * p.nS;
   p.bytes = p.b_off + 1024 * p.nS;
-  p.ntiles = (N + 63) / 64;
+  p.ntiles = (N + kGemmBN - 1) / kGemmBN;
   const int64_t tiles = (int64_t)p.ntiles * ((M + 127) / 128);
   p.remap = tiles % 8 == 0;
   if (p.bytes > kQmvMaxLds) p.NC = 0;
