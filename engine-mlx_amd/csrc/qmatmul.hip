@@ -89,6 +89,15 @@ __device__ __forceinline__ uint32_t pair(uint32_t lo, uint32_t hi, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// (x & m) | c in one v_and_or_b32. gfx950's VOP3 encoding takes no 32-bit literal, so with
+// literal masks the compiler splits it into v_and + v_or; as operands of the asm the
+// constants are kept in VGPRs, set once per kernel.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
+  return r;
+}
+
 template <int BITS, bool F16>
 struct Fields {
   // the weight bits take the mantissa of this constant: value kOff + q, exact
@@ -102,16 +111,16 @@ struct Fields {
     u32x4 r;
     if constexpr (BITS == 4) {
       const uint32_t w = wd[st];  // fields 0..7; register i holds fields i and i + 4
-      r[0] = (w & 0x000F000Fu) | kMagicBits;
-      r[1] = ((w >> 4) & 0x000F000Fu) | kMagicBits;
-      r[2] = ((w >> 8) & 0x000F000Fu) | kMagicBits;
-      r[3] = ((w >> 12) & 0x000F000Fu) | kMagicBits;
+      r[0] = and_or(w, 0x000F000Fu, kMagicBits);
+      r[1] = and_or(w >> 4, 0x000F000Fu, kMagicBits);
+      r[2] = and_or(w >> 8, 0x000F000Fu, kMagicBits);
+      r[3] = and_or(w >> 12, 0x000F000Fu, kMagicBits);
     } else if constexpr (F16) {
       const uint32_t w0 = wd[2 * st], w1 = wd[2 * st + 1];  // bytes 0..3, 4..7
-      r[0] = (w0 & 0x00FF00FFu) | kMagicBits;               // bytes 0, 2
-      r[1] = ((w0 >> 8) & 0x00FF00FFu) | kMagicBits;        // bytes 1, 3
-      r[2] = (w1 & 0x00FF00FFu) | kMagicBits;
-      r[3] = ((w1 >> 8) & 0x00FF00FFu) | kMagicBits;
+      r[0] = and_or(w0, 0x00FF00FFu, kMagicBits);           // bytes 0, 2
+      r[1] = and_or(w0 >> 8, 0x00FF00FFu, kMagicBits);      // bytes 1, 3
+      r[2] = and_or(w1, 0x00FF00FFu, kMagicBits);
+      r[3] = and_or(w1 >> 8, 0x00FF00FFu, kMagicBits);
     } else {
       const uint32_t w0 = wd[2 * st], w1 = wd[2 * st + 1];
       // an integer below 256 is exact in the top half of its f32
@@ -300,7 +309,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 //            unit u of the row, then row % 8:  unit (rb, u, row % 8) <- row, bytes [16 u, +16)
 //   x slot   unit u of the chunk, then row r:  unit (u, r) <- x row r, chunk bytes [16 u, +16)
 //   scales   unit (g / 8, row) <- row, groups [g, g + 8); biases likewise
-constexpr uint32_t kQmvMaxLds = 150 * 1024;
+constexpr uint32_t kQmvMaxLds = 160 * 1024;  // all of a gfx950 CU's LDS
 
 struct QmvPlan {
   int NT, KCH, NC, NB;
@@ -476,17 +485,20 @@ __global__ __launch_bounds__(64 * kMaxWaves) void qmv_kernel(QmmArgs a, QmvPlan 
 // Plan of the staged kernel for M <= 32 rows, or NC = 0 when it does not apply: a chunk
 // is whole DMA blocks per weight row block (KCH * bits / 128 a multiple of 8) and whole
 // groups, K is a multiple of it, and K / gs is a multiple of 8 (each 16-byte scale load
-// ends inside its row). Two column tiles share each x chunk from 9 rows of x on, when
-// their weights fit.
-QmvPlan plan_qmv(int K, int gs, int bits, int mx) {
+// ends inside its row).
+QmvPlan plan_qmv(int N, int K, int gs, int bits, int mx, int cus) {
   QmvPlan none{};
   none.NC = 0;
   if ((K / gs) % 8 != 0) return none;
   const int G = K / gs;
-  for (int nt = mx > 8 ? 2 : 1; nt >= 1; --nt) {
+  // two column tiles per workgroup only when 16-column tiles would outnumber the CUs (a
+  // second round of workgroups costs more than doubling each one's columns)
+  const int nt0 = mx >= 8 && (N + 15) / 16 > cus ? 2 : 1;
+  for (int nt = nt0; nt >= 1; --nt) {
     const int rows = 16 * nt;
-    for (int kch = 1024; kch >= 256; kch /= 2) {
+    for (int kch = 1024; kch >= 128; kch /= 2) {
       if (K % kch || kch % gs || (kch * bits / 128) % 8) continue;
+      if (nt == 2 && kch < 256) continue;  // measured: more chunks cost more than a second round
       QmvPlan q{};
       q.NT = nt;
       q.KCH = kch;
@@ -542,9 +554,9 @@ int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, const QmvPlan&
     case 1: return launch_qmv<BITS, GS, F16, 1, 1>(st, a, p);
     case 2: return launch_qmv<BITS, GS, F16, 2, 1>(st, a, p);
     case 4: return launch_qmv<BITS, GS, F16, 4, 1>(st, a, p);
-    case 8: return launch_qmv<BITS, GS, F16, 8, 1>(st, a, p);
-    case 16: return launch_qmv<BITS, GS, F16, 16, 2>(st, a, p);
-    default: return launch_qmv<BITS, GS, F16, 32, 2>(st, a, p);
+    case 8: return p.NT == 2 ? launch_qmv<BITS, GS, F16, 8, 2>(st, a, p) : launch_qmv<BITS, GS, F16, 8, 1>(st, a, p);
+    case 16: return p.NT == 2 ? launch_qmv<BITS, GS, F16, 16, 2>(st, a, p) : launch_qmv<BITS, GS, F16, 16, 1>(st, a, p);
+    default: return p.NT == 2 ? launch_qmv<BITS, GS, F16, 32, 2>(st, a, p) : launch_qmv<BITS, GS, F16, 32, 1>(st, a, p);
   }
 }
 
@@ -754,13 +766,159 @@ int32_t launch_qgemm(hipStream_t st, const QmmArgs& a, const QgemmPlan& p) {
   return check_hip(hipGetLastError(), "quantized_matmul launch");
 }
 
+// ---------------------------------------------------------------- one row of x (M = 1)
+// VALU dot products instead of MFMA (which would spend 15 of its 16 rows on nothing): lane
+// gl of a slot of L lanes takes group gl (+ L i) of a weight row, so a wave reads whole
+// rows coalesced; 64 / L slots cover 64 / L rows at once, and a wave walks R rows. The
+// same exact pairs as the MFMA kernels (C + q against x, v_dot2_f32_bf16 / _f16: exact
+// products, f32 sums) and the same per-group combination y += s a_q + (b - C s) a_1, with
+// a_1 = sum of the group's x. The row sums are reduced across the slot's lanes with xor
+// shuffles. R is chosen so the grid is about one workgroup of eight waves per CU.
+constexpr int kGemvRows = 4;  // most rows per lane
+
+template <bool F16>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (F16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+  } else {
+    return dot2_bf16(a, b, c);
+  }
+}
+
+template <int BITS, int GS, bool F16>
+__global__ __launch_bounds__(512) void qgemv1_kernel(QmmArgs a, int np, int L, int gpl) {
+  using F = Fields<BITS, F16>;
+  constexpr int kWDw = GS * BITS / 32;  // dwords of one group of one weight row
+  constexpr int kXDw = GS / 2;          // dwords of one group of x
+  constexpr int kBlk = GS / 8;          // blocks of 8 weights per group
+  constexpr uint32_t kWBytes = GS * BITS / 8;
+  const int lane = threadIdx.x & 63;
+  const int slots = 64 / L, slot = lane / L, gl = lane % L;
+  const int R = slots * np;  // rows per wave
+  // wave-uniform (an SGPR): the buffer resources below must be uniform, or every load
+  // becomes a loop over the lanes' distinct resources
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row0 = ((int64_t)blockIdx.x * 8 + wave) * R;
+  // waves past the last row still take part in the x staging and its barrier
+  const int rows = (int)max((int64_t)0, min((int64_t)R, (int64_t)a.N - row0));
+  const uint32_t wrow = (uint32_t)a.K * BITS / 8;
+  const uint32_t G2 = (uint32_t)a.G * 2;
+  const auto W = rsrc(a.w + row0 * wrow, rows * wrow);
+  const auto S = rsrc(a.s + row0 * G2, rows * G2);
+  const auto Bi = rsrc(a.b + row0 * G2, rows * G2);
+  const u32x4 ones = {F::kOnes, F::kOnes, F::kOnes, F::kOnes};
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  // x once per workgroup into LDS (LDS-DMA, 1 KB per instruction), issued before the
+  // weights; every wave then reads its x from LDS instead of from L2
+  {
+    const u32x4 X = rsrc4(a.x, (uint32_t)a.K * 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+    const uint32_t nxd = ((uint32_t)a.K * 2 + 1023) / 1024;
+    for (uint32_t i = wave; i < nxd; i += 8)
+      dma16(X, 1024 * i + 16 * lane, __builtin_amdgcn_readfirstlane(lds0 + 1024 * i));
+  }
+
+  float y[kGemvRows];
+#pragma unroll
+  for (int p = 0; p < kGemvRows; ++p) y[p] = 0.0f;
+  for (int i = 0; i < gpl; ++i) {
+    const uint32_t g = gl + L * i;
+    // weights, scale and bias of every row, in the order they are used
+    uint32_t wd[kGemvRows][kWDw], sb[kGemvRows], bb[kGemvRows];
+#pragma unroll
+    for (int p = 0; p < kGemvRows; ++p) {
+      const int r = slot + slots * p;  // row within the wave's rows
+      const bool ok = p < np && r < rows;
+      load_dw<kWDw>(W, ok ? r * wrow + g * kWBytes : kOffRow, wd[p]);
+      sb[p] = __builtin_amdgcn_raw_buffer_load_b16(S, ok ? r * G2 + 2 * g : kOffRow, 0, 0);
+      bb[p] = __builtin_amdgcn_raw_buffer_load_b16(Bi, ok ? r * G2 + 2 * g : kOffRow, 0, 0);
+    }
+    if (i == 0) {
+      // the x DMA came before these loads: wait for it alone, then publish it
+      constexpr uint32_t kPerRow = (kWDw <= 2 ? 1 : kWDw / 4) + 2;
+      wait_vmcnt(kGemvRows * kPerRow);
+      __syncthreads();
+    }
+    uint32_t xd[kXDw];
+#pragma unroll
+    for (int e = 0; e < kXDw / 4; ++e) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + g * (GS * 2) + 16 * e);
+      xd[4 * e] = v[0];
+      xd[4 * e + 1] = v[1];
+      xd[4 * e + 2] = v[2];
+      xd[4 * e + 3] = v[3];
+    }
+    // x paired as the fields are, and its group sum (exact pairs, f32 sums)
+    u32x4 xa[kBlk];
+    float a1 = 0.0f;
+#pragma unroll
+    for (int blk = 0; blk < kBlk; ++blk) {
+      xa[blk] = F::acts(xd + 4 * blk);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a1 = dot2<F16>(xa[blk][e], ones[e], a1);
+    }
+#pragma unroll
+    for (int p = 0; p < kGemvRows; ++p) {
+      if (p >= np) break;
+      float aq = 0.0f;
+#pragma unroll
+      for (int blk = 0; blk < kBlk; ++blk) {
+        const u32x4 B = F::weights(wd[p], blk);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) aq = dot2<F16>(xa[blk][e], B[e], aq);
+      }
+      const float sc = act_to_f32<F16>(sb[p]);
+      const float bc = act_to_f32<F16>(bb[p]) - F::kOff * sc;
+      y[p] = fmaf(sc, aq, fmaf(bc, a1, y[p]));
+    }
+  }
+  // sum over the slot's L lanes (xor partners stay inside the slot)
+#pragma unroll
+  for (int p = 0; p < kGemvRows; ++p) {
+    if (p >= np) break;
+    float v = y[p];
+    for (int m = 1; m < L; m <<= 1) v += __shfl_xor(v, m, 64);
+    const int r = slot + slots * p;
+    if (gl == 0 && r < rows)
+      reinterpret_cast<uint16_t*>(a.y)[row0 + r] = f32_to_act<F16>(v);
+  }
+}
+
+// Whether the one-row kernel takes this call: K / gs a power of two up to 64, or a
+// multiple of 64, and x (2 K bytes) within 64 KB of LDS.
+bool gemv1_fits(int G, int K) { return (G % 64 == 0 || (G <= 64 && (G & (G - 1)) == 0)) && K <= 32768; }
+
+template <int BITS, int GS, bool F16>
+int32_t launch_gemv1(hipStream_t st, const QmmArgs& a, int cus) {
+  const int L = a.G < 64 ? a.G : 64, slots = 64 / L, gpl = a.G / L;
+  // rows per lane: about one workgroup of eight waves per CU, at most kGemvRows
+  const int64_t want = ((int64_t)a.N + 8LL * cus * slots - 1) / (8LL * cus * slots);
+  const int np = (int)(want < 1 ? 1 : want > kGemvRows ? kGemvRows : want);
+  const int64_t waves = ((int64_t)a.N + slots * np - 1) / (slots * np);
+  const uint32_t lds = ((uint32_t)a.K * 2 + 1023) & ~1023u;  // x, in whole DMA blocks
+  hipLaunchKernelGGL((qgemv1_kernel<BITS, GS, F16>), dim3((unsigned)((waves + 7) / 8)), dim3(512), lds, st, a, np,
+                     L, gpl);
+  return check_hip(hipGetLastError(), "quantized_matmul launch");
+}
+
 template <int BITS, int GS, bool F16>
 int32_t launch_t(hipStream_t st, QmmArgs a) {
   int nw = a.G / 8;  // waves per workgroup: about 8 groups each, at most 8 waves
   nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
+  static int cus = 0;  // compute units of the device (queried once)
+  if (!cus) {
+    int dev = 0, n = 0;
+    cus = hipGetDevice(&dev) == hipSuccess &&
+                  hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+              ? n
+              : 256;
+  }
+  if (a.M == 1 && gemv1_fits(a.G, a.K)) return launch_gemv1<BITS, GS, F16>(st, a, cus);
   if (a.M <= 32) {
     const int mx = qmv_rows(a.M);
-    const QmvPlan p = plan_qmv(a.K, GS, BITS, mx);
+    const QmvPlan p = plan_qmv(a.N, a.K, GS, BITS, mx, cus);
     if (p.NC > 0) return launch_qmv_rows<BITS, GS, F16>(st, a, mx, p);
   } else {
     const QgemmPlan p = plan_qgemm(a.M, a.N, a.K, GS, BITS);
