@@ -29,6 +29,33 @@ int32_t check_hip(hipError_t e, const char* what) {
   return set_error(EMA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+namespace {
+constexpr int kMaxDevices = 64;
+int current_device() {
+  int dev = 0;
+  return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices ? dev : 0;
+}
+}  // namespace
+
+int device_cus() {
+  static std::atomic<int> cached[kMaxDevices];
+  const int dev = current_device();
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+int32_t allow_lds_once(const void* fn, int bytes, std::atomic<uint64_t>* done, const char* what) {
+  const uint64_t bit = 1ull << current_device();
+  if (done->load(std::memory_order_acquire) & bit) return EMA_OK;
+  const int32_t rc = check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes), what);
+  if (rc == EMA_OK) done->fetch_or(bit, std::memory_order_release);
+  return rc;
+}
+
 }  // namespace ema
 
 using namespace ema;

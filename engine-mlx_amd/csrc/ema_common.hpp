@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "ema_attn.h"
 
 namespace ema {
@@ -73,6 +75,11 @@ namespace ema {
 
 // Sets the thread-local error message and returns `code`.
 int32_t set_error(int32_t code, const char* fmt, ...);
+// Compute units of the current device (queried once per device).
+int device_cus();
+// Raises `fn`'s dynamic LDS limit to `bytes` once per device; bit d of *done records
+// device d (thread-safe).
+int32_t allow_lds_once(const void* fn, int bytes, std::atomic<uint64_t>* done, const char* what);
 // Maps a HIP error to EMA_ERR_HIP with context, or returns EMA_OK.
 int32_t check_hip(hipError_t e, const char* what);
 

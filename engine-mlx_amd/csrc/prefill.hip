@@ -620,18 +620,12 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
     return set_error(EMA_ERR_UNSUPPORTED,
                      "ema_prefill_attention: capacity %d x stride_pos %lld exceeds the 2 GiB per-head range",
                      c.capacity, (long long)c.stride_pos);
-  static bool attr_set = false;
-  if (!attr_set) {
-    int32_t rc = check_hip(hipFuncSetAttribute((const void*)prefill_kernel<false>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
-                           "ema_prefill_attention: LDS attribute");
-    if (rc) return rc;
-    rc = check_hip(hipFuncSetAttribute((const void*)prefill_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       kLdsBytes),
-                   "ema_prefill_attention: LDS attribute");
-    if (rc) return rc;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set[2];  // per instantiation, one bit per device
+  int32_t rc = allow_lds_once((const void*)prefill_kernel<false>, kLdsBytes, &lds_set[0],
+                              "ema_prefill_attention: LDS attribute");
+  if (rc) return rc;
+  rc = allow_lds_once((const void*)prefill_kernel<true>, kLdsBytes, &lds_set[1], "ema_prefill_attention: LDS attribute");
+  if (rc) return rc;
   PrefillArgs a;
   a.q = (const uint16_t*)q;
   a.k = (const uint16_t*)c.k;
@@ -651,13 +645,7 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
   a.nqb = (T + kBM - 1) / kBM;
   a.flags = flags;
   // pair the query blocks when there are at least two workgroups' worth per CU
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-  }
+  const int cus = device_cus();
   const int64_t items = (int64_t)a.nqb * Hq * c.batch;
   a.paired = a.nqb >= 2 && items >= 2 * (int64_t)cus;
   const int64_t blocks = a.paired ? (int64_t)((a.nqb + 1) / 2) * Hq * c.batch : items;

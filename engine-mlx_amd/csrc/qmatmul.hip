@@ -533,14 +533,10 @@ QmvPlan plan_qmv(int N, int K, int gs, int bits, int mx, int cus) {
 
 template <int BITS, int GS, bool F16, int MX, int NT>
 int32_t launch_qmv(hipStream_t st, const QmmArgs& a, const QmvPlan& p) {
-  static bool attr_set = false;  // each instantiation allows its LDS above 64 KB once
-  if (!attr_set) {
-    const int32_t rc = check_hip(hipFuncSetAttribute((const void*)qmv_kernel<BITS, GS, F16, MX, NT>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kQmvMaxLds),
-                                 "quantized_matmul: LDS attribute");
-    if (rc) return rc;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};  // this instantiation's LDS above 64 KB, per device
+  const int32_t rc = allow_lds_once((const void*)qmv_kernel<BITS, GS, F16, MX, NT>, kQmvMaxLds, &lds_set,
+                                    "quantized_matmul: LDS attribute");
+  if (rc) return rc;
   hipLaunchKernelGGL((qmv_kernel<BITS, GS, F16, MX, NT>), dim3((a.N + 16 * NT - 1) / (16 * NT)),
                      dim3(64 * kMaxWaves), p.bytes, st, a, p);
   return check_hip(hipGetLastError(), "quantized_matmul launch");
@@ -753,14 +749,10 @@ QgemmPlan plan_qgemm(int M, int N, int K, int gs, int bits) {
 
 template <int BITS, int GS, bool F16>
 int32_t launch_qgemm(hipStream_t st, const QmmArgs& a, const QgemmPlan& p) {
-  static bool attr_set = false;  // each instantiation allows its LDS above 64 KB once
-  if (!attr_set) {
-    const int32_t rc = check_hip(hipFuncSetAttribute((const void*)qgemm_kernel<BITS, GS, F16>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kQmvMaxLds),
-                                 "quantized_matmul: LDS attribute");
-    if (rc) return rc;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};  // this instantiation's LDS above 64 KB, per device
+  const int32_t rc = allow_lds_once((const void*)qgemm_kernel<BITS, GS, F16>, kQmvMaxLds, &lds_set,
+                                    "quantized_matmul: LDS attribute");
+  if (rc) return rc;
   const unsigned tiles = (unsigned)(p.ntiles * ((a.M + 127) / 128));
   hipLaunchKernelGGL((qgemm_kernel<BITS, GS, F16>), dim3(tiles), dim3(64 * kGemmWaves), p.bytes, st, a, p);
   return check_hip(hipGetLastError(), "quantized_matmul launch");
@@ -907,14 +899,7 @@ template <int BITS, int GS, bool F16>
 int32_t launch_t(hipStream_t st, QmmArgs a) {
   int nw = a.G / 8;  // waves per workgroup: about 8 groups each, at most 8 waves
   nw = nw < 1 ? 1 : nw > kMaxWaves ? kMaxWaves : nw;
-  static int cus = 0;  // compute units of the device (queried once)
-  if (!cus) {
-    int dev = 0, n = 0;
-    cus = hipGetDevice(&dev) == hipSuccess &&
-                  hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
-              ? n
-              : 256;
-  }
+  const int cus = device_cus();
   if (a.M == 1 && gemv1_fits(a.G, a.K)) return launch_gemv1<BITS, GS, F16>(st, a, cus);
   if (a.M <= 32) {
     const int mx = qmv_rows(a.M);
