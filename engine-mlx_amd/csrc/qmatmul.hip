@@ -531,6 +531,196 @@ QmvPlan plan_qmv(int N, int K, int gs, int bits, int mx, int cus) {
   return none;
 }
 
+// Variant for 16 or 32 rows of x: the weights, scales and biases are staged in LDS as in
+// qmv_kernel (all of K, one round of DMA and one barrier), but x does not pass through LDS:
+// each wave loads its own x straight into registers in MFMA layout, kXD groups ahead and
+// in the order it consumes them, so no chunk barrier stalls the waves on an L2 round trip.
+constexpr int kXD = 4;
+
+template <int BITS, int GS, bool F16, int MX, int NT>
+__global__ __launch_bounds__(64 * kMaxWaves) void qmvx_kernel(QmmArgs a, QmvPlan p) {
+  using F = Fields<BITS, F16>;
+  constexpr int MR = MX > 16 ? 2 : 1;
+  constexpr int kSteps = GS / 32;
+  constexpr int kWDw = GS * BITS / 128;
+  constexpr uint32_t kWBytes = GS * BITS / 8;
+  constexpr int kRows = 16 * NT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+
+  const int n0 = blockIdx.x * kRows;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = kMaxWaves;
+  const int rows_n = min(kRows, a.N - n0), rows_m = min(MX, a.M);
+  const uint32_t wrow = (uint32_t)a.K * BITS / 8;
+  const uint32_t G2 = (uint32_t)a.G * 2;
+  const u32x4 W = rsrc4(a.w + (int64_t)n0 * wrow, rows_n * wrow);
+  const u32x4 S = rsrc4(a.s + (int64_t)n0 * G2, rows_n * G2);
+  const u32x4 B = rsrc4(a.b + (int64_t)n0 * G2, rows_n * G2);
+  const auto X = rsrc(a.x, (rows_m - 1) * (uint32_t)a.ldx * 2 + (uint32_t)a.K * 2);
+
+  // ---- stage all weights (the plan's chunks back to back: Uc = U) and scales
+  for (uint32_t i = wave; i < p.nW + 2 * p.nS; i += nw) {
+    if (i < p.nW) {
+      const uint32_t per_rb = 8 * p.U, rb = (64 * i) / per_rb, first = 64 * i - rb * per_rb, rem = first + lane;
+      const uint32_t row = rb * 8 + (rem & 7), u = rem >> 3;
+      dma16(W, row < (uint32_t)rows_n ? row * wrow + 16 * u : kOffRow,
+            __builtin_amdgcn_readfirstlane(lds0 + rb * p.rb_bytes + 16 * first));
+    } else {
+      const uint32_t j = i - p.nW, jj = j % p.nS, q = 64 * jj + lane, g8 = q / kRows, row = q % kRows;
+      const bool ok = row < (uint32_t)rows_n && 8 * g8 < (uint32_t)a.G;
+      dma16(j < p.nS ? S : B, ok ? row * G2 + 16 * g8 : kOffRow,
+            __builtin_amdgcn_readfirstlane(lds0 + (j < p.nS ? p.s_off : p.b_off) + 1024 * jj));
+    }
+  }
+
+  // ---- wave -> column tile t and a contiguous range of groups
+  const int per_t = nw / NT, t = wave / per_t, wt = wave % per_t;
+  const int g0 = (wt * a.G) / per_t, g1 = ((wt + 1) * a.G) / per_t;
+  const int c16 = lane & 15, j = lane >> 4;
+  const int row = 16 * t + c16;
+  uint32_t xoff[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    const int xr = 16 * r + c16;
+    xoff[r] = xr < rows_m ? xr * (uint32_t)a.ldx * 2 + j * (GS / 2) : kOffRow;
+  }
+  uint32_t xd[kXD][MR][kSteps][4];
+  auto issue_x = [&](int slot, int g) {  // groups past g1 read zeros (and are not used)
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) {
+        const uint32_t off = g < g1 && xoff[r] != kOffRow ? xoff[r] + g * (GS * 2) + 16 * st : kOffRow;
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(X, off, 0, 0);
+        xd[slot][r][st][0] = v[0];
+        xd[slot][r][st][1] = v[1];
+        xd[slot][r][st][2] = v[2];
+        xd[slot][r][st][3] = v[3];
+      }
+  };
+#pragma unroll
+  for (int i = 0; i < kXD; ++i) {
+    issue_x(i, g0 + i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the DMA came before those loads: wait for it alone, then publish the weights
+  wait_vmcnt((uint32_t)(kXD * MR * kSteps));
+  __syncthreads();
+
+  const uint8_t* wbase = smem + (row >> 3) * p.rb_bytes + 16 * (row & 7);
+  const u32x4 ones = {F::kOnes, F::kOnes, F::kOnes, F::kOnes};
+  f32x4 tot[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int turns = (g1 - g0 + kXD - 1) / kXD;
+  for (int turn = 0; turn < turns; ++turn) {
+#pragma unroll
+    for (int i = 0; i < kXD; ++i) {
+      const int g = g0 + turn * kXD + i;
+      if (g < g1) {
+        uint32_t wd[kWDw];
+        const uint32_t bo = g * kWBytes + j * (kWBytes / 4);
+        if constexpr (kWDw <= 4) {
+          const uint8_t* q = wbase + 128 * (bo >> 4) + (bo & 15);
+#pragma unroll
+          for (int e = 0; e < kWDw; ++e) wd[e] = reinterpret_cast<const uint32_t*>(q)[e];
+        } else {
+          const uint8_t* q = wbase + 128 * (bo >> 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wd[e] = reinterpret_cast<const uint32_t*>(q)[e];
+#pragma unroll
+          for (int e = 0; e < kWDw - 4; ++e) wd[4 + e] = reinterpret_cast<const uint32_t*>(q + 128)[e];
+        }
+        const uint32_t so = 16 * ((g >> 3) * kRows + row) + 2 * (g & 7);
+        const float sc = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.s_off + so));
+        const float bc = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.b_off + so)) - F::kOff * sc;
+        f32x4 aq[MR], a1[MR];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) aq[r] = a1[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+          const u32x4 Bw = F::weights(wd, st);
+#pragma unroll
+          for (int r = 0; r < MR; ++r) {
+            const u32x4 A = F::acts(xd[i][r][st]);
+            aq[r] = mma<F16>(A, Bw, aq[r]);
+            a1[r] = mma<F16>(A, ones, a1[r]);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) tot[r][q] = fmaf(sc, aq[r][q], fmaf(bc, a1[r][q], tot[r][q]));
+      }
+      issue_x(i, g + kXD);  // the slot's registers are dead once the MFMAs have read them
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- sum the partial tiles of each column tile's waves
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[(wave * MR + r) * 256 + (4 * j + q) * 16 + c16] = tot[r][q];
+  __syncthreads();
+  for (int e = threadIdx.x; e < NT * MR * 256; e += 64 * nw) {
+    const int tt = e / (MR * 256), r = (e / 256) % MR, rr = (e >> 4) & 15, col = e & 15;
+    float v = 0.0f;
+    for (int w = 0; w < per_t; ++w) v += red[((tt * per_t + w) * MR + r) * 256 + (e & 255)];
+    const int m = 16 * r + rr, n = 16 * tt + col;
+    if (m < rows_m && n < rows_n)
+      reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.ldy + n0 + n] = f32_to_act<F16>(v);
+  }
+}
+
+// Plan of qmvx_kernel: all weights and scales of 16 NT rows in LDS (x not staged).
+QmvPlan plan_qmvx(int N, int K, int gs, int bits, int cus) {
+  QmvPlan none{};
+  none.NC = 0;
+  if ((K / gs) % 8 != 0 || (K * bits / 128) % 8 != 0) return none;
+  const int G = K / gs;
+  const int nt0 = (N + 15) / 16 > cus ? 2 : 1;
+  for (int nt = nt0; nt >= 1; --nt) {
+    const int rows = 16 * nt;
+    QmvPlan q{};
+    q.NT = nt;
+    q.KCH = K;
+    q.NC = 1;
+    q.NB = 1;
+    q.U = (uint32_t)K * bits / 128;
+    q.Uc = q.U;
+    q.rb_bytes = q.U * 128 + 128;
+    q.nW = (uint32_t)rows * q.U / 64;
+    q.nX = 0;
+    q.x_slot = 0;
+    q.nS = ((uint32_t)rows * (G / 8) + 63) / 64;
+    q.x_off = ((2 * nt) * q.rb_bytes + 1023) & ~1023u;
+    q.s_off = q.x_off;
+    q.b_off = q.s_off + 1024 * q.nS;
+    q.z_off = q.b_off + 1024 * q.nS;
+    q.bytes = q.z_off + 16;
+    const uint32_t red = (uint32_t)kMaxWaves * 2 * 1024;
+    if (q.bytes < red) q.bytes = red;
+    if (q.bytes <= kQmvMaxLds) return q;
+  }
+  return none;
+}
+
+template <int BITS, int GS, bool F16, int MX, int NT>
+int32_t launch_qmvx(hipStream_t st, const QmmArgs& a, const QmvPlan& p) {
+  static std::atomic<uint64_t> lds_set{0};  // this instantiation's LDS above 64 KB, per device
+  const int32_t rc = allow_lds_once((const void*)qmvx_kernel<BITS, GS, F16, MX, NT>, kQmvMaxLds, &lds_set,
+                                    "quantized_matmul: LDS attribute");
+  if (rc) return rc;
+  hipLaunchKernelGGL((qmvx_kernel<BITS, GS, F16, MX, NT>), dim3((a.N + 16 * NT - 1) / (16 * NT)),
+                     dim3(64 * kMaxWaves), p.bytes, st, a, p);
+  return check_hip(hipGetLastError(), "quantized_matmul launch");
+}
+
 template <int BITS, int GS, bool F16, int MX, int NT>
 int32_t launch_qmv(hipStream_t st, const QmmArgs& a, const QmvPlan& p) {
   static std::atomic<uint64_t> lds_set{0};  // this instantiation's LDS above 64 KB, per device
@@ -904,6 +1094,19 @@ int32_t launch_t(hipStream_t st, QmmArgs a) {
   if (a.M <= 32) {
     const int mx = qmv_rows(a.M);
     const QmvPlan p = plan_qmv(a.N, a.K, GS, BITS, mx, cus);
+    if (mx >= 16) {
+      // x through an LDS ring shared by the column tiles (qmv_kernel) when it reaches the
+      // wanted tile count, else x through registers (qmvx_kernel), whose LDS holds only
+      // the weights (measured: 4-bit q|k|v at 32 rows 14.9 us against 19.9; 8-bit, where
+      // only qmvx_kernel fits two tiles, 21.9 against 23.7)
+      const int want = (a.N + 15) / 16 > cus ? 2 : 1;
+      const QmvPlan px = p.NC > 0 && p.NT == want ? QmvPlan{} : plan_qmvx(a.N, a.K, GS, BITS, cus);
+      if (px.NC > 0 && (p.NC == 0 || px.NT == want)) {
+        if (mx == 16)
+          return px.NT == 2 ? launch_qmvx<BITS, GS, F16, 16, 2>(st, a, px) : launch_qmvx<BITS, GS, F16, 16, 1>(st, a, px);
+        return px.NT == 2 ? launch_qmvx<BITS, GS, F16, 32, 2>(st, a, px) : launch_qmvx<BITS, GS, F16, 32, 1>(st, a, px);
+      }
+    }
     if (p.NC > 0) return launch_qmv_rows<BITS, GS, F16>(st, a, mx, p);
   } else {
     const QgemmPlan p = plan_qgemm(a.M, a.N, a.K, GS, BITS);

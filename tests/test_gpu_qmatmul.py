@@ -88,6 +88,17 @@ def test_qmatmul_qwen3_8b_qkv_decode_shape(ema, ora, M, N, bits):
     check(ora, y, h, gs, bits, "8B qkv", bar=True)
 
 
+@pytest.mark.parametrize("M,gs,dtype", [(20, 128, "bf16"), (12, 64, "f16")])
+def test_qmatmul_8bit_wide_rows_x_in_registers(ema, ora, M, gs, dtype):
+    # 8-bit weights of two 16-row column tiles fill most of the LDS, so x streams through
+    # registers (qmvx_kernel); ragged rows of x
+    N, K, bits = 6144, 4096, 8
+    say(f"qmatmul 8-bit M={M} N={N} K={K} gs={gs} {dtype}")
+    d, h = make(ora, 60 + M, M, N, K, gs, bits, dtype)
+    y = ema.quantized_matmul(*d, group_size=gs, bits=bits)
+    check(ora, y, h, gs, bits, f"M={M}", dtype)
+
+
 @pytest.mark.parametrize("M,N,K,gs,bits,dtype", [
     (64, 256, 1024, 64, 4, "bf16"),     # tiled GEMM: one 128-row tile, several column tiles
     (300, 256, 1024, 64, 4, "bf16"),    # ragged last row tile
