@@ -10,7 +10,10 @@
 // Work split. The valid rows of every (sequence b, kv head kh) pair form a
 // "segment" of ceil(len_b / 32) tiles of 32 positions. All segments are laid
 // end to end and the flattened tile range is cut into W equal slices, one per
-// workgroup, so ragged lengths cost no load imbalance. A workgroup walks its
+// workgroup, so ragged lengths cost no load imbalance. W is taken on the device
+// from the actual tile count (one tile per wave at least, at most the host plan's
+// workers, which size the workspace for the upper bound of the lengths), so short
+// sequences in a long cache are not cut into more pieces than they have waves. A workgroup walks its
 // slice; each maximal run inside one segment is a "piece". The four waves of
 // the workgroup take the piece's tiles in turn, each keeping its own
 // online-softmax state, and combine the four states through LDS at the end of
@@ -80,6 +83,15 @@ struct DecodeArgs {
 __device__ __forceinline__ int64_t worker_of(int64_t t, int64_t total, int W) {
   return ((t + 1) * (int64_t)W - 1) / total;
 }
+// Workers used for `total` tiles (the tiles of the actual lengths, known on the device):
+// at least one tile per wave of each workgroup, at most the plan's W (which sizes the
+// workspace from the host's upper bound of the lengths). The decode and merge kernels
+// both derive it from the same values.
+__device__ __forceinline__ int active_workers(int64_t total, int W) {
+  const int64_t want = (total + kWaves - 1) / kWaves;
+  return (int)(want < W ? want : W);
+}
+
 __device__ __forceinline__ int64_t worker_begin(int64_t w, int64_t total, int W) {
   return w * total / W;
 }
@@ -244,8 +256,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int w = blockIdx.x;
   const int64_t total = pre[a.B];
-  // never more workers than tiles, so every worker's slice is non-empty
-  const int W = (int)(total < a.W ? total : a.W);
+  const int W = active_workers(total, a.W);
   if (w >= W) return;
   int64_t t = worker_begin(w, total, W);
   const int64_t t_end = worker_begin(w + 1, total, W);
@@ -606,7 +617,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int L = seq_len(a, b);
   const int64_t total = a.hdr[a.B];  // tile prefix published by decode_kernel
   if (L == 0 || total == 0) return;
-  const int W = (int)(total < a.W ? total : a.W);
+  const int W = active_workers(total, a.W);
   const int nb = (L + kTile - 1) / kTile;
   const int64_t seg_first = a.hdr[b] + (int64_t)kh * nb;
   const int64_t w0 = worker_of(seg_first, total, W);
