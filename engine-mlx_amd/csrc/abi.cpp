@@ -67,14 +67,28 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
   if (!c) return set_error(EMA_ERR_INVALID_ARG, "%s: cache descriptor is null", op);
   if (!c->k || !c->v) return set_error(EMA_ERR_INVALID_ARG, "%s: KV cache is empty (null K/V buffer)", op);
-  if (c->dtype != EMA_DTYPE_BF16 && c->dtype != EMA_DTYPE_FP8_E4M3)
-    return set_error(EMA_ERR_INVALID_ARG, "%s: cache dtype %d is neither bf16 nor fp8 e4m3", op, c->dtype);
+  if (c->dtype != EMA_DTYPE_BF16 && c->dtype != EMA_DTYPE_FP8_E4M3 && c->dtype != EMA_DTYPE_INT4_AFFINE)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: cache dtype %d is not bf16, fp8 e4m3 or int4 affine", op, c->dtype);
   if (c->dtype == EMA_DTYPE_FP8_E4M3) {
     if (!c->k_exp || !c->v_exp) return set_error(EMA_ERR_INVALID_ARG, "%s: fp8 cache without block exponents", op);
     if (c->head_dim != 128)
       return set_error(EMA_ERR_UNSUPPORTED, "%s: fp8 cache with head_dim %d not supported (128)", op, c->head_dim);
     if (c->stride_pos % 16 || c->stride_head % 16 || c->stride_batch % 16)
       return set_error(EMA_ERR_SHAPE, "%s: fp8 cache strides must be multiples of 16 bytes", op);
+  }
+  if (c->dtype == EMA_DTYPE_INT4_AFFINE) {
+    if (!c->k_scales || !c->k_biases || !c->v_scales || !c->v_biases)
+      return set_error(EMA_ERR_INVALID_ARG, "%s: int4 cache without scales/biases", op);
+    if (!aligned16(c->k_scales) || !aligned16(c->k_biases) || !aligned16(c->v_scales) || !aligned16(c->v_biases))
+      return set_error(EMA_ERR_INVALID_ARG, "%s: int4 scales/biases must be 16-byte aligned", op);
+    if (c->head_dim != 128)
+      return set_error(EMA_ERR_UNSUPPORTED, "%s: int4 cache with head_dim %d not supported (128)", op, c->head_dim);
+    if (c->capacity % 32)
+      return set_error(EMA_ERR_UNSUPPORTED, "%s: int4 cache capacity %d is not a multiple of 32", op, c->capacity);
+    if (c->flags & EMA_KV_ROTATING)
+      return set_error(EMA_ERR_UNSUPPORTED, "%s: rotating int4 caches are not supported", op);
+    if (c->stride_pos % 32 || c->stride_head % 32 || c->stride_batch % 32)
+      return set_error(EMA_ERR_SHAPE, "%s: int4 cache strides must be multiples of 32 elements (16 bytes)", op);
   }
   if (c->flags & ~EMA_KV_ROTATING) return set_error(EMA_ERR_INVALID_ARG, "%s: unknown cache flags 0x%x", op, c->flags);
   if (c->batch <= 0 || c->n_kv_heads <= 0 || c->capacity <= 0 || c->head_dim <= 0)
@@ -190,11 +204,80 @@ int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv
   return ema_kvcache_init_fp8(out, p[0], p[1], p[2], p[3], batch, n_kv_heads, capacity, head_dim);
 }
 
+int32_t ema_kvcache_init_int4(ema_kvcache_desc* d, void* k, void* v, void* k_scales, void* k_biases,
+                              void* v_scales, void* v_biases, int32_t batch, int32_t n_kv_heads, int32_t capacity,
+                              int32_t head_dim) {
+  if (!d) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_init_int4: descriptor is null");
+  memset(d, 0, sizeof(*d));
+  d->k = k;
+  d->v = v;
+  d->k_scales = k_scales;
+  d->k_biases = k_biases;
+  d->v_scales = v_scales;
+  d->v_biases = v_biases;
+  d->batch = batch;
+  d->n_kv_heads = n_kv_heads;
+  d->capacity = capacity;
+  d->head_dim = head_dim;
+  d->stride_pos = head_dim;  // in 4-bit elements
+  d->stride_head = (int64_t)capacity * head_dim;
+  d->stride_batch = (int64_t)n_kv_heads * capacity * head_dim;
+  d->dtype = EMA_DTYPE_INT4_AFFINE;
+  return check_cache("ema_kvcache_init_int4", d);
+}
+
+int32_t ema_kvcache_alloc_int4(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads, int32_t capacity,
+                               int32_t head_dim) {
+  const char* op = "ema_kvcache_alloc_int4";
+  if (!out) return set_error(EMA_ERR_INVALID_ARG, "%s: descriptor is null", op);
+  memset(out, 0, sizeof(*out));
+  if (batch <= 0 || n_kv_heads <= 0 || capacity <= 0 || head_dim != 128 || capacity % 32)
+    return set_error(head_dim > 0 && capacity > 0 ? EMA_ERR_UNSUPPORTED : EMA_ERR_SHAPE,
+                     "%s: bad dims (batch=%d n_kv_heads=%d capacity=%d head_dim=%d; int4 needs head_dim 128 and "
+                     "a capacity that is a multiple of 32)", op, batch, n_kv_heads, capacity, head_dim);
+  const size_t rows = (size_t)batch * n_kv_heads * capacity;
+  const size_t word_bytes = rows * head_dim / 2, meta_bytes = rows * (head_dim / 64) * 2;
+  void* p[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  const size_t sz[6] = {word_bytes, word_bytes, meta_bytes, meta_bytes, meta_bytes, meta_bytes};
+  int32_t rc = EMA_OK;
+  for (int i = 0; i < 6 && !rc; ++i) {
+    rc = check_hip(hipMalloc(&p[i], sz[i]), "ema_kvcache_alloc_int4: hipMalloc");
+    if (!rc) rc = check_hip(hipMemset(p[i], 0, sz[i]), "ema_kvcache_alloc_int4: zero");
+  }
+  if (rc) {
+    for (int i = 0; i < 6; ++i)
+      if (p[i]) (void)hipFree(p[i]);
+    return rc;
+  }
+  return ema_kvcache_init_int4(out, p[0], p[1], p[2], p[3], p[4], p[5], batch, n_kv_heads, capacity, head_dim);
+}
+
+int32_t ema_kvcache_quantize_int4(ema_stream_t stream, const ema_kvcache_desc* src, int32_t src_row,
+                                  const ema_kvcache_desc* dst, int32_t dst_row, int32_t n_rows) {
+  const char* op = "ema_kvcache_quantize_int4";
+  int32_t rc = check_cache(op, src);
+  if (rc) return rc;
+  if ((rc = check_cache(op, dst))) return rc;
+  if (src->dtype != EMA_DTYPE_BF16 || dst->dtype != EMA_DTYPE_INT4_AFFINE)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: needs a bf16 source and an int4 destination (dtypes %d, %d)", op,
+                     src->dtype, dst->dtype);
+  if (src->batch != dst->batch || src->n_kv_heads != dst->n_kv_heads || src->head_dim != dst->head_dim)
+    return set_error(EMA_ERR_SHAPE, "%s: source (%d, %d, %d) and destination (%d, %d, %d) shapes differ", op,
+                     src->batch, src->n_kv_heads, src->head_dim, dst->batch, dst->n_kv_heads, dst->head_dim);
+  if (n_rows < 0 || src_row < 0 || dst_row < 0 || (int64_t)src_row + n_rows > src->capacity ||
+      (int64_t)dst_row + n_rows > dst->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: rows [%d, +%d) of the source (capacity %d) or [%d, +%d) of the "
+                     "destination (capacity %d) out of range", op, src_row, n_rows, src->capacity, dst_row, n_rows,
+                     dst->capacity);
+  if (n_rows == 0) return EMA_OK;
+  return launch_quantize_int4((hipStream_t)stream, *src, src_row, *dst, dst_row, n_rows);
+}
+
 int32_t ema_kvcache_free(ema_kvcache_desc* d) {
   if (!d) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_free: descriptor is null");
   int32_t rc = EMA_OK;
-  void* const bufs[4] = {d->k, d->v, d->k_exp, d->v_exp};
-  for (int i = 0; i < 4; ++i)
+  void* const bufs[8] = {d->k, d->v, d->k_exp, d->v_exp, d->k_scales, d->k_biases, d->v_scales, d->v_biases};
+  for (int i = 0; i < 8; ++i)
     if (bufs[i]) {
       const int32_t r2 = check_hip(hipFree(bufs[i]), "ema_kvcache_free");
       rc = rc ? rc : r2;
@@ -208,7 +291,9 @@ int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* d, uint64_t* bytes) {
   int32_t rc = check_cache("ema_kvcache_memory_bytes", d);
   if (rc) return rc;
   const uint64_t rows = 2ull * d->batch * d->n_kv_heads * d->capacity;  // K and V
-  *bytes = d->dtype == EMA_DTYPE_FP8_E4M3 ? rows * (d->head_dim + d->head_dim / 64) : rows * d->head_dim * 2ull;
+  if (d->dtype == EMA_DTYPE_FP8_E4M3) *bytes = rows * (d->head_dim + d->head_dim / 64);
+  else if (d->dtype == EMA_DTYPE_INT4_AFFINE) *bytes = rows * (d->head_dim / 2 + 4ull * (d->head_dim / 64));
+  else *bytes = rows * d->head_dim * 2ull;
   return EMA_OK;
 }
 
@@ -341,6 +426,9 @@ int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_k
                      n_tokens, cache->capacity);
   if (cache->dtype == EMA_DTYPE_BF16)
     return launch_prefill((hipStream_t)stream, q, *cache, q_offsets, n_tokens, n_heads, scale, flags, out);
+  if (cache->dtype == EMA_DTYPE_INT4_AFFINE)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over an int4 cache is not supported (attend a bf16 cache and "
+                     "store the rows with ema_kvcache_quantize_int4)", op);
   if (cache->flags & EMA_KV_ROTATING)
     return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over a rotating fp8 cache is not supported", op);
   const uint64_t need = prefill_ws_bytes(cache, max_kv_len);
@@ -384,7 +472,8 @@ int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvca
   if (!(scale > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: scale must be > 0", op);
   if (!aligned16(q) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: q/out must be 16-byte aligned", op);
   if (cache->dtype != EMA_DTYPE_BF16)
-    return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over an fp8 cache is not supported (bf16 only)", op);
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over an %s cache is not supported (bf16 only)", op,
+                     cache->dtype == EMA_DTYPE_FP8_E4M3 ? "fp8" : "int4");
   return launch_prefill((hipStream_t)stream, q, *cache, q_offsets, n_tokens, n_heads, scale, flags, out);
 }
 

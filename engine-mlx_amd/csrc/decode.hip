@@ -78,6 +78,12 @@ struct DecodeArgs {
   // fp8 cache: block exponents [B, Hkv, cap, 2] (k, v then hold E4M3FN codes)
   const int8_t* kexp;
   const int8_t* vexp;
+  // int4 cache: (group 0, group 1) bf16 scale and bias pairs [B, Hkv, cap] (k, v then hold
+  // the packed codes; strides count 4-bit elements)
+  uint32_t* ks;
+  uint32_t* kb;
+  uint32_t* vs;
+  uint32_t* vb;
 };
 
 __device__ __forceinline__ int64_t worker_of(int64_t t, int64_t total, int W) {
@@ -173,6 +179,44 @@ __device__ __forceinline__ uint32_t fp8_quant_lane(float x, int* e_out, uint16_t
   return code;
 }
 
+// ---- int4 cache ----
+// The codes enter the MFMAs exactly as bf16 values 128 + code (0x4300 | code), and the
+// affine parameters are applied around them:
+//   scores: S[p, g] = sum_grp s_grp[p] acc_grp[p, g] + (b_grp[p] - 128 s_grp[p]) Qsum_grp[g]
+//     with acc_grp the MFMA sum over the group's 64 dims of (128 + code) q and Qsum_grp the
+//     sum of the (bf16) q over those dims;
+//   output: O[d, g] = sum_p (128 + code[p, d]) P'_grp[p, g] + sum_p (P[p, g] b_grp[p] - 128
+//     P'_grp[p, g]) with P'_grp = bf16(P s_grp) as the B operand.
+// Both use the exact affine values s * code + b (no bf16 rounding of K and V).
+//
+// (x & m) | c in one v_and_or_b32 (gfx950's VOP3 takes no literal; the constants stay in
+// VGPRs as asm operands).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
+  return r;
+}
+// The 8 codes of a word (value i at bits 4i) as the bf16 A-operand registers of one MFMA
+// step, k-slot order (0, 4), (1, 5), (2, 6), (3, 7).
+__device__ __forceinline__ bf16x8 i4_kop(uint32_t w) {
+  u32x4 r;
+  r[0] = and_or(w, 0x000F000Fu, 0x43004300u);
+  r[1] = and_or(w >> 4, 0x000F000Fu, 0x43004300u);
+  r[2] = and_or(w >> 8, 0x000F000Fu, 0x43004300u);
+  r[3] = and_or(w >> 12, 0x000F000Fu, 0x43004300u);
+  return as_bf16x8(r);
+}
+// bf16 pairs (0, 1), (2, 3), (4, 5), (6, 7) -> (0, 4), (1, 5), (2, 6), (3, 7): the q operand in
+// the k-slot order of i4_kop
+__device__ __forceinline__ u32x4 i4_qperm(u32x4 w) {
+  u32x4 r;
+  r[0] = (w[0] & 0xffffu) | (w[2] << 16);
+  r[1] = (w[0] >> 16) | (w[2] & 0xffff0000u);
+  r[2] = (w[1] & 0xffffu) | (w[3] << 16);
+  r[3] = (w[1] >> 16) | (w[3] & 0xffff0000u);
+  return r;
+}
+
 // LDS used to combine the four waves' states at the end of a piece.
 struct Combine {
   float m[kWaves][16];
@@ -233,8 +277,9 @@ __device__ __forceinline__ void unpack32(const u32x4 (&r)[4], float (&x)[32]) {
     for (int j = 0; j < 8; ++j) x[8 * s + j] = (j & 1) ? bf16_hi(r[s][j >> 1]) : bf16_lo(r[s][j >> 1]);
 }
 
-template <bool kFused, bool kFp8>
+template <bool kFused, bool kFp8, bool kI4 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
+  constexpr bool kNarrow = kFp8 || kI4;  // the fp8 head-dim order (kdim)
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
   __shared__ float2 rope_cs[kWaves][kD / 2];  // fused: each wave's RoPE (cos, sin) table at the offset
@@ -341,6 +386,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         vr[kk] = ld16_stream(Vb + (int64_t)p * a.sp + 8 * m);
       }
     };
+    // int4: per tile a lane loads the words of its two K rows (steps 2i, 2i+1: dims
+    // 64i + 16c .. +15, one 8-byte load), the word of dims 8m .. 8m+7 of each of its 8 V
+    // positions, and the scale and bias pairs of its 8 score positions p0 + 8c + 4h + e
+    // (16 bytes per 4 positions; the capacity is a multiple of 32, so these stay inside the
+    // cache, and positions past L are masked where they are used)
+    const uint8_t* const Kb4 = (const uint8_t*)a.k + ((int64_t)b * a.sb + (int64_t)kh * a.sh) / 2;
+    const uint8_t* const Vb4 = (const uint8_t*)a.v + ((int64_t)b * a.sb + (int64_t)kh * a.sh) / 2;
+    const int64_t sp4 = a.sp / 2;
+    u32x2 k4[2][2], k4n[2][2];
+    uint32_t v4[8], v4n[8];
+    u32x4 mk[2][2], mkn[2][2], mv[2][2], mvn[2][2];  // [scale | bias][h]
+    auto load_tile4 = [&](int tile, u32x2 (&kr)[2][2], uint32_t (&vr)[8], u32x4 (&mkr)[2][2], u32x4 (&mvr)[2][2]) {
+      const int p0 = tile * kTile;
+      for (int r = 0; r < 2; ++r) {
+        int p = p0 + krow0 + 4 * r;
+        p = p < L ? p : L - 1;
+        const uint8_t* row = Kb4 + (int64_t)p * sp4;
+        for (int i = 0; i < 2; ++i) kr[r][i] = __builtin_nontemporal_load((const u32x2*)(row + 32 * i + 8 * c));
+      }
+      for (int kk = 0; kk < 8; ++kk) {
+        int p = p0 + 8 * c + kk;
+        p = p < L ? p : L - 1;
+        vr[kk] = __builtin_nontemporal_load((const uint32_t*)(Vb4 + (int64_t)p * sp4 + 4 * m));
+      }
+      const int64_t pm = erow + p0 + 8 * c;
+      for (int h = 0; h < 2; ++h) {
+        mkr[0][h] = __builtin_nontemporal_load((const u32x4*)(a.ks + pm + 4 * h));
+        mkr[1][h] = __builtin_nontemporal_load((const u32x4*)(a.kb + pm + 4 * h));
+        mvr[0][h] = __builtin_nontemporal_load((const u32x4*)(a.vs + pm + 4 * h));
+        mvr[1][h] = __builtin_nontemporal_load((const u32x4*)(a.vb + pm + 4 * h));
+      }
+    };
 
     // q loads, then this wave's first tile loads, then the q work: the work below
     // runs while the tile is in flight. B operand Q^T: step s <-> dims kdim(s, c) .. +7;
@@ -352,7 +429,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                 : a.q + ((int64_t)b * a.Hq + (int64_t)kh * a.G + gc) * kD;
     u32x4 qraw[4], qwv[4];
     uint16_t kr1 = 0, kr2 = 0, kw1 = 0, kw2 = 0, vr1 = 0, vr2 = 0;
-    for (int s = 0; s < 4; ++s) qraw[s] = ld16(qh + kdim<kFp8>(s, c));
+    for (int s = 0; s < 4; ++s) qraw[s] = ld16(qh + kdim<kNarrow>(s, c));
     // fused: the new k, v row goes to row w of the cache (the offset; offset % cap for a
     // rotating cache) when it is written at all (a static cache skips an offset past the
     // capacity). The wave that will run the tile holding row w forms the row; its inputs
@@ -369,7 +446,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // the norm weights may be null with EMA_PRE_NO_NORM: read only when used
       const bool norm = !(a.flags & EMA_PRE_NO_NORM);
       if (norm)
-        for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + kdim<kFp8>(s, c));
+        for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + kdim<kNarrow>(s, c));
       if (owner) {  // lane i: dims i and i + 64 (a RoPE pair)
         const uint16_t* kr = a.qkv + (int64_t)b * F + ((int64_t)a.Hq + kh) * kD;
         const uint16_t* vr = kr + (int64_t)a.Hkv * kD;
@@ -384,14 +461,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
     if (first < tile1) {
-      if (kFp8) load_tile8(first, k8, v8, ke, ve);
+      if (kI4) load_tile4(first, k4, v4, mk, mv);
+      else if (kFp8) load_tile8(first, k8, v8, ke, ve);
       else load_tile(first, kc, vc);
     }
     bf16x8 qop[4];
     const float2* const cs_tab = rope_cs[wave];
     if (!kFused) {
       const u32x4 z = {0u, 0u, 0u, 0u};
-      for (int s = 0; s < 4; ++s) qop[s] = as_bf16x8(g < a.G ? qraw[s] : z);
+      for (int s = 0; s < 4; ++s) qop[s] = as_bf16x8(g < a.G ? (kI4 ? i4_qperm(qraw[s]) : qraw[s]) : z);
     } else {
       // q = rope(norm(q_raw)) of this head, from the fused qkv row. Each wave forms the 64
       // RoPE angles of this sequence's offset into its own table (lane i: angle i), so no
@@ -408,11 +486,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float x[32];
       unpack32(qraw, x);
-      norm_rope<kFp8>(a, x, qwv, cs_tab);
+      norm_rope<kNarrow>(a, x, qwv, cs_tab);
       for (int s = 0; s < 4; ++s) {
         u32x4 v;
         for (int e = 0; e < 4; ++e) v[e] = g < a.G ? pack_bf16x2(x[8 * s + 2 * e], x[8 * s + 2 * e + 1]) : 0u;
-        qop[s] = as_bf16x8(v);
+        qop[s] = as_bf16x8(kI4 ? i4_qperm(v) : v);
       }
       if (owner) {
         // the new row (lane i: dims i, i + 64): k = rope(norm(k_raw)), v a bit copy; it
@@ -434,7 +512,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           k2 = r2;
         }
         const uint16_t kb1 = (uint16_t)f32_to_bf16_bits(k1), kb2 = (uint16_t)f32_to_bf16_bits(k2);
-        if (kFp8) {
+        if (kI4) {
+          // the row is quantised per 64-dim group (lane i holds dims i and i + 64) and kept
+          // in LDS in its stored form: K words 0..15, V words 16..31, then the K scale, K
+          // bias, V scale and V bias pairs
+          const float nv[4] = {bf16_to_f32(kb1), bf16_to_f32(kb2), bf16_to_f32(vr1), bf16_to_f32(vr2)};
+          uint32_t* const nw = (uint32_t*)&new_kv[0][0];
+          float sq[4], bq[4];
+          uint32_t cw4[4];
+          for (int q = 0; q < 4; ++q) {
+            float mn = nv[q], mx = nv[q];
+            for (int mm = 32; mm >= 1; mm >>= 1) {
+              mn = fminf(mn, __shfl_xor(mn, mm, 64));
+              mx = fmaxf(mx, __shfl_xor(mx, mm, 64));
+            }
+            i4_params(mn, mx, sq[q], bq[q]);
+            uint32_t t = i4_code(nv[q], sq[q], bq[q]) << (4 * (lane & 7));
+            t |= __shfl_xor(t, 1, 64);
+            t |= __shfl_xor(t, 2, 64);
+            t |= __shfl_xor(t, 4, 64);
+            cw4[q] = t;  // word lane / 8 of the group: dims 64 (q % 2) + 8 (lane / 8) .. +7
+          }
+          const int64_t roff = ((int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)w_row * a.sp) / 2;
+          uint32_t* const kd = (uint32_t*)((uint8_t*)a.k + roff);
+          uint32_t* const vd = (uint32_t*)((uint8_t*)a.v + roff);
+          if ((lane & 7) == 0) {
+            const int wi = lane >> 3;
+            nw[wi] = cw4[0];
+            nw[8 + wi] = cw4[1];
+            nw[16 + wi] = cw4[2];
+            nw[24 + wi] = cw4[3];
+            kd[wi] = cw4[0];
+            kd[8 + wi] = cw4[1];
+            vd[wi] = cw4[2];
+            vd[8 + wi] = cw4[3];
+          }
+          if (lane == 0) {
+            const uint32_t ksw = f32_to_bf16_bits(sq[0]) | (f32_to_bf16_bits(sq[1]) << 16);
+            const uint32_t kbw = f32_to_bf16_bits(bq[0]) | (f32_to_bf16_bits(bq[1]) << 16);
+            const uint32_t vsw = f32_to_bf16_bits(sq[2]) | (f32_to_bf16_bits(sq[3]) << 16);
+            const uint32_t vbw = f32_to_bf16_bits(bq[2]) | (f32_to_bf16_bits(bq[3]) << 16);
+            nw[32] = ksw;
+            nw[33] = kbw;
+            nw[34] = vsw;
+            nw[35] = vbw;
+            a.ks[erow + w_row] = ksw;
+            a.kb[erow + w_row] = kbw;
+            a.vs[erow + w_row] = vsw;
+            a.vb[erow + w_row] = vbw;
+          }
+        } else if (kFp8) {
           // the row is stored as E4M3FN codes and attended in its decoded form
           uint16_t d[4];
           int e[4];
@@ -474,21 +601,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
 
+    // int4: sums of the (bf16) q over each 64-dim group, per column g; the per-column
+    // output corrections (bias and code offset) of the two dim groups
+    float qs0 = 0.f, qs1 = 0.f, cor0 = 0.f, cor1 = 0.f;
+    if (kI4) {
+      for (int s = 0; s < 4; ++s) {
+        const u32x4 w = __builtin_bit_cast(u32x4, qop[s]);
+        float t = 0.f;
+        for (int e = 0; e < 4; ++e) t += bf16_lo(w[e]) + bf16_hi(w[e]);
+        if (s < 2) qs0 += t;
+        else qs1 += t;
+      }
+      qs0 += __shfl_xor(qs0, 16, 64);
+      qs0 += __shfl_xor(qs0, 32, 64);
+      qs1 += __shfl_xor(qs1, 16, 64);
+      qs1 += __shfl_xor(qs1, 32, 64);
+    }
+    // int4 V: lane m and lane m ^ 8 swap half words, so that nibble j of a lane's word is
+    // dim 64 (j / 4) + 8 (m % 8) + 4 (m / 8) + j % 4 and the first four nibbles are group 0
+    const uint32_t vsel = m < 8 ? 0x05040100u : 0x03020706u;
+
     for (int tile = first; tile < tile1; tile += kWaves) {
       const bool more = tile + kWaves < tile1;
-      if (kFp8) {
+      if (kI4) {
+        if (more) load_tile4(tile + kWaves, k4n, v4n, mkn, mvn);
+      } else if (kFp8) {
         if (more) load_tile8(tile + kWaves, k8n, v8n, ken, ven);
         decode_tile8();
       } else if (more) {
         load_tile(tile + kWaves, kn, vn);
       }
       const int p0 = tile * kTile;
-      if (kFused && owner && tile == w_tile) {
+      if (kI4 && kFused && owner && tile == w_tile) {
+        // the stored form of row w (LDS), into the registers that loaded it
+        const uint32_t* nw = (const uint32_t*)&new_kv[0][0];
+        for (int r = 0; r < 2; ++r) {
+          const int p = p0 + krow0 + 4 * r;
+          if ((p < L ? p : L - 1) == w_row)
+            for (int i = 0; i < 2; ++i) k4[r][i] = u32x2{nw[8 * i + 2 * c], nw[8 * i + 2 * c + 1]};
+        }
+        for (int kk = 0; kk < 8; ++kk) {
+          const int p = p0 + 8 * c + kk;
+          if ((p < L ? p : L - 1) == w_row) v4[kk] = nw[16 + m];
+        }
+        for (int h = 0; h < 2; ++h)
+          for (int e = 0; e < 4; ++e)
+            if (p0 + 8 * c + 4 * h + e == w_row) {
+              mk[0][h][e] = nw[32];
+              mk[1][h][e] = nw[33];
+              mv[0][h][e] = nw[34];
+              mv[1][h][e] = nw[35];
+            }
+      }
+      if (!kI4 && kFused && owner && tile == w_tile) {
         // rows whose (clamped) load position is w
         for (int r = 0; r < 2; ++r) {
           const int p = p0 + krow0 + 4 * r;
           if ((p < L ? p : L - 1) == w_row)
-            for (int s = 0; s < 4; ++s) kc[r][s] = *(const u32x4*)&new_kv[0][kdim<kFp8>(s, c)];
+            for (int s = 0; s < 4; ++s) kc[r][s] = *(const u32x4*)&new_kv[0][kdim<kNarrow>(s, c)];
         }
         for (int kk = 0; kk < 8; ++kk) {
           const int p = p0 + 8 * c + kk;
@@ -497,10 +667,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
 
       f32x4 sc[2];
-      for (int r = 0; r < 2; ++r) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < 4; ++s) acc = mfma16(as_bf16x8(kc[r][s]), qop[s], acc);
-        sc[r] = acc;
+      if (kI4) {
+        for (int r = 0; r < 2; ++r) {
+          f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+          acc0 = mfma16(i4_kop(k4[r][0][0]), qop[0], acc0);
+          acc0 = mfma16(i4_kop(k4[r][0][1]), qop[1], acc0);
+          acc1 = mfma16(i4_kop(k4[r][1][0]), qop[2], acc1);
+          acc1 = mfma16(i4_kop(k4[r][1][1]), qop[3], acc1);
+          // C row 4c + i of set r is position p0 + 8c + 4r + i: meta word [r][i]
+          for (int i = 0; i < 4; ++i) {
+            const float s0 = bf16_lo(mk[0][r][i]), s1 = bf16_hi(mk[0][r][i]);
+            const float b0 = bf16_lo(mk[1][r][i]), b1 = bf16_hi(mk[1][r][i]);
+            sc[r][i] = s0 * acc0[i] + s1 * acc1[i] + (b0 - 128.f * s0) * qs0 + (b1 - 128.f * s1) * qs1;
+          }
+        }
+      } else {
+        for (int r = 0; r < 2; ++r) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int s = 0; s < 4; ++s) acc = mfma16(as_bf16x8(kc[r][s]), qop[s], acc);
+          sc[r] = acc;
+        }
       }
       // running max on raw scores (scale > 0), exponent as one fma
       float x[8];
@@ -524,6 +710,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       l_run = l_run * alpha + psum;
       m_run = m_new;
       for (int j = 0; j < 8; ++j) o[j] *= alpha;
+
+      if (kI4) {
+        cor0 *= alpha;
+        cor1 *= alpha;
+        uint32_t cw[8];
+        for (int kk = 0; kk < 8; ++kk) {
+          const uint32_t pw = (uint32_t)__builtin_amdgcn_mov_dpp((int)v4[kk], 0x128, 0xF, 0xF, false);  // row_ror:8
+          cw[kk] = __builtin_amdgcn_perm(pw, v4[kk], vsel);
+        }
+        // B operands P'_grp = bf16(P s_grp) (0 past L, where the parameters are not read),
+        // k = 4h + e <-> position p0 + 8c + k
+        float pv0[8], pv1[8];
+        for (int k = 0; k < 8; ++k) {
+          const bool valid = p0 + 8 * c + k < L;
+          const uint32_t sw = valid ? mv[0][k >> 2][k & 3] : 0u;
+          const uint32_t bw = valid ? mv[1][k >> 2][k & 3] : 0u;
+          pv0[k] = x[k] * bf16_lo(sw);
+          pv1[k] = x[k] * bf16_hi(sw);
+          cor0 += x[k] * bf16_lo(bw);
+          cor1 += x[k] * bf16_hi(bw);
+        }
+        u32x4 pw0, pw1;
+        for (int e = 0; e < 4; ++e) {
+          pw0[e] = pack_bf16x2(pv0[2 * e], pv0[2 * e + 1]);
+          pw1[e] = pack_bf16x2(pv1[2 * e], pv1[2 * e + 1]);
+          cor0 -= 128.f * (bf16_lo(pw0[e]) + bf16_hi(pw0[e]));
+          cor1 -= 128.f * (bf16_lo(pw1[e]) + bf16_hi(pw1[e]));
+        }
+        const bf16x8 pop0 = as_bf16x8(pw0), pop1 = as_bf16x8(pw1);
+        // A operand of dim slot j: row m, k-slots (2tt, 2tt + 1) = nibble j of the words of
+        // positions p0 + 8c + 2tt, +1 (byte j / 2 of both gathered by one v_perm)
+        for (int bb = 0; bb < 4; ++bb) {
+          u32x4 a0, a1;
+          for (int tt = 0; tt < 4; ++tt) {
+            const uint32_t t = __builtin_amdgcn_perm(cw[2 * tt + 1], cw[2 * tt], 0x0C000C00u | (uint32_t)bb | ((4u + bb) << 16));
+            a0[tt] = and_or(t, 0x000F000Fu, 0x43004300u);
+            a1[tt] = and_or(t >> 4, 0x000F000Fu, 0x43004300u);
+          }
+          o[2 * bb] = mfma16(as_bf16x8(a0), bb < 2 ? pop0 : pop1, o[2 * bb]);
+          o[2 * bb + 1] = mfma16(as_bf16x8(a1), bb < 2 ? pop0 : pop1, o[2 * bb + 1]);
+        }
+        if (more) {
+          for (int r = 0; r < 2; ++r)
+            for (int i = 0; i < 2; ++i) k4[r][i] = k4n[r][i];
+          for (int kk = 0; kk < 8; ++kk) v4[kk] = v4n[kk];
+          for (int h = 0; h < 2; ++h)
+            for (int q = 0; q < 2; ++q) {
+              mk[q][h] = mkn[q][h];
+              mv[q][h] = mvn[q][h];
+            }
+        }
+        continue;
+      }
 
       // P^T B operand: k = 4r + i <-> position p0 + 8c + k
       u32x4 pw;
@@ -568,10 +807,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       cmb.m[wave][g] = m_run;
       cmb.l[wave][g] = l_tot;
     }
-    for (int i = 0; i < 4; ++i) {
-      float* dst = &cmb.o[wave][g][32 * c + 8 * i];
-      *(f32x4*)dst = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
-      *(f32x4*)(dst + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
+    if (kI4) {
+      // add the corrections of the column; row 4c + i of slot j is dim
+      // 64 (j / 4) + 32 (c % 2) + 8i + 4 (c / 2) + j % 4
+      cor0 += __shfl_xor(cor0, 16, 64);
+      cor0 += __shfl_xor(cor0, 32, 64);
+      cor1 += __shfl_xor(cor1, 16, 64);
+      cor1 += __shfl_xor(cor1, 32, 64);
+      for (int i = 0; i < 4; ++i) {
+        float* dst = &cmb.o[wave][g][32 * (c & 1) + 8 * i + 4 * (c >> 1)];
+        *(f32x4*)dst = f32x4{o[0][i] + cor0, o[1][i] + cor0, o[2][i] + cor0, o[3][i] + cor0};
+        *(f32x4*)(dst + 64) = f32x4{o[4][i] + cor1, o[5][i] + cor1, o[6][i] + cor1, o[7][i] + cor1};
+      }
+    } else {
+      for (int i = 0; i < 4; ++i) {
+        float* dst = &cmb.o[wave][g][32 * c + 8 * i];
+        *(f32x4*)dst = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
+        *(f32x4*)(dst + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
+      }
     }
     __syncthreads();
 
@@ -720,9 +973,16 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.flags = fused ? fused->flags : 0u;
   a.kexp = (const int8_t*)c.k_exp;
   a.vexp = (const int8_t*)c.v_exp;
+  a.ks = (uint32_t*)c.k_scales;
+  a.kb = (uint32_t*)c.k_biases;
+  a.vs = (uint32_t*)c.v_scales;
+  a.vb = (uint32_t*)c.v_biases;
   const bool fp8 = c.dtype == EMA_DTYPE_FP8_E4M3;
+  const bool i4 = c.dtype == EMA_DTYPE_INT4_AFFINE;
   const dim3 grid(plan.workers), block(kWaves * 64);
-  if (a.fused && fp8) hipLaunchKernelGGL((decode_kernel<true, true>), grid, block, 0, s, a);
+  if (a.fused && i4) hipLaunchKernelGGL((decode_kernel<true, false, true>), grid, block, 0, s, a);
+  else if (i4) hipLaunchKernelGGL((decode_kernel<false, false, true>), grid, block, 0, s, a);
+  else if (a.fused && fp8) hipLaunchKernelGGL((decode_kernel<true, true>), grid, block, 0, s, a);
   else if (a.fused) hipLaunchKernelGGL((decode_kernel<true, false>), grid, block, 0, s, a);
   else if (fp8) hipLaunchKernelGGL((decode_kernel<false, true>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((decode_kernel<false, false>), grid, block, 0, s, a);

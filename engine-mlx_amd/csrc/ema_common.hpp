@@ -68,6 +68,62 @@ __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }
 
+// ---- 4-bit affine KV rows (MLX "affine" quantisation, group 64) ----
+// Parameters of one group with minimum mn and maximum mx, as MLX's affine quantiser forms
+// them: scale = max((mx - mn) / 15, 1e-7), negated unless |mn| > |mx|; the end of larger
+// magnitude (the edge) is moved onto the grid, scale = edge / round(edge / scale), and is
+// the bias (bias 0 and the unadjusted scale when round(edge / scale) is 0). f32 with
+// correctly rounded division; round() is half away from zero.
+__device__ __forceinline__ void i4_params(float mn, float mx, float& scale, float& bias) {
+  float sc = fmaxf(__fdiv_rn(mx - mn, 15.0f), 1.0e-7f);
+  const bool side = fabsf(mn) > fabsf(mx);
+  sc = side ? sc : -sc;
+  const float edge = side ? mn : mx;
+  const float q0 = roundf(__fdiv_rn(edge, sc));
+  const bool at_zero = q0 == 0.0f;
+  scale = at_zero ? sc : __fdiv_rn(edge, q0);
+  bias = at_zero ? 0.0f : edge;
+}
+// Code of x in its group: round((x - bias) / scale), at most 15 (and at least 0).
+__device__ __forceinline__ uint32_t i4_code(float x, float scale, float bias) {
+  const float t = fminf(roundf(__fdiv_rn(x - bias, scale)), 15.0f);
+  return t > 0.0f ? (uint32_t)t : 0u;
+}
+// Quantise and store one 128-value row held by 8 consecutive lanes, lane j (= lane8) with
+// values 8j .. 8j+7 in x[0..8) and 64+8j .. 64+8j+7 in x[8..16): words[j] and words[8 + j]
+// get the codes (value i at bits 4(i % 8)), *scale_pair / *bias_pair the two groups' bf16
+// parameters (group 0 in the low half), written by lane j = 0.
+__device__ __forceinline__ void i4_store_row8(const float (&x)[16], uint32_t* words, uint32_t* scale_pair,
+                                              uint32_t* bias_pair, int lane8) {
+  float mn0 = x[0], mx0 = x[0], mn1 = x[8], mx1 = x[8];
+  for (int e = 1; e < 8; ++e) {
+    mn0 = fminf(mn0, x[e]);
+    mx0 = fmaxf(mx0, x[e]);
+    mn1 = fminf(mn1, x[8 + e]);
+    mx1 = fmaxf(mx1, x[8 + e]);
+  }
+  for (int o = 4; o >= 1; o >>= 1) {
+    mn0 = fminf(mn0, __shfl_xor(mn0, o, 8));
+    mx0 = fmaxf(mx0, __shfl_xor(mx0, o, 8));
+    mn1 = fminf(mn1, __shfl_xor(mn1, o, 8));
+    mx1 = fmaxf(mx1, __shfl_xor(mx1, o, 8));
+  }
+  float s0, b0, s1, b1;
+  i4_params(mn0, mx0, s0, b0);
+  i4_params(mn1, mx1, s1, b1);
+  uint32_t w0 = 0u, w1 = 0u;
+  for (int e = 0; e < 8; ++e) {
+    w0 |= i4_code(x[e], s0, b0) << (4 * e);
+    w1 |= i4_code(x[8 + e], s1, b1) << (4 * e);
+  }
+  words[lane8] = w0;
+  words[8 + lane8] = w1;
+  if (lane8 == 0) {
+    *scale_pair = f32_to_bf16_bits(s0) | (f32_to_bf16_bits(s1) << 16);
+    *bias_pair = f32_to_bf16_bits(b0) | (f32_to_bf16_bits(b1) << 16);
+  }
+}
+
 }  // namespace ema
 
 // ---------------------------------------------------------------- host side
@@ -120,6 +176,9 @@ int32_t launch_gdn_scan(hipStream_t s, const void* q, const void* k, const void*
 int32_t launch_qmatmul(hipStream_t s, const void* x, int64_t ldx, const void* w, const void* scales,
                        const void* biases, void* y, int64_t ldy, int M, int N, int K, int gs, int bits,
                        int dtype);
+// Quantise bf16 cache rows into an int4 affine cache (arguments validated by the caller).
+int32_t launch_quantize_int4(hipStream_t s, const ema_kvcache_desc& src, int src_row, const ema_kvcache_desc& dst,
+                             int dst_row, int n_rows);
 // Decode the fp8 rows a prefill call attends to into bf16 [B, Hkv, R, D] K then V at ws.
 int32_t launch_fp8_to_bf16(hipStream_t s, const ema_kvcache_desc& c, const int32_t* q_off, int T,
                            uint32_t flags, int R, void* ws);

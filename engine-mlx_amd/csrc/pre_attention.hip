@@ -95,6 +95,10 @@ struct PreArgs {
   uint16_t* vc;
   int8_t* kexp;  // fp8 cache: block exponents [B, Hkv, cap, D/64]
   int8_t* vexp;
+  uint32_t* ks;  // int4 cache: (group 0, group 1) bf16 scale and bias pairs [B, Hkv, cap]
+  uint32_t* kb;
+  uint32_t* vs;
+  uint32_t* vb;
   int64_t sb, sh, sp;
   float eps;
   float log2_theta;
@@ -134,7 +138,7 @@ __device__ __forceinline__ u32x2 fp8_encode8(const uint16_t* x, int e) {
   return w;
 }
 
-template <int D, bool kFp8>
+template <int D, bool kFp8, bool kI4 = false>
 __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
   constexpr int HALF = D / 2;
   constexpr int E = D / 16;  // elements per lane in each half of the row
@@ -181,6 +185,16 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       *(uint16_t*)(exps + 2 * r) = (uint16_t)((uint8_t)e0 | ((uint32_t)(uint8_t)e1 << 8));
     }
   };
+  // int4 cache row (b, kh, pos) from the bf16 values x[0..2E) of this lane (E = 8); the
+  // strides count 4-bit elements
+  auto store_i4 = [&](const uint16_t* x, uint16_t* words16, uint32_t* sc, uint32_t* bi, int b_, int kh, int p_) {
+    float f[16];
+    for (int e = 0; e < 16; ++e) f[e] = bf16_to_f32(x[e]);
+    uint32_t* words =
+        (uint32_t*)((uint8_t*)words16 + ((int64_t)b_ * a.sb + (int64_t)kh * a.sh + (int64_t)p_ * a.sp) / 2);
+    const int64_t r = ((int64_t)b_ * a.Hkv + kh) * a.cap + p_;
+    i4_store_row8(f, words, sc + r, bi + r, lane8);
+  };
   for (int h = threadIdx.x >> 3; h < H; h += 32) {
     const uint16_t* src = a.qkv + (bt * H + h) * D;
     uint16_t x[2 * E];
@@ -192,6 +206,10 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       const int kh = h - a.Hq - a.Hkv;
       if (kFp8) {
         store_fp8(x, a.vc, a.vexp, b, kh, row);
+        continue;
+      }
+      if (kI4) {
+        store_i4(x, a.vc, a.vs, a.vb, b, kh, row);
         continue;
       }
       uint16_t* dst = a.vc + (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)row * a.sp;
@@ -239,6 +257,10 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       store_fp8(o, a.kc, a.kexp, b, h - a.Hq, row);
       continue;
     }
+    if (kI4 && !is_q) {
+      store_i4(o, a.kc, a.ks, a.kb, b, h - a.Hq, row);
+      continue;
+    }
     uint16_t* dst;
     if (is_q) dst = a.q_out + (((int64_t)b * a.Hq + h) * a.T + t) * D;
     else dst = a.kc + (int64_t)b * a.sb + (int64_t)(h - a.Hq) * a.sh + (int64_t)row * a.sp;
@@ -263,6 +285,10 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   a.vc = (uint16_t*)c.v;
   a.kexp = (int8_t*)c.k_exp;
   a.vexp = (int8_t*)c.v_exp;
+  a.ks = (uint32_t*)c.k_scales;
+  a.kb = (uint32_t*)c.k_biases;
+  a.vs = (uint32_t*)c.v_scales;
+  a.vb = (uint32_t*)c.v_biases;
   a.sb = c.stride_batch;
   a.sh = c.stride_head;
   a.sp = c.stride_pos;
@@ -280,6 +306,10 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many tokens");
   if (c.dtype == EMA_DTYPE_FP8_E4M3) {  // head_dim 128 (checked with the descriptor)
     hipLaunchKernelGGL((pre_attention_kernel<128, true>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
+    return check_hip(hipGetLastError(), "ema_pre_attention launch");
+  }
+  if (c.dtype == EMA_DTYPE_INT4_AFFINE) {  // head_dim 128 (checked with the descriptor)
+    hipLaunchKernelGGL((pre_attention_kernel<128, false, true>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
     return check_hip(hipGetLastError(), "ema_pre_attention launch");
   }
   switch (D) {

@@ -30,6 +30,7 @@ EMA_DTYPE_BF16 = 1
 EMA_DTYPE_FP8_E4M3 = 2
 EMA_DTYPE_F16 = 3
 EMA_DTYPE_F32 = 4
+EMA_DTYPE_INT4_AFFINE = 5
 EMA_PRE_NO_NORM = 1
 EMA_PRE_NO_ROPE = 2
 EMA_KV_ROTATING = 1
@@ -38,7 +39,8 @@ EMA_PREFILL_CHUNK_ONLY = 2
 
 EXPORTED = (
     "ema_last_error", "ema_version", "ema_kvcache_init", "ema_kvcache_alloc", "ema_kvcache_free",
-    "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8",
+    "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8", "ema_kvcache_init_int4", "ema_kvcache_alloc_int4",
+    "ema_kvcache_quantize_int4",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
     "ema_decode_attention", "ema_decode_step", "ema_prefill_attention", "ema_prefill_workspace_size",
     "ema_prefill_attention_ws", "ema_gdn_scan", "ema_quantized_matmul",
@@ -61,6 +63,8 @@ class KvCacheDesc(ctypes.Structure):
         ("stride_batch", ctypes.c_int64), ("stride_head", ctypes.c_int64),
         ("stride_pos", ctypes.c_int64), ("dtype", ctypes.c_int32), ("flags", ctypes.c_int32),
         ("k_exp", ctypes.c_void_p), ("v_exp", ctypes.c_void_p),
+        ("k_scales", ctypes.c_void_p), ("k_biases", ctypes.c_void_p),
+        ("v_scales", ctypes.c_void_p), ("v_biases", ctypes.c_void_p),
     ]
 
 
@@ -83,6 +87,9 @@ def lib() -> ctypes.CDLL:
             "ema_kvcache_alloc": (i32, [D, i32, i32, i32, i32]),
             "ema_kvcache_init_fp8": (i32, [D, vp, vp, vp, vp, i32, i32, i32, i32]),
             "ema_kvcache_alloc_fp8": (i32, [D, i32, i32, i32, i32]),
+            "ema_kvcache_init_int4": (i32, [D, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+            "ema_kvcache_alloc_int4": (i32, [D, i32, i32, i32, i32]),
+            "ema_kvcache_quantize_int4": (i32, [vp, D, i32, D, i32, i32]),
             "ema_kvcache_free": (i32, [D]),
             "ema_kvcache_memory_bytes": (i32, [D, ctypes.POINTER(u64)]),
             "ema_pre_attention": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, i32, i32, i32, u32, vp, D]),
@@ -142,13 +149,20 @@ class StaticCache:
     ``k_exp``/``v_exp`` int8 [B, Hkv, cap, D/64] block exponents
     (value = code * 2^exp); head_dim 128.
 
+    ``dtype="int4"``: the reference's int4 KV buffers (alloc_kv_int4,
+    crates/serve/src/engine_ext.rs:92-129): ``k``/``v`` are int32 words [B, Hkv, cap, D/8]
+    (8 four-bit codes each, lowest bits first) and ``k_scales``/``k_biases``/``v_scales``/
+    ``v_biases`` bf16 [B, Hkv, cap, D/64] (value = scale * code + bias); head_dim 128,
+    capacity a multiple of 32, not rotating, decode only.
+
     ``rotating=True``: the reference's RotatingCache (crates/kvcache/src/rotating.rs) as a
     ring of ``capacity`` rows (EMA_KV_ROTATING): position p lives in row p % capacity and
     attention covers the last ``capacity`` tokens; ``len`` is then min(tokens, capacity).
     """
 
     def __init__(self, batch: int, n_kv_heads: int, capacity: int, head_dim: int, device="cuda",
-                 k=None, v=None, dtype="bf16", k_exp=None, v_exp=None, rotating=False):
+                 k=None, v=None, dtype="bf16", k_exp=None, v_exp=None, rotating=False, k_scales=None,
+                 k_biases=None, v_scales=None, v_biases=None):
         import torch
 
         shape = (batch, n_kv_heads, capacity, head_dim)
@@ -169,8 +183,20 @@ class StaticCache:
             _check(lib().ema_kvcache_init_fp8(ctypes.byref(self.desc), _ptr(self.k), _ptr(self.v), _ptr(self.k_exp),
                                               _ptr(self.v_exp), batch, n_kv_heads, capacity, head_dim),
                    "ema_kvcache_init_fp8")
+        elif dtype == "int4":
+            mshape = (batch, n_kv_heads, capacity, head_dim // 64)
+            self.k = k if k is not None else torch.zeros(shape[:3] + (head_dim // 8,), dtype=torch.int32, device=device)
+            self.v = v if v is not None else torch.zeros(shape[:3] + (head_dim // 8,), dtype=torch.int32, device=device)
+            self.k_exp = self.v_exp = None
+            self.k_scales, self.k_biases, self.v_scales, self.v_biases = (
+                t if t is not None else torch.zeros(mshape, dtype=torch.bfloat16, device=device)
+                for t in (k_scales, k_biases, v_scales, v_biases))
+            _check(lib().ema_kvcache_init_int4(ctypes.byref(self.desc), _ptr(self.k), _ptr(self.v),
+                                               _ptr(self.k_scales), _ptr(self.k_biases), _ptr(self.v_scales),
+                                               _ptr(self.v_biases), batch, n_kv_heads, capacity, head_dim),
+                   "ema_kvcache_init_int4")
         else:
-            raise ValueError(f"unknown cache dtype {dtype!r} (bf16 or fp8)")
+            raise ValueError(f"unknown cache dtype {dtype!r} (bf16, fp8 or int4)")
         self.rotating = bool(rotating)
         if self.rotating:
             self.desc.flags = EMA_KV_ROTATING
@@ -194,6 +220,15 @@ class StaticCache:
         out = ctypes.c_uint64()
         _check(lib().ema_kvcache_memory_bytes(ctypes.byref(self.desc), ctypes.byref(out)), "ema_kvcache_memory_bytes")
         return out.value
+
+
+def quantize_int4(src: StaticCache, dst: StaticCache, n_rows: int, src_row: int = 0, dst_row: int = 0,
+                  stream=None) -> None:
+    """Rows [src_row, src_row + n_rows) of the bf16 cache ``src`` quantised into rows
+    [dst_row, ...) of the int4 cache ``dst`` (convert_kv_to_int4,
+    crates/serve/src/engine_ext.rs:158-210)."""
+    _check(lib().ema_kvcache_quantize_int4(_stream(stream), ctypes.byref(src.desc), src_row, ctypes.byref(dst.desc),
+                                           dst_row, n_rows), "ema_kvcache_quantize_int4")
 
 
 def pre_attention(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: StaticCache, flags=0,

@@ -20,6 +20,13 @@
  *              crates/kvcache/src/fp8.rs:47-68, crates/ops/src/fp8.rs:71-92
  *                                                               ema_kvcache_init_fp8 / _alloc_fp8
  *                                                               (stored, not simulated)
+ *   int4 KV (quantize_kv_native / dequantize_kv_native, group 64, 4 bits)
+ *              crates/serve/src/engine_ext.rs:92-157, crates/mlx-ffi/src/ops/real/quant.rs:8-64
+ *                                                               ema_kvcache_init_int4 / _alloc_int4,
+ *                                                               ema_decode_attention / _step read it
+ *   convert_kv_to_int4 and the int4 prefill store
+ *              crates/serve/src/engine_ext.rs:158-210, forward_qwen3.rs:69-120
+ *                                                               ema_kvcache_quantize_int4
  *   gdn_step / gdn_step_metal and the per-token scan of gdn_forward
  *              crates/ops/src/gdn.rs:83-150, gdn_metal.rs:56-88, gdn_forward.rs:173-192
  *                                                               ema_gdn_scan
@@ -70,6 +77,17 @@ extern "C" {
  * whole head is quantised, i.e. n_rot = 0). Decoded exactly to bf16 by the readers.
  * head_dim 128 only. Values must be finite. */
 #define EMA_DTYPE_FP8_E4M3 2
+/* 4-bit affine codes (MLX "affine" quantisation, group 64, the layout of the reference's
+ * int4 KV buffers, crates/serve/src/engine_ext.rs:92-129): per row of head_dim values,
+ * head_dim / 8 uint32 words (value i in bits 4(i % 8) of word i / 8) plus one bf16 scale and
+ * one bf16 bias per 64 values; value = scale * code + bias. Rows are written with MLX's
+ * affine quantiser (per group: scale = max((max - min) / 15, 1e-7), signed towards the
+ * larger-magnitude end, which is moved onto the grid and becomes the bias; codes
+ * round((x - bias) / scale), half away from zero, at most 15). Readers use the exact affine
+ * value scale * code + bias; MLX's dequantize to bf16 rounds it once (at most half a bf16
+ * step per element). head_dim 128, capacity a multiple of 32, static (not
+ * rotating) caches; decode only (prefill attends bf16 keys, as the reference's does). */
+#define EMA_DTYPE_INT4_AFFINE 5
 /* activation types of ema_gdn_scan (besides EMA_DTYPE_BF16) */
 #define EMA_DTYPE_F16 3
 #define EMA_DTYPE_F32 4
@@ -110,7 +128,10 @@ typedef void* ema_stream_t; /* hipStream_t */
  * crates/serve/src/engine_ext.rs:266-306, and reuses them across requests).
  * FP8: k/v hold the codes (strides in elements = bytes, multiples of 16) and
  * k_exp/v_exp the block exponents, int8 [batch, n_kv_heads, capacity, head_dim / 64],
- * contiguous. */
+ * contiguous.
+ * INT4: k/v hold the packed words (strides in 4-bit elements, multiples of 32, i.e. 16
+ * bytes) and k_scales/k_biases/v_scales/v_biases the bf16 group parameters
+ * [batch, n_kv_heads, capacity, head_dim / 64], contiguous. */
 typedef struct ema_kvcache_desc {
   void* k;
   void* v;
@@ -125,6 +146,10 @@ typedef struct ema_kvcache_desc {
   int32_t flags;        /* 0 or EMA_KV_ROTATING (set by the caller after init/alloc) */
   void* k_exp;          /* EMA_DTYPE_FP8_E4M3: block exponents of K and V (else NULL) */
   void* v_exp;
+  void* k_scales;       /* EMA_DTYPE_INT4_AFFINE: group scales and biases (else NULL) */
+  void* k_biases;
+  void* v_scales;
+  void* v_biases;
 } ema_kvcache_desc;
 
 /* Thread-local message of the last failed call on this thread ("" if none). */
@@ -146,9 +171,28 @@ EMA_API int32_t ema_kvcache_init_fp8(ema_kvcache_desc* desc, void* k, void* v, v
 /* Allocate a zeroed FP8 cache (codes and exponents). Not for the hot path. */
 EMA_API int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads,
                                       int32_t capacity, int32_t head_dim);
-/* Free buffers obtained from ema_kvcache_alloc or ema_kvcache_alloc_fp8 and clear the descriptor. */
+/* int4 affine cache over caller-owned words [batch, n_kv_heads, capacity, head_dim / 8]
+ * (uint32) and scales/biases [batch, n_kv_heads, capacity, head_dim / 64] (bf16), all
+ * contiguous: the six buffers of alloc_kv_int4 (crates/serve/src/engine_ext.rs:92-129). */
+EMA_API int32_t ema_kvcache_init_int4(ema_kvcache_desc* desc, void* k, void* v, void* k_scales, void* k_biases,
+                                      void* v_scales, void* v_biases, int32_t batch, int32_t n_kv_heads,
+                                      int32_t capacity, int32_t head_dim);
+/* Allocate a zeroed int4 cache (alloc_kv_int4, engine_ext.rs:98-129). Not for the hot path. */
+EMA_API int32_t ema_kvcache_alloc_int4(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads,
+                                       int32_t capacity, int32_t head_dim);
+/* Quantise rows [src_row, src_row + n_rows) of every (sequence, kv head) of the bf16 cache
+ * `src` into rows [dst_row, dst_row + n_rows) of the int4 cache `dst` (same batch, heads and
+ * head_dim): convert_kv_to_int4 (crates/serve/src/engine_ext.rs:158-210, src_row = dst_row
+ * = 0, n_rows = the prompt length) and the per-position store of the int4 prefill
+ * (crates/serve/src/forward_qwen3.rs:69-120: the chunk's k/v after norm and RoPE, e.g. from a
+ * bf16 staging cache written by ema_pre_attention). Rows outside either capacity are an
+ * error (EMA_ERR_CAPACITY). */
+EMA_API int32_t ema_kvcache_quantize_int4(ema_stream_t stream, const ema_kvcache_desc* src, int32_t src_row,
+                                          const ema_kvcache_desc* dst, int32_t dst_row, int32_t n_rows);
+/* Free buffers obtained from ema_kvcache_alloc, _alloc_fp8 or _alloc_int4 and clear the descriptor. */
 EMA_API int32_t ema_kvcache_free(ema_kvcache_desc* desc);
-/* Bytes held by K and V, exponents included (KvCache::memory_bytes, crates/kvcache/src/lib.rs:75). */
+/* Bytes held by K and V, exponents or scales and biases included (KvCache::memory_bytes,
+ * crates/kvcache/src/lib.rs:75). */
 EMA_API int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* desc, uint64_t* bytes);
 
 /* Fused Qwen3 pre-attention for `batch` sequences of `n_tokens` new tokens.
@@ -163,7 +207,9 @@ EMA_API int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* desc, uint64_t*
  * Offsets are read on the device; offsets[b] + n_tokens > capacity writes nothing
  * for that sequence (callers guard on the host as decode_compiled.rs:18-20 does).
  * FP8 cache: each written K and V row is quantised per 64-element block (the bf16 k
- * after norm and RoPE, v as given), as Fp8Cache::append does (crates/kvcache/src/fp8.rs:47-68). */
+ * after norm and RoPE, v as given), as Fp8Cache::append does (crates/kvcache/src/fp8.rs:47-68).
+ * int4 cache: each written K and V row is quantised per 64-value group with MLX's affine
+ * quantiser, as int4_update_and_dequant does (crates/serve/src/engine_ext.rs:131-157). */
 EMA_API int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_norm_w,
                           const void* k_norm_w, float eps, float theta, const int32_t* offsets,
                           int32_t batch, int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads,
@@ -184,7 +230,9 @@ EMA_API int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_
  *   out      [batch, n_heads * head_dim] bf16 (the o_proj input layout)
  * GQA: q head h reads kv head h / (n_heads / n_kv_heads).
  * FP8 cache: K/V rows are decoded exactly to bf16 (code value times 2^exp) and attended
- * as a bf16 cache holding those values would be. */
+ * as a bf16 cache holding those values would be.
+ * int4 cache: attends the affine values scale * code + bias of every row (the reference
+ * dequantizes the whole cache and runs the masked SDPA over it, decode_eager.rs:78-104). */
 EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                              const int32_t* lengths, int32_t max_len, int32_t n_heads,
                              float scale, void* out, void* workspace, uint64_t workspace_bytes);
@@ -200,8 +248,8 @@ EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const e
  *   max_len  host upper bound of offsets[b] + 1 (sizes the split; <= capacity)
  *   out      [batch, n_heads * head_dim] bf16
  * The workspace is the one ema_decode_workspace_size gives for max_len.
- * FP8 cache: the new k/v row is quantised as in ema_pre_attention and attended in
- * its decoded form, like every other row. */
+ * FP8 and int4 caches: the new k/v row is quantised as in ema_pre_attention and attended
+ * in its decoded form, like every other row. */
 EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w,
                                 const void* k_norm_w, float eps, float theta,
                                 const int32_t* offsets, int32_t max_len, int32_t n_heads,
@@ -216,7 +264,9 @@ EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void
  *              [0, q_offsets[b] + n_tokens) (or [q_offsets[b], ...) with CHUNK_ONLY)
  *   out        [batch, n_tokens, n_heads * head_dim] bf16
  * With EMA_PREFILL_CAUSAL, query i sees key j iff j <= q_offsets[b] + i.
- * bf16 caches only (EMA_ERR_UNSUPPORTED for FP8: use ema_prefill_attention_ws). */
+ * bf16 caches only (EMA_ERR_UNSUPPORTED for FP8: use ema_prefill_attention_ws; for int4,
+ * whose prefill the reference runs over the chunk's bf16 keys, use a bf16 cache and
+ * ema_kvcache_quantize_int4). */
 EMA_API int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                               const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads,
                               float scale, uint32_t flags, void* out);

@@ -474,6 +474,59 @@ void ora_fp8_dequantize_rows(const uint8_t* codes, const int8_t* exps, int64_t r
       out[r * D + i] = ldexpf(ora_e4m3_value(codes[r * D + i]), exps[r * (D / 64) + i / 64]);
 }
 
+/* ------------------------------------------------------ int4 affine KV */
+
+static void int4_params(float mn, float mx, float* scale, float* bias) {
+  float sc = fmaxf((mx - mn) / 15.0f, 1e-7f);
+  const int side = fabsf(mn) > fabsf(mx);
+  sc = side ? sc : -sc;
+  const float edge = side ? mn : mx;
+  const float q0 = roundf(edge / sc);
+  if (q0 != 0.0f) {
+    *scale = edge / q0;
+    *bias = edge;
+  } else {
+    *scale = sc;
+    *bias = 0.0f;
+  }
+}
+
+void ora_int4_quantize_rows(const float* x, int64_t rows, int D, uint32_t* words, uint16_t* scales,
+                            uint16_t* biases) {
+  const int G = D / 64;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int g = 0; g < G; ++g) {
+      const float* v = x + r * D + 64 * g;
+      float mn = v[0], mx = v[0];
+      for (int i = 1; i < 64; ++i) {
+        mn = fminf(mn, v[i]);
+        mx = fmaxf(mx, v[i]);
+      }
+      float scale, bias;
+      int4_params(mn, mx, &scale, &bias);
+      scales[r * G + g] = ora_f32_to_bf16(scale);
+      biases[r * G + g] = ora_f32_to_bf16(bias);
+      uint32_t* w = words + r * (D / 8) + 8 * g;
+      for (int i = 0; i < 8; ++i) w[i] = 0u;
+      for (int i = 0; i < 64; ++i) {
+        float t = fminf(roundf((v[i] - bias) / scale), 15.0f);
+        const uint32_t code = t > 0.0f ? (uint32_t)t : 0u;
+        w[i / 8] |= code << (4 * (i % 8));
+      }
+    }
+}
+
+void ora_int4_dequantize_rows(const uint32_t* words, const uint16_t* scales, const uint16_t* biases, int64_t rows,
+                              int D, float* out) {
+  const int G = D / 64;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int i = 0; i < D; ++i) {
+      const uint32_t code = (words[r * (D / 8) + i / 8] >> (4 * (i % 8))) & 15u;
+      const float s = bf(scales[r * G + i / 64]), b = bf(biases[r * G + i / 64]);
+      out[r * D + i] = bf(ora_f32_to_bf16((float)code * s + b)); /* code * s exact in f32 */
+    }
+}
+
 /* ------------------------------------------------------ gated deltanet */
 
 void ora_gdn_scan(const float* q, const float* k, const float* v, const float* g, const float* beta,

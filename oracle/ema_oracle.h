@@ -17,6 +17,7 @@
  *   - op order norm -> transpose -> rope -> write -> sdpa
  *                                 crates/serve/src/forward_qwen3.rs:52-152
  *   - FP8 KV format               crates/ops/src/fp8.rs, crates/kvcache/src/fp8.rs
+ *   - int4 affine KV format       crates/serve/src/engine_ext.rs:92-157 (MLX affine quantize)
  *   - Gated DeltaNet step/scan    crates/ops/src/gdn.rs:83-150, gdn_forward.rs:173-192
  *   - affine quantized_matmul     crates/mlx-ffi/src/ops/real/transform.rs:77-88 via
  *                                 crates/ops/src/quant.rs:57-76 (transpose = true)
@@ -136,6 +137,31 @@ void ora_fp8_round_trip(float* x, int64_t rows, int D, int n_rot);
 void ora_fp8_quantize_rows(const float* x, int64_t rows, int D, uint8_t* codes, int8_t* exps);
 /* value = e4m3(code) * 2^exp, exact in f32. */
 void ora_fp8_dequantize_rows(const uint8_t* codes, const int8_t* exps, int64_t rows, int D, float* out);
+
+/* ---- 4-bit affine KV format: the reference's int4 KV buffers (crates/serve/src/engine_ext.rs:92-157)
+ * filled by quantize_kv_native and read through dequantize_kv_native
+ * (crates/mlx-ffi/src/ops/real/quant.rs:8-64): mlx_quantize / mlx_dequantize with mode "affine",
+ * group 64, 4 bits. MLX itself (mlx-sys 0.2 over mlx-c, with the global_scale argument of MLX
+ * 0.29 and later) is a third-party dependency absent here; these restate its published
+ * affine kernels (affine_quantize / affine_dequantize), the same ones the reference's Metal
+ * stream runs. Per group of 64 values, f32 arithmetic:
+ *   scale = max((max - min) / 15, 1e-7); side = |min| > |max|; scale = side ? scale : -scale;
+ *   edge = side ? min : max; q0 = round(edge / scale);
+ *   q0 != 0: scale = edge / q0, bias = edge;  q0 == 0: bias = 0;
+ *   code = min(round((x - bias) / scale), 15)   (round: half away from zero; codes >= 0)
+ * scale and bias are stored rounded to bf16 (the input dtype); codes use the f32 values.
+ * Words: value i of a row at bits 4(i % 8) of word i / 8 (lowest bits first).
+ * Parity against MLX itself is unpinned (no MLX here and no int4 vectors in the reference's
+ * tests); tests/test_oracle_int4.py pins the properties that the algorithm fixes. */
+void ora_int4_quantize_rows(const float* x, int64_t rows, int D, uint32_t* words, uint16_t* scales,
+                            uint16_t* biases);
+/* MLX affine_dequantize into bf16: out = bf16(scale * code + bias), one rounding of the exact
+ * affine value. MLX's kernel evaluates `scale * d + bias` as one expression, which its
+ * clang-based Metal compiler contracts into a fused multiply-add (scale * code is exact in
+ * f32 in any case); were the product rounded to bf16 first, values whose product and bias
+ * cancel would differ by up to half a bf16 step of scale * code. Not pinned against MLX. */
+void ora_int4_dequantize_rows(const uint32_t* words, const uint16_t* scales, const uint16_t* biases, int64_t rows,
+                              int D, float* out);
 
 /* ---- Gated DeltaNet recurrent scan ----
  * gdn_step (crates/ops/src/gdn.rs:83-150; the fused kernel body gdn_metal.rs:16-50 does the

@@ -82,6 +82,8 @@ def lib():
         L.ora_gdn_scan.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f64p, _f64p] + [ctypes.c_int] * 6
         L.ora_qmatmul.argtypes = [_f32p, _u32p, _f32p, _f32p] + [ctypes.c_int] * 5 + [_f64p]
         L.ora_dequantize.argtypes = [_u32p, _f32p, _f32p] + [ctypes.c_int] * 4 + [_f64p]
+        L.ora_int4_quantize_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _u32p, _u16p, _u16p]
+        L.ora_int4_dequantize_rows.argtypes = [_u32p, _u16p, _u16p, ctypes.c_int64, ctypes.c_int, _f32p]
         _lib = L
     return _lib
 
@@ -265,6 +267,44 @@ def fp8_dequantize(codes, exps) -> np.ndarray:
     out = np.empty(codes.shape, dtype=np.float32)
     lib().ora_fp8_dequantize_rows(_p(codes, _u8p), _p(exps, _i8p), codes.size // D, D, _p(out, _f32p))
     return out
+
+
+def int4_quantize(x):
+    """Rows of D (multiple of 64) f32 values -> (words uint32 [..., D/8], scales and biases as
+    bf16 bits [..., D/64]): MLX affine quantisation, group 64, 4 bits (quantize_kv_native,
+    crates/mlx-ffi/src/ops/real/quant.rs:8-40; ora_int4_quantize_rows)."""
+    x = _c(np.asarray(x, dtype=np.float32), np.float32)
+    D = x.shape[-1]
+    assert D % 64 == 0
+    rows = x.size // D
+    words = np.empty(x.shape[:-1] + (D // 8,), dtype=np.uint32)
+    scales = np.empty(x.shape[:-1] + (D // 64,), dtype=np.uint16)
+    biases = np.empty_like(scales)
+    lib().ora_int4_quantize_rows(_p(x, _f32p), rows, D, _p(words, _u32p), _p(scales, _u16p), _p(biases, _u16p))
+    return words, scales, biases
+
+
+def int4_dequantize(words, scales, biases) -> np.ndarray:
+    """MLX affine dequantize to bf16 (dequantize_kv_native, quant.rs:41-64): f32 values
+    bf16(scale * code + bias), one rounding, shape [..., D]."""
+    words = _c(np.asarray(words), np.uint32)
+    scales = _c(np.asarray(scales), np.uint16)
+    biases = _c(np.asarray(biases), np.uint16)
+    D = words.shape[-1] * 8
+    rows = words.size // (D // 8)
+    out = np.empty(words.shape[:-1] + (D,), dtype=np.float32)
+    lib().ora_int4_dequantize_rows(_p(words, _u32p), _p(scales, _u16p), _p(biases, _u16p), rows, D, _p(out, _f32p))
+    return out
+
+
+def int4_affine_values(words, scales, biases) -> np.ndarray:
+    """The exact affine values scale * code + bias (float64) of int4 rows [..., D]."""
+    D = np.asarray(words).shape[-1] * 8
+    codes = unpack_bits(words, 4).astype(np.float64)
+    s = np.repeat(f32_from_bf16(scales).astype(np.float64), 64, axis=-1)
+    b = np.repeat(f32_from_bf16(biases).astype(np.float64), 64, axis=-1)
+    assert codes.shape[-1] == D == s.shape[-1]
+    return codes * s + b
 
 
 def gdn_scan(q, k, v, g, beta, state):

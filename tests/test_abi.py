@@ -276,3 +276,39 @@ def test_quantized_matmul_argument_errors(ema):
     assert call(ldx=4100) == ema.EMA_ERR_INVALID_ARG
     assert call(s=p + 1) == ema.EMA_ERR_INVALID_ARG
     assert call(K=1 << 21, ldx=1 << 21) == ema.EMA_ERR_SHAPE and "too large" in ema.last_error()
+
+
+def test_int4_cache_descriptor_and_errors(ema):
+    L = ema.lib()
+    a = 0x40000  # 16-byte aligned stand-ins; no call below reaches HIP
+    d = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_int4(ctypes.byref(d), a, a, a, a, a, a, 2, 8, 64, 128) == 0
+    assert d.dtype == ema.EMA_DTYPE_INT4_AFFINE and d.stride_pos == 128 and d.stride_head == 64 * 128
+    n = ctypes.c_uint64()
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 8 * 64 * (64 + 2 * 2 * 2)  # K and V: 64 bytes of codes + 2 scales + 2 biases per row
+    # capacity not a multiple of 32, head_dim 64, a missing bias buffer, a misaligned scale buffer
+    assert L.ema_kvcache_init_int4(ctypes.byref(d), a, a, a, a, a, a, 2, 8, 48, 128) == ema.EMA_ERR_UNSUPPORTED
+    assert "multiple of 32" in ema.last_error()
+    assert L.ema_kvcache_init_int4(ctypes.byref(d), a, a, a, a, a, a, 2, 8, 64, 64) == ema.EMA_ERR_UNSUPPORTED
+    assert L.ema_kvcache_init_int4(ctypes.byref(d), a, a, a, None, a, a, 2, 8, 64, 128) == ema.EMA_ERR_INVALID_ARG
+    assert L.ema_kvcache_init_int4(ctypes.byref(d), a, a, a + 2, a, a, a, 2, 8, 64, 128) == ema.EMA_ERR_INVALID_ARG
+    assert L.ema_kvcache_init_int4(ctypes.byref(d), a, a, a, a, a, a, 2, 8, 64, 128) == 0
+    d.flags = ema.EMA_KV_ROTATING
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == ema.EMA_ERR_UNSUPPORTED
+    d.flags = 0
+    # prefill over int4 is rejected by both entries
+    assert L.ema_prefill_attention(None, a, ctypes.byref(d), a, 8, 16, 0.088, 1, a) == ema.EMA_ERR_UNSUPPORTED
+    assert "int4" in ema.last_error()
+    rc = L.ema_prefill_attention_ws(None, a, ctypes.byref(d), a, 8, 16, 0.088, 1, a, 48, a, 1 << 30)
+    assert rc == ema.EMA_ERR_UNSUPPORTED and "int4" in ema.last_error()
+    # the converter: bf16 source and int4 destination of one shape, rows inside both capacities
+    s = ema.KvCacheDesc()
+    assert L.ema_kvcache_init(ctypes.byref(s), a, a, 2, 8, 40, 128) == 0
+    assert L.ema_kvcache_quantize_int4(None, ctypes.byref(s), 0, ctypes.byref(d), 0, 0) == 0  # nothing to do
+    assert L.ema_kvcache_quantize_int4(None, ctypes.byref(s), 0, ctypes.byref(d), 30, 41) == ema.EMA_ERR_CAPACITY
+    assert L.ema_kvcache_quantize_int4(None, ctypes.byref(s), 8, ctypes.byref(d), 60, 8) == ema.EMA_ERR_CAPACITY
+    assert L.ema_kvcache_quantize_int4(None, ctypes.byref(d), 0, ctypes.byref(d), 0, 8) == ema.EMA_ERR_INVALID_ARG
+    s2 = ema.KvCacheDesc()
+    assert L.ema_kvcache_init(ctypes.byref(s2), a, a, 2, 4, 40, 128) == 0
+    assert L.ema_kvcache_quantize_int4(None, ctypes.byref(s2), 0, ctypes.byref(d), 0, 8) == ema.EMA_ERR_SHAPE
