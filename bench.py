@@ -44,8 +44,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk", "fp8", "gdn", "gdn_step",
-                                       "qmm"],
+    p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "prefill_chunk", "fp8", "int4", "gdn",
+                                       "gdn_step", "qmm"],
                    default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -327,6 +327,65 @@ def bench_fp8_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
     return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
 
 
+def int4_cache(ctx, ema, B, Hkv, cap, D):
+    """int4 affine cache of random codes with group scales near 0.3 and biases near -2.2
+    (values of N(0,1) size)."""
+    torch = ctx.torch
+
+    def words():
+        return torch.randint(-2 ** 31, 2 ** 31 - 1, (B, Hkv, cap, D // 8), generator=ctx.gen, device=ctx.dev,
+                             dtype=torch.int64).to(torch.int32)
+
+    def meta(mean, std):
+        return ctx.randn((B, Hkv, cap, D // 64), mean, std)
+
+    return ema.StaticCache(B, Hkv, cap, D, dtype="int4", k=words(), v=words(), k_scales=meta(0.3, 0.05),
+                           k_biases=meta(-2.2, 0.1), v_scales=meta(0.3, 0.05), v_biases=meta(-2.2, 0.1))
+
+
+def int4_decode_bytes(lengths, Hq, Hkv, D):
+    """K and V codes + bf16 group scales and biases of the valid rows, q in, out."""
+    B = len(lengths)
+    return sum(2 * Hkv * int(L) * (D // 2 + 4 * (D // 64)) for L in lengths) + 2 * B * Hq * D * 2
+
+
+def bench_int4_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
+    torch = ctx.torch
+    cache = int4_cache(ctx, ema, B, Hkv, cap, D)
+    q = ctx.randn((B, Hq, D))
+    ld = ctx.i32(lengths)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+    ms = time_calls(torch, lambda: ema.decode_attention(q, cache, ld, int(max(lengths)), out=out, workspace=ws),
+                    steps, 5)
+    by = int4_decode_bytes(lengths, Hq, Hkv, D)
+    gbs = by / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM)")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
+
+
+def bench_int4_step(ctx, ema, name, steps=20):
+    """The batch-32 Qwen3-8B-shape decode step (fused ema_decode_step) over an int4 cache."""
+    import numpy as np
+
+    torch = ctx.torch
+    B, Hq, Hkv, D, cap = 32, 32, 8, 128, 8192
+    lengths = np.random.default_rng(1234).integers(512, 8193, size=B)
+    cache = int4_cache(ctx, ema, B, Hkv, cap, D)
+    qkv = ctx.randn((B, (Hq + 2 * Hkv) * D))
+    qw, kw = ctx.randn((D,), 1.0, 0.02), ctx.randn((D,), 1.0, 0.02)
+    off_d = ctx.i32(lengths - 1)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+    ms = time_calls(torch, lambda: ema.decode_step(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, cap, out=out,
+                                                   workspace=ws), steps, 5)
+    by = (int4_decode_bytes(lengths, Hq, Hkv, D) + B * (Hq + 2 * Hkv) * D * 2 +
+          B * Hkv * 2 * (D // 2 + 4 * (D // 64)))
+    gbs = by / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: step {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM)")
+    return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
+
+
 def bench_fp8_prefill(ctx, ema, name, B, Hq, Hkv, D, cap, T, off, steps=20):
     """Prefill over an FP8 cache: decode of the attended rows into the bf16 workspace + the
     bf16 prefill, per call."""
@@ -483,6 +542,10 @@ def main():
                                           [32768] * 8))
         secondary.append(bench_fp8_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_fp8_cache", 1, 32, 8, 128, 4096,
                                            2048, 0))
+    if args.only in ("all", "int4"):
+        secondary.append(bench_int4_step(ctx, ema, "decode_step_B32_32q8kv_int4_cache"))
+        secondary.append(bench_int4_decode(ctx, ema, "decode_B8_32q4kv_L32768_int4_cache", 8, 32, 4, 128, 32768,
+                                           [32768] * 8))
     if args.only in ("all", "gdn", "gdn_step"):
         # Gated DeltaNet layer of Qwen3-Next shape: 16 key / 32 value heads, head dims 128
         secondary.append(bench_gdn(ctx, ema, "gdn_decode_step_B32_16k32v_dk128_dv128", 32, 1, 16, 32, 128, 128))
