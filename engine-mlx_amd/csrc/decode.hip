@@ -443,19 +443,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int w_tile = w_row >= 0 ? w_row / kTile : -1;
     const bool owner = kFused && w_row >= 0 && tile0 <= w_tile && w_tile < tile1 && wave == (w_tile - tile0) % kWaves;
     if (kFused) {
-      // the norm weights may be null with EMA_PRE_NO_NORM: read only when used
-      const bool norm = !(a.flags & EMA_PRE_NO_NORM);
-      if (norm)
-        for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + kdim<kNarrow>(s, c));
+      // unconditional loads: without norm weights (EMA_PRE_NO_NORM) the launcher points
+      // qw / kw at the qkv rows, and the values are not used (with a branch here the
+      // fused fp8 step spilled 11 VGPRs to scratch and ran 82 us instead of 68.7)
+      for (int s = 0; s < 4; ++s) qwv[s] = ld16(a.qw + kdim<kNarrow>(s, c));
       if (owner) {  // lane i: dims i and i + 64 (a RoPE pair)
         const uint16_t* kr = a.qkv + (int64_t)b * F + ((int64_t)a.Hq + kh) * kD;
         const uint16_t* vr = kr + (int64_t)a.Hkv * kD;
         kr1 = kr[lane];
         kr2 = kr[lane + 64];
-        if (norm) {
-          kw1 = a.kw[lane];
-          kw2 = a.kw[lane + 64];
-        }
+        kw1 = a.kw[lane];
+        kw2 = a.kw[lane + 64];
         vr1 = vr[lane];
         vr2 = vr[lane + 64];
       }
@@ -965,8 +963,9 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.fused = fused != nullptr;
   a.rot = (c.flags & EMA_KV_ROTATING) != 0;
   a.qkv = fused ? (const uint16_t*)fused->qkv : nullptr;
-  a.qw = fused ? (const uint16_t*)fused->q_norm_w : nullptr;
-  a.kw = fused ? (const uint16_t*)fused->k_norm_w : nullptr;
+  // null norm weights (EMA_PRE_NO_NORM): the kernel still reads 128 values, from the qkv rows
+  a.qw = fused ? (const uint16_t*)(fused->q_norm_w ? fused->q_norm_w : fused->qkv) : nullptr;
+  a.kw = fused ? (const uint16_t*)(fused->k_norm_w ? fused->k_norm_w : fused->qkv) : nullptr;
   a.off = fused ? fused->offsets : nullptr;
   a.eps = fused ? fused->eps : 0.f;
   a.log2_theta = fused ? log2f(fused->theta) : 0.f;
