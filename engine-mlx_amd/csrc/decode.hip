@@ -700,6 +700,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       mx = wave_max_xor(mx, 32);
       const float m_new = fmaxf(m_run, mx * a.qk_scale);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      const float m_run_prev = m_run;
       float psum = 0.f;
       for (int e = 0; e < 8; ++e) {
         x[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a.qk_scale, -m_new));
@@ -707,23 +708,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       l_run = l_run * alpha + psum;
       m_run = m_new;
-      for (int j = 0; j < 8; ++j) o[j] *= alpha;
-
-      if (kI4) {
+      if (!kI4) {
+        for (int j = 0; j < 8; ++j) o[j] *= alpha;
+      } else if (__any(m_new > m_run_prev)) {
+        // int4 is VALU-bound: rescale only when some column's maximum grew (alpha is
+        // exactly 1 elsewhere)
+        for (int j = 0; j < 8; ++j) o[j] *= alpha;
         cor0 *= alpha;
         cor1 *= alpha;
+      }
+
+      if (kI4) {
         uint32_t cw[8];
         for (int kk = 0; kk < 8; ++kk) {
           const uint32_t pw = (uint32_t)__builtin_amdgcn_mov_dpp((int)v4[kk], 0x128, 0xF, 0xF, false);  // row_ror:8
           cw[kk] = __builtin_amdgcn_perm(pw, v4[kk], vsel);
         }
-        // B operands P'_grp = bf16(P s_grp) (0 past L, where the parameters are not read),
-        // k = 4h + e <-> position p0 + 8c + k
+        // B operands P'_grp = bf16(P s_grp), k = 4h + e <-> position p0 + 8c + k; in the
+        // segment's last tile the parameters of positions past L (stale, possibly not
+        // finite) are zeroed first
+        if (p0 + kTile > L)
+          for (int k = 0; k < 8; ++k)
+            if (p0 + 8 * c + k >= L) {
+              mv[0][k >> 2][k & 3] = 0u;
+              mv[1][k >> 2][k & 3] = 0u;
+            }
         float pv0[8], pv1[8];
         for (int k = 0; k < 8; ++k) {
-          const bool valid = p0 + 8 * c + k < L;
-          const uint32_t sw = valid ? mv[0][k >> 2][k & 3] : 0u;
-          const uint32_t bw = valid ? mv[1][k >> 2][k & 3] : 0u;
+          const uint32_t sw = mv[0][k >> 2][k & 3];
+          const uint32_t bw = mv[1][k >> 2][k & 3];
           pv0[k] = x[k] * bf16_lo(sw);
           pv1[k] = x[k] * bf16_hi(sw);
           cor0 += x[k] * bf16_lo(bw);
