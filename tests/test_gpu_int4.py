@@ -249,3 +249,46 @@ def test_int4_fused_step(ema, ora, flags):
     dv = ora.bf16_from_f32(ora.int4_dequantize(g[3].view(np.uint32), g[4].view(np.uint16), g[5].view(np.uint16)))
     assert_close(host(fused), ora.sdpa(host(q), ora.bf16_from_f32(dk_f), dv, L, scale_of(D), False),
                  "int4 fused vs oracle")
+
+
+def test_int4_graph_replay_matches_eager(ema, ora):
+    """The fused int4 step captured in a HIP graph: every replay, with eager work and
+    synchronisation in between, equals the eager result (and rewrites the same row)."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 4, 16, 8, 128, 1024
+    off = np.array([100, 1023, 0, 512], np.int32)
+    (kq, _), (vq, _) = quantized_kv(ora, (B, Hkv, cap, D), seed=860)
+    qkv = dev(ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=862))
+    qw = dev(ora.normal_bf16(D, seed=863, mean=1.0, std=0.02))
+    kw = dev(ora.normal_bf16(D, seed=864, mean=1.0, std=0.02))
+    cache = int4_cache(ema, kq, vq)
+    off_d = dev(off)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device="cuda")
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+
+    def step():
+        ema.decode_step(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, cap, out=out, workspace=ws)
+
+    say("int4 fused step graph replay")
+    step()
+    torch.cuda.synchronize()
+    eager = host(out).copy()
+    stored = [host(t).copy() for t in (cache.k, cache.k_scales, cache.k_biases, cache.v_scales)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), eager), f"replay {i}"
+        for t, ref in zip((cache.k, cache.k_scales, cache.k_biases, cache.v_scales), stored):
+            assert np.array_equal(host(t), ref)
+        step()
+        torch.cuda.synchronize()
