@@ -742,13 +742,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           cor0 += x[k] * bf16_lo(bw);
           cor1 += x[k] * bf16_hi(bw);
         }
+        // the offset's share uses the rounded operands themselves: sum of each bf16 pair
+        // by a dot product with (1, 1)
         u32x4 pw0, pw1;
+        float t0 = 0.f, t1 = 0.f;
         for (int e = 0; e < 4; ++e) {
           pw0[e] = pack_bf16x2(pv0[2 * e], pv0[2 * e + 1]);
           pw1[e] = pack_bf16x2(pv1[2 * e], pv1[2 * e + 1]);
-          cor0 -= 128.f * (bf16_lo(pw0[e]) + bf16_hi(pw0[e]));
-          cor1 -= 128.f * (bf16_lo(pw1[e]) + bf16_hi(pw1[e]));
+          t0 = dot2_bf16(pw0[e], 0x3F803F80u, t0);
+          t1 = dot2_bf16(pw1[e], 0x3F803F80u, t1);
         }
+        cor0 = __builtin_fmaf(-128.f, t0, cor0);
+        cor1 = __builtin_fmaf(-128.f, t1, cor1);
         const bf16x8 pop0 = as_bf16x8(pw0), pop1 = as_bf16x8(pw1);
         // A operand of dim slot j: row m, k-slots (2tt, 2tt + 1) = nibble j of the words of
         // positions p0 + 8c + 2tt, +1 (byte j / 2 of both gathered by one v_perm)
