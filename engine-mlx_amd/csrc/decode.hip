@@ -44,6 +44,7 @@
 #include <cstdlib>
 
 #include "ema_common.hpp"
+#include "ema_schedule.hpp"
 
 namespace ema {
 namespace {
@@ -87,20 +88,10 @@ struct DecodeArgs {
 };
 
 __device__ __forceinline__ int64_t worker_of(int64_t t, int64_t total, int W) {
-  return ((t + 1) * (int64_t)W - 1) / total;
+  return split_worker_of(t, total, W);
 }
-// Workers used for `total` tiles (the tiles of the actual lengths, known on the device):
-// at least one tile per wave of each workgroup, at most the plan's W (which sizes the
-// workspace from the host's upper bound of the lengths). The decode and merge kernels
-// both derive it from the same values.
-__device__ __forceinline__ int active_workers(int64_t total, int W) {
-  const int64_t want = (total + kWaves - 1) / kWaves;
-  return (int)(want < W ? want : W);
-}
-
-__device__ __forceinline__ int64_t worker_begin(int64_t w, int64_t total, int W) {
-  return w * total / W;
-}
+__device__ __forceinline__ int active_workers(int64_t total, int W) { return split_active_workers(total, W, kWaves); }
+__device__ __forceinline__ int64_t worker_begin(int64_t w, int64_t total, int W) { return split_begin(w, total, W); }
 
 __device__ __forceinline__ int clamp_len(int L, int cap) { return L < 0 ? 0 : (L > cap ? cap : L); }
 

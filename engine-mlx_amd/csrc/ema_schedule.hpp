@@ -1,0 +1,80 @@
+// Integer work schedules of the attention kernels: which (sequence, head, query block) a
+// prefill workgroup runs, and how the decode split cuts the tile range of all
+// (sequence, kv head) segments into worker slices. The kernels call these functions on
+// the device; the CPU tests (tests/cpp/test_schedule.cpp, built with a host compiler)
+// call the same definitions to check that every work item is covered exactly once.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define EMA_HD __host__ __device__ __forceinline__
+#else
+#define EMA_HD inline
+#endif
+
+namespace ema {
+
+// ------------------------------------------------------------------ prefill
+// MI355X dispatches consecutive workgroups round-robin over its 8 XCDs (workgroup x
+// runs on XCD x % 8), each XCD with its own L2.
+constexpr int kSchedXcds = 8;
+
+struct PrefillItem {
+  int b;          // sequence
+  int kh;         // kv head
+  int h;          // query head
+  int qb_first;   // query block run first
+  int qb_second;  // query block run second (== qb_first: none)
+};
+
+// Work item of prefill workgroup x out of `grid`, for B sequences, Hkv kv heads with G
+// query heads each, and nqb query blocks per head.
+//
+// When the (sequence, kv head) groups divide evenly over the XCDs (and so does the grid),
+// all query heads of a group run on the group's XCD, so its K/V stream is read from HBM
+// once and served from that L2 to every workgroup attending over it. Inside an XCD (or
+// over the whole grid otherwise) work items are ranked heaviest first, because a later
+// query block sees more keys under the causal mask. With `paired`, a workgroup takes the
+// heavy query block nqb-1-p and then the light block p of the same head (grid =
+// ceil(nqb/2) * B * Hkv * G); with odd nqb the middle block is paired with itself and run
+// once.
+EMA_HD PrefillItem prefill_item(int64_t x, int64_t grid, int B, int Hkv, int G, int nqb, int paired) {
+  const int groups = B * Hkv;
+  const bool by_xcd = groups % kSchedXcds == 0 && grid % kSchedXcds == 0;
+  const int64_t rank = by_xcd ? x / kSchedXcds : x;
+  const int groups_local = by_xcd ? groups / kSchedXcds : groups;
+  const int64_t per_qb = (int64_t)groups_local * G;
+  PrefillItem it;
+  it.qb_first = nqb - 1 - (int)(rank / per_qb);
+  it.qb_second = paired ? nqb - 1 - it.qb_first : it.qb_first;
+  const int rest = (int)(rank % per_qb);
+  const int grp = by_xcd ? (rest / G) * kSchedXcds + (int)(x % kSchedXcds) : rest / G;
+  it.b = grp / Hkv;
+  it.kh = grp % Hkv;
+  it.h = it.kh * G + rest % G;
+  return it;
+}
+
+// Grid size for prefill_item: nqb * B * Hq items, or ceil(nqb/2) * B * Hq pairs.
+EMA_HD int64_t prefill_grid(int B, int Hq, int nqb, int paired) {
+  return (int64_t)(paired ? (nqb + 1) / 2 : nqb) * B * Hq;
+}
+
+// ------------------------------------------------------------------ decode split
+// The valid rows of every (sequence b, kv head kh) pair form a segment of ceil(len/32)
+// tiles; segments are laid end to end (sequence-major, then kv head) and the flattened
+// range of `total` tiles is cut into W slices, slice w = [split_begin(w), split_begin(w+1)).
+
+// Workers used for `total` tiles: at least one tile per wave (`waves` per workgroup), at
+// most the plan's W, which sizes the workspace from the host's upper bound of the lengths.
+EMA_HD int split_active_workers(int64_t total, int W, int waves) {
+  const int64_t want = (total + waves - 1) / waves;
+  return (int)(want < W ? want : W);
+}
+// First tile of slice w.
+EMA_HD int64_t split_begin(int64_t w, int64_t total, int W) { return w * total / W; }
+// Slice holding tile t (the inverse of split_begin).
+EMA_HD int64_t split_worker_of(int64_t t, int64_t total, int W) { return ((t + 1) * (int64_t)W - 1) / total; }
+
+}  // namespace ema

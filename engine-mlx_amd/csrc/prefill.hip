@@ -250,19 +250,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // o and l relative to the base m_use (p = 2^(s - m_use)); the score MFMA starts from
   // -m_use, so it yields s - m_use directly. m_use only changes on the slow path of the
   // softmax step.
-  float m_use = 0.f, l_run = 0.f;
+  float m_use = 0.f;
   bool seen = false;      // m_use is this row's running max (some score was finite)
   bool all_seen = false;  // wave-uniform: every row of the wave is seen
-  bool rescale = false;   // wave-uniform: o is to be scaled by o_scale before the next PV
-  float o_scale = 1.f;
+  bool rescale = false;   // wave-uniform: o and the row sums are to be scaled before the next PV
+  float o_scale = 1.f;    // factor of this lane's row
   f32x16 o[4], sc[2];
+  // Row sums of P, accumulated on the matrix pipe by a 16x16x32 MFMA whose A operand selects
+  // (B = the P^T chunk of a PV step: lane l holds row l % 32, so column n of the 16-wide view
+  // holds rows n (lanes n, n+32: k 0-7, 16-23) and n+16 (lanes n+16, n+48: k 8-15, 24-31)).
+  // A row 0 is one over k 0-7 and 16-23, row 1 over k 8-15 and 24-31, the rest zero, so
+  // lane n < 16 accumulates row n's sum in lsum[0] and row n+16's in lsum[1]. These sums are
+  // taken over the bf16-rounded P that PV multiplies, and VALU dot products would cost about
+  // 40 cycles each beside the other wave's MFMAs.
+  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
+  const bool sel = ((lane & 15) == 0 && ((lane >> 4) & 1) == 0) || ((lane & 15) == 1 && ((lane >> 4) & 1) == 1);
+  const uint32_t sel_w = sel ? 0x3F803F80u : 0u;
+  const bf16x8 sum_sel = as_bf16x8(u32x4{sel_w, sel_w, sel_w, sel_w});
   for (int dt = 0; dt < 4; ++dt)
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
   for (int kt = 0; kt < 2; ++kt)
     for (int i = 0; i < 16; ++i) sc[kt][i] = 0.f;
   u32x4 pw[4] = {};  // P^T of the last softmax step as bf16 pairs, for the next PV
   bf16x8 qop[8];     // Q^T operand (set after the prologue)
-  const uint32_t ones = 0x3F803F80u;  // bf16 pair (1, 1)
 
   // K operand reads: row (lane & 31) (+32 for sub-tile 1), column chunk 2s + hh, stored
   // at chunk (2s + hh) ^ (lane & 15)
@@ -293,6 +303,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // change of the softmax step before is applied to o first.
   auto pv = [&](int jb) __attribute__((always_inline)) {
     const uint16_t* Vt = Vs + (jb & 1) * kTile;
+    for (int st = 0; st < 4; ++st) lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sum_sel, as_bf16x8(pw[st]), lsum, 0, 0, 0);
     for (int st = 0; st < 4; ++st) {
       const int kt = st >> 1, q2 = st & 1;
       const bf16x8 pop = as_bf16x8(pw[st]);
@@ -325,6 +336,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   constexpr int kRA = 4;
   auto pv_qk_schedule = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * kRA, 0);  // V^T reads of the first kRA PV MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);        // row-sum MFMAs (register operands)
     for (int i = 0; i < 16 - kRA; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // PV MFMA i
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // V^T reads of PV MFMA i + kRA
@@ -342,6 +354,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto apply_rescale = [&]() __attribute__((always_inline)) {
     if (rescale) {
       for (int dt = 0; dt < 4; ++dt) o[dt] *= o_scale;
+      lsum[0] *= o_scale;
+      lsum[1] *= __shfl(o_scale, (lane & 15) + 16, 64);  // lanes 0-15 hold row (lane & 15) + 16's sum
       rescale = false;
     }
   };
@@ -385,14 +399,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             sc[kt][i] = koff <= hi && koff >= lo ? sc[kt][i] : -INFINITY;
           }
       }
-      // P^T as bf16 pairs for the PV steps (step st: slots 8*(st&1) .. +7 of sub-tile
-      // st>>1) and this lane's share of the block row sum, taken over the rounded
-      // values the PV product uses.
-      float ps0 = 0.f, ps1 = 0.f;
-      // Fast path: p = 2^(s - m_use) as is. It is kept when every lane's sum is at most
-      // 256, which bounds every p by 256 (as a lazy rescale with threshold 8 would), so
-      // neither the max nor a rescale is needed.
-      bool fast = all_seen;
+      // P^T as bf16 pairs for the PV steps (step st: slots 8*(st&1) .. +7 of sub-tile st>>1).
+      // Fast path: p = 2^(s - m_use) with the running base m_use as is, taken when every
+      // score of the wave is at most 8 above the base, which bounds every p by 256 (a lazy
+      // rescale with threshold 8), so no row max is formed and nothing is rescaled.
+      float mx = sc[0][0];
+      for (int kt = 0; kt < 2; ++kt)
+        for (int i = kt ? 0 : 1; i < 16; ++i) mx = fmaxf(mx, sc[kt][i]);
+      const bool fast = all_seen && !__any(!(mx <= 8.f));  // NaN falls to the slow path too
       if (fast) {
         const uint32_t kob = blk_off(j + 2), vob = blk_off(j + 1);
         const int kwrap = wrap_rows(j + 2), vwrap = wrap_rows(j + 1);
@@ -402,44 +416,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           dma_part(v_rsrc, vob, voff, vdst, st, vwrap);
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
-            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i]), __builtin_amdgcn_exp2f(sc[kt][i + 1]));
-            pw[st][e] = w;
-            if (e & 1) ps1 = dot2_bf16(w, ones, ps1);
-            else ps0 = dot2_bf16(w, ones, ps0);
+            pw[st][e] = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i]), __builtin_amdgcn_exp2f(sc[kt][i + 1]));
           }
         }
-        fast = !__any(!(ps0 + ps1 <= 256.f));  // NaN/inf fall to the slow path too
       } else {
         load_k(j + 2);
         load_v(j + 1);
-      }
-      if (!fast) {
         // Slow path (first block of a row, or a row max that grew): move the base to
         // the row's running max and rescale what was accumulated.
-        float bm = -INFINITY;
-        for (int kt = 0; kt < 2; ++kt)
-          for (int i = 0; i < 16; ++i) bm = fmaxf(bm, sc[kt][i]);
-        bm = wave_max_xor(bm, 32);
+        const float bm = wave_max_xor(mx, 32);
         const float delta = seen ? fmaxf(bm, 0.f) : (bm == -INFINITY ? 0.f : bm);
         seen = seen || bm != -INFINITY;
         const float alpha = __builtin_amdgcn_exp2f(-delta);
-        l_run *= alpha;
         o_scale = alpha;
         rescale = true;
         m_use += delta;
-        ps0 = ps1 = 0.f;
         for (int st = 0; st < 4; ++st)
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
-            const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - delta),
-                                           __builtin_amdgcn_exp2f(sc[kt][i + 1] - delta));
-            pw[st][e] = w;
-            if (e & 1) ps1 = dot2_bf16(w, ones, ps1);
-            else ps0 = dot2_bf16(w, ones, ps0);
+            pw[st][e] = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i] - delta),
+                                    __builtin_amdgcn_exp2f(sc[kt][i + 1] - delta));
           }
         all_seen = __all(seen);
       }
-      l_run += ps0 + ps1;
     } else {
       load_k(j + 2);
       load_v(j + 1);
@@ -539,11 +538,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // staging tile in the Q area (Q is in registers since the prologue), from which all
   // eight waves store whole 256-byte rows with 16-byte stores.
   //   xo[g]: [d][i4][wq][lane] f32x4, the dims of group g that the other group finishes
-  //   xm[g], xl[g]: [wq][lane] this group's m (or -inf) and l share of the row
+  //   xm[g], xl[g]: [wq][lane] this group's m (or -inf) and row sum l
   float* const xo = (float*)lds;
   float* const xm = xo + 2 * 2 * 4 * 4 * 64 * 4;
   float* const xl = xm + 2 * 4 * 64;
   const int rr = 32 * wq + (lane & 31);  // row inside the workgroup
+  // this lane's row sum (the whole row: both key halves of the wave are in it)
+  const float l_lo = __shfl(lsum[0], lane & 15, 64), l_hi = __shfl(lsum[1], lane & 15, 64);
+  const float l_run = (lane & 16) ? l_hi : l_lo;
   {
     float* const mx = xo + g * (2 * 4 * 4 * 64 * 4);
     auto publish = [&](const int dt0) __attribute__((always_inline)) {
@@ -566,8 +568,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const float m = fmaxf(m0, m1);
     const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
     const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-    const float l_half = l0 * a0 + l1 * a1;
-    const float l_tot = l_half + __shfl_xor(l_half, 32, 64);
+    const float l_tot = l0 * a0 + l1 * a1;
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     const float a_mine = g ? a1 : a0, a_other = g ? a0 : a1;
     const float* const ox = xo + (1 - g) * (2 * 4 * 4 * 64 * 4);

@@ -288,31 +288,58 @@ def test_prefill_xcd_grid_mapping(ema, ora, causal, chunk):
 
 
 def test_prefill_qwen3_1p7b_2k(ema, ora):
-    """1 x 2048 tokens, 16q/8kv, causal from offset 0 (heads 0-3 checked)."""
-    say("prefill T=2048 16q/8kv causal")
-    got, ref = _prefill_case(ema, ora, 1, 16, 8, 128, 4096, 2048, [0], True, False, seed=310, heads=[0, 3])
-    assert_close(got, ref, "prefill 2k")
+    """1 x 2048 tokens, 16q/8kv, causal from offset 0: every head and row."""
+    say("prefill T=2048 16q/8kv causal, all heads")
+    got, ref = _prefill_case(ema, ora, 1, 16, 8, 128, 4096, 2048, [0], True, False, seed=310)
+    assert_close(got, ref, "prefill 2k 16q")
 
 
-def test_prefill_chunk_on_existing_cache_sampled_rows(ema, ora):
-    """64q/8kv, 14336 cached + 2048 new (16384 capacity); sampled rows of two heads."""
+def test_prefill_qwen3_8b_2k_all_heads(ema, ora):
+    """The benchmarked prefill shape: 1 x 2048 tokens, 32q/8kv, causal from offset 0, every
+    head and row. With 16 query blocks x 32 heads = 512 items the launch pairs query blocks
+    (a workgroup runs block 15-p, then block p)."""
+    say("prefill T=2048 32q/8kv causal, all heads (paired blocks)")
+    got, ref = _prefill_case(ema, ora, 1, 32, 8, 128, 4096, 2048, [0], True, False, seed=315)
+    assert_close(got, ref, "prefill 2k 32q")
+
+
+# Shapes with at least 2 x 256 query-block items, so the launch pairs query blocks, checked
+# in full: odd block counts (the middle block paired with itself), ragged offsets, chunk-only
+# windows, non-causal attention, and batch x kv heads not a multiple of the 8 XCDs.
+@pytest.mark.parametrize("B,Hq,Hkv,T,q_off,causal,chunk", [
+    (4, 16, 4, 1000, [0, 0, 0, 0], True, False),
+    (4, 16, 4, 1100, [0, 37, 300, 129], True, False),
+    (4, 16, 4, 1100, [64, 0, 250, 7], True, True),
+    (4, 16, 4, 1000, [0, 100, 3, 400], False, False),
+    (4, 16, 4, 1100, [10, 0, 128, 33], False, True),
+    (3, 24, 3, 900, [0, 17, 200], True, False),
+])
+def test_prefill_paired_blocks(ema, ora, B, Hq, Hkv, T, q_off, causal, chunk):
+    say(f"prefill paired B={B} Hq={Hq} Hkv={Hkv} T={T} q_off={q_off} causal={causal} chunk={chunk}")
+    got, ref = _prefill_case(ema, ora, B, Hq, Hkv, 128, 1536, T, q_off, causal, chunk, seed=370 + T + B)
+    assert_close(got, ref, "prefill paired")
+
+
+def test_prefill_chunk_on_existing_cache_every_block(ema, ora):
+    """64q/8kv, 14336 cached + 2048 new (16384 capacity): all 64 heads at the first and
+    last four rows of every 128-row query block."""
     import torch
 
     B, Hq, Hkv, D, cap, T, off = 1, 64, 8, 128, 16384, 2048, 14336
-    say("prefill chunked 64q/8kv off 14336 T 2048")
+    say("prefill chunked 64q/8kv off 14336 T 2048, every query block")
     q = ora.normal_bf16((B, Hq, T, D), seed=320)
     kc = ora.normal_bf16((B, Hkv, cap, D), seed=321)
     vc = ora.normal_bf16((B, Hkv, cap, D), seed=322)
     cache = make_cache(ema, kc, vc)
     out = host(ema.prefill_attention(dev(q), cache, dev(np.array([off], np.int32)), causal=True))
     torch.cuda.synchronize()
-    out = out.reshape(T, Hq, D)
-    rows = np.r_[0:4, 1021:1025, T - 4:T]
-    for h in (0, 37):
-        for i in rows:
-            ref = ora.sdpa(q[:, h:h + 1, i:i + 1].copy(), kc[:, h // 8:h // 8 + 1].copy(),
-                           vc[:, h // 8:h // 8 + 1].copy(), [off + i + 1], scale_of(D), False)
-            assert_close(out[i, h][None], ref.reshape(1, D), f"row {i} head {h}")
+    out = out.reshape(T, Hq * D)
+    for qb in range(T // 128):
+        for r0 in (qb * 128, qb * 128 + 124):
+            # four consecutive rows: end-aligned causal over kv_len = off + r0 + 4 gives row
+            # r0 + i the keys <= off + r0 + i
+            ref = ora.sdpa(q[:, :, r0:r0 + 4].copy(), kc, vc, [off + r0 + 4], scale_of(D), True)
+            assert_close(out[r0:r0 + 4][None], ref, f"rows {r0}..{r0 + 3}")
 
 
 @pytest.mark.parametrize("causal,chunk,q_off", [(True, True, 100), (True, True, 64), (False, True, 37),
