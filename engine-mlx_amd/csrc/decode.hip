@@ -41,8 +41,6 @@
 // 8 bf16 values, plus the row's two block exponents, and turns them into the same bf16
 // operands just before use (code value times 2^exp is exact in bf16). Half the bytes,
 // identical arithmetic after the decode step.
-#include <cstdlib>
-
 #include "ema_common.hpp"
 #include "ema_schedule.hpp"
 
@@ -913,15 +911,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   a.out[((int64_t)b * a.Hq + (int64_t)kh * a.G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(acc / Lsum);
 }
 
-int max_workers() {
-  static int w = [] {
-    const char* e = getenv("EMA_DECODE_WORKERS");
-    int v = e ? atoi(e) : 0;
-    return v > 0 && v <= kMaxWorkers ? v : kMaxWorkers;
-  }();
-  return w;
-}
-
 }  // namespace
 
 DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len) {
@@ -929,7 +918,7 @@ DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len) {
   // at least one tile per wave of each workgroup
   const int64_t tiles = (int64_t)B * Hkv * ((max_len + kTile - 1) / kTile);
   const int64_t want = (tiles + kWaves - 1) / kWaves;
-  int64_t w = want < max_workers() ? want : max_workers();
+  int64_t w = want < kMaxWorkers ? want : kMaxWorkers;
   if (w < 1) w = 1;
   p.workers = (int)w;
   p.segments = B * Hkv;

@@ -72,9 +72,13 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 // Raw buffer resource (V#) over `bytes` bytes from `base`: stride 0, gfx9 dword3 with a
 // 32-bit data format. Loads at offsets at or past `bytes` return zeros.
+// Every argument is wave-uniform; readfirstlane keeps the words in scalar registers for the
+// asm operands that take them.
 __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   const uint64_t addr = (uint64_t)base;
-  return u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xffffu, bytes, 0x00020000u};
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)addr),
+               (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32) & 0xffffu),
+               (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
 }
 
 // 16 bytes per lane from buffer offset `voff` + 1024 * I straight into LDS at lds_addr +
@@ -93,6 +97,13 @@ __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_ad
 // Block offset that no buffer range reaches (ranges stay below 2^31 bytes, and a per-lane
 // offset added to it stays below 2^32): the load returns zeros and touches no memory.
 constexpr uint32_t kNoRow = 0xF0000000u;
+
+// Elementwise maximum of three f16 pairs (v_pk_maximum3_f16, NaN-propagating).
+__device__ __forceinline__ uint32_t pk_max3_f16(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_pk_maximum3_f16 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 // kRot: rotating cache (EMA_KV_ROTATING). The keys of a sequence are the positions
 // [base, q_off + T) with base = max(0, q_off + T - cap), position p in row p % cap; the
@@ -168,15 +179,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   uint16_t* const Ks = lds + g * kGroupElems;     // this group's K tiles: buffer i at Ks + i * kTile
   uint16_t* const Vs = Ks + 2 * kTile;            // and V tiles
 
-  // K/V of this (batch, kv head) through buffer loads. One resource per tensor covers the
-  // rows below kv_len, so rows past the valid length read as zeros (finite, and masked
-  // out) without per-lane clamping; a block is addressed by adding its byte offset to the
-  // per-lane offsets.
+  // K/V of this (batch, kv head) through buffer loads. A resource covers the rows below
+  // kv_len, so rows past the valid length read as zeros (finite, and masked out) without
+  // per-lane clamping. Static cache: each tile load gets a resource of its own whose base
+  // is the tile's first row (scalar arithmetic), so the per-lane offsets never change.
+  // Rotating cache: one resource per tensor, the block's offset added to the per-lane
+  // offsets (rows may wrap around the ring).
   const char* Kg = (const char*)(a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh);
   const char* Vg = (const char*)(a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh);
   const uint32_t row_bytes = (uint32_t)a.sp * 2;
-  const u32x4 k_rsrc = buffer_rsrc(Kg, (uint32_t)kv_len * row_bytes);
-  const u32x4 v_rsrc = buffer_rsrc(Vg, (uint32_t)kv_len * row_bytes);
+  const uint32_t kv_bytes = (uint32_t)kv_len * row_bytes;
+  const u32x4 k_rsrc = buffer_rsrc(Kg, kv_bytes);
+  const u32x4 v_rsrc = buffer_rsrc(Vg, kv_bytes);
+  // resource of the tile at byte offset ob of `base` (blk_off: below kv_bytes, or kNoRow
+  // for an empty range that reads all zeros)
+  auto tile_rsrc = [&](const char* base, uint32_t ob) __attribute__((always_inline)) {
+    const bool none = ob == kNoRow;
+    return buffer_rsrc(base + (none ? 0u : ob), none ? 0u : kv_bytes - ob);
+  };
 
   // Global -> LDS without registers (buffer_load_dwordx4 ... lds): one instruction moves
   // 1 KB, lane l's 16 bytes landing at byte 16l of the destination, i.e. 4 tile rows.
@@ -209,8 +229,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
   // one of the 4 instructions of a tile load (spread over the softmax step so the four
   // waves of a group do not queue 32 KB at the address unit at once)
-  auto dma_part = [&](const u32x4 r, uint32_t off_blk, const uint32_t* off, uint32_t dst, int i, int wrap)
-      __attribute__((always_inline)) {
+  // r: the tensor's resource (rotating cache) or the tile's (static cache: off_blk is used
+  // only to empty this lane's row when it is kNoRow and `lane_rows` is set)
+  auto dma_part = [&](const u32x4 r, uint32_t off_blk, const uint32_t* off, uint32_t dst, int i, int wrap,
+                      bool lane_rows = false) __attribute__((always_inline)) {
     if (kRot) {
       // true offsets (the instruction offset unused, the LDS address moved through M0), so
       // a row past the ring's end, moved cap rows back, never goes below zero
@@ -219,7 +241,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       dma16<0>(r, o, dst + 1024u * i);
       return;
     }
-    const uint32_t o = off[i] + off_blk;
+    const uint32_t o = lane_rows && off_blk == kNoRow ? kNoRow : off[i];
     switch (i) {
       case 0: dma16<0>(r, o, dst); break;
       case 1: dma16<1>(r, o, dst); break;
@@ -227,8 +249,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       default: dma16<3>(r, o, dst); break;
     }
   };
-  auto dma = [&](const u32x4 r, int j, const uint32_t* off, const uint16_t* tile) __attribute__((always_inline)) {
+  auto dma = [&](const char* tensor, const u32x4 tensor_r, int j, const uint32_t* off, const uint16_t* tile)
+      __attribute__((always_inline)) {
     const uint32_t ob = blk_off(j), dst = tile_dst(tile);
+    const u32x4 r = kRot ? tensor_r : tile_rsrc(tensor, ob);
     const int wrap = wrap_rows(j);
     const int base = (gb0 + j) * kBN;
     if (j < ng && base < kv_begin) {
@@ -237,14 +261,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       // the cache holds there (even NaN) cannot reach the masked products
       for (int i = 0; i < 4; ++i) {
         const int row = base + 16 * wq + 4 * i + r4;
-        dma_part(r, row < kv_begin ? kNoRow : ob, off, dst, i, row < kv_begin ? kBN : wrap);
+        dma_part(r, row < kv_begin ? kNoRow : ob, off, dst, i, row < kv_begin ? kBN : wrap, true);
       }
     } else {
       for (int i = 0; i < 4; ++i) dma_part(r, ob, off, dst, i, wrap);
     }
   };
-  auto load_k = [&](int j) __attribute__((always_inline)) { dma(k_rsrc, j, koff, Ks + (j & 1) * kTile); };
-  auto load_v = [&](int j) __attribute__((always_inline)) { dma(v_rsrc, j, voff, Vs + (j & 1) * kTile); };
+  auto load_k = [&](int j) __attribute__((always_inline)) { dma(Kg, k_rsrc, j, koff, Ks + (j & 1) * kTile); };
+  auto load_v = [&](int j) __attribute__((always_inline)) { dma(Vg, v_rsrc, j, voff, Vs + (j & 1) * kTile); };
 
   // Online softmax state of this lane's row, in the log2 domain. The accumulators hold
   // o and l relative to the base m_use (p = 2^(s - m_use)); the score MFMA starts from
@@ -303,7 +327,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // change of the softmax step before is applied to o first.
   auto pv = [&](int jb) __attribute__((always_inline)) {
     const uint16_t* Vt = Vs + (jb & 1) * kTile;
-    for (int st = 0; st < 4; ++st) lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sum_sel, as_bf16x8(pw[st]), lsum, 0, 0, 0);
     for (int st = 0; st < 4; ++st) {
       const int kt = st >> 1, q2 = st & 1;
       const bf16x8 pop = as_bf16x8(pw[st]);
@@ -317,6 +340,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         const s16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[dt] = mfma32(__builtin_bit_cast(bf16x8, av), pop, o[dt]);
       }
+      lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sum_sel, pop, lsum, 0, 0, 0);
     }
   };
   auto qk = [&](int jb) __attribute__((always_inline)) {
@@ -335,14 +359,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // the first K reads are issued under the last PV MFMAs.
   constexpr int kRA = 4;
   auto pv_qk_schedule = [&]() __attribute__((always_inline)) {
+    // 20 MFMAs: per PV step st, its 4 PV MFMAs and the row-sum MFMA of its P chunk
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * kRA, 0);  // V^T reads of the first kRA PV MFMAs
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);        // row-sum MFMAs (register operands)
     for (int i = 0; i < 16 - kRA; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // PV MFMA i
+      if ((i & 3) == 3) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // row sum of step i / 4
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // V^T reads of PV MFMA i + kRA
     }
     for (int i = 0; i < kRA; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // PV MFMA 16 - kRA + i
+      if (i == kRA - 1) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // row sum of the last step
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // K read of QK MFMA i
     }
     for (int i = 0; i < 16 - kRA; ++i) {
@@ -400,30 +426,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           }
       }
       // P^T as bf16 pairs for the PV steps (step st: slots 8*(st&1) .. +7 of sub-tile st>>1).
-      // Fast path: p = 2^(s - m_use) with the running base m_use as is, taken when every
-      // score of the wave is at most 8 above the base, which bounds every p by 256 (a lazy
-      // rescale with threshold 8), so no row max is formed and nothing is rescaled.
-      float mx = sc[0][0];
-      for (int kt = 0; kt < 2; ++kt)
-        for (int i = kt ? 0 : 1; i < 16; ++i) mx = fmaxf(mx, sc[kt][i]);
-      const bool fast = all_seen && !__any(!(mx <= 8.f));  // NaN falls to the slow path too
+      // Fast path: p = 2^(s - m_use) with the running base m_use as is, kept when every p
+      // of the wave is at most 256 (a lazy rescale with threshold 8 in the log2 domain), so
+      // no row max is formed and nothing is rescaled. The check takes the maximum of the
+      // packed bf16 words read as f16 pairs: for p >= 0 the bit patterns below 0x7C00 are
+      // ordered alike in both formats, and larger ones (p >= 2^121, inf, NaN) read as f16
+      // inf or NaN, which the maximum keeps.
+      bool fast = all_seen;
       if (fast) {
         const uint32_t kob = blk_off(j + 2), vob = blk_off(j + 1);
         const int kwrap = wrap_rows(j + 2), vwrap = wrap_rows(j + 1);
+        const u32x4 kr = kRot ? k_rsrc : tile_rsrc(Kg, kob), vr = kRot ? v_rsrc : tile_rsrc(Vg, vob);
         const uint32_t kdst = tile_dst(Ks + (j & 1) * kTile), vdst = tile_dst(Vs + ((j + 1) & 1) * kTile);
         for (int st = 0; st < 4; ++st) {
-          dma_part(k_rsrc, kob, koff, kdst, st, kwrap);
-          dma_part(v_rsrc, vob, voff, vdst, st, vwrap);
+          dma_part(kr, kob, koff, kdst, st, kwrap);
+          dma_part(vr, vob, voff, vdst, st, vwrap);
           for (int e = 0; e < 4; ++e) {
             const int kt = st >> 1, i = 8 * (st & 1) + 2 * e;
             pw[st][e] = pack_bf16x2(__builtin_amdgcn_exp2f(sc[kt][i]), __builtin_amdgcn_exp2f(sc[kt][i + 1]));
           }
         }
+        uint32_t pm = pk_max3_f16(pw[0][0], pw[0][1], pw[0][2]);
+        pm = pk_max3_f16(pm, pw[0][3], pw[1][0]);
+        pm = pk_max3_f16(pm, pw[1][1], pw[1][2]);
+        pm = pk_max3_f16(pm, pw[1][3], pw[2][0]);
+        pm = pk_max3_f16(pm, pw[2][1], pw[2][2]);
+        pm = pk_max3_f16(pm, pw[2][3], pw[3][0]);
+        pm = pk_max3_f16(pm, pw[3][1], pw[3][2]);
+        pm = pk_max3_f16(pm, pw[3][3], pw[3][3]);
+        fast = !__any((pm & 0xffffu) > 0x4380u || pm > 0x4380ffffu);  // some p > 256
       } else {
         load_k(j + 2);
         load_v(j + 1);
+      }
+      if (!fast) {
         // Slow path (first block of a row, or a row max that grew): move the base to
         // the row's running max and rescale what was accumulated.
+        float mx = sc[0][0];
+        for (int kt = 0; kt < 2; ++kt)
+          for (int i = kt ? 0 : 1; i < 16; ++i) mx = fmaxf(mx, sc[kt][i]);
         const float bm = wave_max_xor(mx, 32);
         const float delta = seen ? fmaxf(bm, 0.f) : (bm == -INFINITY ? 0.f : bm);
         seen = seen || bm != -INFINITY;
