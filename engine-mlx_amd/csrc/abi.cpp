@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "ema_common.hpp"
 
@@ -99,6 +100,35 @@ int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
       c->stride_head < 0 || c->stride_batch < 0)
     return set_error(EMA_ERR_SHAPE, "%s: cache strides must be >= head_dim and multiples of 8 elements", op);
   if (!aligned16(c->k) || !aligned16(c->v)) return set_error(EMA_ERR_INVALID_ARG, "%s: cache buffers must be 16-byte aligned", op);
+  return EMA_OK;
+}
+
+// Static scratch of ema_decode_step_noalloc (the split's header and partial softmax
+// states), one copy per device, held until the process ends. In host code `scratch` is only
+// a stand-in for the symbol: its device address comes from hipGetSymbolAddress, looked up
+// once per device with that device current, and only that address is passed to kernels.
+// The decode kernels write every byte they later read, so nothing needs clearing; calls
+// that overlap on one device share the array and race.
+__device__ __align__(256) unsigned char scratch[EMA_NOALLOC_SCRATCH_BYTES];
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int32_t noalloc_scratch(const char* op, void** addr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(EMA_ERR_HIP, "%s: no usable current device (%d)", op, dev);
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return set_error(EMA_ERR_HIP, "%s: static scratch address on device %d: %s", op, dev, hipGetErrorString(e));
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
   return EMA_OK;
 }
 
@@ -354,11 +384,9 @@ int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcac
   return launch_decode((hipStream_t)stream, q, *cache, lengths, n_heads, scale, out, workspace, p);
 }
 
-int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
-                        float eps, float theta, const int32_t* offsets, int32_t max_len, int32_t n_heads,
-                        uint32_t flags, float scale, const ema_kvcache_desc* cache, void* out, void* workspace,
-                        uint64_t workspace_bytes) {
-  const char* op = "ema_decode_step";
+static int32_t check_decode_step(const char* op, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                 float eps, float theta, const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                                 uint32_t flags, float scale, const ema_kvcache_desc* cache, void* out) {
   int32_t rc = check_cache(op, cache);
   if (rc) return rc;
   if (!qkv || !out || !offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null qkv/out/offsets", op);
@@ -371,6 +399,17 @@ int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm
   if (!(eps >= 0.f) || !(theta > 0.f) || !(scale > 0.f))
     return set_error(EMA_ERR_INVALID_ARG, "%s: eps must be >= 0, theta and scale > 0", op);
   if (!aligned16(qkv) || !aligned16(out)) return set_error(EMA_ERR_INVALID_ARG, "%s: qkv/out must be 16-byte aligned", op);
+  return EMA_OK;
+}
+
+int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                        float eps, float theta, const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                        uint32_t flags, float scale, const ema_kvcache_desc* cache, void* out, void* workspace,
+                        uint64_t workspace_bytes) {
+  const char* op = "ema_decode_step";
+  int32_t rc = check_decode_step(op, qkv, q_norm_w, k_norm_w, eps, theta, offsets, max_len, n_heads, flags, scale,
+                                 cache, out);
+  if (rc) return rc;
   DecodePlan p = plan_decode(cache->batch, n_heads, cache->n_kv_heads, cache->head_dim, max_len);
   const uint64_t need = decode_workspace_bytes(p);
   if (!workspace || workspace_bytes < need)
@@ -379,6 +418,26 @@ int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm
   if (!aligned16(workspace)) return set_error(EMA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", op);
   FusedPre f{qkv, q_norm_w, k_norm_w, offsets, eps, theta, flags};
   return launch_decode((hipStream_t)stream, nullptr, *cache, nullptr, n_heads, scale, out, workspace, p, &f);
+}
+
+int32_t ema_decode_step_noalloc(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                float eps, float theta, const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                                uint32_t flags, float scale, const ema_kvcache_desc* cache, void* out) {
+  const char* op = "ema_decode_step_noalloc";
+  int32_t rc = check_decode_step(op, qkv, q_norm_w, k_norm_w, eps, theta, offsets, max_len, n_heads, flags, scale,
+                                 cache, out);
+  if (rc) return rc;
+  DecodePlan p = plan_decode(cache->batch, n_heads, cache->n_kv_heads, cache->head_dim, max_len);
+  const uint64_t need = decode_workspace_bytes(p);
+  if (need > EMA_NOALLOC_SCRATCH_BYTES)
+    return set_error(EMA_ERR_WORKSPACE,
+                     "%s: this shape needs %llu bytes of scratch, more than the %llu-byte static scratch; "
+                     "use ema_decode_step with a workspace",
+                     op, (unsigned long long)need, (unsigned long long)EMA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = noalloc_scratch(op, &ws))) return rc;
+  FusedPre f{qkv, q_norm_w, k_norm_w, offsets, eps, theta, flags};
+  return launch_decode((hipStream_t)stream, nullptr, *cache, nullptr, n_heads, scale, out, ws, p, &f);
 }
 
 static int32_t check_prefill(const char* op, const void* q, const ema_kvcache_desc* cache,

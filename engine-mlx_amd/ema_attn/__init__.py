@@ -42,7 +42,7 @@ EXPORTED = (
     "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8", "ema_kvcache_init_int4", "ema_kvcache_alloc_int4",
     "ema_kvcache_quantize_int4",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
-    "ema_decode_attention", "ema_decode_step", "ema_prefill_attention", "ema_prefill_workspace_size",
+    "ema_decode_attention", "ema_decode_step", "ema_decode_step_noalloc", "ema_prefill_attention", "ema_prefill_workspace_size",
     "ema_prefill_attention_ws", "ema_gdn_scan", "ema_quantized_matmul",
 )
 
@@ -96,6 +96,7 @@ def lib() -> ctypes.CDLL:
             "ema_decode_workspace_size": (i32, [i32, i32, i32, i32, i32, ctypes.POINTER(u64)]),
             "ema_decode_attention": (i32, [vp, vp, D, vp, i32, i32, f32, vp, vp, u64]),
             "ema_decode_step": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, u32, f32, D, vp, vp, u64]),
+            "ema_decode_step_noalloc": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, u32, f32, D, vp]),
             "ema_prefill_attention": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp]),
             "ema_prefill_workspace_size": (i32, [D, i32, ctypes.POINTER(u64)]),
             "ema_prefill_attention_ws": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp, i32, vp, u64]),
@@ -297,6 +298,19 @@ def decode_step(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: St
     _check(lib().ema_decode_step(_stream(stream), _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), eps, theta,
                                  _ptr(offsets), max_len, n_heads, flags, scale, ctypes.byref(cache.desc), _ptr(out),
                                  _ptr(workspace), workspace.numel()), "ema_decode_step")
+    return out
+
+
+def decode_step_noalloc(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: StaticCache, max_len, out,
+                        scale=None, flags=0, stream=None):
+    """ema_decode_step over the library's static per-device scratch: no workspace and no
+    device allocation in the call (out is the caller's [B, Hq*D] bf16 buffer)."""
+    D = cache.desc.head_dim
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    _check(lib().ema_decode_step_noalloc(_stream(stream), _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), eps, theta,
+                                         _ptr(offsets), max_len, n_heads, flags, scale, ctypes.byref(cache.desc),
+                                         _ptr(out)), "ema_decode_step_noalloc")
     return out
 
 

@@ -256,6 +256,23 @@ EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void
                                 uint32_t flags, float scale, const ema_kvcache_desc* cache,
                                 void* out, void* workspace, uint64_t workspace_bytes);
 
+/* Size of the static scratch behind ema_decode_step_noalloc (8 MiB per device). */
+#define EMA_NOALLOC_SCRATCH_BYTES (8ull << 20)
+/* ema_decode_step without a workspace argument and without any device allocation: the
+ * split's scratch lives in a static device array of EMA_NOALLOC_SCRATCH_BYTES per device,
+ * located on the first call on each device. No counterpart in the reference (MLX
+ * allocates inside its ops); it is for callers that cannot allocate device memory around
+ * the step: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation. Same arguments and results as ema_decode_step. A shape whose workspace
+ * (ema_decode_workspace_size for max_len) exceeds the scratch returns EMA_ERR_WORKSPACE.
+ * Every call on one device shares the array: calls that overlap on a device (concurrent
+ * streams) race; stream-ordered calls do not. */
+EMA_API int32_t ema_decode_step_noalloc(ema_stream_t stream, const void* qkv, const void* q_norm_w,
+                                        const void* k_norm_w, float eps, float theta,
+                                        const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                                        uint32_t flags, float scale, const ema_kvcache_desc* cache,
+                                        void* out);
+
 /* Prefill / chunked-prefill attention over the static cache
  * (MlxCtx::sdpa(causal), blas.rs:82-101 via forward_qwen3.rs:150 and
  * attend_and_project, crates/ops/src/attention.rs:162-177).

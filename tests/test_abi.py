@@ -137,6 +137,27 @@ def test_decode_step_argument_errors(ema):
     assert rc == ema.EMA_ERR_SHAPE
 
 
+def test_decode_step_noalloc_argument_errors(ema):
+    """The allocation-free step validates like ema_decode_step, and a shape whose split
+    workspace exceeds the static scratch is refused on the host (no HIP call)."""
+    L = ema.lib()
+    _, d = _desc(ema)
+    g = 0x40000
+    rc = L.ema_decode_step_noalloc(None, g, None, None, 1e-6, 1e6, g, 64, 16, 0, 0.088, ctypes.byref(d), g)
+    assert rc == ema.EMA_ERR_INVALID_ARG and "norm" in ema.last_error()
+    rc = L.ema_decode_step_noalloc(None, g, g, g, 1e-6, 1e6, g, 65, 16, 0, 0.088, ctypes.byref(d), g)
+    assert rc == ema.EMA_ERR_CAPACITY
+    rc = L.ema_decode_step_noalloc(None, g, g, g, 1e-6, 1e6, g, 64, 12, 0, 0.088, ctypes.byref(d), g)
+    assert rc == ema.EMA_ERR_SHAPE
+    # batch 1024 x 8 kv heads x 16 q heads each: the split state needs far more than 8 MiB
+    _, big = _desc(ema, B=1024, Hkv=8, cap=4096)
+    need = ctypes.c_uint64()
+    assert L.ema_decode_workspace_size(1024, 128, 8, 128, 4096, ctypes.byref(need)) == 0
+    assert need.value > (8 << 20)
+    rc = L.ema_decode_step_noalloc(None, g, g, g, 1e-6, 1e6, g, 4096, 128, 0, 0.088, ctypes.byref(big), g)
+    assert rc == ema.EMA_ERR_WORKSPACE and "static scratch" in ema.last_error()
+
+
 def test_prefill_argument_errors(ema):
     L = ema.lib()
     _, d = _desc(ema)
