@@ -390,7 +390,8 @@ static int32_t check_decode_step(const char* op, const void* qkv, const void* q_
   int32_t rc = check_cache(op, cache);
   if (rc) return rc;
   if (!qkv || !out || !offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null qkv/out/offsets", op);
-  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE)) return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
+  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE | EMA_STEP_ADVANCE))
+    return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
   if (!(flags & EMA_PRE_NO_NORM) && (!q_norm_w || !k_norm_w))
     return set_error(EMA_ERR_INVALID_ARG, "%s: norm weights are null (pass EMA_PRE_NO_NORM for models without q/k norm)", op);
   if ((rc = check_heads(op, n_heads, cache->n_kv_heads))) return rc;
@@ -403,7 +404,7 @@ static int32_t check_decode_step(const char* op, const void* qkv, const void* q_
 }
 
 int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
-                        float eps, float theta, const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                        float eps, float theta, int32_t* offsets, int32_t max_len, int32_t n_heads,
                         uint32_t flags, float scale, const ema_kvcache_desc* cache, void* out, void* workspace,
                         uint64_t workspace_bytes) {
   const char* op = "ema_decode_step";
@@ -421,7 +422,7 @@ int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm
 }
 
 int32_t ema_decode_step_noalloc(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
-                                float eps, float theta, const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                                float eps, float theta, int32_t* offsets, int32_t max_len, int32_t n_heads,
                                 uint32_t flags, float scale, const ema_kvcache_desc* cache, void* out) {
   const char* op = "ema_decode_step_noalloc";
   int32_t rc = check_decode_step(op, qkv, q_norm_w, k_norm_w, eps, theta, offsets, max_len, n_heads, flags, scale,

@@ -48,11 +48,11 @@ namespace ema {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kTile = 32;
-constexpr int kWaves = 4;       // waves per workgroup, each an independent worker
+constexpr int kTile = kSplitTile;
+constexpr int kWaves = kSplitWaves;  // waves per workgroup, each an independent worker
 constexpr int kMaxB = 1024;     // batch rows held in the LDS prefix table
 constexpr int kPieceStride = kD + 4;  // floats per (piece, head): m, l, pad, pad, o[D]
-constexpr int kMaxWorkers = 512;      // workgroups of the split (and staging rows of the merge)
+constexpr int kMaxWorkers = kSplitMaxWorkers;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -70,6 +70,7 @@ struct DecodeArgs {
   const uint16_t* qw;
   const uint16_t* kw;
   const int32_t* off;
+  int32_t* adv;  // EMA_STEP_ADVANCE: the offsets, advanced by decode_merge_kernel (else null)
   float eps, log2_theta;
   uint32_t flags;
   int fused;
@@ -865,18 +866,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // Log-sum-exp merge of the segments that span several workgroups, one thread per
 // (segment, head, dim). Every piece's (m, l, o[dim]) is loaded independently, so a
 // thread's loads are in flight together (one memory round trip per 8 pieces).
+// With EMA_STEP_ADVANCE it also moves each sequence's offset past the row the step
+// wrote (thread b for sequence b): decode_kernel, which reads the offsets, has finished,
+// and no thread here reads them (segment sizes come from the tile prefix).
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (a.adv && e < a.B) {
+    const int o = a.adv[e];
+    if (o >= 0 && o < INT32_MAX && (a.rot || o < a.cap)) a.adv[e] = o + 1;
+  }
   const int per_seg = a.G * kD;
   const int64_t s = e / per_seg;
   if (s >= (int64_t)a.B * a.Hkv) return;
   const int gg = (int)(e % per_seg) / kD, d = (int)(e % kD);
   const int b = (int)(s / a.Hkv), kh = (int)(s % a.Hkv);
-  const int L = seq_len(a, b);
   const int64_t total = a.hdr[a.B];  // tile prefix published by decode_kernel
-  if (L == 0 || total == 0) return;
+  const int nb = (a.hdr[b + 1] - a.hdr[b]) / a.Hkv;  // tiles per kv head of sequence b
+  if (nb == 0 || total == 0) return;
   const int W = active_workers(total, a.W);
-  const int nb = (L + kTile - 1) / kTile;
   const int64_t seg_first = a.hdr[b] + (int64_t)kh * nb;
   const int64_t w0 = worker_of(seg_first, total, W);
   const int64_t w1 = worker_of(seg_first + nb - 1, total, W);
@@ -915,12 +922,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 
 DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len) {
   DecodePlan p;
-  // at least one tile per wave of each workgroup
-  const int64_t tiles = (int64_t)B * Hkv * ((max_len + kTile - 1) / kTile);
-  const int64_t want = (tiles + kWaves - 1) / kWaves;
-  int64_t w = want < kMaxWorkers ? want : kMaxWorkers;
-  if (w < 1) w = 1;
-  p.workers = (int)w;
+  p.workers = split_plan_workers(B, Hkv, max_len);
   p.segments = B * Hkv;
   const int G = Hkv > 0 ? Hq / Hkv : 1;
   p.part_bytes = (uint64_t)(p.workers + p.segments) * G * kPieceStride * sizeof(float);
@@ -965,6 +967,7 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.qw = fused ? (const uint16_t*)(fused->q_norm_w ? fused->q_norm_w : fused->qkv) : nullptr;
   a.kw = fused ? (const uint16_t*)(fused->k_norm_w ? fused->k_norm_w : fused->qkv) : nullptr;
   a.off = fused ? fused->offsets : nullptr;
+  a.adv = fused && (fused->flags & EMA_STEP_ADVANCE) ? fused->offsets : nullptr;
   a.eps = fused ? fused->eps : 0.f;
   a.log2_theta = fused ? log2f(fused->theta) : 0.f;
   a.flags = fused ? fused->flags : 0u;
@@ -985,7 +988,7 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   else hipLaunchKernelGGL((decode_kernel<false, false>), grid, block, 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");
   if (rc) return rc;
-  if (plan.workers > 1) {
+  if (plan.workers > 1 || a.adv) {  // one worker: the merge kernel only advances the offsets
     const int64_t threads = (int64_t)plan.segments * G * kD;
     hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
     rc = check_hip(hipGetLastError(), "ema_decode_attention merge launch");

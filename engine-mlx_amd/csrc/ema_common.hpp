@@ -156,7 +156,7 @@ struct FusedPre {
   const void* qkv;
   const void* q_norm_w;
   const void* k_norm_w;
-  const int32_t* offsets;
+  int32_t* offsets;  // advanced in place with EMA_STEP_ADVANCE
   float eps;
   float theta;
   uint32_t flags;

@@ -66,6 +66,19 @@ EMA_HD int64_t prefill_grid(int B, int Hq, int nqb, int paired) {
 // tiles; segments are laid end to end (sequence-major, then kv head) and the flattened
 // range of `total` tiles is cut into W slices, slice w = [split_begin(w), split_begin(w+1)).
 
+constexpr int kSplitTile = 32;         // positions per tile
+constexpr int kSplitWaves = 4;         // waves per decode workgroup, each an independent worker
+constexpr int kSplitMaxWorkers = 512;  // workgroups of the split (and staging rows of the merge)
+
+// Workgroups the plan sizes the workspace for, from the host's upper bound of the lengths:
+// at least one tile per wave, at most kSplitMaxWorkers.
+EMA_HD int split_plan_workers(int B, int Hkv, int max_len) {
+  const int64_t tiles = (int64_t)B * Hkv * ((max_len + kSplitTile - 1) / kSplitTile);
+  const int64_t want = (tiles + kSplitWaves - 1) / kSplitWaves;
+  const int64_t w = want < kSplitMaxWorkers ? want : kSplitMaxWorkers;
+  return (int)(w < 1 ? 1 : w);
+}
+
 // Workers used for `total` tiles: at least one tile per wave (`waves` per workgroup), at
 // most the plan's W, which sizes the workspace from the host's upper bound of the lengths.
 EMA_HD int split_active_workers(int64_t total, int W, int waves) {

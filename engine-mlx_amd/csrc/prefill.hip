@@ -31,6 +31,7 @@
 // in the next phase the roles swap. The matrix pipe and the vector pipe of a SIMD are fed
 // by different waves throughout.
 #include "ema_common.hpp"
+#include "ema_schedule.hpp"
 
 namespace ema {
 namespace {
@@ -49,7 +50,6 @@ constexpr int kTile = kBN * kD;                    // elements of one K or V til
 constexpr int kGroupElems = 4 * kTile;              // one group: K0 K1 V0 V1
 constexpr int kQElems = kBM * kD;                   // the workgroup's Q rows (32 KB)
 constexpr int kLdsBytes = (2 * kGroupElems + kQElems) * 2;  // 163840 B: one workgroup per CU
-constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dispatched round-robin
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -118,28 +118,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int g = wave >> 2;         // key-range group
   const int wq = wave & 3;         // row tile of the wave inside the workgroup
-  // Grid mapping. Workgroups are dispatched round-robin over the 8 XCDs (x % 8), each
-  // with its own L2. When the (batch, kv head) groups divide evenly over the XCDs, all
-  // query heads of a group run on the group's XCD, so its K/V stream is read from HBM
-  // once and served from that L2 to every workgroup that attends over it. Inside an XCD
-  // (or over the whole grid otherwise) work items are ranked heaviest first: a later
-  // query block sees more keys. With two workgroups' worth of query blocks or more per
-  // CU, a workgroup takes a pair instead -- the heavy query block nqb-1-p, then the light
-  // one p of the same head -- which balances the causal work per workgroup and pays the
-  // launch of one workgroup per pair.
-  const int groups = a.B * a.Hkv;
-  const bool by_xcd = groups % kXcds == 0 && gridDim.x % kXcds == 0;
-  const int64_t x = blockIdx.x;
-  const int64_t rank = by_xcd ? x / kXcds : x;
-  const int groups_local = by_xcd ? groups / kXcds : groups;
-  const int per_qb = groups_local * a.G;
-  const int qb_first = a.nqb - 1 - (int)(rank / per_qb);
-  const int qb_second = a.paired ? a.nqb - 1 - qb_first : qb_first;  // == qb_first: no second
-  const int rest = (int)(rank % per_qb);
-  const int grp_id = by_xcd ? (rest / a.G) * kXcds + (int)(x % kXcds) : rest / a.G;
-  const int b = grp_id / a.Hkv;
-  const int h = (grp_id % a.Hkv) * a.G + rest % a.G;
-  const int kh = grp_id % a.Hkv;
+  // Grid mapping (prefill_item): XCD-local (batch, kv head) groups, heaviest query
+  // blocks first, and with two workgroups' worth of query blocks or more per CU a pair
+  // per workgroup -- the heavy block nqb-1-p, then the light one p of the same head --
+  // which balances the causal work per workgroup and pays one launch per pair.
+  const PrefillItem item = prefill_item(blockIdx.x, gridDim.x, a.B, a.Hkv, a.G, a.nqb, a.paired);
+  const int qb_first = item.qb_first;
+  const int qb_second = item.qb_second;  // == qb_first: no second
+  const int b = item.b;
+  const int h = item.h;
+  const int kh = item.kh;
 
   int q_off = a.q_off[b];
   q_off = q_off < 0 ? 0 : q_off;
@@ -690,7 +678,7 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
   const int cus = device_cus();
   const int64_t items = (int64_t)a.nqb * Hq * c.batch;
   a.paired = a.nqb >= 2 && items >= 2 * (int64_t)cus;
-  const int64_t blocks = a.paired ? (int64_t)((a.nqb + 1) / 2) * Hq * c.batch : items;
+  const int64_t blocks = prefill_grid(c.batch, Hq, a.nqb, a.paired);
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_prefill_attention: grid too large");
   if (c.flags & EMA_KV_ROTATING)
     hipLaunchKernelGGL(prefill_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);

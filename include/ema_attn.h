@@ -107,6 +107,14 @@ extern "C" {
 /* ema_pre_attention flags */
 #define EMA_PRE_NO_NORM 1u /* q_norm/k_norm are None: crates/ops/src/attention.rs:57-76 */
 #define EMA_PRE_NO_ROPE 2u /* NoPE layer (use_rope=false): crates/ops/src/rope.rs:38-40  */
+/* ema_decode_step / ema_decode_step_noalloc only: after the step, offsets[b] += 1 on the
+ * device for every sequence whose new row was written (0 <= offset < capacity; any
+ * offset >= 0 for a rotating cache). An offset that wrote nothing is left as it is, so a
+ * sequence that reached the capacity stays there and the caller can see it. This is the
+ * reference's per-token bookkeeping (crates/serve/src/decode_compiled.rs:49,
+ * `self.offset += 1` after each step) kept on the device, so that one captured graph of
+ * N steps decodes N tokens per sequence with no host work in between. */
+#define EMA_STEP_ADVANCE 4u
 
 /* ema_prefill_attention flags */
 #define EMA_PREFILL_CAUSAL 1u     /* MLX "causal", query block end-aligned to the keys   */
@@ -244,7 +252,8 @@ EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const e
  * registers (not written out). Replaces the per-layer attention slice of the
  * compiled decode step, crates/serve/src/compiled.rs:134-163.
  *   qkv      [batch, (n_heads + 2*n_kv_heads) * head_dim] bf16, order q|k|v
- *   offsets  device int32 [batch]; an offset outside [0, capacity) writes nothing
+ *   offsets  device int32 [batch]; an offset outside [0, capacity) writes nothing; read
+ *            only, unless flags hold EMA_STEP_ADVANCE (then advanced in place)
  *   max_len  host upper bound of offsets[b] + 1 (sizes the split; <= capacity)
  *   out      [batch, n_heads * head_dim] bf16
  * The workspace is the one ema_decode_workspace_size gives for max_len.
@@ -252,7 +261,7 @@ EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const e
  * in its decoded form, like every other row. */
 EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void* q_norm_w,
                                 const void* k_norm_w, float eps, float theta,
-                                const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                                int32_t* offsets, int32_t max_len, int32_t n_heads,
                                 uint32_t flags, float scale, const ema_kvcache_desc* cache,
                                 void* out, void* workspace, uint64_t workspace_bytes);
 
@@ -269,7 +278,7 @@ EMA_API int32_t ema_decode_step(ema_stream_t stream, const void* qkv, const void
  * streams) race; stream-ordered calls do not. */
 EMA_API int32_t ema_decode_step_noalloc(ema_stream_t stream, const void* qkv, const void* q_norm_w,
                                         const void* k_norm_w, float eps, float theta,
-                                        const int32_t* offsets, int32_t max_len, int32_t n_heads,
+                                        int32_t* offsets, int32_t max_len, int32_t n_heads,
                                         uint32_t flags, float scale, const ema_kvcache_desc* cache,
                                         void* out);
 

@@ -1,0 +1,160 @@
+// CPU checks of the attention kernels' integer work schedules (engine-mlx_amd/csrc/
+// ema_schedule.hpp, the same definitions the kernels call on the device):
+//  - prefill: every (sequence, query head, query block) is run by exactly one workgroup,
+//    paired or not, with and without the XCD grouping; the heavy block of a pair runs
+//    first; with the XCD grouping every item of a (sequence, kv head) group lands on the
+//    group's XCD; ranks run heaviest first;
+//  - decode split: the worker slices tile [0, total) exactly once, split_worker_of
+//    inverts split_begin, the merge's slot range [w0, w1] of every segment is exactly the
+//    set of slices that intersect it, and the partial-state slots (w + segment) of split
+//    segments are distinct and inside the workspace the plan sizes.
+// Built with g++ (no HIP), also under -fsanitize=address,undefined. Prints one line per
+// group of checks and exits non-zero on the first failure.
+#include <cstdio>
+#include <cstdlib>
+#include <set>
+#include <vector>
+
+#include "ema_schedule.hpp"
+
+using namespace ema;
+
+static int g_checks = 0;
+#define CHECK(cond, ...)                                   \
+  do {                                                     \
+    ++g_checks;                                            \
+    if (!(cond)) {                                         \
+      std::fprintf(stderr, "FAIL %s:%d: ", __FILE__, __LINE__); \
+      std::fprintf(stderr, __VA_ARGS__);                   \
+      std::fprintf(stderr, "\n");                          \
+      std::exit(1);                                        \
+    }                                                      \
+  } while (0)
+
+static void prefill_case(int B, int Hkv, int G, int nqb, int paired) {
+  const int Hq = Hkv * G;
+  const int64_t grid = prefill_grid(B, Hq, nqb, paired);
+  std::vector<int> seen((size_t)B * Hq * nqb, 0);
+  const bool by_xcd = (B * Hkv) % kSchedXcds == 0 && grid % kSchedXcds == 0;
+  std::vector<int> last_qb(kSchedXcds, 1 << 30);
+  for (int64_t x = 0; x < grid; ++x) {
+    const PrefillItem it = prefill_item(x, grid, B, Hkv, G, nqb, paired);
+    CHECK(it.b >= 0 && it.b < B && it.kh >= 0 && it.kh < Hkv, "x=%lld b=%d kh=%d", (long long)x, it.b, it.kh);
+    CHECK(it.h / G == it.kh && it.h >= 0 && it.h < Hq, "x=%lld h=%d kh=%d G=%d", (long long)x, it.h, it.kh, G);
+    CHECK(it.qb_first >= 0 && it.qb_first < nqb && it.qb_second >= 0 && it.qb_second < nqb,
+          "x=%lld qb %d/%d of %d", (long long)x, it.qb_first, it.qb_second, nqb);
+    CHECK(it.qb_first >= it.qb_second, "pair must run its heavy block first (x=%lld)", (long long)x);
+    if (!paired) CHECK(it.qb_first == it.qb_second, "unpaired grid ran two blocks (x=%lld)", (long long)x);
+    const size_t base = ((size_t)it.b * Hq + it.h) * nqb;
+    ++seen[base + it.qb_first];
+    if (it.qb_second != it.qb_first) ++seen[base + it.qb_second];
+    const int lane = by_xcd ? (int)(x % kSchedXcds) : 0;
+    if (by_xcd)
+      CHECK((it.b * Hkv + it.kh) % kSchedXcds == lane, "group %d off its XCD %d (x=%lld)", it.b * Hkv + it.kh, lane,
+            (long long)x);
+    CHECK(it.qb_first <= last_qb[lane], "ranks must run heaviest first (x=%lld)", (long long)x);
+    last_qb[lane] = it.qb_first;
+  }
+  for (size_t i = 0; i < seen.size(); ++i)
+    CHECK(seen[i] == 1, "B=%d Hkv=%d G=%d nqb=%d paired=%d: item (b=%zu h=%zu qb=%zu) run %d times", B, Hkv, G, nqb,
+          paired, i / ((size_t)Hq * nqb), i / nqb % Hq, i % nqb, seen[i]);
+}
+
+static void test_prefill() {
+  const int shapes[][4] = {
+      // B, Hkv, G, nqb
+      {1, 8, 4, 16},   // 8B shape, T 2048 (XCD-grouped, paired on MI355X)
+      {1, 8, 2, 16},   // 1.7B shape
+      {4, 4, 4, 8},    // B 4, 16q/4kv, T 1000
+      {4, 4, 4, 9},    // odd block count: the middle block pairs with itself
+      {3, 3, 8, 7},    // groups not a multiple of the XCD count
+      {1, 8, 8, 1},    // one query block
+      {2, 1, 1, 5},    // MHA-like, tiny
+      {16, 8, 8, 33},  // chunk shape, long
+      {5, 2, 3, 4},    // grid not divisible by 8
+      {8, 1, 3, 3},    // groups == XCDs, odd nqb
+  };
+  for (const auto& s : shapes)
+    for (int paired = 0; paired < 2; ++paired) prefill_case(s[0], s[1], s[2], s[3], paired);
+  std::printf("prefill schedule: %zu shapes x {unpaired, paired}: every (b, h, qb) exactly once\n",
+              sizeof(shapes) / sizeof(shapes[0]));
+}
+
+// Decode split for tile counts nb[s] per segment s (segments in sequence-major order).
+static void decode_case(const std::vector<int>& nb, int plan_workers, int waves) {
+  std::vector<int64_t> first(nb.size() + 1, 0);
+  for (size_t s = 0; s < nb.size(); ++s) first[s + 1] = first[s] + nb[s];
+  const int64_t total = first.back();
+  if (total == 0) return;
+  const int W = split_active_workers(total, plan_workers, waves);
+  CHECK(W >= 1 && W <= plan_workers, "active workers %d of %d", W, plan_workers);
+  // slices tile the range exactly once; worker_of inverts begin
+  CHECK(split_begin(0, total, W) == 0 && split_begin(W, total, W) == total, "slice ends");
+  for (int w = 0; w < W; ++w) {
+    const int64_t a = split_begin(w, total, W), b = split_begin(w + 1, total, W);
+    CHECK(a < b, "empty slice %d of %d (total %lld)", w, W, (long long)total);
+    for (int64_t t = a; t < b; ++t)
+      CHECK(split_worker_of(t, total, W) == w, "worker_of(%lld) = %lld, not %d", (long long)t,
+            (long long)split_worker_of(t, total, W), w);
+  }
+  // merge ranges and partial slots
+  std::set<int64_t> slots;
+  for (size_t s = 0; s < nb.size(); ++s) {
+    if (nb[s] == 0) continue;
+    const int64_t w0 = split_worker_of(first[s], total, W), w1 = split_worker_of(first[s + 1] - 1, total, W);
+    for (int w = 0; w < W; ++w) {
+      const bool meets = split_begin(w, total, W) < first[s + 1] && split_begin(w + 1, total, W) > first[s];
+      CHECK(meets == (w >= w0 && w <= w1), "segment %zu, worker %d: merge range [%lld, %lld]", s, w, (long long)w0,
+            (long long)w1);
+    }
+    if (w0 == w1) continue;  // written directly, no partial state
+    for (int64_t w = w0; w <= w1; ++w) {
+      const int64_t slot = w + (int64_t)s;
+      CHECK(slot < (int64_t)plan_workers + (int64_t)nb.size(), "slot %lld outside the workspace", (long long)slot);
+      CHECK(slots.insert(slot).second, "slot %lld written twice", (long long)slot);
+    }
+  }
+}
+
+static void test_decode() {
+  unsigned rng = 12345u;
+  auto next = [&rng]() {
+    rng = rng * 1664525u + 1013904223u;
+    return rng >> 8;
+  };
+  int cases = 0;
+  for (int rep = 0; rep < 400; ++rep) {
+    const int B = 1 + (int)(next() % 40), Hkv = 1 + (int)(next() % 8);
+    const int cap = 1 + (int)(next() % 9000);
+    std::vector<int> len(B);
+    int max_len = 0;
+    for (int b = 0; b < B; ++b) {
+      const unsigned r = next() % 10;
+      len[b] = r == 0 ? 0 : (r == 1 ? cap : (int)(next() % (unsigned)(cap + 1)));
+      if (len[b] > max_len) max_len = len[b];
+    }
+    // the plan sizes the split from the host's upper bound (here: the capacity or the
+    // true maximum), the kernel splits the actual tile count
+    const int plan_workers = split_plan_workers(B, Hkv, (rep & 1) ? cap : max_len);
+    std::vector<int> nb;
+    for (int b = 0; b < B; ++b)
+      for (int kh = 0; kh < Hkv; ++kh) nb.push_back((len[b] + kSplitTile - 1) / kSplitTile);
+    decode_case(nb, plan_workers, kSplitWaves);
+    ++cases;
+  }
+  // edges: one segment, one tile, more workers than tiles, the worker cap
+  decode_case({1}, 1, kSplitWaves);
+  decode_case({3}, kSplitMaxWorkers, kSplitWaves);
+  decode_case({256}, 64, kSplitWaves);
+  decode_case(std::vector<int>(32 * 8, 256), split_plan_workers(32, 8, 8192), kSplitWaves);
+  decode_case({0, 0, 5, 0, 7}, 2, kSplitWaves);
+  std::printf("decode split: %d random batches + 5 edge cases: tiles covered once, merge ranges and slots exact\n",
+              cases);
+}
+
+int main() {
+  test_prefill();
+  test_decode();
+  std::printf("%d checks passed\n", g_checks);
+  return 0;
+}

@@ -158,6 +158,21 @@ def test_decode_step_noalloc_argument_errors(ema):
     assert rc == ema.EMA_ERR_WORKSPACE and "static scratch" in ema.last_error()
 
 
+def test_step_advance_flag_belongs_to_the_decode_step(ema):
+    """EMA_STEP_ADVANCE passes the decode step's flag check (the call then fails later, on
+    its missing workspace, without touching the GPU) and is an unknown flag elsewhere."""
+    L = ema.lib()
+    _, d = _desc(ema)
+    g = 0x40000
+    adv = ema.EMA_STEP_ADVANCE
+    rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 64, 16, adv, 0.088, ctypes.byref(d), g, None, 0)
+    assert rc == ema.EMA_ERR_WORKSPACE
+    rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 64, 16, 8, 0.088, ctypes.byref(d), g, None, 0)
+    assert rc == ema.EMA_ERR_INVALID_ARG and "flags" in ema.last_error()
+    rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 2, 1, 16, 4, 128, adv, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_INVALID_ARG and "flags" in ema.last_error()
+
+
 def test_prefill_argument_errors(ema):
     L = ema.lib()
     _, d = _desc(ema)
