@@ -212,6 +212,26 @@ def prefill_flops(Hq, D, T, off):
     return 4 * Hq * D * (T * off + T * (T + 1) // 2)
 
 
+# Counter readings of prefill_kernel (rocprofv3 --pmc runs of this script's prefill
+# workloads; the commands and raw figures are in profiles/prefill_causal_T2048_32q8kv.md):
+# matrix-pipe busy fraction at 2.4 GHz, executed MFMA flops over algorithmic flops, and
+# HBM bytes per call (FETCH_SIZE x 2 + WRITE_SIZE, the copy-kernel calibration).
+PREFILL_COUNTERS = {
+    "prefill_causal_T2048_32q8kv_qwen3_8b": {"mfma_busy": 0.327, "executed_over_algorithmic": 1.095,
+                                             "traffic": 58315366},
+    "prefill_chunk_off14336_T2048_64q8kv": {"mfma_busy": 0.507, "executed_over_algorithmic": 1.065,
+                                            "traffic": 354643046},
+}
+
+
+def prefill_roofline(name, tf, fl):
+    roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops_per_call": fl}
+    if name in PREFILL_COUNTERS:
+        roof.update(PREFILL_COUNTERS[name], counter_source="profiles/prefill_causal_T2048_32q8kv.md")
+    return roof
+
+
 def bench_prefill(ctx, ema, name, B, Hq, Hkv, D, cap, T, off, steps=20):
     torch = ctx.torch
     cache = ema.StaticCache(B, Hkv, cap, D, k=ctx.randn((B, Hkv, cap, D)), v=ctx.randn((B, Hkv, cap, D)))
@@ -222,7 +242,8 @@ def bench_prefill(ctx, ema, name, B, Hq, Hkv, D, cap, T, off, steps=20):
     fl = B * prefill_flops(Hq, D, T, off)
     tf = fl / (ms * 1e-3) / 1e12
     log(f"[bench] {name}: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s ({tf/BF16_PEAK_TFLOPS:.1%} of bf16 peak)")
-    return {"workload": name, "us": ms * 1e3, "tflops": tf, "frac_of_peak": tf / BF16_PEAK_TFLOPS, "flops": fl}
+    return {"workload": name, "us": ms * 1e3, "tflops": tf, "frac_of_peak": tf / BF16_PEAK_TFLOPS, "flops": fl,
+            "roofline": prefill_roofline(name, tf, fl)}
 
 
 def bench_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
