@@ -327,6 +327,17 @@ int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* d, uint64_t* bytes) {
   return EMA_OK;
 }
 
+// A norm weight may be null only when its norm is switched off.
+static int32_t check_norm_weights(const char* op, const void* q_norm_w, const void* k_norm_w, uint32_t flags) {
+  const bool q_norm = !(flags & (EMA_PRE_NO_NORM | EMA_PRE_NO_Q_NORM));
+  const bool k_norm = !(flags & (EMA_PRE_NO_NORM | EMA_PRE_NO_K_NORM));
+  if ((q_norm && !q_norm_w) || (k_norm && !k_norm_w))
+    return set_error(EMA_ERR_INVALID_ARG,
+                     "%s: norm weights are null (pass EMA_PRE_NO_NORM for models without q/k norm, "
+                     "EMA_PRE_NO_Q_NORM / EMA_PRE_NO_K_NORM for one of them)", op);
+  return EMA_OK;
+}
+
 int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
                           float eps, float theta, const int32_t* offsets, int32_t batch, int32_t n_tokens,
                           int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, uint32_t flags, void* q_out,
@@ -335,9 +346,9 @@ int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_no
   int32_t rc = check_cache(op, cache);
   if (rc) return rc;
   if (!qkv || !q_out || !offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null qkv/q_out/offsets", op);
-  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE)) return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
-  if (!(flags & EMA_PRE_NO_NORM) && (!q_norm_w || !k_norm_w))
-    return set_error(EMA_ERR_INVALID_ARG, "%s: norm weights are null (pass EMA_PRE_NO_NORM for models without q/k norm)", op);
+  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE | EMA_PRE_NO_Q_NORM | EMA_PRE_NO_K_NORM))
+    return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
+  if ((rc = check_norm_weights(op, q_norm_w, k_norm_w, flags))) return rc;
   if ((rc = check_heads(op, n_heads, n_kv_heads))) return rc;
   if (batch <= 0 || n_tokens <= 0) return set_error(EMA_ERR_SHAPE, "%s: batch=%d n_tokens=%d must be positive", op, batch, n_tokens);
   if (batch != cache->batch || n_kv_heads != cache->n_kv_heads || head_dim != cache->head_dim)
@@ -390,10 +401,9 @@ static int32_t check_decode_step(const char* op, const void* qkv, const void* q_
   int32_t rc = check_cache(op, cache);
   if (rc) return rc;
   if (!qkv || !out || !offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null qkv/out/offsets", op);
-  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE | EMA_STEP_ADVANCE))
+  if (flags & ~(EMA_PRE_NO_NORM | EMA_PRE_NO_ROPE | EMA_PRE_NO_Q_NORM | EMA_PRE_NO_K_NORM | EMA_STEP_ADVANCE))
     return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
-  if (!(flags & EMA_PRE_NO_NORM) && (!q_norm_w || !k_norm_w))
-    return set_error(EMA_ERR_INVALID_ARG, "%s: norm weights are null (pass EMA_PRE_NO_NORM for models without q/k norm)", op);
+  if ((rc = check_norm_weights(op, q_norm_w, k_norm_w, flags))) return rc;
   if ((rc = check_heads(op, n_heads, cache->n_kv_heads))) return rc;
   if (max_len < 0 || max_len > cache->capacity)
     return set_error(EMA_ERR_CAPACITY, "%s: max_len %d outside [0, capacity %d]", op, max_len, cache->capacity);

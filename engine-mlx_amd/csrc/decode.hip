@@ -52,7 +52,6 @@ constexpr int kTile = kSplitTile;
 constexpr int kWaves = kSplitWaves;  // waves per workgroup, each an independent worker
 constexpr int kMaxB = 1024;     // batch rows held in the LDS prefix table
 constexpr int kPieceStride = kD + 4;  // floats per (piece, head): m, l, pad, pad, o[D]
-constexpr int kMaxWorkers = kSplitMaxWorkers;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -235,7 +234,7 @@ template <bool kFp8>
 __device__ __forceinline__ void norm_rope(const DecodeArgs& a, float (&x)[32], const u32x4 (&wv)[4],
                                           const float2* cs_tab) {
   const int c = (threadIdx.x & 63) >> 4;
-  if (!(a.flags & EMA_PRE_NO_NORM)) {
+  if (!(a.flags & (EMA_PRE_NO_NORM | EMA_PRE_NO_Q_NORM))) {
     float ss = 0.f;
     for (int e = 0; e < 32; ++e) ss += x[e] * x[e];
     ss += __shfl_xor(ss, 16, 64);
@@ -486,7 +485,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // tile that load row w (with a static cache, also the rows past L - 1 = w, which
         // the loads clamp to it)
         float k1 = bf16_to_f32(kr1), k2 = bf16_to_f32(kr2);
-        if (!(a.flags & EMA_PRE_NO_NORM)) {
+        if (!(a.flags & (EMA_PRE_NO_NORM | EMA_PRE_NO_K_NORM))) {
           float ss = k1 * k1 + k2 * k2;
           for (int mm = 32; mm >= 1; mm >>= 1) ss += __shfl_xor(ss, mm, 64);
           const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);

@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
     const bool is_q = h < a.Hq;
     if (!is_q && !in_cap) continue;
     float y[2 * E];
-    if (!(a.flags & EMA_PRE_NO_NORM)) {
+    if (!(a.flags & (EMA_PRE_NO_NORM | (is_q ? EMA_PRE_NO_Q_NORM : EMA_PRE_NO_K_NORM)))) {
       float ss = 0.f;
       for (int e = 0; e < 2 * E; ++e) {
         const float f = bf16_to_f32(x[e]);

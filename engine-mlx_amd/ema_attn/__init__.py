@@ -33,6 +33,8 @@ EMA_DTYPE_F32 = 4
 EMA_DTYPE_INT4_AFFINE = 5
 EMA_PRE_NO_NORM = 1
 EMA_PRE_NO_ROPE = 2
+EMA_PRE_NO_Q_NORM = 8
+EMA_PRE_NO_K_NORM = 16
 EMA_STEP_ADVANCE = 4
 EMA_KV_ROTATING = 1
 EMA_PREFILL_CAUSAL = 1

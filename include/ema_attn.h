@@ -107,6 +107,11 @@ extern "C" {
 /* ema_pre_attention flags */
 #define EMA_PRE_NO_NORM 1u /* q_norm/k_norm are None: crates/ops/src/attention.rs:57-76 */
 #define EMA_PRE_NO_ROPE 2u /* NoPE layer (use_rope=false): crates/ops/src/rope.rs:38-40  */
+/* One of the two norms absent: optional_qk_norm applies q_norm and k_norm independently
+ * (crates/ops/src/attention.rs:57-76). The absent weight may be null. EMA_PRE_NO_NORM is
+ * both together. Accepted by ema_pre_attention and the decode steps. */
+#define EMA_PRE_NO_Q_NORM 8u
+#define EMA_PRE_NO_K_NORM 16u
 /* ema_decode_step / ema_decode_step_noalloc only: after the step, offsets[b] += 1 on the
  * device for every sequence whose new row was written (0 <= offset < capacity; any
  * offset >= 0 for a rotating cache). An offset that wrote nothing is left as it is, so a

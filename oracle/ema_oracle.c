@@ -148,7 +148,10 @@ int ora_pre_attention(const uint16_t* qkv, const uint16_t* q_norm_w, const uint1
           continue;
         }
         const uint16_t* cur = x;
-        if (!(flags & ORA_FLAG_NO_NORM)) {
+        /* optional_qk_norm (crates/ops/src/attention.rs:57-76) applies each norm
+         * independently of the other */
+        const uint32_t skip = ORA_FLAG_NO_NORM | (h < Hq ? ORA_FLAG_NO_Q_NORM : ORA_FLAG_NO_K_NORM);
+        if (!(flags & skip)) {
           rms_norm_row(cur, h < Hq ? q_norm_w : k_norm_w, D, eps, tmp);
           cur = tmp;
         }

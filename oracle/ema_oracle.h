@@ -45,6 +45,8 @@ extern "C" {
 
 #define ORA_FLAG_NO_NORM 1u /* q_norm/k_norm are None (optional_qk_norm no-op) */
 #define ORA_FLAG_NO_ROPE 2u /* NoPE layer (apply_rope with use_rope=false)     */
+#define ORA_FLAG_NO_Q_NORM 8u  /* q_norm None, k_norm given (each norm is optional on its own) */
+#define ORA_FLAG_NO_K_NORM 16u /* k_norm None, q_norm given                                      */
 
 /* bf16 <-> f32 (RNE, NaN kept quiet). */
 uint16_t ora_f32_to_bf16(float f);

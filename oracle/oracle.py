@@ -19,6 +19,8 @@ _lib = None
 
 FLAG_NO_NORM = 1
 FLAG_NO_ROPE = 2
+FLAG_NO_Q_NORM = 8
+FLAG_NO_K_NORM = 16
 
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _i32p = ctypes.POINTER(ctypes.c_int32)

@@ -119,8 +119,20 @@ def test_pre_attention_argument_errors(ema):
     rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 2, 65, 16, 8, 128, 0, g, ctypes.byref(d))
     assert rc == ema.EMA_ERR_CAPACITY and "overflow" in ema.last_error()
     # unknown flag bits
-    rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 2, 4, 16, 8, 128, 8, g, ctypes.byref(d))
-    assert rc == ema.EMA_ERR_INVALID_ARG
+    rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 2, 4, 16, 8, 128, 32, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_INVALID_ARG and "flags" in ema.last_error()
+    # one norm switched off: only that weight may be null
+    # (batch 3 against the cache's 2: a call that passes the norm check stops at the shape
+    # check, before any launch)
+    no_q, no_k = ema.EMA_PRE_NO_Q_NORM, ema.EMA_PRE_NO_K_NORM
+    rc = L.ema_pre_attention(None, g, None, g, 1e-6, 1e6, g, 3, 4, 16, 8, 128, no_q, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_SHAPE
+    rc = L.ema_pre_attention(None, g, g, None, 1e-6, 1e6, g, 3, 4, 16, 8, 128, no_k, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_SHAPE
+    rc = L.ema_pre_attention(None, g, g, None, 1e-6, 1e6, g, 3, 4, 16, 8, 128, no_q, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_INVALID_ARG and "norm" in ema.last_error()
+    rc = L.ema_pre_attention(None, g, None, g, 1e-6, 1e6, g, 3, 4, 16, 8, 128, no_k, g, ctypes.byref(d))
+    assert rc == ema.EMA_ERR_INVALID_ARG and "norm" in ema.last_error()
 
 
 def test_decode_step_argument_errors(ema):
@@ -167,7 +179,7 @@ def test_step_advance_flag_belongs_to_the_decode_step(ema):
     adv = ema.EMA_STEP_ADVANCE
     rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 64, 16, adv, 0.088, ctypes.byref(d), g, None, 0)
     assert rc == ema.EMA_ERR_WORKSPACE
-    rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 64, 16, 8, 0.088, ctypes.byref(d), g, None, 0)
+    rc = L.ema_decode_step(None, g, g, g, 1e-6, 1e6, g, 64, 16, 32, 0.088, ctypes.byref(d), g, None, 0)
     assert rc == ema.EMA_ERR_INVALID_ARG and "flags" in ema.last_error()
     rc = L.ema_pre_attention(None, g, g, g, 1e-6, 1e6, g, 2, 1, 16, 4, 128, adv, g, ctypes.byref(d))
     assert rc == ema.EMA_ERR_INVALID_ARG and "flags" in ema.last_error()

@@ -32,8 +32,10 @@ def make_cache(ema, kc: np.ndarray, vc: np.ndarray):
 
 # ------------------------------------------------------------ pre-attention
 @pytest.mark.parametrize("D", [64, 128, 256])
-@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+@pytest.mark.parametrize("flags", [0, 1, 2, 3, 8, 16, 10])
 def test_pre_attention_small(ema, ora, D, flags):
+    """flags: 1 no norms, 2 no RoPE, 8 no q norm, 16 no k norm (each norm is optional on
+    its own, crates/ops/src/attention.rs:57-76); the absent weights are passed as null."""
     import torch
 
     B, T, Hq, Hkv, cap = 2, 5, 4, 2, 16
@@ -46,7 +48,9 @@ def test_pre_attention_small(ema, ora, D, flags):
     kr, vr = junk.copy(), junk.copy()
     q_ref = ora.pre_attention(qkv, qw, kw, 1e-6, 1e6, off, Hq, Hkv, kr, vr, flags=flags)
     cache = make_cache(ema, junk, junk)
-    q = ema.pre_attention(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, cache, flags=flags)
+    qw_d = None if flags & (1 | 8) else dev(qw)
+    kw_d = None if flags & (1 | 16) else dev(kw)
+    q = ema.pre_attention(dev(qkv), qw_d, kw_d, 1e-6, 1e6, dev(off), Hq, cache, flags=flags)
     torch.cuda.synchronize()
     kg, vg = host(cache.k), host(cache.v)
     assert np.array_equal(vg, vr), "V rows must be a bit copy at [off, off+T)"
@@ -480,7 +484,7 @@ def _fused_case(ema, ora, B, Hq, Hkv, D, cap, off, seed, flags=0):
             kr[bb], vr[bb] = kb[0], vb[0]
         else:  # nothing is written; q is still normalised and rotated at the offset
             x = qkv[bb, :Hq * D].reshape(Hq, D).copy()
-            if not flags & 1:
+            if not flags & (1 | 8):
                 x = ora.rms_norm(x, qw, 1e-6)
             if not flags & 2:
                 x = ora.rope(x, np.full(Hq, off[bb], np.int32), 1e6)
@@ -493,7 +497,7 @@ def _fused_case(ema, ora, B, Hq, Hkv, D, cap, off, seed, flags=0):
     return host(out), ref, host(cache.k), host(cache.v), kr, vr, kc
 
 
-@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+@pytest.mark.parametrize("flags", [0, 1, 2, 3, 8, 16, 18])
 def test_decode_step_fused_small(ema, ora, flags):
     B, Hq, Hkv, D, cap = 6, 16, 4, 128, 200
     off = [0, 31, 32, 100, 199, 63]
@@ -512,7 +516,7 @@ def test_decode_step_fused_out_of_capacity(ema, ora):
     assert_close(got, ref, "fused out of capacity")
 
 
-@pytest.mark.parametrize("flags", [1, 3])
+@pytest.mark.parametrize("flags", [1, 3, 8, 16])
 def test_decode_step_fused_null_norm_weights(ema, ora, flags):
     """With EMA_PRE_NO_NORM the norm weights may be null (they are never read): the result
     equals the call that passes (unused) weights, bit for bit."""
@@ -525,7 +529,8 @@ def test_decode_step_fused_null_norm_weights(ema, ora, flags):
     kc = ora.normal_bf16((B, Hkv, cap, D), seed=662)
     vc = ora.normal_bf16((B, Hkv, cap, D), seed=663)
     c1, c2 = make_cache(ema, kc, vc), make_cache(ema, kc, vc)
-    o1 = ema.decode_step(qkv, None, None, 1e-6, 1e6, dev(off), Hq, c1, cap, flags=flags)
+    o1 = ema.decode_step(qkv, None if flags & (1 | 8) else w, None if flags & (1 | 16) else w, 1e-6, 1e6, dev(off),
+                         Hq, c1, cap, flags=flags)
     o2 = ema.decode_step(qkv, w, w, 1e-6, 1e6, dev(off), Hq, c2, cap, flags=flags)
     torch.cuda.synchronize()
     assert np.array_equal(host(o1), host(o2)) and np.array_equal(host(c1.k), host(c2.k))

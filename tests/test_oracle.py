@@ -213,6 +213,37 @@ def test_pre_attention_prefill_equals_token_by_token(ora):
     assert np.array_equal(k1[0, :, off[0]:off[0] + T], kref)
 
 
+@pytest.mark.parametrize("one_sided", ["q", "k"])
+def test_pre_attention_one_sided_norm(ora, one_sided):
+    """optional_qk_norm (crates/ops/src/attention.rs:57-76) normalises q and k each on its
+    own: with only k_norm given, q is the un-normalised (rotated) q of the NO_NORM call and
+    k the normalised k of the full call; and the other way round."""
+    B, T, Hq, Hkv, D, cap = 2, 3, 4, 2, 128, 16
+    qkv = ora.normal_bf16((B, T, (Hq + 2 * Hkv) * D), seed=21)
+    qw = ora.normal_bf16(D, seed=22, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=23, mean=1.0, std=0.02)
+    off = np.array([2, 7], np.int32)
+    junk = ora.normal_bf16((B, Hkv, cap, D), seed=24)
+    runs = {}
+    for name, flags in (("both", 0), ("none", ora.FLAG_NO_NORM),
+                        ("q", ora.FLAG_NO_Q_NORM), ("k", ora.FLAG_NO_K_NORM)):
+        kc, vc = junk.copy(), junk.copy()
+        q = ora.pre_attention(qkv, None if name in ("none", "q") else qw, None if name in ("none", "k") else kw,
+                              1e-6, 1e6, off, Hq, Hkv, kc, vc, flags=flags)
+        runs[name] = (q, kc, vc)
+    q1, k1, v1 = runs[one_sided]
+    q_src = runs["none"] if one_sided == "q" else runs["both"]
+    k_src = runs["both"] if one_sided == "q" else runs["none"]
+    assert np.array_equal(q1, q_src[0]) and np.array_equal(k1, k_src[1]) and np.array_equal(v1, junk_v(runs))
+    assert not np.array_equal(q1, runs["both" if one_sided == "q" else "none"][0])
+
+
+def junk_v(runs):
+    v = runs["both"][2]
+    assert all(np.array_equal(r[2], v) for r in runs.values())  # v never normalised
+    return v
+
+
 def test_pre_attention_overflow_raises(ora):
     kc = np.zeros((1, 1, 8, 128), np.uint16)
     qkv = np.zeros((1, 2, 3 * 128), np.uint16)
