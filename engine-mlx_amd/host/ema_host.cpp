@@ -24,15 +24,38 @@ void check_hip(hipError_t e, const char* what) {
   if (e != hipSuccess) throw Error(EMA_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-void* grow(void*& buf, size_t& have, size_t need, const char* what) {
-  if (need > have) {
-    if (buf) check_hip(hipFree(buf), what);
-    buf = nullptr;
-    have = 0;
-    check_hip(hipMalloc(&buf, need), what);
-    have = need;
+constexpr size_t kAlign = 256;
+size_t aligned(size_t n) { return (n + kAlign - 1) & ~(kAlign - 1); }
+
+// Carves a call's temporaries out of ctx's arena, in order; throws EMA_ERR_WORKSPACE
+// with the total the call needs when the arena is smaller.
+class Arena {
+ public:
+  Arena(const Ctx& ctx, const char* op) : base_((char*)ctx.workspace), have_(ctx.workspace ? ctx.workspace_bytes : 0), op_(op) {}
+  void* take(size_t bytes) {
+    const size_t at = used_;
+    used_ += aligned(bytes);
+    return base_ + at;
   }
-  return buf;
+  // Call after the last take(): the pointers are valid only if this does not throw.
+  void check() const {
+    if (used_ > have_ || ((uintptr_t)base_ & (kAlign - 1)))
+      throw Error(EMA_ERR_WORKSPACE, std::string(op_) + ": a 256-byte aligned ctx workspace of " +
+                                         std::to_string(used_) + " bytes is needed, " + std::to_string(have_) +
+                                         " given");
+  }
+
+ private:
+  char* base_;
+  size_t have_;
+  size_t used_ = 0;
+  const char* op_;
+};
+
+// Writes v into *dst on the stream: the rotating cache's position slot. The address
+// depends on the lane, so the store is a vector store.
+__global__ void set_slot_kernel(int32_t* dst, int32_t v) {
+  if (threadIdx.x < 1) dst[threadIdx.x] = v;
 }
 
 std::string shape_str(const std::vector<int64_t>& s) {
@@ -65,9 +88,6 @@ StaticCache::StaticCache(int32_t n_kv_heads, int32_t capacity, int32_t head_dim)
 StaticCache::~StaticCache() {
   ema_kvcache_free(&desc_);
   if (positions_) (void)hipFree(positions_);
-  if (q_buf_) (void)hipFree(q_buf_);
-  if (o_buf_) (void)hipFree(o_buf_);
-  if (ws_) (void)hipFree(ws_);
 }
 
 size_t StaticCache::memory_bytes() const {
@@ -88,6 +108,13 @@ void StaticCache::advance(int32_t n) {
     throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string(offset_ + n) + " cap=" +
                                       std::to_string(desc_.capacity));
   offset_ += n;
+}
+
+void StaticCache::set_len(int64_t n) {
+  if (n < 0 || n > desc_.capacity)
+    throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string(n) + " cap=" +
+                                      std::to_string(desc_.capacity));
+  offset_ = (int32_t)n;
 }
 
 void StaticCache::append(const Ctx& ctx, const Array& k, const Array& v) {
@@ -127,29 +154,18 @@ std::pair<Array, Array> StaticCache::get(const Ctx&) const {
   return {k, v};
 }
 
-void* StaticCache::q_scratch(size_t bytes) { return grow(q_buf_, q_bytes_, bytes, "StaticCache: q scratch"); }
-void* StaticCache::out_scratch(size_t bytes) { return grow(o_buf_, o_bytes_, bytes, "StaticCache: out scratch"); }
-
-void* StaticCache::decode_workspace(int32_t n_heads, uint64_t* bytes) {
-  uint64_t need = 0;
-  check(ema_decode_workspace_size(1, n_heads, desc_.n_kv_heads, desc_.head_dim, desc_.capacity, &need),
-        "decode_workspace_size");
-  size_t have = (size_t)ws_bytes_;
-  grow(ws_, have, (size_t)need, "StaticCache: decode workspace");
-  ws_bytes_ = have;
-  *bytes = ws_bytes_;
-  return ws_;
-}
-
 RotatingCache::RotatingCache(int32_t window_size, int32_t n_kv_heads, int32_t head_dim) {
   check(ema_kvcache_alloc(&desc_, 1, n_kv_heads, window_size, head_dim), "kvcache_alloc");
   desc_.flags = EMA_KV_ROTATING;
+  if (hipMalloc((void**)&slot_, sizeof(int32_t)) != hipSuccess) {
+    ema_kvcache_free(&desc_);
+    throw Error(EMA_ERR_HIP, "RotatingCache: position slot");
+  }
 }
 
 RotatingCache::~RotatingCache() {
   ema_kvcache_free(&desc_);
-  for (void* p : {(void*)positions_, q_buf_, o_buf_, ws_, get_buf_})
-    if (p) (void)hipFree(p);
+  if (slot_) (void)hipFree(slot_);
 }
 
 size_t RotatingCache::memory_bytes() const {
@@ -158,28 +174,11 @@ size_t RotatingCache::memory_bytes() const {
   return (size_t)b;
 }
 
-const int32_t* RotatingCache::device_position(int64_t p) {
+const int32_t* RotatingCache::position(const Ctx& ctx, int64_t p) const {
   if (p < 0 || p >= ((int64_t)1 << 31)) throw Error(EMA_ERR_CAPACITY, "rotating KV position " + std::to_string(p));
-  if (p >= n_positions_) {
-    int64_t n = n_positions_ ? n_positions_ : 4096;
-    while (n <= p) n *= 2;
-    std::vector<int32_t> pos((size_t)n);
-    std::iota(pos.begin(), pos.end(), 0);
-    int32_t* fresh = nullptr;
-    check_hip(hipMalloc((void**)&fresh, pos.size() * sizeof(int32_t)), "RotatingCache: positions");
-    if (hipMemcpy(fresh, pos.data(), pos.size() * sizeof(int32_t), hipMemcpyHostToDevice) != hipSuccess) {
-      (void)hipFree(fresh);
-      throw Error(EMA_ERR_HIP, "RotatingCache: positions upload");
-    }
-    if (positions_) {
-      // earlier pointers may still be read by queued work
-      check_hip(hipDeviceSynchronize(), "RotatingCache: positions");
-      (void)hipFree(positions_);
-    }
-    positions_ = fresh;
-    n_positions_ = n;
-  }
-  return positions_ + p;
+  hipLaunchKernelGGL(set_slot_kernel, dim3(1), dim3(64), 0, (hipStream_t)ctx.stream, slot_, (int32_t)p);
+  check_hip(hipGetLastError(), "RotatingCache: position slot");
+  return slot_;
 }
 
 void RotatingCache::append(const Ctx& ctx, const Array& k, const Array& v) {
@@ -223,19 +222,14 @@ std::pair<Array, Array> RotatingCache::get(const Ctx& ctx) const {
     return {k, v};
   }
   // wrapped: oldest token in row total % W; copy rows [start, W) then [0, start)
-  const size_t bytes = (size_t)2 * Hkv * W * D * 2;
-  if (bytes > get_bytes_) {
-    if (get_buf_) check_hip(hipFree(get_buf_), "RotatingCache: get scratch");
-    get_buf_ = nullptr;
-    get_bytes_ = 0;
-    check_hip(hipMalloc(&get_buf_, bytes), "RotatingCache: get scratch");
-    get_bytes_ = bytes;
-  }
+  Arena arena(ctx, "RotatingCache::get");
+  char* buf = (char*)arena.take((size_t)2 * Hkv * W * D * 2);
+  arena.check();
   const int64_t start = total_ % W;
   hipStream_t s = (hipStream_t)ctx.stream;
   for (int i = 0; i < 2; ++i) {
     const char* src = (const char*)(i == 0 ? desc_.k : desc_.v);
-    char* dst = (char*)get_buf_ + (size_t)i * Hkv * W * D * 2;
+    char* dst = buf + (size_t)i * Hkv * W * D * 2;
     const size_t pitch_src = (size_t)desc_.stride_head * 2, pitch_dst = (size_t)W * D * 2;
     check_hip(hipMemcpy2DAsync(dst, pitch_dst, src + (size_t)start * desc_.stride_pos * 2, pitch_src,
                                (size_t)(W - start) * D * 2, (size_t)Hkv, hipMemcpyDeviceToDevice, s),
@@ -245,104 +239,227 @@ std::pair<Array, Array> RotatingCache::get(const Ctx& ctx) const {
                                  (size_t)Hkv, hipMemcpyDeviceToDevice, s),
                 "RotatingCache::get copy");
   }
-  k.data = get_buf_;
-  v.data = (char*)get_buf_ + (size_t)Hkv * W * D * 2;
+  k.data = buf;
+  v.data = buf + (size_t)Hkv * W * D * 2;
   return {k, v};
-}
-
-void* RotatingCache::q_scratch(size_t bytes) { return grow(q_buf_, q_bytes_, bytes, "RotatingCache: q scratch"); }
-void* RotatingCache::out_scratch(size_t bytes) { return grow(o_buf_, o_bytes_, bytes, "RotatingCache: out scratch"); }
-
-void* RotatingCache::decode_workspace(int32_t n_heads, uint64_t* bytes) {
-  uint64_t need = 0;
-  check(ema_decode_workspace_size(1, n_heads, desc_.n_kv_heads, desc_.head_dim, desc_.capacity, &need),
-        "decode_workspace_size");
-  size_t have = (size_t)ws_bytes_;
-  grow(ws_, have, (size_t)need, "RotatingCache: decode workspace");
-  ws_bytes_ = have;
-  *bytes = ws_bytes_;
-  return ws_;
 }
 
 namespace {
 
-// The attention layer over either cache: pre-attention writes the chunk's K/V (ring rows
-// for a rotating cache), then causal prefill (T > 1, gqa.rs:78) or decode (T == 1).
-template <class Cache>
-Array attend(const Ctx& ctx, const Array& qkv, const GqaWeights& weights, Cache& cache, const GqaConfig& config,
-             int32_t offset, bool rotating, const char* op) {
-  const int32_t Hq = config.n_heads, Hkv = config.n_kv_heads, D = config.head_dim;
-  const std::string name(op);
-  if (Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv)
-    throw Error(EMA_ERR_SHAPE, name + ": bad head config n_heads=" + std::to_string(Hq) +
-                                   " n_kv_heads=" + std::to_string(Hkv) + " head_dim=" + std::to_string(D));
-  if (Hkv != cache.n_kv_heads() || D != cache.head_dim())
-    throw Error(EMA_ERR_SHAPE, name + ": config does not match the cache");
-  if (!qkv.data || qkv.shape.size() != 3 || qkv.shape[0] != 1 || qkv.shape[2] != (int64_t)(Hq + 2 * Hkv) * D ||
-      !qkv.strides.empty())
-    throw Error(EMA_ERR_SHAPE, name + ": qkv must be contiguous [1, seq, " + std::to_string((Hq + 2 * Hkv) * D) +
-                                   "], got " + shape_str(qkv.shape));
-  const int32_t T = (int32_t)qkv.shape[1];
-  const int32_t cap = cache.desc().capacity;
-  if (T <= 0) throw Error(EMA_ERR_SHAPE, name + ": empty sequence");
+void check_config(const GqaConfig& c, const std::string& op) {
+  if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.n_heads % c.n_kv_heads)
+    throw Error(EMA_ERR_SHAPE, op + ": bad head config n_heads=" + std::to_string(c.n_heads) +
+                                   " n_kv_heads=" + std::to_string(c.n_kv_heads) +
+                                   " head_dim=" + std::to_string(c.head_dim));
+}
+
+uint64_t decode_ws_bytes(const GqaConfig& c, int32_t capacity) {
+  uint64_t need = 0;
+  check(ema_decode_workspace_size(1, c.n_heads, c.n_kv_heads, c.head_dim, capacity, &need), "decode_workspace_size");
+  return need;
+}
+
+// Temporaries of the attention core, carved in this order: q (prefill only), the
+// attention output, the decode split state (decode only).
+struct CoreBuffers {
+  void* q = nullptr;
+  void* attn = nullptr;
+  void* ws = nullptr;
+  uint64_t ws_bytes = 0;
+};
+
+CoreBuffers take_core(Arena& arena, const GqaConfig& c, int32_t T, int32_t capacity) {
+  CoreBuffers b;
+  const size_t HD = (size_t)c.n_heads * c.head_dim;
+  if (T > 1) b.q = arena.take(HD * T * 2);
+  b.attn = arena.take((size_t)T * HD * 2);
+  if (T == 1) {
+    b.ws_bytes = decode_ws_bytes(c, capacity);
+    b.ws = arena.take((size_t)b.ws_bytes);
+  }
+  return b;
+}
+
+// The attention layer over either cache, on q|k|v rows already in device memory:
+// pre-attention writes the chunk's K/V (ring rows for a rotating cache) and causal
+// prefill attends (T > 1, gqa.rs:78), or the fused decode step does both (T == 1).
+void check_range(int32_t cap, int32_t offset, int32_t T, bool rotating, const std::string& name) {
   if (!rotating && (offset < 0 || (int64_t)offset + T > cap))
     throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string((int64_t)offset + T - 1) +
                                       " cap=" + std::to_string(cap));
   if (rotating && (offset < 0 || T > cap))
     throw Error(EMA_ERR_CAPACITY, name + ": " + std::to_string(T) + " tokens exceed the window " + std::to_string(cap));
-  if (weights.q_norm.has_value() != weights.k_norm.has_value())
-    throw Error(EMA_ERR_UNSUPPORTED, name + ": q_norm and k_norm must be both present or both absent");
-  uint32_t flags = 0;
-  if (!weights.q_norm) flags |= EMA_PRE_NO_NORM;
-  if (!config.use_rope) flags |= EMA_PRE_NO_ROPE;
-  const float scale = 1.0f / std::sqrt((float)D);  // crates/attention/src/gqa.rs:73
+}
 
-  void* q = cache.q_scratch((size_t)Hq * T * D * 2);
-  void* out = cache.out_scratch((size_t)T * Hq * D * 2);
-  check(ema_pre_attention(ctx.stream, qkv.data, weights.q_norm ? weights.q_norm->data : nullptr,
-                          weights.k_norm ? weights.k_norm->data : nullptr, config.norm_eps, config.rope_theta,
-                          cache.device_position(offset), 1, T, Hq, Hkv, D, flags, q, &cache.desc()),
-        "pre_attention");
+template <class Cache>
+void attend(const Ctx& ctx, const void* qkv, int32_t T, const std::optional<Array>& q_norm,
+            const std::optional<Array>& k_norm, Cache& cache, const GqaConfig& config, int32_t offset,
+            const CoreBuffers& buf) {
+  const int32_t Hq = config.n_heads, Hkv = config.n_kv_heads, D = config.head_dim;
+  const int32_t cap = cache.desc().capacity;
+  // optional_qk_norm (crates/ops/src/attention.rs:57-76): each norm on its own
+  uint32_t flags = 0;
+  if (!q_norm) flags |= EMA_PRE_NO_Q_NORM;
+  if (!k_norm) flags |= EMA_PRE_NO_K_NORM;
+  if (!config.use_rope) flags |= EMA_PRE_NO_ROPE;
+  const void* qw = q_norm ? q_norm->data : nullptr;
+  const void* kw = k_norm ? k_norm->data : nullptr;
+  const float scale = 1.0f / std::sqrt((float)D);  // crates/attention/src/gqa.rs:73
+  const int32_t* pos = cache.position(ctx, offset);
   if (T > 1) {  // is_prefill (gqa.rs:78): causal over the cache
-    check(ema_prefill_attention(ctx.stream, q, &cache.desc(), cache.device_position(offset), T, Hq, scale,
-                                EMA_PREFILL_CAUSAL, out),
+    check(ema_pre_attention(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, T, Hq, Hkv, D, flags,
+                            buf.q, &cache.desc()),
+          "pre_attention");
+    check(ema_prefill_attention(ctx.stream, buf.q, &cache.desc(), pos, T, Hq, scale, EMA_PREFILL_CAUSAL, buf.attn),
           "prefill_attention");
-  } else {
-    uint64_t ws_bytes = 0;
-    void* ws = cache.decode_workspace(Hq, &ws_bytes);
+  } else {  // the decode step writes the row at the offset and attends offset + 1 rows
     const int32_t max_len = offset + 1 < cap ? offset + 1 : cap;
-    check(ema_decode_attention(ctx.stream, q, &cache.desc(), cache.device_position(offset + 1), max_len, Hq, scale,
-                               out, ws, ws_bytes),
-          "decode_attention");
+    check(ema_decode_step(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, const_cast<int32_t*>(pos),
+                          max_len, Hq, flags, scale, &cache.desc(), buf.attn, buf.ws, buf.ws_bytes),
+          "decode_step");
   }
-  cache.reset();
-  cache.advance(offset + T);
+  cache.set_len((int64_t)offset + T);
+}
+
+template <class Cache>
+void check_cache_config(const Cache& cache, const GqaConfig& config, const std::string& name) {
+  check_config(config, name);
+  if (config.n_kv_heads != cache.n_kv_heads() || config.head_dim != cache.head_dim())
+    throw Error(EMA_ERR_SHAPE, name + ": config does not match the cache");
+}
+
+int32_t seq_len_of(const Array& a, int64_t width, const std::string& name, const char* what) {
+  if (!a.data || a.shape.size() != 3 || a.shape[0] != 1 || a.shape[2] != width || !a.strides.empty() ||
+      a.shape[1] <= 0 || a.shape[1] > INT32_MAX)
+    throw Error(EMA_ERR_SHAPE, name + ": " + what + " must be contiguous [1, seq, " + std::to_string(width) +
+                                   "], got " + shape_str(a.shape));
+  return (int32_t)a.shape[1];
+}
+
+template <class Cache>
+Array qkv_layer(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
+                const std::optional<Array>& k_norm, Cache& cache, const GqaConfig& config, int32_t offset,
+                bool rotating, const std::string& name) {
+  check_cache_config(cache, config, name);
+  const int32_t T = seq_len_of(qkv, (int64_t)(config.n_heads + 2 * config.n_kv_heads) * config.head_dim, name, "qkv");
+  check_range(cache.desc().capacity, offset, T, rotating, name);
+  Arena arena(ctx, name.c_str());
+  const CoreBuffers buf = take_core(arena, config, T, cache.desc().capacity);
+  arena.check();
+  attend(ctx, qkv.data, T, q_norm, k_norm, cache, config, offset, buf);
   Array r;
-  r.data = out;
-  r.shape = {1, T, (int64_t)Hq * D};
+  r.data = buf.attn;
+  r.shape = {1, T, (int64_t)config.n_heads * config.head_dim};
+  return r;
+}
+
+// A projection's weights for y = x W^T with W [N, K].
+void check_proj(const QuantWeights& w, int32_t N, int32_t K, const std::string& name, const char* which) {
+  const std::string what = name + ": " + which;
+  if (!w.is_quantized())
+    throw Error(EMA_ERR_UNSUPPORTED, what + " holds plain (dequantized) weights; only MLX affine-quantised ones "
+                                            "are supported");
+  if (!w.mode || std::string(w.mode) != "affine")
+    throw Error(EMA_ERR_UNSUPPORTED, what + ": quantisation mode '" + (w.mode ? w.mode : "") + "' (affine only)");
+  if (w.bits <= 0 || 32 % w.bits || K % w.group_size)
+    throw Error(EMA_ERR_SHAPE, what + ": bits " + std::to_string(w.bits) + " / group_size " +
+                                   std::to_string(w.group_size) + " do not fit K=" + std::to_string(K));
+  const std::vector<int64_t> ws = {N, (int64_t)K * w.bits / 32}, ss = {N, K / w.group_size};
+  if (w.weight.shape != ws || w.scales.shape != ss || w.biases.shape != ss || !w.weight.data || !w.scales.data ||
+      !w.biases.data)
+    throw Error(EMA_ERR_SHAPE, what + ": expected weight " + shape_str(ws) + " and scales/biases " + shape_str(ss) +
+                                   ", got " + shape_str(w.weight.shape) + " / " + shape_str(w.scales.shape) + " / " +
+                                   shape_str(w.biases.shape));
+}
+
+// One projection y[:, col:col+N] = x W^T (ldy = the row width of y), weights checked.
+void project(const Ctx& ctx, const void* x, int64_t ldx, const QuantWeights& w, int32_t M, int32_t N, int32_t K,
+             void* y, int64_t ldy) {
+  check(ema_quantized_matmul(ctx.stream, x, ldx, (const uint32_t*)w.weight.data, w.scales.data, w.biases.data, y, ldy,
+                             M, N, K, w.group_size, w.bits, EMA_DTYPE_BF16),
+        "quantized_matmul");
+}
+
+// gqa.rs:62-107: project q, k, v into one q|k|v row (run_qkv's separate pieces without
+// the concatenation, crates/serve/src/forward/projection.rs:105-128), attend, o_proj
+// (attend_and_project, crates/ops/src/attention.rs:162-177).
+template <class Cache>
+Array gqa_layer(const Ctx& ctx, const Array& x, const GqaWeights& w, Cache& cache, const GqaConfig& config,
+                int32_t offset, bool rotating, const std::string& name) {
+  check_cache_config(cache, config, name);
+  if (!x.data || x.shape.size() != 3 || x.shape[2] <= 0)
+    throw Error(EMA_ERR_SHAPE, name + ": x must be contiguous [1, seq, hidden], got " + shape_str(x.shape));
+  const int64_t hidden = x.shape[2];
+  if (hidden > INT32_MAX) throw Error(EMA_ERR_SHAPE, name + ": hidden size too large");
+  const int32_t T = seq_len_of(x, hidden, name, "x");
+  const int32_t Hq = config.n_heads, Hkv = config.n_kv_heads, D = config.head_dim;
+  const int64_t F = (int64_t)(Hq + 2 * Hkv) * D;
+  check_range(cache.desc().capacity, offset, T, rotating, name);
+  const int32_t K = (int32_t)hidden;
+  check_proj(w.q_proj, Hq * D, K, name, "q_proj");
+  check_proj(w.k_proj, Hkv * D, K, name, "k_proj");
+  check_proj(w.v_proj, Hkv * D, K, name, "v_proj");
+  check_proj(w.o_proj, K, Hq * D, name, "o_proj");
+  Arena arena(ctx, name.c_str());
+  void* qkv = arena.take((size_t)T * F * 2);
+  void* y = arena.take((size_t)T * hidden * 2);
+  const CoreBuffers buf = take_core(arena, config, T, cache.desc().capacity);
+  arena.check();
+  project(ctx, x.data, hidden, w.q_proj, T, Hq * D, K, qkv, F);
+  project(ctx, x.data, hidden, w.k_proj, T, Hkv * D, K, (char*)qkv + (size_t)Hq * D * 2, F);
+  project(ctx, x.data, hidden, w.v_proj, T, Hkv * D, K, (char*)qkv + (size_t)(Hq + Hkv) * D * 2, F);
+  attend(ctx, qkv, T, w.q_norm, w.k_norm, cache, config, offset, buf);
+  project(ctx, buf.attn, (int64_t)Hq * D, w.o_proj, T, K, Hq * D, y, hidden);
+  Array r;
+  r.data = y;
+  r.shape = {1, T, hidden};
   return r;
 }
 
 }  // namespace
 
-Array gqa_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights, StaticCache& cache,
-                    const GqaConfig& config, int32_t offset) {
-  return attend(ctx, qkv, weights, cache, config, offset, false, "gqa_attention");
+size_t qkv_attention_workspace_bytes(const GqaConfig& config, int32_t max_seq_len, int32_t capacity) {
+  check_config(config, "qkv_attention_workspace_bytes");
+  const size_t HD = (size_t)config.n_heads * config.head_dim, T = (size_t)(max_seq_len > 1 ? max_seq_len : 1);
+  return aligned(HD * T * 2) + aligned(T * HD * 2) + aligned((size_t)decode_ws_bytes(config, capacity));
 }
 
-Array sliding_window_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights, StaticCache& cache,
+size_t gqa_workspace_bytes(const GqaConfig& config, int64_t hidden_size, int32_t max_seq_len, int32_t capacity) {
+  const size_t T = (size_t)(max_seq_len > 1 ? max_seq_len : 1);
+  const size_t F = (size_t)(config.n_heads + 2 * config.n_kv_heads) * config.head_dim;
+  return aligned(T * F * 2) + aligned(T * (size_t)hidden_size * 2) +
+         qkv_attention_workspace_bytes(config, max_seq_len, capacity);
+}
+
+Array gqa_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, StaticCache& cache,
+                    const GqaConfig& config, int32_t offset) {
+  return gqa_layer(ctx, x, weights, cache, config, offset, false, "gqa_attention");
+}
+
+Array sliding_window_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, StaticCache& cache,
                                const SlidingWindowConfig& config, int32_t offset) {
   // The reference delegates to gqa_attention and leaves the window to the
   // cache backend (crates/attention/src/sliding_window.rs:40-50).
-  return gqa_attention(ctx, qkv, weights, cache, config.gqa, offset);
+  return gqa_attention(ctx, x, weights, cache, config.gqa, offset);
 }
 
-Array sliding_window_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights, RotatingCache& cache,
+Array sliding_window_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, RotatingCache& cache,
                                const SlidingWindowConfig& config, int32_t offset) {
   if (config.window_size != (size_t)cache.window_size())
     throw Error(EMA_ERR_SHAPE, "sliding_window_attention: window_size " + std::to_string(config.window_size) +
                                    " differs from the cache's " + std::to_string(cache.window_size()));
-  return attend(ctx, qkv, weights, cache, config.gqa, offset, true, "sliding_window_attention");
+  return gqa_layer(ctx, x, weights, cache, config.gqa, offset, true, "sliding_window_attention");
+}
+
+Array qkv_attention(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
+                    const std::optional<Array>& k_norm, StaticCache& cache, const GqaConfig& config, int32_t offset) {
+  return qkv_layer(ctx, qkv, q_norm, k_norm, cache, config, offset, false, "qkv_attention");
+}
+
+Array qkv_attention(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
+                    const std::optional<Array>& k_norm, RotatingCache& cache, const GqaConfig& config,
+                    int32_t offset) {
+  return qkv_layer(ctx, qkv, q_norm, k_norm, cache, config, offset, true, "qkv_attention");
 }
 
 }  // namespace ema

@@ -9,14 +9,18 @@
 //                                                            class StaticCache
 //   struct RotatingCache     crates/kvcache/src/rotating.rs:22-122  class RotatingCache (a ring)
 //   struct GqaConfig         crates/attention/src/gqa.rs:27-42  struct GqaConfig
-//   struct GqaWeights        crates/attention/src/gqa.rs:45-53  struct GqaWeights (q/k norm only)
+//   struct QuantWeights      crates/ops/src/quant.rs:16-40      struct QuantWeights (affine)
+//   struct GqaWeights        crates/attention/src/gqa.rs:45-53  struct GqaWeights
 //   fn gqa_attention         crates/attention/src/gqa.rs:62-107 gqa_attention
 //   fn sliding_window_attention crates/attention/src/sliding_window.rs:40-50
 //                                                            sliding_window_attention
+//   MlxCtx (stream + allocator)                              struct Ctx (stream + arena)
 //
-// The projections (q/k/v/o_proj quantised matmuls) are outside this path:
-// gqa_attention takes the fused projection output qkv [1, T, (Hq+2Hkv)*D] and
-// returns the attention output [1, T, Hq*D] that o_proj consumes.
+// gqa_attention takes the hidden state x [1, T, hidden] and returns [1, T, hidden]: the
+// q, k and v projections (ema_quantized_matmul into one q|k|v row), the q/k norms, RoPE
+// and the cache write (ema_pre_attention, or the fused ema_decode_step for T == 1), the
+// attention (ema_prefill_attention for T > 1), then o_proj (ema_quantized_matmul).
+// qkv_attention is the same layer without the projections.
 // Errors are thrown as ema::Error with the reference's message texts
 // ("KV cache is empty", "static KV overflow offset=.. cap=..").
 #pragma once
@@ -44,9 +48,16 @@ class EMA_HOST_API Error : public std::runtime_error {
   int32_t code_;
 };
 
-// Analogue of MlxCtx for this path: the HIP stream work is enqueued on.
+// Analogue of MlxCtx for this path: the HIP stream work is enqueued on, and the device
+// arena the layer calls take their temporaries from (the role of MLX's allocator): q|k|v
+// rows, q, the attention output, the o_proj output and the decode split's state. The
+// caller sizes it once (gqa_workspace_bytes / qkv_attention_workspace_bytes) and no call
+// allocates device memory. An Array a call returns that points into the arena stays valid
+// until the next call that uses the same arena.
 struct Ctx {
   ema_stream_t stream = nullptr;
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
 };
 
 // Analogue of mlx_array for this path: a non-owning view of a bf16 device
@@ -95,25 +106,16 @@ class EMA_HOST_API StaticCache final : public KvCache {
   // the pre-built static_offsets scalars (crates/serve/src/engine_ext.rs:293-299),
   // so a step passes its offset without a host-to-device copy.
   const int32_t* device_position(int32_t p) const;
+  // The same, for the layer calls (the ring's counterpart writes a slot).
+  const int32_t* position(const Ctx&, int64_t p) const { return device_position((int32_t)p); }
   // Record that rows [offset, offset + n) were written in place.
   void advance(int32_t n);
-
-  // Scratch owned by the cache for gqa_attention (grown on demand, outside
-  // the steady state): q [Hq * T * D], output [T * Hq * D], decode workspace.
-  void* q_scratch(size_t bytes);
-  void* out_scratch(size_t bytes);
-  void* decode_workspace(int32_t n_heads, uint64_t* bytes);
+  void set_len(int64_t n);
 
  private:
   ema_kvcache_desc desc_{};
   int32_t offset_ = 0;
   int32_t* positions_ = nullptr;  // device int32 [capacity + 1] = 0, 1, ..., capacity
-  void* q_buf_ = nullptr;
-  size_t q_bytes_ = 0;
-  void* o_buf_ = nullptr;
-  size_t o_bytes_ = 0;
-  void* ws_ = nullptr;
-  uint64_t ws_bytes_ = 0;
 };
 
 // Rotating (sliding-window) bf16 cache of one layer: the reference's RotatingCache
@@ -132,7 +134,8 @@ class EMA_HOST_API RotatingCache final : public KvCache {
   // window_size tokens are kept (rotating.rs:81-92).
   void append(const Ctx& ctx, const Array& k, const Array& v) override;
   // The held tokens in order, [1, Hkv, len, head_dim]: the ring itself until it wraps,
-  // then a rotated copy in cache-owned scratch (valid until the next call).
+  // then a rotated copy in ctx's arena (2 * Hkv * window * head_dim * 2 bytes; valid
+  // until the next call that uses the arena).
   std::pair<Array, Array> get(const Ctx& ctx) const override;
   size_t len() const override { return total_ < (int64_t)desc_.capacity ? (size_t)total_ : (size_t)desc_.capacity; }
   void reset() override { total_ = 0; }
@@ -143,29 +146,18 @@ class EMA_HOST_API RotatingCache final : public KvCache {
   int32_t head_dim() const { return desc_.head_dim; }
   int64_t total_len() const { return total_; }
   const ema_kvcache_desc& desc() const { return desc_; }
-  // Device pointer to the int32 value p (any p >= 0 below 2^31; the table grows on
-  // demand, outside the steady state).
-  const int32_t* device_position(int64_t p);
+  // Device pointer to an int32 slot holding p (0 <= p < 2^31), written on ctx's stream
+  // by a one-thread kernel (stream-ordered: a later call rewrites it after the work
+  // that read it).
+  const int32_t* position(const Ctx& ctx, int64_t p) const;
   // Record that the tokens [total, total + n) were written in place.
   void advance(int32_t n) { total_ += n; }
-
-  void* q_scratch(size_t bytes);
-  void* out_scratch(size_t bytes);
-  void* decode_workspace(int32_t n_heads, uint64_t* bytes);
+  void set_len(int64_t n) { total_ = n; }
 
  private:
   ema_kvcache_desc desc_{};
   int64_t total_ = 0;
-  int32_t* positions_ = nullptr;
-  int64_t n_positions_ = 0;
-  void* q_buf_ = nullptr;
-  size_t q_bytes_ = 0;
-  void* o_buf_ = nullptr;
-  size_t o_bytes_ = 0;
-  void* ws_ = nullptr;
-  uint64_t ws_bytes_ = 0;
-  mutable void* get_buf_ = nullptr;
-  mutable size_t get_bytes_ = 0;
+  int32_t* slot_ = nullptr;  // device int32 [1], allocated with the cache
 };
 
 struct GqaConfig {
@@ -177,9 +169,24 @@ struct GqaConfig {
   bool use_rope = true;
 };
 
-// Only the parts of GqaWeights this path consumes: the optional per-head
-// q/k RMSNorm weights ([head_dim] bf16 device views).
+// A quantised linear layer, MLX affine format (crates/ops/src/quant.rs:16-40):
+// weight [N, K * bits / 32] uint32 (lowest bits first), scales and biases
+// [N, K / group_size] bf16; y = x W^T. group_size 0 (plain weights) and the mxfp4 mode
+// are refused with EMA_ERR_UNSUPPORTED.
+struct QuantWeights {
+  Array weight;
+  Array scales;
+  Array biases;
+  int32_t bits = 4;
+  int32_t group_size = 64;
+  const char* mode = "affine";
+  bool is_quantized() const { return group_size > 0; }
+};
+
+// crates/attention/src/gqa.rs:45-53: the four projections and the optional per-head
+// q/k RMSNorm weights ([head_dim] bf16), each norm optional on its own.
 struct GqaWeights {
+  QuantWeights q_proj, k_proj, v_proj, o_proj;
   std::optional<Array> q_norm;
   std::optional<Array> k_norm;
 };
@@ -189,15 +196,21 @@ struct SlidingWindowConfig {
   size_t window_size = 0;
 };
 
-// qkv [1, T, (Hq + 2*Hkv) * head_dim] -> attention output [1, T, Hq * head_dim]
-// (a view into cache-owned scratch, valid until the next call on this cache).
-// T > 1: causal attention over the cache rows [0, offset + T); T == 1: decode
-// over offset + 1 rows. K/V are written at [offset, offset + T) and the cache
-// length advances to offset + T.
-EMA_HOST_API Array gqa_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights, StaticCache& cache,
+// Arena bytes gqa_attention needs for up to max_seq_len tokens of hidden size
+// `hidden_size` over a cache of `capacity` rows (the window for a rotating cache).
+EMA_HOST_API size_t gqa_workspace_bytes(const GqaConfig& config, int64_t hidden_size, int32_t max_seq_len,
+                                        int32_t capacity);
+// Arena bytes qkv_attention needs.
+EMA_HOST_API size_t qkv_attention_workspace_bytes(const GqaConfig& config, int32_t max_seq_len, int32_t capacity);
+
+// x [1, T, hidden] bf16 -> [1, T, hidden] bf16 (in ctx's arena). T > 1: causal
+// attention over the cache rows [0, offset + T) (gqa.rs:78, is_prefill); T == 1: decode
+// over offset + 1 rows. K/V are written at [offset, offset + T) and the cache length
+// becomes offset + T.
+EMA_HOST_API Array gqa_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, StaticCache& cache,
                                  const GqaConfig& config, int32_t offset);
 
-EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights,
+EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights,
                                             StaticCache& cache, const SlidingWindowConfig& config, int32_t offset);
 
 // The same over a RotatingCache, which enforces the window (config.window_size must
@@ -205,7 +218,17 @@ EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& qkv, co
 // attends causally over the window the cache holds after the append (keys
 // [max(0, offset + T - window), p] for query position p), T == 1 over the last window
 // tokens. T must not exceed the window.
-EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& qkv, const GqaWeights& weights,
+EMA_HOST_API Array sliding_window_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights,
                                             RotatingCache& cache, const SlidingWindowConfig& config, int32_t offset);
+
+// The layer without its projections: qkv [1, T, (Hq + 2*Hkv) * head_dim] (the q|k|v
+// rows) -> the o_proj input [1, T, Hq * head_dim] (in ctx's arena). Same cache
+// semantics as gqa_attention / sliding_window_attention.
+EMA_HOST_API Array qkv_attention(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
+                                 const std::optional<Array>& k_norm, StaticCache& cache, const GqaConfig& config,
+                                 int32_t offset);
+EMA_HOST_API Array qkv_attention(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
+                                 const std::optional<Array>& k_norm, RotatingCache& cache, const GqaConfig& config,
+                                 int32_t offset);
 
 }  // namespace ema

@@ -3,7 +3,9 @@
 //   crates/kvcache/tests/lib.rs     (KvCache trait contract, InMemoryCache)
 //   crates/kvcache/tests/concat.rs  (new_is_empty, reset, get bails when empty)
 //   crates/attention/tests/gqa.rs   (GqaConfig constructible, gqa_attention errors)
-// plus GPU checks of StaticCache and gqa_attention against the CPU oracle.
+// plus GPU checks of StaticCache, RotatingCache, gqa_attention (projections, norms, RoPE,
+// cache write, attention, o_proj), sliding_window_attention and qkv_attention against
+// the CPU oracle chain ora_qmatmul -> ora_pre_attention -> ora_sdpa -> ora_qmatmul.
 //
 // usage: test_host_api cpu|gpu   (exit status 0 = all passed)
 #include <hip/hip_runtime.h>
@@ -117,9 +119,123 @@ static void expect_close(const std::vector<uint16_t>& got, const std::vector<uin
   std::printf("     %s: max_abs=%.3e mean_abs=%.3e\n", what, mx, mean);
   EXPECT(mx <= 2e-2 && mean <= 2e-3);
 }
+// The layer output after o_proj: the same bar, with the max-abs bound widened by one bf16
+// rounding step of the value itself (2^-7 relative) for outputs above 1.
+static void expect_close_out(const std::vector<uint16_t>& got, const std::vector<uint16_t>& ref, const char* what) {
+  double worst = 0, sum = 0;
+  for (size_t i = 0; i < got.size(); ++i) {
+    const double r = ora_bf16_to_f32(ref[i]);
+    double d = std::fabs((double)ora_bf16_to_f32(got[i]) - r);
+    if (!(d == d)) d = 1e9;
+    worst = std::max(worst, d / (2e-2 + std::fabs(r) / 128.0));
+    sum += d;
+  }
+  const double mean = sum / (double)got.size();
+  std::printf("     %s: worst/bound=%.3f mean_abs=%.3e\n", what, worst, mean);
+  EXPECT(worst <= 1.0 && mean <= 2e-3);
+}
+
+// MLX affine 4-bit weights, group 64, for y = x W^T with W [N, K]: random codes,
+// scales `scale` * (1 + N(0, 0.1)) and biases -7.5 * scale (centred codes).
+struct HostQW {
+  std::vector<uint32_t> w;
+  std::vector<uint16_t> s, b;
+  int N = 0, K = 0;
+};
+static HostQW random_qw(int N, int K, uint64_t seed, float scale) {
+  HostQW q;
+  q.N = N;
+  q.K = K;
+  q.w.resize((size_t)N * K / 8);
+  q.s.resize((size_t)N * K / 64);
+  q.b.resize(q.s.size());
+  uint64_t st = seed * 0x9E3779B97F4A7C15ull + 12345;
+  for (auto& x : q.w) {
+    st ^= st << 13;
+    st ^= st >> 7;
+    st ^= st << 17;
+    x = (uint32_t)(st >> 16);
+  }
+  auto noise = normal(q.s.size(), seed + 7, 1.f, 0.1f);
+  for (size_t i = 0; i < q.s.size(); ++i) {
+    const float sc = scale * ora_bf16_to_f32(noise[i]);
+    q.s[i] = ora_f32_to_bf16(sc);
+    q.b[i] = ora_f32_to_bf16(-7.5f * ora_bf16_to_f32(q.s[i]));
+  }
+  return q;
+}
+// y [M, N] bf16 = x [M, K] W^T through the oracle (f64 sums, one rounding to bf16).
+static std::vector<uint16_t> ora_project(const std::vector<uint16_t>& x, int M, const HostQW& q) {
+  std::vector<float> xf(x.size()), sf(q.s.size()), bf(q.b.size());
+  ora_bf16_to_f32_array(x.data(), xf.data(), x.size());
+  ora_bf16_to_f32_array(q.s.data(), sf.data(), q.s.size());
+  ora_bf16_to_f32_array(q.b.data(), bf.data(), q.b.size());
+  std::vector<double> y((size_t)M * q.N);
+  ora_qmatmul(xf.data(), q.w.data(), sf.data(), bf.data(), M, q.N, q.K, 64, 4, y.data());
+  std::vector<uint16_t> out(y.size());
+  for (size_t i = 0; i < y.size(); ++i) out[i] = ora_f32_to_bf16((float)y[i]);
+  return out;
+}
+static void* upload_bytes(const void* h, size_t n) {
+  void* d = nullptr;
+  if (hipMalloc(&d, n) != hipSuccess) throw std::runtime_error("hipMalloc");
+  if (hipMemcpy(d, h, n, hipMemcpyHostToDevice) != hipSuccess) throw std::runtime_error("H2D");
+  return d;
+}
+struct DevQW {
+  QuantWeights qw;
+  explicit DevQW(const HostQW& h) {
+    qw.weight = Array{upload_bytes(h.w.data(), h.w.size() * 4), {h.N, h.K / 8}, {}};
+    qw.scales = Array{upload(h.s), {h.N, h.K / 64}, {}};
+    qw.biases = Array{upload(h.b), {h.N, h.K / 64}, {}};
+  }
+  ~DevQW() {
+    for (void* p : {qw.weight.data, qw.scales.data, qw.biases.data}) (void)hipFree(p);
+  }
+};
+
+// The reference layer on the host (gqa.rs:62-107 with the oracle's ops): q|k|v
+// projections, norms (null = absent), RoPE and the cache write at `off`, SDPA over
+// [begin, off + T) (causal for T > 1), o_proj. kref/vref are the chronological caches.
+struct OracleLayer {
+  HostQW q, k, v, o;
+  int Hq, Hkv, D, cap;
+  std::vector<uint16_t> kref, vref;
+  OracleLayer(int hidden, int Hq_, int Hkv_, int D_, int cap_, uint64_t seed)
+      : q(random_qw(Hq_ * D_, hidden, seed, 0.0068f)), k(random_qw(Hkv_ * D_, hidden, seed + 1, 0.0068f)),
+        v(random_qw(Hkv_ * D_, hidden, seed + 2, 0.0068f)), o(random_qw(hidden, Hq_ * D_, seed + 3, 0.0034f)),
+        Hq(Hq_), Hkv(Hkv_), D(D_), cap(cap_), kref((size_t)Hkv_ * cap_ * D_, 0), vref((size_t)Hkv_ * cap_ * D_, 0) {}
+  std::vector<uint16_t> run(const std::vector<uint16_t>& x, int T, int off, int begin, const uint16_t* qw,
+                            const uint16_t* kw) {
+    const int F = (Hq + 2 * Hkv) * D;
+    auto pq = ora_project(x, T, q), pk = ora_project(x, T, k), pv = ora_project(x, T, v);
+    std::vector<uint16_t> qkv((size_t)T * F);
+    for (int t = 0; t < T; ++t) {
+      std::copy_n(&pq[(size_t)t * Hq * D], Hq * D, &qkv[(size_t)t * F]);
+      std::copy_n(&pk[(size_t)t * Hkv * D], Hkv * D, &qkv[(size_t)t * F + Hq * D]);
+      std::copy_n(&pv[(size_t)t * Hkv * D], Hkv * D, &qkv[(size_t)t * F + (Hq + Hkv) * D]);
+    }
+    const uint32_t flags = (qw ? 0u : (uint32_t)ORA_FLAG_NO_Q_NORM) | (kw ? 0u : (uint32_t)ORA_FLAG_NO_K_NORM);
+    std::vector<uint16_t> qh((size_t)Hq * T * D), attn((size_t)T * Hq * D);
+    int32_t o32 = off, len = off + T, b32 = begin;
+    if (ora_pre_attention(qkv.data(), qw, kw, 1e-6f, 1e6f, &o32, 1, T, Hq, Hkv, D, flags, qh.data(), kref.data(),
+                          vref.data(), cap) != 0)
+      throw std::runtime_error("oracle overflow");
+    ora_sdpa(qh.data(), kref.data(), vref.data(), &len, &b32, 1, Hq, Hkv, T, D, cap, 1.0f / std::sqrt((float)D),
+             T > 1 ? 1 : 0, 0, attn.data());
+    return ora_project(attn, T, o);
+  }
+};
 
 static void gpu_tests() {
-  const int Hkv = 2, D = 128, cap = 256, Hq = 8;
+  const int Hkv = 2, D = 128, cap = 256, Hq = 8, hidden = 1024;
+  const int F = (Hq + 2 * Hkv) * D;
+  const GqaConfig cfg{Hq, Hkv, D, 1e6f, 1e-6f, true};
+  // one arena for every layer call below (gqa_workspace_bytes covers the largest)
+  Ctx ctx;
+  ctx.workspace_bytes = gqa_workspace_bytes(cfg, hidden, 64, cap);
+  if (hipMalloc(&ctx.workspace, ctx.workspace_bytes) != hipSuccess) throw std::runtime_error("hipMalloc arena");
+
   run("static_cache_new_is_empty", [&] {
     StaticCache c(Hkv, cap, D);
     EXPECT(c.len() == 0 && c.is_empty());
@@ -156,32 +272,92 @@ static void gpu_tests() {
     EXPECT(c.len() == 0);
     (void)hipFree(dk);
   });
-  run("gqa_attention_rejects_bad_shapes", [&] {
+  run("gqa_attention_rejects_bad_arguments", [&] {
+    // every case throws before any launch (fake device pointers are never read)
     StaticCache c(Hkv, cap, D);
-    GqaConfig cfg{Hq, Hkv, D, 1e6f, 1e-6f, true};
-    Array qkv{(void*)0x1000, {1, 4, 100}, {}};
-    EXPECT(error_of([&] { gqa_attention(Ctx{}, qkv, GqaWeights{}, c, cfg, 0); }).find("qkv must be") !=
+    void* fake = (void*)0x1000;
+    auto qw_of = [&](int N, int K) {
+      QuantWeights w;
+      w.weight = Array{fake, {N, K / 8}, {}};
+      w.scales = w.biases = Array{fake, {N, K / 64}, {}};
+      return w;
+    };
+    GqaWeights w{qw_of(Hq * D, hidden), qw_of(Hkv * D, hidden), qw_of(Hkv * D, hidden), qw_of(hidden, Hq * D),
+                 std::nullopt, std::nullopt};
+    Array x{fake, {1, 4, hidden}, {}};
+    EXPECT(error_of([&] { gqa_attention(ctx, Array{fake, {4, hidden}, {}}, w, c, cfg, 0); }).find("x must be") !=
            std::string::npos);
     GqaConfig bad{12, 8, D, 1e6f, 1e-6f, true};
-    EXPECT(!error_of([&] { gqa_attention(Ctx{}, qkv, GqaWeights{}, c, bad, 0); }).empty());
-    Array ok{(void*)0x1000, {1, 4, (int64_t)(Hq + 2 * Hkv) * D}, {}};
-    EXPECT(error_of([&] { gqa_attention(Ctx{}, ok, GqaWeights{}, c, cfg, cap - 2); }).find("static KV overflow") !=
+    EXPECT(!error_of([&] { gqa_attention(ctx, x, w, c, bad, 0); }).empty());
+    EXPECT(error_of([&] { gqa_attention(ctx, x, w, c, cfg, cap - 2); }).find("static KV overflow") !=
            std::string::npos);
+    GqaWeights plain = w;
+    plain.k_proj.group_size = 0;
+    EXPECT(error_of([&] { gqa_attention(ctx, x, plain, c, cfg, 0); }).find("plain") != std::string::npos);
+    GqaWeights mx = w;
+    mx.v_proj.mode = "mxfp4";
+    EXPECT(error_of([&] { gqa_attention(ctx, x, mx, c, cfg, 0); }).find("affine only") != std::string::npos);
+    GqaWeights wrong = w;
+    wrong.o_proj = qw_of(hidden, hidden * 2);
+    EXPECT(error_of([&] { gqa_attention(ctx, x, wrong, c, cfg, 0); }).find("o_proj: expected weight") !=
+           std::string::npos);
+    Ctx small = ctx;
+    small.workspace_bytes = 4096;
+    try {
+      gqa_attention(small, x, w, c, cfg, 0);
+      EXPECT(false);
+    } catch (const Error& e) {
+      EXPECT(e.code() == EMA_ERR_WORKSPACE && std::string(e.what()).find("ctx workspace") != std::string::npos);
+    }
+    EXPECT(c.is_empty());
   });
-  run("gqa_attention_prefill_then_decode_matches_oracle", [&] {
+  // gqa.rs:62-107 end to end: prefill 37 tokens, then 4 decode steps
+  auto layer_case = [&](const char* name, bool q_norm, bool k_norm, uint64_t seed) {
+    run(name, [&] {
+      StaticCache c(Hkv, cap, D);
+      OracleLayer ref(hidden, Hq, Hkv, D, cap, seed);
+      DevQW dq(ref.q), dk(ref.k), dv(ref.v), dout(ref.o);
+      auto qw = normal(D, seed + 10, 1.f, 0.02f), kw = normal(D, seed + 11, 1.f, 0.02f);
+      void *dqw = upload(qw), *dkw = upload(kw);
+      GqaWeights w{dq.qw, dk.qw, dv.qw, dout.qw, std::nullopt, std::nullopt};
+      if (q_norm) w.q_norm = Array{dqw, {D}, {}};
+      if (k_norm) w.k_norm = Array{dkw, {D}, {}};
+      const int T = 37, steps = 4;
+      for (int step = 0; step <= steps; ++step) {
+        const int t = step == 0 ? T : 1, off = step == 0 ? 0 : T + step - 1;
+        auto x = normal((size_t)t * hidden, seed + 100 + step);
+        void* dx = upload(x);
+        Array y = gqa_attention(ctx, Array{dx, {1, t, hidden}, {}}, w, c, cfg, off);
+        (void)hipDeviceSynchronize();
+        EXPECT(c.len() == (size_t)(off + t) && y.shape == std::vector<int64_t>({1, t, hidden}));
+        auto want = ref.run(x, t, off, 0, q_norm ? qw.data() : nullptr, k_norm ? kw.data() : nullptr);
+        expect_close_out(download(y.data, want.size()), want, step == 0 ? "layer prefill" : "layer decode");
+        (void)hipFree(dx);
+      }
+      // V rows hold the v projection's output: within its rounding of the oracle's (the
+      // bit copy of the projected row into the cache is pinned by the pre-attention tests)
+      expect_close_out(download(c.desc().v, ref.vref.size()), ref.vref, "V cache");
+      c.reset();
+      EXPECT(c.is_empty() && c.memory_bytes() == (size_t)2 * Hkv * cap * D * 2);
+      (void)hipFree(dqw);
+      (void)hipFree(dkw);
+    });
+  };
+  layer_case("gqa_attention_projections_prefill_then_decode_matches_oracle", true, true, 1000);
+  layer_case("gqa_attention_k_norm_only_matches_oracle", false, true, 2000);
+  layer_case("gqa_attention_without_norms_matches_oracle", false, false, 3000);
+  run("qkv_attention_prefill_then_decode_matches_oracle", [&] {
     StaticCache c(Hkv, cap, D);
-    GqaConfig cfg{Hq, Hkv, D, 1e6f, 1e-6f, true};
-    const int F = (Hq + 2 * Hkv) * D, T = 37, steps = 4;
     auto qw = normal(D, 10, 1.f, 0.02f), kw = normal(D, 11, 1.f, 0.02f);
     void *dqw = upload(qw), *dkw = upload(kw);
-    GqaWeights w{Array{dqw, {D}, {}}, Array{dkw, {D}, {}}};
     std::vector<uint16_t> kref((size_t)Hkv * cap * D, 0), vref((size_t)Hkv * cap * D, 0);
     const float scale = 1.0f / std::sqrt((float)D);
+    const int T = 37, steps = 4;
     for (int step = 0; step <= steps; ++step) {
       const int t = step == 0 ? T : 1, off = step == 0 ? 0 : T + step - 1;
       auto qkv = normal((size_t)t * F, 100 + step);
       void* dqkv = upload(qkv);
-      Array out = gqa_attention(Ctx{}, Array{dqkv, {1, t, F}, {}}, w, c, cfg, off);
+      Array out = qkv_attention(ctx, Array{dqkv, {1, t, F}, {}}, Array{dqw, {D}, {}}, Array{dkw, {D}, {}}, c, cfg, off);
       (void)hipDeviceSynchronize();
       EXPECT(c.len() == (size_t)(off + t));
       std::vector<uint16_t> q((size_t)Hq * t * D), ref((size_t)t * Hq * D);
@@ -193,9 +369,12 @@ static void gpu_tests() {
       (void)hipFree(dqkv);
     }
     EXPECT(download(c.desc().v, vref.size()) == vref);
-    // reset keeps the buffers, rewinds the length (crates/serve/src/engine_ext.rs:10-36)
-    c.reset();
-    EXPECT(c.is_empty() && c.memory_bytes() == (size_t)2 * Hkv * cap * D * 2);
+    Array ok{(void*)0x1000, {1, 4, (int64_t)F}, {}};
+    EXPECT(error_of([&] { qkv_attention(ctx, Array{(void*)0x1000, {1, 4, 100}, {}}, std::nullopt, std::nullopt, c,
+                                        cfg, 0); })
+               .find("qkv must be") != std::string::npos);
+    EXPECT(error_of([&] { qkv_attention(ctx, ok, std::nullopt, std::nullopt, c, cfg, cap - 2); })
+               .find("static KV overflow") != std::string::npos);
     (void)hipFree(dqw);
     (void)hipFree(dkw);
   });
@@ -215,7 +394,7 @@ static void gpu_tests() {
     auto push = [&](int T, uint64_t seed) {
       auto k = normal((size_t)H * T * D, seed);
       void* dk = upload(k);
-      c.append(Ctx{}, Array{dk, {1, H, T, D}, {}}, Array{dk, {1, H, T, D}, {}});
+      c.append(ctx, Array{dk, {1, H, T, D}, {}}, Array{dk, {1, H, T, D}, {}});
       (void)hipDeviceSynchronize();
       for (int t = 0; t < T; ++t) {
         std::vector<uint16_t> tok((size_t)H * D);
@@ -229,7 +408,7 @@ static void gpu_tests() {
       push(T, seed);
       const size_t n = std::min<size_t>(seq.size(), W);
       EXPECT(c.len() == n);
-      auto kv = c.get(Ctx{});
+      auto kv = c.get(ctx);
       (void)hipDeviceSynchronize();
       EXPECT(kv.first.shape[2] == (int64_t)n);
       const int64_t sh = kv.first.strides.empty() ? (int64_t)n * D : kv.first.strides[1];
@@ -242,54 +421,63 @@ static void gpu_tests() {
             ok &= all[(size_t)h * sh + i * sp + d] == seq[seq.size() - n + i][(size_t)h * D + d];
       EXPECT(ok);
     }
+    // a wrapped get() needs the arena for its ordered copy
+    EXPECT(error_of([&] { c.get(Ctx{}); }).find("ctx workspace") != std::string::npos);
   });
   run("sliding_window_attention_matches_oracle", [&] {
     const int W = 48, cap_ref = 256;
     RotatingCache c(W, Hkv, D);
-    GqaConfig cfg{Hq, Hkv, D, 1e6f, 1e-6f, true};
     SlidingWindowConfig sw{cfg, (size_t)W};
-    const int F = (Hq + 2 * Hkv) * D;
+    OracleLayer ref(hidden, Hq, Hkv, D, cap_ref, 4000);
+    DevQW dq(ref.q), dk(ref.k), dv(ref.v), dout(ref.o);
     auto qw = normal(D, 20, 1.f, 0.02f), kw = normal(D, 21, 1.f, 0.02f);
     void *dqw = upload(qw), *dkw = upload(kw);
-    GqaWeights w{Array{dqw, {D}, {}}, Array{dkw, {D}, {}}};
-    std::vector<uint16_t> kref((size_t)Hkv * cap_ref * D, 0), vref((size_t)Hkv * cap_ref * D, 0);
-    const float scale = 1.0f / std::sqrt((float)D);
+    GqaWeights w{dq.qw, dk.qw, dv.qw, dout.qw, Array{dqw, {D}, {}}, Array{dkw, {D}, {}}};
     // prefill 40, 20 decode steps (the ring wraps), then a 30-token chunk that wraps within it
     std::vector<std::pair<int, int>> calls{{0, 40}};
     for (int i = 0; i < 20; ++i) calls.push_back({40 + i, 1});
     calls.push_back({60, 30});
     int step = 0;
     for (auto [off, t] : calls) {
-      auto qkv = normal((size_t)t * F, 300 + step);
-      void* dqkv = upload(qkv);
-      Array out = sliding_window_attention(Ctx{}, Array{dqkv, {1, t, F}, {}}, w, c, sw, off);
+      auto x = normal((size_t)t * hidden, 300 + step);
+      void* dx = upload(x);
+      Array y = sliding_window_attention(ctx, Array{dx, {1, t, hidden}, {}}, w, c, sw, off);
       (void)hipDeviceSynchronize();
       EXPECT(c.len() == (size_t)std::min(off + t, W) && c.total_len() == off + t);
-      std::vector<uint16_t> q((size_t)Hq * t * D), ref((size_t)t * Hq * D);
-      int32_t o32 = off, len = off + t, begin = std::max(0, off + t - W);
-      EXPECT(ora_pre_attention(qkv.data(), qw.data(), kw.data(), 1e-6f, 1e6f, &o32, 1, t, Hq, Hkv, D, 0, q.data(),
-                               kref.data(), vref.data(), cap_ref) == 0);
-      ora_sdpa(q.data(), kref.data(), vref.data(), &len, &begin, 1, Hq, Hkv, t, D, cap_ref, scale, t > 1 ? 1 : 0, 0,
-               ref.data());
-      if (step == 0 || step == 20 || step == 21)
-        expect_close(download(out.data, ref.size()), ref, t > 1 ? "window prefill" : "window decode");
-      else {
-        double mx = 0;
-        auto got = download(out.data, ref.size());
-        for (size_t i = 0; i < got.size(); ++i)
-          mx = std::max(mx, std::fabs((double)ora_bf16_to_f32(got[i]) - (double)ora_bf16_to_f32(ref[i])));
-        EXPECT(mx <= 2e-2);
-      }
-      (void)hipFree(dqkv);
+      auto want = ref.run(x, t, off, std::max(0, off + t - W), qw.data(), kw.data());
+      expect_close_out(download(y.data, want.size()), want, t > 1 ? "window prefill" : "window decode");
+      (void)hipFree(dx);
       ++step;
     }
     SlidingWindowConfig bad{cfg, (size_t)W + 1};
-    Array ok{(void*)0x1000, {1, 1, (int64_t)F}, {}};
-    EXPECT(error_of([&] { sliding_window_attention(Ctx{}, ok, w, c, bad, 90); }).find("window_size") !=
+    Array ok{(void*)0x1000, {1, 1, (int64_t)hidden}, {}};
+    EXPECT(error_of([&] { sliding_window_attention(ctx, ok, w, c, bad, 90); }).find("window_size") !=
            std::string::npos);
     (void)hipFree(dqw);
     (void)hipFree(dkw);
   });
+  run("qkv_attention_over_the_ring_matches_oracle", [&] {
+    const int W = 48, cap_ref = 128;
+    RotatingCache c(W, Hkv, D);
+    std::vector<uint16_t> kref((size_t)Hkv * cap_ref * D, 0), vref((size_t)Hkv * cap_ref * D, 0);
+    const float scale = 1.0f / std::sqrt((float)D);
+    int step = 0;
+    for (auto [off, t] : std::vector<std::pair<int, int>>{{0, 40}, {40, 1}, {41, 30}, {71, 1}}) {
+      auto qkv = normal((size_t)t * F, 500 + step++);
+      void* dqkv = upload(qkv);
+      Array out = qkv_attention(ctx, Array{dqkv, {1, t, F}, {}}, std::nullopt, std::nullopt, c, cfg, off);
+      (void)hipDeviceSynchronize();
+      std::vector<uint16_t> q((size_t)Hq * t * D), ref((size_t)t * Hq * D);
+      int32_t o32 = off, len = off + t, begin = std::max(0, off + t - W);
+      EXPECT(ora_pre_attention(qkv.data(), nullptr, nullptr, 1e-6f, 1e6f, &o32, 1, t, Hq, Hkv, D, ORA_FLAG_NO_NORM,
+                               q.data(), kref.data(), vref.data(), cap_ref) == 0);
+      ora_sdpa(q.data(), kref.data(), vref.data(), &len, &begin, 1, Hq, Hkv, t, D, cap_ref, scale, t > 1 ? 1 : 0, 0,
+               ref.data());
+      expect_close(download(out.data, ref.size()), ref, t > 1 ? "ring prefill" : "ring decode");
+      (void)hipFree(dqkv);
+    }
+  });
+  (void)hipFree(ctx.workspace);
 }
 
 int main(int argc, char** argv) {
