@@ -208,6 +208,60 @@ def test_int4_decode_qwen3_8b_batched_shape(ema, ora):
     assert_close(host(o4), ora.sdpa(q, kd, vd, L, scale_of(D), False), "int4 decode 8B batched")
 
 
+def _poison_rows(qkv_parts, lengths):
+    """Copy of (words, scales, biases) whose rows >= lengths[b] hold all-ones code words,
+    NaN scales and +inf biases (bf16 0x7FC0 / 0x7F80)."""
+    w, sc, bi = (a.copy() for a in qkv_parts)
+    for b, L in enumerate(lengths):
+        w.view(np.uint32)[b, :, L:] = 0xFFFFFFFF
+        sc.view(np.uint16)[b, :, L:] = 0x7FC0
+        bi.view(np.uint16)[b, :, L:] = 0x7F80
+    return w, sc, bi
+
+
+def test_int4_decode_ignores_poisoned_rows_past_the_length(ema, ora):
+    """Rows at or past a sequence's length never reach the output: codes, scales and biases
+    set to garbage / NaN / inf there give a bit-identical result (lengths not multiples of
+    the 32-row tile; a 1000-row segment split over several workers)."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 3, 16, 4, 128, 4096
+    L = np.array([37, 1000, 2017], np.int32)
+    say(f"int4 decode NaN poison past lengths {L.tolist()}")
+    (kq, _), (vq, _) = quantized_kv(ora, (B, Hkv, cap, D), seed=870)
+    q = dev(ora.normal_bf16((B, Hq, 1, D), seed=872))
+    clean = ema.decode_attention(q, int4_cache(ema, kq, vq), dev(L), cap)
+    poisoned = ema.decode_attention(q, int4_cache(ema, _poison_rows(kq, L), _poison_rows(vq, L)), dev(L), cap)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(clean), host(poisoned))
+    assert np.isfinite(f32(host(clean))).all()
+
+
+def test_int4_fused_step_ignores_poisoned_rows_past_the_offset(ema, ora):
+    """The fused step writes row offset (poisoned beforehand too) and attends offset + 1 rows:
+    poisoned rows after it leave the output and the written row bit-identical."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 3, 16, 4, 128, 4096
+    off = np.array([36, 999, 2016], np.int32)
+    say(f"int4 fused step NaN poison past offsets {off.tolist()}")
+    (kq, _), (vq, _) = quantized_kv(ora, (B, Hkv, cap, D), seed=880)
+    qkv = dev(ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=882))
+    qw = dev(ora.normal_bf16(D, seed=883, mean=1.0, std=0.02))
+    kw = dev(ora.normal_bf16(D, seed=884, mean=1.0, std=0.02))
+    c_clean = int4_cache(ema, kq, vq)
+    c_pois = int4_cache(ema, _poison_rows(kq, off), _poison_rows(vq, off))
+    clean = ema.decode_step(qkv, qw, kw, 1e-6, 1e6, dev(off), Hq, c_clean, cap)
+    poisoned = ema.decode_step(qkv, qw, kw, 1e-6, 1e6, dev(off), Hq, c_pois, cap)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(clean), host(poisoned))
+    assert np.isfinite(f32(host(clean))).all()
+    for a, b in ((c_clean.k, c_pois.k), (c_clean.k_scales, c_pois.k_scales), (c_clean.v_biases, c_pois.v_biases)):
+        ha, hb = host(a), host(b)
+        for s in range(B):
+            assert np.array_equal(ha[s, :, off[s]], hb[s, :, off[s]]), "the written row"
+
+
 # ------------------------------------------------------------------ fused step
 @pytest.mark.parametrize("flags", [0, 3])
 def test_int4_fused_step(ema, ora, flags):
