@@ -57,6 +57,10 @@ pub mod sys {
     pub const EMA_PREFILL_CAUSAL: u32 = 1;
     pub const EMA_PREFILL_CHUNK_ONLY: u32 = 2;
 
+    /// Arrival counters at the start of every decode workspace: zero before its first use;
+    /// every call leaves them at zero.
+    pub const EMA_DECODE_COUNTER_BYTES: u64 = 131072;
+
     /// Size of the static scratch behind `ema_decode_step_noalloc` (per device).
     pub const EMA_NOALLOC_SCRATCH_BYTES: u64 = 8 << 20;
 
@@ -177,6 +181,7 @@ pub mod hip {
         pub fn hipMalloc(ptr: *mut *mut c_void, size: usize) -> c_int;
         pub fn hipFree(ptr: *mut c_void) -> c_int;
         pub fn hipMemcpy(dst: *mut c_void, src: *const c_void, size: usize, kind: c_int) -> c_int;
+        pub fn hipMemset(dst: *mut c_void, value: c_int, size: usize) -> c_int;
         pub fn hipMemcpy2DAsync(dst: *mut c_void, dpitch: usize, src: *const c_void, spitch: usize, width: usize,
                                 height: usize, kind: c_int, stream: *mut c_void) -> c_int;
         pub fn hipGetErrorString(err: c_int) -> *const c_char;
@@ -229,8 +234,10 @@ impl DeviceArray {
 
 /// The role of `MlxCtx` here: the HIP stream work is enqueued on, and the device arena
 /// the layer calls take their temporaries from (sized once with
-/// [`gqa_workspace_bytes`]; 256-byte aligned). An array a call returns from the arena is
-/// valid until the next call that uses it.
+/// [`gqa_workspace_bytes`]; 256-byte aligned; zero-filled once, because its first
+/// `EMA_DECODE_COUNTER_BYTES` hold the decode split's arrival counters, which every call
+/// leaves at zero). An array a call returns from the arena is valid until the next call
+/// that uses it.
 pub struct HipCtx {
     pub stream: sys::EmaStream,
     pub workspace: *mut c_void,
@@ -238,11 +245,13 @@ pub struct HipCtx {
 }
 
 impl HipCtx {
-    /// A context on `stream` with an arena of `workspace_bytes` allocated once.
+    /// A context on `stream` with a zero-filled arena of `workspace_bytes` allocated once.
     pub fn with_workspace(stream: sys::EmaStream, workspace_bytes: usize) -> Result<Self> {
         let mut p: *mut c_void = std::ptr::null_mut();
         check_hip(unsafe { hip::hipMalloc(&mut p, workspace_bytes) }, "HipCtx: workspace")?;
-        Ok(HipCtx { stream, workspace: p, workspace_bytes })
+        let ctx = HipCtx { stream, workspace: p, workspace_bytes };
+        check_hip(unsafe { hip::hipMemset(p, 0, workspace_bytes) }, "HipCtx: workspace")?;
+        Ok(ctx)
     }
 }
 
@@ -493,16 +502,25 @@ pub fn gqa_workspace_bytes(config: &GqaConfig, hidden_size: i64, max_seq_len: i3
         + aligned(decode_ws_bytes(config, capacity)?))
 }
 
+/// Carves a call's temporaries out of the arena, in order. The decode counters stay at
+/// its start in every layout: a decode workspace starts there, nothing else covers them.
 struct Arena {
     base: *mut u8,
     have: usize,
     used: usize,
 }
 
+const COUNTERS: usize = sys::EMA_DECODE_COUNTER_BYTES as usize;
+
 impl Arena {
     fn new(ctx: &HipCtx) -> Self {
         let have = if ctx.workspace.is_null() { 0 } else { ctx.workspace_bytes };
-        Arena { base: ctx.workspace as *mut u8, have, used: 0 }
+        Arena { base: ctx.workspace as *mut u8, have, used: COUNTERS }
+    }
+    /// The decode workspace of `bytes` (counters first); taken before anything else.
+    fn take_decode_workspace(&mut self, bytes: usize) -> *mut c_void {
+        self.used += aligned(bytes.saturating_sub(COUNTERS));
+        self.base as *mut c_void
     }
     fn take(&mut self, bytes: usize) -> *mut c_void {
         let at = self.used;
@@ -587,12 +605,12 @@ pub fn gqa_attention(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache:
     let f = ((hq + 2 * hkv) * d) as i64;
     let hd = (hq * d) as usize;
     let mut arena = Arena::new(ctx);
+    let ws_bytes = if t == 1 { decode_ws_bytes(config, cap)? } else { 0 };
+    let ws = if t == 1 { arena.take_decode_workspace(ws_bytes) } else { std::ptr::null_mut() };
     let qkv = arena.take(t as usize * f as usize * 2);
     let y = arena.take(t as usize * hidden as usize * 2);
     let q = if t > 1 { arena.take(hd * t as usize * 2) } else { std::ptr::null_mut() };
     let attn = arena.take(t as usize * hd * 2);
-    let ws_bytes = if t == 1 { decode_ws_bytes(config, cap)? } else { 0 };
-    let ws = if t == 1 { arena.take(ws_bytes) } else { std::ptr::null_mut() };
     arena.check(op)?;
 
     // 1. q|k|v projections (project_qkv, crates/ops/src/attention.rs:31-51)

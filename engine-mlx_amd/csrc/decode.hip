@@ -20,10 +20,12 @@
 // the piece. A segment covered by a single workgroup is normalised and written
 // directly; otherwise the combined state (m, l, unnormalised o) goes to
 // partial slot (w + segment index) -- unique because w and the segment index
-// never both stay constant from one piece to the next -- and
-// decode_merge_kernel folds the slots of each segment by log-sum-exp after the
-// kernel boundary, which is also what makes the partials of other XCDs
-// visible without cache maintenance inside the kernel.
+// never both stay constant from one piece to the next -- and the workgroup
+// counts itself in at the segment's arrival counter in the workspace. The last of
+// the segment's workgroups to arrive folds its slots by log-sum-exp and writes the
+// output, so one launch does the whole call. The partials cross XCDs (each with its
+// own L2) as device-coherent stores and loads (see part_store); the merger returns the
+// counter to zero for the next call.
 //
 // Per 32-position tile a wave issues 16 MFMA 16x16x32 (bf16 in, f32 acc):
 //   S^T[pos, g] = K[pos, :] . Q^T[:, g]    A = K rows (straight from HBM),
@@ -59,7 +61,8 @@ struct DecodeArgs {
   const uint16_t* v;
   const int32_t* len;
   uint16_t* out;
-  int32_t* hdr;  // workspace header: tile prefix per batch row (pre[0..B]) for the merge
+  int32_t* cnt;  // workspace counters: arrivals per (sequence, kv head) segment, then the grid's
+  int32_t* hdr;  // workspace: tile prefix per batch row (pre[0..B]), for decode_merge_kernel
   float* part;   // partial slots
   int64_t sb, sh, sp;
   float qk_scale;  // scale * log2(e): scores live in the log2 domain
@@ -69,11 +72,12 @@ struct DecodeArgs {
   const uint16_t* qw;
   const uint16_t* kw;
   const int32_t* off;
-  int32_t* adv;  // EMA_STEP_ADVANCE: the offsets, advanced by decode_merge_kernel (else null)
+  int32_t* adv;  // EMA_STEP_ADVANCE: the offsets, advanced by the grid's last workgroup (else null)
   float eps, log2_theta;
   uint32_t flags;
   int fused;
   int rot;  // rotating cache: the fused step's new row is row off % cap
+  int inline_merge;  // merge split segments in this kernel (else decode_merge_kernel does)
   // fp8 cache: block exponents [B, Hkv, cap, 2] (k, v then hold E4M3FN codes)
   const int8_t* kexp;
   const int8_t* vexp;
@@ -211,7 +215,40 @@ struct Combine {
   float m[kWaves][16];
   float l[kWaves][16];
   float o[kWaves][16][kD];
+  int last;  // this workgroup arrived last (at a segment's counter or the grid's)
 };
+
+// Partial states cross XCDs, each with its own L2, without cache maintenance: they are
+// written and read with device-coherent (agent-scope) stores and loads, which go past the
+// XCD's L2 (sc1), and a writer's stores have completed before its workgroup counts in.
+__device__ __forceinline__ void part_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float part_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival at counter i: every wave waits for its stores to complete (vmcnt(0): the
+// partial states have reached the device-coherent level), then thread 0 counts the
+// workgroup in. The workgroup that brings the count to n is the last of the n and
+// returns the counter to zero for the next call. Returns (to every thread) whether this
+// workgroup was last. The counter's index goes through a VGPR so that the atomic is a
+// vector one.
+__device__ bool arrive_last(const DecodeArgs& a, int64_t i, int n, Combine& cmb) {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int idx = (int)i;
+    asm volatile("" : "+v"(idx));
+    int32_t* c = a.cnt + idx;
+    const int old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = old == n - 1;
+    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    cmb.last = last;
+  }
+  __syncthreads();
+  return cmb.last != 0;
+}
 
 // Head dims lane group c feeds to the QK MFMA of step s (8 of them, d .. d+7). bf16
 // cache: d = 8(4s + c), so that the four lanes of a K row read 64 contiguous bytes per
@@ -266,6 +303,49 @@ __device__ __forceinline__ void unpack32(const u32x4 (&r)[4], float (&x)[32]) {
     for (int j = 0; j < 8; ++j) x[8 * s + j] = (j & 1) ? bf16_hi(r[s][j >> 1]) : bf16_lo(r[s][j >> 1]);
 }
 
+// Log-sum-exp merge of segment s = (b, kh), whose pieces are the partial states of
+// workers w0..w1, one thread per (head, dim). Every piece's (m, l, o[dim]) is loaded
+// independently, so a thread's loads are in flight together (one memory round trip per 8
+// pieces).
+// kCoherent: the partial states come from workgroups of the same launch (device-coherent
+// loads); else from a finished launch (plain loads).
+template <bool kCoherent>
+__device__ __forceinline__ void merge_element(const DecodeArgs& a, int b, int kh, int64_t s, int64_t w0, int64_t w1,
+                                              int gg, int d) {
+    float M = -INFINITY, Lsum = 0.f, acc = 0.f;
+    for (int64_t c0 = w0; c0 <= w1; c0 += 8) {
+      float m[8], l[8], v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t w = c0 + i <= w1 ? c0 + i : w1;  // clamped: duplicates get weight 0 below
+        const float* P = a.part + ((w + s) * a.G + gg) * kPieceStride;
+        m[i] = kCoherent ? part_load(P) : P[0];
+        l[i] = kCoherent ? part_load(P + 1) : P[1];
+        v[i] = kCoherent ? part_load(P + 4 + d) : P[4 + d];
+      }
+      float Mc = M;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i <= w1) Mc = fmaxf(Mc, m[i]);
+      const float r = __builtin_amdgcn_exp2f(M - Mc);
+      Lsum *= r;
+      acc *= r;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i <= w1) {
+          const float sc = __builtin_amdgcn_exp2f(m[i] - Mc);
+          Lsum += sc * l[i];
+          acc += sc * v[i];
+        }
+      M = Mc;
+    }
+    a.out[((int64_t)b * a.Hq + (int64_t)kh * a.G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(acc / Lsum);
+}
+
+__device__ void merge_segment(const DecodeArgs& a, int b, int kh, int64_t s, int64_t w0, int64_t w1) {
+  for (int e = threadIdx.x; e < a.G * kD; e += blockDim.x) merge_element<true>(a, b, kh, s, w0, w1, e / kD, e % kD);
+}
+
 template <bool kFused, bool kFp8, bool kI4 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
   constexpr bool kNarrow = kFp8 || kI4;  // the fp8 head-dim order (kdim)
@@ -274,7 +354,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float2 rope_cs[kWaves][kD / 2];  // fused: each wave's RoPE (cos, sin) table at the offset
   __shared__ __attribute__((aligned(16))) uint16_t new_kv[2][kD];  // fused: the new row, for its owner wave
   build_prefix(a, pre);
-  if (blockIdx.x == 0)
+  if (!a.inline_merge && blockIdx.x == 0)
     for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.hdr[i] = pre[i];
 
   // sequences with no valid position produce zeros (nothing else visits them)
@@ -291,9 +371,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int w = blockIdx.x;
   const int64_t total = pre[a.B];
   const int W = active_workers(total, a.W);
-  if (w >= W) return;
-  int64_t t = worker_begin(w, total, W);
-  const int64_t t_end = worker_begin(w + 1, total, W);
+  // workgroups past the active workers have no tiles (they still arrive at the grid's
+  // counter below when the offsets advance)
+  int64_t t = w < W ? worker_begin(w, total, W) : 0;
+  const int64_t t_end = w < W ? worker_begin(w + 1, total, W) : 0;
 
   const int g = lane & 15;  // query head inside the kv group (B-operand column)
   const int c = lane >> 4;  // 16-lane group
@@ -834,7 +915,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
 
     // combine the four waves; thread e covers (head e / 128, dim e % 128)
-    const bool single = worker_of(seg_first, total, W) == worker_of(seg_end - 1, total, W);
+    const int64_t w0 = worker_of(seg_first, total, W), w1 = worker_of(seg_end - 1, total, W);
+    const bool single = w0 == w1;
     const int64_t s = (int64_t)b * a.Hkv + kh;
     for (int e = tid; e < a.G * kD; e += blockDim.x) {
       const int gg = e / kD, d = e % kD;
@@ -850,24 +932,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         a.out[((int64_t)b * a.Hq + (int64_t)kh * a.G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(acc / Lsum);
       } else {
         float* P = a.part + (((int64_t)w + s) * a.G + gg) * kPieceStride;
-        if (d == 0) {
-          P[0] = M;
-          P[1] = Lsum;
+        if (a.inline_merge) {  // read by a workgroup of this launch
+          if (d == 0) {
+            part_store(P, M);
+            part_store(P + 1, Lsum);
+          }
+          part_store(P + 4 + d, acc);
+        } else {  // read by decode_merge_kernel
+          if (d == 0) {
+            P[0] = M;
+            P[1] = Lsum;
+          }
+          P[4 + d] = acc;
         }
-        P[4 + d] = acc;
       }
     }
+    // a segment over several workgroups: the last of them to finish merges the pieces
+    if (!single && a.inline_merge && arrive_last(a, s, (int)(w1 - w0 + 1), cmb)) merge_segment(a, b, kh, s, w0, w1);
     __syncthreads();  // cmb is reused by the next piece
     t = piece_end;
   }
+
+  // EMA_STEP_ADVANCE with the merge in this kernel: the grid's last workgroup moves each
+  // sequence's offset past the row the step wrote; every other workgroup has finished
+  // reading the offsets by then.
+  if (a.adv && a.inline_merge && arrive_last(a, (int64_t)a.B * a.Hkv, (int)gridDim.x, cmb)) {
+    for (int i = threadIdx.x; i < a.B; i += blockDim.x) {
+      const int o = a.adv[i];
+      if (o >= 0 && o < INT32_MAX && (a.rot || o < a.cap)) a.adv[i] = o + 1;
+    }
+  }
 }
 
-// Log-sum-exp merge of the segments that span several workgroups, one thread per
-// (segment, head, dim). Every piece's (m, l, o[dim]) is loaded independently, so a
-// thread's loads are in flight together (one memory round trip per 8 pieces).
-// With EMA_STEP_ADVANCE it also moves each sequence's offset past the row the step
-// wrote (thread b for sequence b): decode_kernel, which reads the offsets, has finished,
-// and no thread here reads them (segment sizes come from the tile prefix).
+// The merge of full grids, after the kernel boundary: one thread per (segment, head, dim)
+// runs merge_segment's fold for its element. With EMA_STEP_ADVANCE it also moves each
+// sequence's offset past the row the step wrote (thread b for sequence b): decode_kernel,
+// which reads the offsets, has finished, and no thread here reads them (segment sizes come
+// from the tile prefix).
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (a.adv && e < a.B) {
@@ -887,34 +988,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int64_t w0 = worker_of(seg_first, total, W);
   const int64_t w1 = worker_of(seg_first + nb - 1, total, W);
   if (w0 == w1) return;  // written directly by decode_kernel
-  float M = -INFINITY, Lsum = 0.f, acc = 0.f;
-  for (int64_t c0 = w0; c0 <= w1; c0 += 8) {
-    float m[8], l[8], v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t w = c0 + i <= w1 ? c0 + i : w1;  // clamped: duplicates get weight 0 below
-      const float* P = a.part + ((w + s) * a.G + gg) * kPieceStride;
-      m[i] = P[0];
-      l[i] = P[1];
-      v[i] = P[4 + d];
-    }
-    float Mc = M;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (c0 + i <= w1) Mc = fmaxf(Mc, m[i]);
-    const float r = __builtin_amdgcn_exp2f(M - Mc);
-    Lsum *= r;
-    acc *= r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (c0 + i <= w1) {
-        const float sc = __builtin_amdgcn_exp2f(m[i] - Mc);
-        Lsum += sc * l[i];
-        acc += sc * v[i];
-      }
-    M = Mc;
-  }
-  a.out[((int64_t)b * a.Hq + (int64_t)kh * a.G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(acc / Lsum);
+  merge_element<false>(a, b, kh, s, w0, w1, gg, d);
 }
 
 }  // namespace
@@ -930,7 +1004,13 @@ DecodePlan plan_decode(int B, int Hq, int Hkv, int D, int max_len) {
 
 constexpr uint64_t kHeaderBytes = ((kMaxB + 1) * sizeof(int32_t) + 255) & ~(uint64_t)255;
 
-uint64_t decode_workspace_bytes(const DecodePlan& p) { return kHeaderBytes + p.part_bytes; }
+uint64_t decode_workspace_bytes(const DecodePlan& p) { return kDecodeCounterBytes + kHeaderBytes + p.part_bytes; }
+
+// Grids of at most one workgroup per CU are latency-bound: the merge of their split
+// segments runs inside the kernel (one launch per call). Fuller grids merge in
+// decode_merge_kernel, whose launch is small beside theirs and which keeps the arrival
+// round trips out of their workgroups' slices.
+constexpr int kInlineMergeMaxWorkers = 256;
 
 int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, const int32_t* len,
                       int Hq, float scale, void* out, void* ws, const DecodePlan& plan, const FusedPre* fused) {
@@ -938,6 +1018,9 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
     return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: head_dim %d not supported (128)", c.head_dim);
   if (c.batch > kMaxB)
     return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: batch %d exceeds %d", c.batch, kMaxB);
+  if ((int64_t)c.batch * c.n_kv_heads + 1 > kDecodeCounterSlots)
+    return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: batch x kv heads %lld exceeds %d",
+                     (long long)c.batch * c.n_kv_heads, kDecodeCounterSlots - 1);
   const int G = Hq / c.n_kv_heads;
   if (G > 16)
     return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: %d query heads per kv head exceeds 16", G);
@@ -947,8 +1030,10 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.v = (const uint16_t*)c.v;
   a.len = len;
   a.out = (uint16_t*)out;
-  a.hdr = (int32_t*)ws;
-  a.part = (float*)((char*)ws + kHeaderBytes);
+  a.cnt = (int32_t*)ws;
+  a.hdr = (int32_t*)((char*)ws + kDecodeCounterBytes);
+  a.part = (float*)((char*)ws + kDecodeCounterBytes + kHeaderBytes);
+  a.inline_merge = plan.workers <= kInlineMergeMaxWorkers;
   a.sb = c.stride_batch;
   a.sh = c.stride_head;
   a.sp = c.stride_pos;
@@ -986,13 +1071,10 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   else if (fp8) hipLaunchKernelGGL((decode_kernel<false, true>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((decode_kernel<false, false>), grid, block, 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");
-  if (rc) return rc;
-  if (plan.workers > 1 || a.adv) {  // one worker: the merge kernel only advances the offsets
-    const int64_t threads = (int64_t)plan.segments * G * kD;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
-    rc = check_hip(hipGetLastError(), "ema_decode_attention merge launch");
-  }
-  return rc;
+  if (rc || a.inline_merge || (plan.workers == 1 && !a.adv)) return rc;
+  const int64_t threads = (int64_t)plan.segments * G * kD;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
+  return check_hip(hipGetLastError(), "ema_decode_attention merge launch");
 }
 
 }  // namespace ema

@@ -144,6 +144,14 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
                              int Hkv, int D, uint32_t flags, void* q_out,
                              const ema_kvcache_desc& c);
 
+// Arrival counters at the start of every decode workspace: one per (sequence, kv head)
+// segment, then one for the grid. The region has a fixed size, so that a workspace reused
+// across shapes never holds partial states where a later call keeps counters. Every call
+// returns the counters it uses to zero; the region must be zero before the first call.
+constexpr int kDecodeCounterSlots = 32768;
+constexpr uint64_t kDecodeCounterBytes = (uint64_t)kDecodeCounterSlots * sizeof(int32_t);
+static_assert(kDecodeCounterBytes == EMA_DECODE_COUNTER_BYTES, "counter region of the public header");
+
 struct DecodePlan {
   int workers;        // independent wave workers over the flattened (b, kv-head, tile) space
   int segments;       // B * Hkv

@@ -36,6 +36,7 @@ EMA_PRE_NO_ROPE = 2
 EMA_PRE_NO_Q_NORM = 8
 EMA_PRE_NO_K_NORM = 16
 EMA_STEP_ADVANCE = 4
+EMA_DECODE_COUNTER_BYTES = 131072
 EMA_KV_ROTATING = 1
 EMA_PREFILL_CAUSAL = 1
 EMA_PREFILL_CHUNK_ONLY = 2
@@ -259,11 +260,12 @@ def decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_len) -> int:
 
 
 def decode_workspace(batch, n_heads, n_kv_heads, head_dim, max_len, device="cuda", stream=None):
-    """Allocate a decode workspace (reusable across calls on one stream)."""
+    """Allocate a decode workspace (reusable across calls on one stream, any shape): zero-
+    filled, as the arrival counters at its start must be before the first call."""
     import torch
 
     n = decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_len)
-    return torch.empty(n, dtype=torch.uint8, device=device)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
 def decode_attention(q, cache: StaticCache, lengths, max_len, scale=None, out=None, workspace=None, stream=None):

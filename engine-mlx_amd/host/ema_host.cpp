@@ -28,14 +28,25 @@ constexpr size_t kAlign = 256;
 size_t aligned(size_t n) { return (n + kAlign - 1) & ~(kAlign - 1); }
 
 // Carves a call's temporaries out of ctx's arena, in order; throws EMA_ERR_WORKSPACE
-// with the total the call needs when the arena is smaller.
+// with the total the call needs when the arena is smaller. The decode split's arrival
+// counters (EMA_DECODE_COUNTER_BYTES) stay at the start of the arena in every layout:
+// a decode workspace starts there, and nothing else is carved over them.
 class Arena {
  public:
-  Arena(const Ctx& ctx, const char* op) : base_((char*)ctx.workspace), have_(ctx.workspace ? ctx.workspace_bytes : 0), op_(op) {}
+  Arena(const Ctx& ctx, const char* op)
+      : base_((char*)ctx.workspace), have_(ctx.workspace ? ctx.workspace_bytes : 0), used_(EMA_DECODE_COUNTER_BYTES),
+        op_(op) {}
   void* take(size_t bytes) {
     const size_t at = used_;
     used_ += aligned(bytes);
     return base_ + at;
+  }
+  // The decode workspace of `bytes` (counters first): call before any take().
+  void* take_decode_workspace(size_t bytes) {
+    if (used_ != EMA_DECODE_COUNTER_BYTES || bytes < EMA_DECODE_COUNTER_BYTES)
+      throw Error(EMA_ERR_INVALID_ARG, std::string(op_) + ": decode workspace carved out of order");
+    used_ += aligned(bytes - EMA_DECODE_COUNTER_BYTES);
+    return base_;
   }
   // Call after the last take(): the pointers are valid only if this does not throw.
   void check() const {
@@ -48,7 +59,7 @@ class Arena {
  private:
   char* base_;
   size_t have_;
-  size_t used_ = 0;
+  size_t used_;
   const char* op_;
 };
 
@@ -268,15 +279,16 @@ struct CoreBuffers {
   uint64_t ws_bytes = 0;
 };
 
+// Carved first (the decode workspace must start the arena).
 CoreBuffers take_core(Arena& arena, const GqaConfig& c, int32_t T, int32_t capacity) {
   CoreBuffers b;
   const size_t HD = (size_t)c.n_heads * c.head_dim;
-  if (T > 1) b.q = arena.take(HD * T * 2);
-  b.attn = arena.take((size_t)T * HD * 2);
   if (T == 1) {
     b.ws_bytes = decode_ws_bytes(c, capacity);
-    b.ws = arena.take((size_t)b.ws_bytes);
+    b.ws = arena.take_decode_workspace((size_t)b.ws_bytes);
   }
+  if (T > 1) b.q = arena.take(HD * T * 2);
+  b.attn = arena.take((size_t)T * HD * 2);
   return b;
 }
 
@@ -401,9 +413,9 @@ Array gqa_layer(const Ctx& ctx, const Array& x, const GqaWeights& w, Cache& cach
   check_proj(w.v_proj, Hkv * D, K, name, "v_proj");
   check_proj(w.o_proj, K, Hq * D, name, "o_proj");
   Arena arena(ctx, name.c_str());
+  const CoreBuffers buf = take_core(arena, config, T, cache.desc().capacity);
   void* qkv = arena.take((size_t)T * F * 2);
   void* y = arena.take((size_t)T * hidden * 2);
-  const CoreBuffers buf = take_core(arena, config, T, cache.desc().capacity);
   arena.check();
   project(ctx, x.data, hidden, w.q_proj, T, Hq * D, K, qkv, F);
   project(ctx, x.data, hidden, w.k_proj, T, Hkv * D, K, (char*)qkv + (size_t)Hq * D * 2, F);

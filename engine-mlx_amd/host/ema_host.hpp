@@ -51,9 +51,11 @@ class EMA_HOST_API Error : public std::runtime_error {
 // Analogue of MlxCtx for this path: the HIP stream work is enqueued on, and the device
 // arena the layer calls take their temporaries from (the role of MLX's allocator): q|k|v
 // rows, q, the attention output, the o_proj output and the decode split's state. The
-// caller sizes it once (gqa_workspace_bytes / qkv_attention_workspace_bytes) and no call
-// allocates device memory. An Array a call returns that points into the arena stays valid
-// until the next call that uses the same arena.
+// caller sizes it once (gqa_workspace_bytes / qkv_attention_workspace_bytes), zero-fills
+// it once (its first EMA_DECODE_COUNTER_BYTES hold the decode split's arrival counters,
+// which every call leaves at zero) and no call allocates device memory. An Array a call
+// returns that points into the arena stays valid until the next call that uses the same
+// arena.
 struct Ctx {
   ema_stream_t stream = nullptr;
   void* workspace = nullptr;

@@ -229,9 +229,15 @@ EMA_API int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const vo
                           int32_t head_dim, uint32_t flags, void* q_out,
                           const ema_kvcache_desc* cache);
 
-/* Workspace (bytes) ema_decode_attention needs for this shape: per-piece
- * partial softmax states of the split (no initialisation needed; calls that
- * share one workspace must not overlap). */
+/* Bytes at the start of every decode workspace that hold the split's arrival counters
+ * (one per (sequence, kv head) segment, and one for the grid). They must be zero before a
+ * workspace's first use (a zero-filled allocation, or one memset); every call returns them
+ * to zero, so a workspace needs no clearing between calls, whatever their shapes. */
+#define EMA_DECODE_COUNTER_BYTES 131072
+/* Workspace (bytes) ema_decode_attention and ema_decode_step need for this shape: the
+ * counters, then per-piece partial softmax states of the split (which need no
+ * initialisation). Calls that share one workspace must not overlap. batch * n_kv_heads
+ * is limited to EMA_DECODE_COUNTER_BYTES / 4 - 1 (EMA_ERR_UNSUPPORTED beyond). */
 EMA_API int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_t n_kv_heads,
                                   int32_t head_dim, int32_t max_len, uint64_t* bytes);
 /* Batched single-token decode attention over the static cache

@@ -234,7 +234,9 @@ static void gpu_tests() {
   // one arena for every layer call below (gqa_workspace_bytes covers the largest)
   Ctx ctx;
   ctx.workspace_bytes = gqa_workspace_bytes(cfg, hidden, 64, cap);
-  if (hipMalloc(&ctx.workspace, ctx.workspace_bytes) != hipSuccess) throw std::runtime_error("hipMalloc arena");
+  if (hipMalloc(&ctx.workspace, ctx.workspace_bytes) != hipSuccess ||
+      hipMemset(ctx.workspace, 0, ctx.workspace_bytes) != hipSuccess)
+    throw std::runtime_error("hipMalloc arena");
 
   run("static_cache_new_is_empty", [&] {
     StaticCache c(Hkv, cap, D);

@@ -221,6 +221,75 @@ def test_decode_workspace_reuse_is_clean(ema, ora):
         assert_close(shared, ora.sdpa(q, kc, vc, L, scale_of(D), False), "reused workspace")
 
 
+def test_decode_workspace_reuse_across_shapes(ema, ora):
+    """One workspace shared by calls of different batch sizes and head counts: its arrival
+    counters are left at zero by every call, whatever partial states a call of another
+    shape wrote next to them, so each call gives the bits of a fresh workspace."""
+    import torch
+
+    D = 128
+    ws = ema.decode_workspace(64, 32, 8, D, 8192)  # large enough for every shape below
+    for step, (B, Hq, Hkv, cap, seed) in enumerate([(32, 32, 8, 4096, 240), (1, 16, 8, 4096, 241),
+                                                      (3, 64, 4, 1024, 242), (32, 32, 8, 4096, 243),
+                                                      (64, 8, 8, 512, 244)]):
+        rng = np.random.default_rng(seed)
+        L = rng.integers(1, cap + 1, size=B).astype(np.int32)
+        q = ora.normal_bf16((B, Hq, 1, D), seed=seed)
+        kc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 1)
+        vc = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 2)
+        cache = make_cache(ema, kc, vc)
+        say(f"decode workspace reuse across shapes: step {step} B={B} {Hq}q/{Hkv}kv cap={cap}")
+        shared = host(ema.decode_attention(dev(q), cache, dev(L), cap, workspace=ws))
+        fresh = host(ema.decode_attention(dev(q), cache, dev(L), cap))
+        torch.cuda.synchronize()
+        assert np.array_equal(shared, fresh), f"step {step}"
+        if step < 3:
+            assert_close(shared, ora.sdpa(q, kc, vc, L, scale_of(D), False), f"step {step}")
+    assert not host(ws)[:ema.EMA_DECODE_COUNTER_BYTES].any(), "counters left at zero"
+
+
+def test_decode_merge_in_kernel_and_after_agree(ema, ora):
+    """The split's merge runs inside the decode kernel for grids of at most one workgroup
+    per CU and in a second kernel for fuller ones; the host's bound of the lengths picks
+    the grid. The same inputs through both (bound = the true maximum: 252 workgroups;
+    bound = the capacity: 512) match the oracle, for attention and for the fused step with
+    the device-side offset advance."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 2, 16, 8, 128, 8192
+    L = np.array([1000, 2000], np.int32)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=250)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=251)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=252)
+    ref = ora.sdpa(q, kc, vc, L, scale_of(D), False)
+    cache = make_cache(ema, kc, vc)
+    outs = {}
+    for bound in (int(L.max()), cap):
+        say(f"decode merge paths: max_len bound {bound}")
+        outs[bound] = host(ema.decode_attention(dev(q), cache, dev(L), bound))
+        torch.cuda.synchronize()
+        assert_close(outs[bound], ref, f"decode, bound {bound}")
+    assert_close(outs[cap], outs[int(L.max())], "the two merge paths", max_abs=1e-2, mean_abs=1e-4)
+    # fused step with EMA_STEP_ADVANCE through both paths, on _fused_case's inputs (its
+    # seeds) against its oracle result
+    seed = 253
+    got, ref_s, _, _, _, vr, _ = _fused_case(ema, ora, B, Hq, Hkv, D, cap, L - 1, seed=seed)
+    assert_close(got, ref_s, "fused step, bound = capacity")
+    qkv = ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=seed)
+    qw = ora.normal_bf16(D, seed=seed + 1, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=seed + 2, mean=1.0, std=0.02)
+    kc2 = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 3)
+    vc2 = ora.normal_bf16((B, Hkv, cap, D), seed=seed + 4)
+    for bound in (int(L.max()), cap):
+        c = make_cache(ema, kc2, vc2)
+        off = dev(L - 1)
+        out = ema.decode_step(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, off, Hq, c, bound, flags=ema.EMA_STEP_ADVANCE)
+        torch.cuda.synchronize()
+        assert_close(host(out), ref_s, f"fused step with advance, bound {bound}")
+        assert np.array_equal(host(c.v), vr)
+        assert np.array_equal(host(off), L), f"offsets advanced, bound {bound}"
+
+
 def test_decode_qwen3_1p7b_shape(ema, ora):
     """batch 1, 16q/8kv, D 128, cap 4096, 1024 valid positions."""
     say("decode B1 16q/8kv cap 4096 L 1024")
