@@ -86,8 +86,6 @@ int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
       return set_error(EMA_ERR_UNSUPPORTED, "%s: int4 cache with head_dim %d not supported (128)", op, c->head_dim);
     if (c->capacity % 32)
       return set_error(EMA_ERR_UNSUPPORTED, "%s: int4 cache capacity %d is not a multiple of 32", op, c->capacity);
-    if (c->flags & EMA_KV_ROTATING)
-      return set_error(EMA_ERR_UNSUPPORTED, "%s: rotating int4 caches are not supported", op);
     if (c->stride_pos % 32 || c->stride_head % 32 || c->stride_batch % 32)
       return set_error(EMA_ERR_SHAPE, "%s: int4 cache strides must be multiples of 32 elements (16 bytes)", op);
   }
@@ -499,8 +497,6 @@ int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_k
   if (cache->dtype == EMA_DTYPE_INT4_AFFINE)
     return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over an int4 cache is not supported (attend a bf16 cache and "
                      "store the rows with ema_kvcache_quantize_int4)", op);
-  if (cache->flags & EMA_KV_ROTATING)
-    return set_error(EMA_ERR_UNSUPPORTED, "%s: prefill over a rotating fp8 cache is not supported", op);
   const uint64_t need = prefill_ws_bytes(cache, max_kv_len);
   if (!workspace || workspace_bytes < need)
     return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes needed, %llu given", op,
@@ -523,6 +519,9 @@ int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_k
   w.stride_head = (int64_t)max_kv_len * cache->head_dim;
   w.stride_batch = (int64_t)cache->n_kv_heads * max_kv_len * cache->head_dim;
   w.dtype = EMA_DTYPE_BF16;
+  // a ring stays a ring: the copy holds the cache's rows at the same row indices (all
+  // max_kv_len of them, which is the capacity once positions wrap)
+  w.flags = cache->flags & EMA_KV_ROTATING;
   return launch_prefill((hipStream_t)stream, q, w, q_offsets, n_tokens, n_heads, scale, flags, out);
 }
 

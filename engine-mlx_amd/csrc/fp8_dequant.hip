@@ -10,7 +10,8 @@
 // Mapping: 8 threads per 128-dim row, 16 codes (one 16-byte load) each, 32 rows per
 // 256-thread workgroup pass; blockIdx.y = (batch, kv head). Rows [lo, hi) of a sequence
 // are decoded, hi = min(q_off + T, rows), lo = q_off with EMA_PREFILL_CHUNK_ONLY (0
-// otherwise) -- exactly the rows the prefill kernel reads.
+// otherwise) -- exactly the rows the prefill kernel reads. A rotating cache (position p in
+// row p % cap) has every held row decoded, lo = 0 (a chunk's rows may wrap the ring).
 #include "ema_common.hpp"
 
 namespace ema {
@@ -29,6 +30,7 @@ struct DequantArgs {
   int64_t sb, sh, sp;  // code strides (bytes)
   int Hkv, cap, R, T;
   uint32_t flags;
+  int rot;
 };
 
 __global__ __launch_bounds__(256) void fp8_to_bf16_kernel(DequantArgs a) {
@@ -39,7 +41,7 @@ __global__ __launch_bounds__(256) void fp8_to_bf16_kernel(DequantArgs a) {
   int hi = q_off + a.T;
   hi = hi < a.cap ? hi : a.cap;
   hi = hi < a.R ? hi : a.R;
-  int lo = (a.flags & EMA_PREFILL_CHUNK_ONLY) ? q_off : 0;
+  int lo = (a.flags & EMA_PREFILL_CHUNK_ONLY) && !a.rot ? q_off : 0;
   lo = lo < hi ? lo : hi;
   const int t8 = threadIdx.x & 7;  // 16-code piece of the row: dims 16 t8 .. +15
   const int row = blockIdx.x * 32 + (threadIdx.x >> 3);
@@ -85,6 +87,7 @@ int32_t launch_fp8_to_bf16(hipStream_t s, const ema_kvcache_desc& c, const int32
   a.R = R;
   a.T = T;
   a.flags = flags;
+  a.rot = (c.flags & EMA_KV_ROTATING) != 0;
   const dim3 grid((unsigned)((R + 31) / 32), (unsigned)(c.batch * c.n_kv_heads));
   hipLaunchKernelGGL(fp8_to_bf16_kernel, grid, dim3(256), 0, s, a);
   return check_hip(hipGetLastError(), "ema_prefill_attention_ws: fp8 decode launch");

@@ -158,7 +158,7 @@ class StaticCache:
     crates/serve/src/engine_ext.rs:92-129): ``k``/``v`` are int32 words [B, Hkv, cap, D/8]
     (8 four-bit codes each, lowest bits first) and ``k_scales``/``k_biases``/``v_scales``/
     ``v_biases`` bf16 [B, Hkv, cap, D/64] (value = scale * code + bias); head_dim 128,
-    capacity a multiple of 32, not rotating, decode only.
+    capacity a multiple of 32, decode only (static or rotating).
 
     ``rotating=True``: the reference's RotatingCache (crates/kvcache/src/rotating.rs) as a
     ring of ``capacity`` rows (EMA_KV_ROTATING): position p lives in row p % capacity and

@@ -85,8 +85,9 @@ extern "C" {
  * larger-magnitude end, which is moved onto the grid and becomes the bias; codes
  * round((x - bias) / scale), half away from zero, at most 15). Readers use the exact affine
  * value scale * code + bias; MLX's dequantize to bf16 rounds it once (at most half a bf16
- * step per element). head_dim 128, capacity a multiple of 32, static (not
- * rotating) caches; decode only (prefill attends bf16 keys, as the reference's does). */
+ * step per element). head_dim 128, capacity a multiple of 32, static or
+ * rotating (EMA_KV_ROTATING) caches; decode only (prefill attends bf16 keys, as the
+ * reference's does). */
 #define EMA_DTYPE_INT4_AFFINE 5
 /* activation types of ema_gdn_scan (besides EMA_DTYPE_BF16) */
 #define EMA_DTYPE_F16 3

@@ -165,3 +165,115 @@ def test_rotating_prefill_without_wrap_equals_static(ema, ora):
     b = ema.prefill_attention(dev(q), ring_cache(ema, kc, vc), dev(qo))
     torch.cuda.synchronize()
     assert np.array_equal(host(a), host(b))
+
+
+def ring_any(ora, big, totals, window, fill):
+    """ring_from for any element type and trailing shape: unheld rows hold `fill`."""
+    B, Hkv = big.shape[:2]
+    ring = np.empty((B, Hkv, window) + big.shape[3:], big.dtype)
+    ring[...] = fill
+    for b in range(B):
+        for r, p in ora.ring_rows(int(totals[b]), window).items():
+            ring[b, :, r] = big[b, :, p]
+    return ring
+
+
+@pytest.mark.parametrize("q_off,T,W,chunk", [
+    ((200, 150), 100, 256, False),  # ends past the ring
+    ((500, 433), 128, 192, True),   # several wraps, chunk-only keys
+    ((0, 37), 100, 256, False),     # no wrap
+])
+def test_rotating_fp8_prefill_equals_bf16_ring(ema, ora, q_off, T, W, chunk):
+    """Prefill over a rotating FP8 cache: its held rows decoded into a ring-shaped bf16
+    copy, then the ring prefill. Bit-identical to a bf16 ring holding the decoded values;
+    within the bf16 tolerance of the oracle over the window."""
+    import torch
+    from test_gpu_fp8 import quantized_pair
+
+    B, Hq, Hkv, D = 2, 8, 2, 128
+    qo = np.asarray(q_off, np.int32)
+    L = qo + T
+    n = int(L.max())
+    say(f"rotating fp8 prefill W={W} q_off={qo.tolist()} T={T} chunk_only={chunk}")
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, n, D), seed=W + 7)
+    q = ora.normal_bf16((B, Hq, T, D), seed=W + 9)
+    c8 = ema.StaticCache(B, Hkv, W, D, dtype="fp8", rotating=True,
+                         k=dev(ring_any(ora, kc, L, W, 0x7F)), v=dev(ring_any(ora, vc, L, W, 0x7F)),
+                         k_exp=dev(ring_any(ora, ke, L, W, 0)), v_exp=dev(ring_any(ora, ve, L, W, 0)))
+    c16 = ring_cache(ema, ring_from(ora, kd, L, W), ring_from(ora, vd, L, W))
+    max_kv = W if n > W else n
+    o8 = ema.prefill_attention(dev(q), c8, dev(qo), causal=True, chunk_only=chunk, max_kv_len=max_kv)
+    o16 = ema.prefill_attention(dev(q), c16, dev(qo), causal=True, chunk_only=chunk)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(o8), host(o16)), "decoded ring == the bf16 ring"
+    lo = np.maximum(L - W, 0)
+    if chunk:
+        lo = np.maximum(lo, qo)
+    assert_close(host(o8), ora.sdpa(q, kd, vd, L, scale_of(D), True, kv_begin=lo), f"rotating fp8 prefill W={W}")
+
+
+def _int4_ring(ema, ora, big_bf16, totals, W):
+    """int4 ring over the oracle's quantisation of a chronological bf16 cache; unheld rows
+    hold all-ones code words, NaN scales and +inf biases. Returns (cache, MLX-dequantized
+    chronological values)."""
+    out, deq = [], []
+    for x in big_bf16:
+        w, s, bias = ora.int4_quantize(ora.f32_from_bf16(x))
+        out.append((ring_any(ora, w, totals, W, 0xFFFFFFFF), ring_any(ora, s, totals, W, 0x7FC0),
+                    ring_any(ora, bias, totals, W, 0x7F80)))
+        deq.append(ora.bf16_from_f32(ora.int4_dequantize(w, s, bias)))
+    (kw, ks, kb), (vw, vs, vb) = out
+    B, Hkv = kw.shape[:2]
+    cache = ema.StaticCache(B, Hkv, W, kw.shape[3] * 8, dtype="int4", rotating=True, k=dev(kw.view(np.int32)),
+                            v=dev(vw.view(np.int32)), k_scales=dev(ks), k_biases=dev(kb), v_scales=dev(vs),
+                            v_biases=dev(vb))
+    return cache, deq[0], deq[1]
+
+
+@pytest.mark.parametrize("W", [64, 96])
+def test_rotating_int4_decode_attends_the_window(ema, ora, W):
+    import torch
+
+    B, Hq, Hkv, D = 3, 16, 4, 128
+    N = np.array([W - 5, W + 37, 3 * W + 1], np.int32)  # tokens seen
+    say(f"rotating int4 decode W={W} N={N.tolist()}")
+    big_k = ora.normal_bf16((B, Hkv, int(N.max()), D), seed=W + 20)
+    big_v = ora.normal_bf16((B, Hkv, int(N.max()), D), seed=W + 21)
+    cache, kd, vd = _int4_ring(ema, ora, (big_k, big_v), N, W)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=W + 22)
+    out = ema.decode_attention(dev(q), cache, dev(N), W)
+    torch.cuda.synchronize()
+    ref = ora.sdpa(q, kd, vd, N, scale_of(D), False, kv_begin=np.maximum(N - W, 0))
+    assert_close(host(out), ref, f"rotating int4 decode W={W}")
+
+
+def test_rotating_int4_fused_step_writes_the_ring_row(ema, ora):
+    """The fused step on an int4 ring writes row offset % W (quantised as pre-attention's)
+    and attends the window: it equals pre-attention + decode attention on the same ring,
+    and only that row changes."""
+    import torch
+
+    B, Hq, Hkv, D, W = 3, 16, 4, 128, 64
+    off = np.array([W - 1, W + 10, 2 * W + 63], np.int32)
+    say(f"rotating int4 fused step W={W} off={off.tolist()}")
+    big_k = ora.normal_bf16((B, Hkv, int(off.max()), D), seed=31)
+    big_v = ora.normal_bf16((B, Hkv, int(off.max()), D), seed=32)
+    qkv = ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=33)
+    qw = ora.normal_bf16(D, seed=34, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=35, mean=1.0, std=0.02)
+    c_f, _, _ = _int4_ring(ema, ora, (big_k, big_v), off, W)
+    c_p, _, _ = _int4_ring(ema, ora, (big_k, big_v), off, W)
+    before = [host(t).copy() for t in (c_f.k, c_f.k_scales, c_f.v, c_f.v_biases)]
+    fused = ema.decode_step(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c_f, W)
+    q = ema.pre_attention(dev(qkv.reshape(B, 1, -1)), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c_p)
+    pair = ema.decode_attention(q, c_p, dev(off + 1), W)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(c_f.v), host(c_p.v)) and np.array_equal(host(c_f.v_scales), host(c_p.v_scales))
+    assert_close(host(fused), host(pair), "int4 ring fused vs pair", max_abs=1e-2, mean_abs=1e-4)
+    after = [host(t) for t in (c_f.k, c_f.k_scales, c_f.v, c_f.v_biases)]
+    for b in range(B):
+        r = int(off[b]) % W
+        others = np.r_[0:r, r + 1:W]
+        for x, y in zip(before, after):
+            assert np.array_equal(x[b][:, others], y[b][:, others]), "rows other than offset % W"
+        assert not np.array_equal(before[2][b][:, r], after[2][b][:, r]), "the ring row was written"
