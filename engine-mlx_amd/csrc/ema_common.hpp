@@ -180,6 +180,11 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
 int32_t launch_gdn_scan(hipStream_t s, const void* q, const void* k, const void* v, const float* g,
                         const float* beta, float* state, void* y, int B, int T, int hk, int hv, int dk,
                         int dv, int dtype);
+// Chunkwise scan on the matrix cores (bf16 activations, n_tokens >= kGdnChunkMinTokens).
+constexpr int kGdnChunkMinTokens = 32;
+int32_t launch_gdn_chunked(hipStream_t s, const void* q, const void* k, const void* v, const float* g,
+                           const float* beta, float* state, void* y, int B, int T, int hk, int hv, int dk,
+                           int dv);
 // Affine-quantised matmul y = x W^T over MLX-packed W (arguments validated by the caller).
 int32_t launch_qmatmul(hipStream_t s, const void* x, int64_t ldx, const void* w, const void* scales,
                        const void* biases, void* y, int64_t ldy, int M, int N, int K, int gs, int bits,

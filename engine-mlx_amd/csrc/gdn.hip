@@ -327,6 +327,8 @@ int32_t launch_gdn_scan(hipStream_t s, const void* q, const void* k, const void*
   a.dv = dv;
   const int64_t bh = (int64_t)B * hv;
   if (bh * (dv / 4) > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_gdn_scan: grid too large");
+  if (dtype == EMA_DTYPE_BF16 && T >= kGdnChunkMinTokens)
+    return launch_gdn_chunked(s, q, k, v, g, beta, state, y, B, T, hk, hv, dk, dv);
   const hipError_t e = dk == 64 ? launch_dk<64>(s, dtype, a, bh) : launch_dk<128>(s, dtype, a, bh);
   return check_hip(e, "ema_gdn_scan launch");
 }

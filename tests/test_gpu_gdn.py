@@ -7,8 +7,11 @@ Inputs follow gdn_forward's scaling: q = rms_norm(q) / dk, k = rms_norm(k) / sqr
 the same quantised activations (as f32) and the same f32 state, and computes in f64.
 
 Bars: state (f32) within 2e-5 absolute + 1e-5 relative of the oracle; y within 1e-4 for
-f32 activations, 2e-3 for f16, and the bf16 bar (max-abs 2e-2, mean-abs 2e-3) for bf16;
-a scan over T tokens bit-identical to T single-token calls.
+f32 activations, 2e-3 for f16, and the bf16 bar (max-abs 2e-2, mean-abs 2e-3) for bf16.
+Scans of f16 / f32 activations, and bf16 scans under 32 tokens, run the token-by-token
+kernel and are bit-identical to single-token calls; bf16 scans of 32 tokens or more run
+the chunkwise kernel (32-token chunks on the matrix cores), held to the same bars against
+the oracle and checked against the token-by-token kernel at the bench shape.
 """
 import numpy as np
 import pytest
@@ -157,3 +160,58 @@ def test_gdn_long_scan_vs_oracle(ema, ora):
     host_in = host_in[:5] + (np.zeros_like(host_in[5]),)
     y = ema.gdn_scan(dq, dk_, dv_, dg, db, dS)
     check_against_oracle(ora, y, dS, host_in, "f32", "long scan")
+
+
+@pytest.mark.parametrize("T,Dk,Dv", [(32, 128, 64), (33, 128, 48), (64, 64, 32), (100, 128, 80), (257, 64, 128),
+                                     (300, 128, 16)])
+def test_gdn_chunked_scan_matches_oracle(ema, ora, T, Dk, Dv):
+    # whole and partial last chunks; Dv not a multiple of the 64 rows of a workgroup
+    B, Hk, Hv = 2, 2, 4
+    say(f"gdn chunked scan B={B} T={T} Hk={Hk} Hv={Hv} Dk={Dk} Dv={Dv}")
+    dev_in, host_in = make_inputs(200 + T + Dk + Dv, B, T, Hk, Hv, Dk, Dv, "bf16")
+    dq, dk_, dv_, dg, db, dS = dev_in
+    y = ema.gdn_scan(dq, dk_, dv_, dg, db, dS)
+    check_against_oracle(ora, y, dS, host_in, "bf16", f"chunked T={T} Dk={Dk} Dv={Dv}")
+
+
+def test_gdn_chunked_scan_gate_extremes(ema, ora):
+    # g = 0 (the state is reset mid-chunk), g = 1 and beta = 0 / 1 runs, across chunk edges
+    B, T, Hk, Hv, Dk, Dv = 1, 96, 1, 2, 128, 32
+    say(f"gdn chunked scan gate extremes T={T}")
+    dev_in, host_in = make_inputs(31, B, T, Hk, Hv, Dk, Dv, "bf16")
+    dq, dk_, dv_, dg, db, dS = dev_in
+    dg[:, 5] = 0.0
+    dg[:, 40:70] = 1.0
+    dg[:, 31, 0] = 0.0
+    db[:, 10:20] = 0.0
+    db[:, 60:80, 1] = 1.0
+    host_in = host_in[:3] + (dg.cpu().numpy(), db.cpu().numpy(), host_in[5])
+    y = ema.gdn_scan(dq, dk_, dv_, dg, db, dS)
+    check_against_oracle(ora, y, dS, host_in, "bf16", "gate extremes")
+
+
+def test_gdn_chunked_scan_bench_shape(ema, ora):
+    # the prefill shape of a Qwen3-Next linear-attention layer: 2048 tokens, 16 key and
+    # 32 value heads of 128; against the oracle, and against the token-by-token kernel
+    # run over 31-token pieces
+    import torch
+
+    B, T, Hk, Hv, Dk, Dv = 1, 2048, 16, 32, 128, 128
+    say(f"gdn chunked scan bench shape B={B} T={T} Hk={Hk} Hv={Hv} Dk={Dk} Dv={Dv}")
+    dev_in, host_in = make_inputs(41, B, T, Hk, Hv, Dk, Dv, "bf16")
+    dq, dk_, dv_, dg, db, dS = dev_in
+    S_seq = dS.clone()
+    y = ema.gdn_scan(dq, dk_, dv_, dg, db, dS)
+    check_against_oracle(ora, y, dS, host_in, "bf16", "bench shape")
+    ys = []
+    for t0 in range(0, T, 31):
+        sl = slice(t0, min(T, t0 + 31))
+        ys.append(ema.gdn_scan(dq[:, sl].contiguous(), dk_[:, sl].contiguous(), dv_[:, sl].contiguous(),
+                               dg[:, sl].contiguous(), db[:, sl].contiguous(), S_seq))
+    y_seq = torch.cat(ys, dim=1)
+    dS_ = (dS - S_seq).abs()
+    tol = 4e-5 + 2e-5 * S_seq.abs()
+    say(f"  chunked vs token-by-token: state max_abs={dS_.max().item():.3e}, "
+        f"y max_abs={(y.float() - y_seq.float()).abs().max().item():.3e}")
+    assert bool((dS_ <= tol).all())
+    assert (y.float() - y_seq.float()).abs().max().item() <= 2e-2
