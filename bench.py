@@ -469,9 +469,9 @@ def bench_qmm(ctx, ema, name, M, N, K, gs=64, bits=4, steps=48, min_set_bytes=30
             "tflops": tf, "weight_sets": L}
 
 
-def bench_gdn(ctx, ema, name, B, T, Hk, Hv, Dk, Dv, steps=20):
-    """Gated DeltaNet scan (ema_gdn_scan), bf16 activations, f32 state updated in place
-    (bounded: unit keys, g and beta in (0, 1))."""
+def bench_gdn(ctx, ema, name, B, T, Hk, Hv, Dk, Dv, steps=20, workspace=False):
+    """Gated DeltaNet scan (ema_gdn_scan, or ema_gdn_scan_ws with a workspace: the WY form),
+    bf16 activations, f32 state updated in place (bounded: unit keys, g and beta in (0, 1))."""
     torch = ctx.torch
     q = ctx.randn((B, T, Hk, Dk), 0.0, 1.0 / Dk)
     k = ctx.randn((B, T, Hk, Dk), 0.0, 1.0)
@@ -481,7 +481,8 @@ def bench_gdn(ctx, ema, name, B, T, Hk, Hv, Dk, Dv, steps=20):
     beta = torch.rand((B, T, Hv), device=ctx.dev)
     S = torch.randn((B, Hv, Dv, Dk), device=ctx.dev) * 0.5
     y = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=ctx.dev)
-    ms = time_calls(torch, lambda: ema.gdn_scan(q, k, v, g, beta, S, y=y), steps, 5)
+    ws = ema.gdn_workspace(B, T, Hk, Hv, Dk, Dv) if workspace else None
+    ms = time_calls(torch, lambda: ema.gdn_scan(q, k, v, g, beta, S, y=y, workspace=ws), steps, 5)
     by = gdn_bytes(B, T, Hk, Hv, Dk, Dv)
     gbs = by / (ms * 1e-3) / 1e9
     tok = B * T / (ms * 1e-3)
@@ -573,7 +574,9 @@ def main():
         secondary.append(bench_gdn(ctx, ema, "gdn_decode_step_B32_16k32v_dk128_dv128", 32, 1, 16, 32, 128, 128))
     if args.only in ("all", "gdn"):
         secondary.append(bench_gdn(ctx, ema, "gdn_scan_T2048_B1_16k32v_dk128_dv128", 1, 2048, 16, 32, 128, 128,
-                                   steps=5))
+                                   steps=10, workspace=True))
+        secondary.append(bench_gdn(ctx, ema, "gdn_scan_T2048_B1_16k32v_dk128_dv128_no_workspace", 1, 2048, 16, 32,
+                                   128, 128, steps=5))
     if args.only in ("all", "qmm"):
         # affine-quantised projections around the attention path (MLX 4-bit, group 64):
         # Qwen3-8B q|k|v (4096 -> 6144) and o_proj (4096 -> 4096) per decode step

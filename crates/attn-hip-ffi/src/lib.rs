@@ -163,6 +163,12 @@ pub mod sys {
         pub fn ema_gdn_scan(stream: EmaStream, q: *const c_void, k: *const c_void, v: *const c_void,
                             g: *const f32, beta: *const f32, state: *mut f32, y: *mut c_void, batch: i32,
                             n_tokens: i32, hk: i32, hv: i32, dk: i32, dv: i32, dtype: i32) -> i32;
+        pub fn ema_gdn_scan_workspace_size(batch: i32, n_tokens: i32, hk: i32, hv: i32, dk: i32, dv: i32,
+                                           bytes: *mut u64) -> i32;
+        pub fn ema_gdn_scan_ws(stream: EmaStream, q: *const c_void, k: *const c_void, v: *const c_void,
+                               g: *const f32, beta: *const f32, state: *mut f32, y: *mut c_void, batch: i32,
+                               n_tokens: i32, hk: i32, hv: i32, dk: i32, dv: i32, dtype: i32,
+                               workspace: *mut c_void, workspace_bytes: u64) -> i32;
         pub fn ema_quantized_matmul(stream: EmaStream, x: *const c_void, ldx: i64, w: *const u32,
                                     scales: *const c_void, biases: *const c_void, y: *mut c_void, ldy: i64,
                                     m: i32, n: i32, k: i32, group_size: i32, bits: i32, dtype: i32) -> i32;

@@ -548,10 +548,9 @@ int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvca
 
 }  // extern "C"
 
-int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, const void* v, const float* g,
-                     const float* beta, float* state, void* y, int32_t batch, int32_t n_tokens, int32_t hk,
-                     int32_t hv, int32_t dk, int32_t dv, int32_t dtype) {
-  const char* op = "ema_gdn_scan";
+static int32_t check_gdn_args(const char* op, const void* q, const void* k, const void* v, const float* g,
+                              const float* beta, const float* state, const void* y, int32_t batch, int32_t n_tokens,
+                              int32_t hk, int32_t hv, int32_t dk, int32_t dv, int32_t dtype) {
   if (!q || !k || !v || !g || !beta || !state || !y)
     return set_error(EMA_ERR_INVALID_ARG, "%s: null q/k/v/g/beta/state/y", op);
   if (dtype != EMA_DTYPE_BF16 && dtype != EMA_DTYPE_F16 && dtype != EMA_DTYPE_F32)
@@ -568,7 +567,49 @@ int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, const vo
     return set_error(EMA_ERR_INVALID_ARG, "%s: misaligned buffer (q, k and state 16-byte aligned)", op);
   if ((int64_t)batch * n_tokens * hv * dv >= ((int64_t)1 << 31) || (int64_t)batch * hv * dv * dk >= ((int64_t)1 << 40))
     return set_error(EMA_ERR_SHAPE, "%s: tensors too large", op);
+  return EMA_OK;
+}
+
+int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, const void* v, const float* g,
+                     const float* beta, float* state, void* y, int32_t batch, int32_t n_tokens, int32_t hk,
+                     int32_t hv, int32_t dk, int32_t dv, int32_t dtype) {
+  const int32_t rc = check_gdn_args("ema_gdn_scan", q, k, v, g, beta, state, y, batch, n_tokens, hk, hv, dk, dv, dtype);
+  if (rc) return rc;
   return launch_gdn_scan((hipStream_t)stream, q, k, v, g, beta, state, y, batch, n_tokens, hk, hv, dk, dv, dtype);
+}
+
+int32_t ema_gdn_scan_workspace_size(int32_t batch, int32_t n_tokens, int32_t hk, int32_t hv, int32_t dk,
+                                    int32_t dv, uint64_t* bytes) {
+  const char* op = "ema_gdn_scan_workspace_size";
+  if (!bytes) return set_error(EMA_ERR_INVALID_ARG, "%s: null bytes", op);
+  *bytes = 0;
+  if (batch <= 0 || n_tokens <= 0 || hk <= 0 || hv <= 0 || dv <= 0)
+    return set_error(EMA_ERR_SHAPE, "%s: dims must be positive", op);
+  if (hv % hk) return set_error(EMA_ERR_SHAPE, "%s: hv %d is not a multiple of hk %d", op, hv, hk);
+  if (dk != 64 && dk != 128) return set_error(EMA_ERR_UNSUPPORTED, "%s: dk %d not supported (64, 128)", op, dk);
+  if (dv % 16) return set_error(EMA_ERR_SHAPE, "%s: dv %d is not a multiple of 16", op, dv);
+  const uint64_t chunks = (uint64_t)(n_tokens + kGdnChunkTokens - 1) / kGdnChunkTokens;
+  *bytes = chunks * gdn_wy_chunk_bytes(batch, hk, hv, dk, dv);
+  return EMA_OK;
+}
+
+int32_t ema_gdn_scan_ws(ema_stream_t stream, const void* q, const void* k, const void* v, const float* g,
+                        const float* beta, float* state, void* y, int32_t batch, int32_t n_tokens, int32_t hk,
+                        int32_t hv, int32_t dk, int32_t dv, int32_t dtype, void* workspace,
+                        uint64_t workspace_bytes) {
+  const char* op = "ema_gdn_scan_ws";
+  const int32_t rc = check_gdn_args(op, q, k, v, g, beta, state, y, batch, n_tokens, hk, hv, dk, dv, dtype);
+  if (rc) return rc;
+  if (dtype != EMA_DTYPE_BF16 || n_tokens < kGdnChunkMinTokens || dv > kGdnWyMaxDv || !aligned16(v))
+    return launch_gdn_scan((hipStream_t)stream, q, k, v, g, beta, state, y, batch, n_tokens, hk, hv, dk, dv, dtype);
+  if (!workspace || !aligned16(workspace))
+    return set_error(EMA_ERR_WORKSPACE, "%s: workspace missing or not 16-byte aligned", op);
+  if (workspace_bytes < gdn_wy_chunk_bytes(batch, hk, hv, dk, dv))
+    return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes is below one chunk's %llu", op,
+                     (unsigned long long)workspace_bytes,
+                     (unsigned long long)gdn_wy_chunk_bytes(batch, hk, hv, dk, dv));
+  return launch_gdn_wy((hipStream_t)stream, q, k, v, g, beta, state, y, batch, n_tokens, hk, hv, dk, dv, workspace,
+                       workspace_bytes);
 }
 
 int32_t ema_quantized_matmul(ema_stream_t stream, const void* x, int64_t ldx, const uint32_t* w, const void* scales,

@@ -181,10 +181,18 @@ int32_t launch_gdn_scan(hipStream_t s, const void* q, const void* k, const void*
                         const float* beta, float* state, void* y, int B, int T, int hk, int hv, int dk,
                         int dv, int dtype);
 // Chunkwise scan on the matrix cores (bf16 activations, n_tokens >= kGdnChunkMinTokens).
+constexpr int kGdnChunkTokens = 32;  // tokens per chunk
 constexpr int kGdnChunkMinTokens = 32;
 int32_t launch_gdn_chunked(hipStream_t s, const void* q, const void* k, const void* v, const float* g,
                            const float* beta, float* state, void* y, int B, int T, int hk, int hv, int dk,
                            int dv);
+// WY-form scan over a workspace (bf16, n_tokens >= kGdnChunkMinTokens, dv <= 512): bytes of
+// one chunk's records, and the launcher (segments the sequence to the workspace).
+constexpr int kGdnWyMaxDv = 512;
+uint64_t gdn_wy_chunk_bytes(int B, int hk, int hv, int dk, int dv);
+int32_t launch_gdn_wy(hipStream_t s, const void* q, const void* k, const void* v, const float* g, const float* beta,
+                      float* state, void* y, int B, int T, int hk, int hv, int dk, int dv, void* ws,
+                      uint64_t ws_bytes);
 // Affine-quantised matmul y = x W^T over MLX-packed W (arguments validated by the caller).
 int32_t launch_qmatmul(hipStream_t s, const void* x, int64_t ldx, const void* w, const void* scales,
                        const void* biases, void* y, int64_t ldy, int M, int N, int K, int gs, int bits,

@@ -47,7 +47,8 @@ EXPORTED = (
     "ema_kvcache_quantize_int4",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
     "ema_decode_attention", "ema_decode_step", "ema_decode_step_noalloc", "ema_prefill_attention", "ema_prefill_workspace_size",
-    "ema_prefill_attention_ws", "ema_gdn_scan", "ema_quantized_matmul",
+    "ema_prefill_attention_ws", "ema_gdn_scan", "ema_gdn_scan_workspace_size", "ema_gdn_scan_ws",
+    "ema_quantized_matmul",
 )
 
 
@@ -105,6 +106,8 @@ def lib() -> ctypes.CDLL:
             "ema_prefill_workspace_size": (i32, [D, i32, ctypes.POINTER(u64)]),
             "ema_prefill_attention_ws": (i32, [vp, vp, D, vp, i32, i32, f32, u32, vp, i32, vp, u64]),
             "ema_gdn_scan": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32]),
+            "ema_gdn_scan_workspace_size": (i32, [i32, i32, i32, i32, i32, i32, ctypes.POINTER(u64)]),
+            "ema_gdn_scan_ws": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, u64]),
             "ema_quantized_matmul": (i32, [vp, vp, i64, vp, vp, vp, vp, i64, i32, i32, i32, i32, i32, i32]),
         }
         for name, (res, args) in sig.items():
@@ -355,10 +358,26 @@ def prefill_attention(q, cache: StaticCache, q_offsets, scale=None, causal=True,
     return out
 
 
-def gdn_scan(q, k, v, g, beta, state, y=None, stream=None):
+def gdn_scan_workspace_size(B, T, Hk, Hv, Dk, Dv) -> int:
+    """Bytes of the workspace with which gdn_scan runs T tokens in one segment
+    (ema_gdn_scan_workspace_size)."""
+    n = ctypes.c_uint64(0)
+    _check(lib().ema_gdn_scan_workspace_size(B, T, Hk, Hv, Dk, Dv, ctypes.byref(n)), "ema_gdn_scan_workspace_size")
+    return n.value
+
+
+def gdn_workspace(B, T, Hk, Hv, Dk, Dv, device="cuda"):
+    """A workspace tensor for gdn_scan (no initialisation needed)."""
+    import torch
+
+    return torch.empty(gdn_scan_workspace_size(B, T, Hk, Hv, Dk, Dv), dtype=torch.uint8, device=device)
+
+
+def gdn_scan(q, k, v, g, beta, state, y=None, stream=None, workspace=None):
     """Gated DeltaNet recurrent scan (ema_gdn_scan): q, k [B,T,Hk,Dk], v [B,T,Hv,Dv] in bf16,
     f16 or f32; g, beta [B,T,Hv] f32; state [B,Hv,Dv,Dk] f32, updated in place. Returns
-    y [B,T,Hv,Dv] in the activation dtype."""
+    y [B,T,Hv,Dv] in the activation dtype. With a workspace (a uint8 tensor, e.g. from
+    gdn_workspace) bf16 scans of 32+ tokens run in WY form (ema_gdn_scan_ws)."""
     import torch
 
     dtypes = {torch.bfloat16: EMA_DTYPE_BF16, torch.float16: EMA_DTYPE_F16, torch.float32: EMA_DTYPE_F32}
@@ -368,8 +387,13 @@ def gdn_scan(q, k, v, g, beta, state, y=None, stream=None):
     Hv, Dv = v.shape[2], v.shape[3]
     if y is None:
         y = torch.empty((B, T, Hv, Dv), dtype=q.dtype, device=q.device)
-    _check(lib().ema_gdn_scan(_stream(stream), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state),
-                              _ptr(y), B, T, Hk, Hv, Dk, Dv, dtypes[q.dtype]), "ema_gdn_scan")
+    if workspace is None:
+        _check(lib().ema_gdn_scan(_stream(stream), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state),
+                                  _ptr(y), B, T, Hk, Hv, Dk, Dv, dtypes[q.dtype]), "ema_gdn_scan")
+    else:
+        _check(lib().ema_gdn_scan_ws(_stream(stream), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state),
+                                     _ptr(y), B, T, Hk, Hv, Dk, Dv, dtypes[q.dtype], _ptr(workspace),
+                                     workspace.numel() * workspace.element_size()), "ema_gdn_scan_ws")
     return y
 
 

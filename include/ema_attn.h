@@ -29,7 +29,7 @@
  *                                                               ema_kvcache_quantize_int4
  *   gdn_step / gdn_step_metal and the per-token scan of gdn_forward
  *              crates/ops/src/gdn.rs:83-150, gdn_metal.rs:56-88, gdn_forward.rs:173-192
- *                                                               ema_gdn_scan
+ *                                                               ema_gdn_scan, ema_gdn_scan_ws
  *   MlxCtx::quantized_matmul (affine, transpose=true)
  *              crates/mlx-ffi/src/ops/real/transform.rs:77-88, via qmatmul
  *              (crates/ops/src/quant.rs:57-76) and run_qkv / o_proj
@@ -347,6 +347,26 @@ EMA_API int32_t ema_gdn_scan(ema_stream_t stream, const void* q, const void* k, 
                              const float* g, const float* beta, float* state, void* y,
                              int32_t batch, int32_t n_tokens, int32_t hk, int32_t hv, int32_t dk,
                              int32_t dv, int32_t dtype);
+
+/* Workspace bytes for ema_gdn_scan_ws to run n_tokens tokens in one segment, into *bytes:
+ * per 32-token chunk, batch * (hv * (128 * (dk + dv) + 5120) + hk * 128 * dk) bytes. Shapes
+ * ema_gdn_scan rejects return its error. No counterpart in the reference, which allocates
+ * its intermediates per call. */
+EMA_API int32_t ema_gdn_scan_workspace_size(int32_t batch, int32_t n_tokens, int32_t hk, int32_t hv, int32_t dk,
+                                            int32_t dv, uint64_t* bytes);
+
+/* ema_gdn_scan with a workspace (the same arguments, semantics and tolerance). Scans of bf16
+ * activations over at least 32 tokens with dv <= 512 and v 16-byte aligned run in WY form:
+ * one parallel pass forms every 32-token chunk's matrices into the workspace, then one pass
+ * carries the state through the chunks. A workspace smaller than
+ * ema_gdn_scan_workspace_size's is used in segments of as many chunks as fit (at least one
+ * chunk's bytes are required). Other calls run as ema_gdn_scan and leave the workspace
+ * unused. The workspace needs no initialisation and must be 16-byte aligned; calls that
+ * share one must not overlap. Replaces the same reference sites as ema_gdn_scan. */
+EMA_API int32_t ema_gdn_scan_ws(ema_stream_t stream, const void* q, const void* k, const void* v,
+                                const float* g, const float* beta, float* state, void* y,
+                                int32_t batch, int32_t n_tokens, int32_t hk, int32_t hv, int32_t dk,
+                                int32_t dv, int32_t dtype, void* workspace, uint64_t workspace_bytes);
 
 /* y = x W^T over an affine-quantised W in MLX's packing: MLX quantized_matmul(x, w,
  * scales, biases, transpose=true, group_size, bits, "affine"), the call behind the

@@ -285,6 +285,34 @@ def test_gdn_scan_argument_errors(ema):
     assert call(v=p + 2, dtype=ema.EMA_DTYPE_F32) == ema.EMA_ERR_INVALID_ARG
 
 
+def test_gdn_scan_workspace_size_and_errors(ema):
+    L = ema.lib()
+    n = ctypes.c_uint64()
+    # per 32-token chunk: batch * (hv * (128 (dk + dv) + 5120) + hk * 128 dk)
+    assert L.ema_gdn_scan_workspace_size(1, 2048, 16, 32, 128, 128, ctypes.byref(n)) == 0
+    assert n.value == 64 * (32 * (128 * 256 + 5120) + 16 * 128 * 128)
+    assert L.ema_gdn_scan_workspace_size(2, 33, 2, 4, 64, 48, ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * (4 * (128 * 112 + 5120) + 2 * 128 * 64)
+    assert L.ema_gdn_scan_workspace_size(1, 64, 2, 4, 96, 32, ctypes.byref(n)) == ema.EMA_ERR_UNSUPPORTED
+    assert n.value == 0
+    assert L.ema_gdn_scan_workspace_size(1, 64, 3, 4, 64, 32, ctypes.byref(n)) == ema.EMA_ERR_SHAPE
+    assert L.ema_gdn_scan_workspace_size(1, 64, 2, 4, 64, 32, None) == ema.EMA_ERR_INVALID_ARG
+    p = 0x40000  # 16-byte aligned stand-in; every call below fails before any HIP call
+    L.ema_gdn_scan_workspace_size(1, 64, 2, 4, 128, 32, ctypes.byref(n))
+    per_chunk = n.value // 2
+
+    def call(ws=p, nbytes=n.value, T=64, dtype=ema.EMA_DTYPE_BF16, **kw):
+        a = dict(q=p, k=p, v=p, g=p, beta=p, state=p, y=p)
+        a.update(kw)
+        return L.ema_gdn_scan_ws(None, a["q"], a["k"], a["v"], a["g"], a["beta"], a["state"], a["y"], 1, T, 2, 4,
+                                 128, 32, dtype, ws, nbytes)
+
+    assert call(state=None) == ema.EMA_ERR_INVALID_ARG  # the ema_gdn_scan checks come first
+    assert call(ws=None) == ema.EMA_ERR_WORKSPACE
+    assert call(ws=p + 8) == ema.EMA_ERR_WORKSPACE and "aligned" in ema.last_error()
+    assert call(nbytes=per_chunk - 16) == ema.EMA_ERR_WORKSPACE and "one chunk" in ema.last_error()
+
+
 def test_rotating_flag_is_validated(ema):
     L = ema.lib()
     rc, d = _desc(ema)

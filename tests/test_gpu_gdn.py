@@ -215,3 +215,90 @@ def test_gdn_chunked_scan_bench_shape(ema, ora):
         f"y max_abs={(y.float() - y_seq.float()).abs().max().item():.3e}")
     assert bool((dS_ <= tol).all())
     assert (y.float() - y_seq.float()).abs().max().item() <= 2e-2
+
+
+# ---- WY form over a workspace (ema_gdn_scan_ws) ----
+
+@pytest.mark.parametrize("T,Dk,Dv", [(32, 128, 64), (33, 128, 48), (64, 64, 32), (100, 128, 80), (257, 64, 128),
+                                     (300, 128, 16), (200, 128, 512)])
+def test_gdn_wy_scan_matches_oracle(ema, ora, T, Dk, Dv):
+    B, Hk, Hv = 2, 2, 4
+    say(f"gdn WY scan B={B} T={T} Hk={Hk} Hv={Hv} Dk={Dk} Dv={Dv}")
+    dev_in, host_in = make_inputs(300 + T + Dk + Dv, B, T, Hk, Hv, Dk, Dv, "bf16")
+    dq, dk_, dv_, dg, db, dS = dev_in
+    ws = ema.gdn_workspace(B, T, Hk, Hv, Dk, Dv)
+    y = ema.gdn_scan(dq, dk_, dv_, dg, db, dS, workspace=ws)
+    check_against_oracle(ora, y, dS, host_in, "bf16", f"WY T={T} Dk={Dk} Dv={Dv}")
+
+
+def test_gdn_wy_segments_are_bit_identical(ema):
+    # a workspace of 1 or 3 chunks runs the sequence in segments, the state passing through
+    # HBM between them: the same arithmetic as one segment, so the same bits
+    import torch
+
+    B, T, Hk, Hv, Dk, Dv = 1, 230, 2, 4, 128, 64
+    say(f"gdn WY segments T={T}")
+    (dq, dk_, dv_, dg, db, dS), _ = make_inputs(51, B, T, Hk, Hv, Dk, Dv, "bf16")
+    full = ema.gdn_scan_workspace_size(B, T, Hk, Hv, Dk, Dv)
+    per_chunk = full // ((T + 31) // 32)
+    outs = []
+    for n in (full, per_chunk, 3 * per_chunk + 100):
+        S = dS.clone()
+        ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        y = ema.gdn_scan(dq, dk_, dv_, dg, db, S, workspace=ws)
+        outs.append((y, S))
+    torch.cuda.synchronize()
+    for y, S in outs[1:]:
+        assert torch.equal(S, outs[0][1])
+        assert torch.equal(y.view(torch.int16), outs[0][0].view(torch.int16))
+
+
+def test_gdn_wy_gate_extremes(ema, ora):
+    B, T, Hk, Hv, Dk, Dv = 1, 96, 1, 2, 128, 32
+    say(f"gdn WY gate extremes T={T}")
+    dev_in, host_in = make_inputs(31, B, T, Hk, Hv, Dk, Dv, "bf16")
+    dq, dk_, dv_, dg, db, dS = dev_in
+    dg[:, 5] = 0.0
+    dg[:, 40:70] = 1.0
+    dg[:, 31, 0] = 0.0
+    db[:, 10:20] = 0.0
+    db[:, 60:80, 1] = 1.0
+    host_in = host_in[:3] + (dg.cpu().numpy(), db.cpu().numpy(), host_in[5])
+    y = ema.gdn_scan(dq, dk_, dv_, dg, db, dS, workspace=ema.gdn_workspace(B, T, Hk, Hv, Dk, Dv))
+    check_against_oracle(ora, y, dS, host_in, "bf16", "WY gate extremes")
+
+
+def test_gdn_wy_bench_shape(ema, ora):
+    # 2048 tokens, 16 key and 32 value heads of 128: against the oracle and the one-kernel
+    # chunkwise scan
+    import torch
+
+    B, T, Hk, Hv, Dk, Dv = 1, 2048, 16, 32, 128, 128
+    say(f"gdn WY scan bench shape B={B} T={T} Hk={Hk} Hv={Hv} Dk={Dk} Dv={Dv}")
+    dev_in, host_in = make_inputs(42, B, T, Hk, Hv, Dk, Dv, "bf16")
+    dq, dk_, dv_, dg, db, dS = dev_in
+    S1 = dS.clone()
+    y = ema.gdn_scan(dq, dk_, dv_, dg, db, dS, workspace=ema.gdn_workspace(B, T, Hk, Hv, Dk, Dv))
+    check_against_oracle(ora, y, dS, host_in, "bf16", "WY bench shape")
+    y1 = ema.gdn_scan(dq, dk_, dv_, dg, db, S1)
+    d = (dS - S1).abs()
+    say(f"  WY vs one-kernel: state max_abs={d.max().item():.3e}, "
+        f"y max_abs={(y.float() - y1.float()).abs().max().item():.3e}")
+    assert bool((d <= 4e-5 + 2e-5 * S1.abs()).all())
+    assert (y.float() - y1.float()).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,T", [("f32", 64), ("bf16", 31)])
+def test_gdn_wy_other_calls_run_the_token_kernel(ema, dtype, T):
+    # f32 activations and scans under 32 tokens leave the workspace unused: bit-identical
+    # to ema_gdn_scan
+    import torch
+
+    B, Hk, Hv, Dk, Dv = 1, 2, 4, 64, 32
+    (dq, dk_, dv_, dg, db, dS), _ = make_inputs(61, B, T, Hk, Hv, Dk, Dv, dtype)
+    S1, S2 = dS.clone(), dS.clone()
+    y1 = ema.gdn_scan(dq, dk_, dv_, dg, db, S1)
+    y2 = ema.gdn_scan(dq, dk_, dv_, dg, db, S2, workspace=torch.empty(16, dtype=torch.uint8, device="cuda"))
+    torch.cuda.synchronize()
+    assert torch.equal(S1, S2)
+    assert torch.equal(y1.view(torch.int16) if dtype == "bf16" else y1, y2.view(torch.int16) if dtype == "bf16" else y2)
