@@ -210,13 +210,76 @@ __device__ __forceinline__ u32x4 i4_qperm(u32x4 w) {
   return r;
 }
 
+// One int4 tile of a wave in registers: the K words of the lane's two rows krow0 + 4r
+// (steps 2i, 2i+1), the V words (dims 8m .. 8m+7) of its 8 positions 8c + kk, and the
+// parameter words it uses. Positions are relative to the tile's first.
+struct I4Tile {
+  u32x2 k[2][2];   // [r][i]: row krow0 + 4r, dims 64i + 16c .. +15
+  uint32_t v[8];   // position 8c + kk
+  u32x4 ks[2];     // K (scale 0, scale 1) pairs of positions 8c + 4r + i
+  uint32_t kb[2];  // K (bias 0, bias 1) pair of row krow0 + 4r
+  u32x4 vs[2];     // V scale pairs of positions 8c + 4h + e
+  u32x4 vb[2];     // V bias pairs of positions 8c + 4h + e
+};
+
+__device__ __forceinline__ float fmax_asm(float x, float y) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+  return r;
+}
+// Maximum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows), by the row
+// swaps of v_permlane16_swap / v_permlane32_swap instead of LDS permutes: after a swap of
+// a value with itself, one result holds the even rows' values in both rows of each pair
+// and the other the odd rows'.
+__device__ __forceinline__ float max_over_rows(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmax_asm(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmax_asm(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Raw buffer resource over `bytes` bytes at `base` (loads past them return zero), as four
+// scalar words for the asm of the LDS loads.
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t addr = (uint64_t)base;
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)addr),
+               (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32) & 0xffffu),
+               (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
+}
+// 16 bytes per lane from buffer offset voff + soff straight into LDS at lds + 16 lane
+// (buffer_load_dwordx4 ... lds, non-temporal; the LDS base goes through M0). Issued as asm,
+// untracked by the compiler: the int4 tile loop orders it with explicit vmcnt waits.
+__device__ __forceinline__ void dma16(u32x4 rs, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
+               :
+               : "v"(voff), "s"(rs), "s"(__builtin_amdgcn_readfirstlane(soff)), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
+}
+// s_waitcnt vmcnt(N), also a compiler memory barrier (the LDS reads after it stay after it)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 // LDS used to combine the four waves' states at the end of a piece.
 struct Combine {
   float m[kWaves][16];
   float l[kWaves][16];
-  float o[kWaves][16][kD];
   int last;  // this workgroup arrived last (at a segment's counter or the grid's)
 };
+// Each wave's share of the workgroup's LDS: its [16][kD] f32 output state at the end of a
+// piece; for the int4 cache, before that, the ring of tile slots its loads stream into.
+// int4 slot: K rows (32 x 64 B), V rows (32 x 64 B), then the K scale, K bias, V scale and
+// V bias words of the tile's 32 positions (128 B each).
+constexpr int kI4Slot = 2 * kTile * 64 + 4 * kTile * 4;
+constexpr int kI4Slots = 3;  // the tile in use and two in flight
+constexpr int kI4SlotK = 0, kI4SlotV = kTile * 64, kI4SlotKs = 2 * kTile * 64, kI4SlotKb = kI4SlotKs + 4 * kTile,
+              kI4SlotVs = kI4SlotKb + 4 * kTile, kI4SlotVb = kI4SlotVs + 4 * kTile;
+constexpr int kStateLds = 16 * kD * 4;
+template <bool kI4>
+constexpr int wave_lds_bytes() { return kI4 && kI4Slots * kI4Slot > kStateLds ? kI4Slots * kI4Slot : kStateLds; }
 
 // Partial states cross XCDs, each with its own L2, without cache maintenance: they are
 // written and read with device-coherent (agent-scope) stores and loads, which go past the
@@ -351,6 +414,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr bool kNarrow = kFp8 || kI4;  // the fp8 head-dim order (kdim)
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
+  __shared__ __attribute__((aligned(16))) uint8_t wave_lds[kWaves][wave_lds_bytes<kI4>()];
   __shared__ float2 rope_cs[kWaves][kD / 2];  // fused: each wave's RoPE (cos, sin) table at the offset
   __shared__ __attribute__((aligned(16))) uint16_t new_kv[2][kD];  // fused: the new row, for its owner wave
   build_prefix(a, pre);
@@ -411,7 +475,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // fp8: codes and exponents of the tile in flight, decoded into kc/vc before use
     const uint8_t* const Kb8 = (const uint8_t*)a.k + (int64_t)b * a.sb + (int64_t)kh * a.sh;
     const uint8_t* const Vb8 = (const uint8_t*)a.v + (int64_t)b * a.sb + (int64_t)kh * a.sh;
-    const int64_t erow = ((int64_t)b * a.Hkv + kh) * a.cap;  // exponent row of position 0
+    const int64_t erow = ((int64_t)b * a.Hkv + kh) * a.cap;  // fp8 exponent / int4 parameter row of position 0
     const uint16_t* const Ke = kFp8 ? (const uint16_t*)a.kexp + erow : nullptr;
     const uint16_t* const Ve = kFp8 ? (const uint16_t*)a.vexp + erow : nullptr;
     u32x2 k8[2][4], v8[8], k8n[2][4], v8n[8];
@@ -456,41 +520,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         vr[kk] = ld16_stream(Vb + (int64_t)p * a.sp + 8 * m);
       }
     };
-    // int4: per tile a lane loads the words of its two K rows (steps 2i, 2i+1: dims
-    // 64i + 16c .. +15, one 8-byte load), the word of dims 8m .. 8m+7 of each of its 8 V
-    // positions, and the scale and bias pairs of its 8 score positions p0 + 8c + 4h + e
-    // (16 bytes per 4 positions; the capacity is a multiple of 32, so these stay inside the
-    // cache, and positions past L are masked where they are used)
-    const uint8_t* const Kb4 = (const uint8_t*)a.k + ((int64_t)b * a.sb + (int64_t)kh * a.sh) / 2;
-    const uint8_t* const Vb4 = (const uint8_t*)a.v + ((int64_t)b * a.sb + (int64_t)kh * a.sh) / 2;
-    const int64_t sp4 = a.sp / 2;
-    u32x2 k4[2][2], k4n[2][2];
-    uint32_t v4[8], v4n[8];
-    u32x4 mk[2][2], mkn[2][2], mv[2][2], mvn[2][2];  // [scale | bias][h]
-    auto load_tile4 = [&](int tile, u32x2 (&kr)[2][2], uint32_t (&vr)[8], u32x4 (&mkr)[2][2], u32x4 (&mvr)[2][2]) {
-      const int p0 = tile * kTile;
-      for (int r = 0; r < 2; ++r) {
-        int p = p0 + krow0 + 4 * r;
-        p = p < L ? p : L - 1;
-        const uint8_t* row = Kb4 + (int64_t)p * sp4;
-        for (int i = 0; i < 2; ++i) kr[r][i] = __builtin_nontemporal_load((const u32x2*)(row + 32 * i + 8 * c));
+    // int4: the wave streams its tiles into a ring of kI4Slots LDS slots, two tiles ahead
+    // of the one in use, by LDS loads from buffer resources over this segment's code and
+    // parameter planes (the tile moves the scalar offset only). Every tile lies inside the
+    // capacity (a multiple of 32), so positions past L load stale rows: their codes are
+    // finite, their scores are masked and their V parameters zeroed before use.
+    const uint32_t rb4 = (uint32_t)(a.sp / 2);  // bytes per cache row of codes
+    const int64_t plane4 = ((int64_t)b * a.sb + (int64_t)kh * a.sh) / 2;
+    const u32x4 k_rs = rsrc_words((const uint8_t*)a.k + plane4, (uint32_t)a.cap * rb4);
+    const u32x4 v_rs = rsrc_words((const uint8_t*)a.v + plane4, (uint32_t)a.cap * rb4);
+    const uint32_t pbytes = (uint32_t)a.cap * 4u;
+    const u32x4 ks_rs = rsrc_words(a.ks + erow, pbytes);
+    const u32x4 kb_rs = rsrc_words(a.kb + erow, pbytes);
+    const u32x4 vs_rs = rsrc_words(a.vs + erow, pbytes);
+    const u32x4 vb_rs = rsrc_words(a.vb + erow, pbytes);
+    // K and V rows: load j, lane l moves bytes 16 (l % 4) .. +15 of row 16 j + l / 4
+    const uint32_t row_off = (uint32_t)(lane >> 2) * rb4 + 16u * (lane & 3);
+    uint8_t* const ring = &wave_lds[wave][0];
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_void*)ring;
+    auto i4_dma = [&](int tile, int slot) __attribute__((always_inline)) {
+      const uint32_t p0 = (uint32_t)tile * kTile;
+      const uint32_t dst = ring_lds + (uint32_t)slot * kI4Slot;
+      for (int j = 0; j < 2; ++j) {
+        dma16(k_rs, row_off, (p0 + 16 * j) * rb4, dst + kI4SlotK + 1024 * j);
+        dma16(v_rs, row_off, (p0 + 16 * j) * rb4, dst + kI4SlotV + 1024 * j);
       }
-      for (int kk = 0; kk < 8; ++kk) {
-        int p = p0 + 8 * c + kk;
-        p = p < L ? p : L - 1;
-        vr[kk] = __builtin_nontemporal_load((const uint32_t*)(Vb4 + (int64_t)p * sp4 + 4 * m));
+      if (lane < 8) {  // 8 lanes x 16 bytes: the words of the tile's 32 positions
+        dma16(ks_rs, 16u * lane, 4 * p0, dst + kI4SlotKs);
+        dma16(kb_rs, 16u * lane, 4 * p0, dst + kI4SlotKb);
+        dma16(vs_rs, 16u * lane, 4 * p0, dst + kI4SlotVs);
+        dma16(vb_rs, 16u * lane, 4 * p0, dst + kI4SlotVb);
       }
-      const int64_t pm = erow + p0 + 8 * c;
+    };
+    auto i4_read = [&](int slot, I4Tile& t) __attribute__((always_inline)) {
+      const uint8_t* const sp = ring + slot * kI4Slot;
+      for (int r = 0; r < 2; ++r)
+        for (int i = 0; i < 2; ++i) t.k[r][i] = *(const u32x2*)(sp + kI4SlotK + 64 * (krow0 + 4 * r) + 32 * i + 8 * c);
+      for (int kk = 0; kk < 8; ++kk) t.v[kk] = *(const uint32_t*)(sp + kI4SlotV + 64 * (8 * c + kk) + 4 * m);
       for (int h = 0; h < 2; ++h) {
-        mkr[0][h] = __builtin_nontemporal_load((const u32x4*)(a.ks + pm + 4 * h));
-        mkr[1][h] = __builtin_nontemporal_load((const u32x4*)(a.kb + pm + 4 * h));
-        mvr[0][h] = __builtin_nontemporal_load((const u32x4*)(a.vs + pm + 4 * h));
-        mvr[1][h] = __builtin_nontemporal_load((const u32x4*)(a.vb + pm + 4 * h));
+        t.ks[h] = *(const u32x4*)(sp + kI4SlotKs + 4 * (8 * c + 4 * h));
+        t.kb[h] = *(const uint32_t*)(sp + kI4SlotKb + 4 * (krow0 + 4 * h));
+        t.vs[h] = *(const u32x4*)(sp + kI4SlotVs + 4 * (8 * c + 4 * h));
+        t.vb[h] = *(const u32x4*)(sp + kI4SlotVb + 4 * (8 * c + 4 * h));
       }
     };
 
-    // q loads, then this wave's first tile loads, then the q work: the work below
-    // runs while the tile is in flight. B operand Q^T: step s <-> dims kdim(s, c) .. +7;
+    // q loads, then this wave's first tile loads, then the q work: the work below runs
+    // while the tiles are in flight. B operand Q^T: step s <-> dims kdim(s, c) .. +7;
     // columns g >= G are zero padding (their clamped, in-bounds loads are discarded).
     const int first = tile0 + wave;
     const int gc = g < a.G ? g : 0;
@@ -529,9 +605,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
     if (first < tile1) {
-      if (kI4) load_tile4(first, k4, v4, mk, mv);
-      else if (kFp8) load_tile8(first, k8, v8, ke, ve);
-      else load_tile(first, kc, vc);
+      if (kI4) {
+        // untracked by the compiler: its waits for the q loads above also wait for these,
+        // which are in flight alongside them (the fused step, whose q work waits on more
+        // loads, issues them after that work instead)
+        if (!kFused) {
+          i4_dma(first, 0);
+          if (first + kWaves < tile1) i4_dma(first + kWaves, 1);
+        }
+      } else if (kFp8) {
+        load_tile8(first, k8, v8, ke, ve);
+      } else {
+        load_tile(first, kc, vc);
+      }
     }
     bf16x8 qop[4];
     const float2* const cs_tab = rope_cs[wave];
@@ -669,9 +755,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
 
-    // int4: sums of the (bf16) q over each 64-dim group, per column g; the per-column
-    // output corrections (bias and code offset) of the two dim groups
-    float qs0 = 0.f, qs1 = 0.f, cor0 = 0.f, cor1 = 0.f;
+    if (kI4 && kFused && first < tile1) {
+      i4_dma(first, 0);
+      if (first + kWaves < tile1) i4_dma(first + kWaves, 1);
+    }
+    // int4: sums Qs of the (bf16) q over each 64-dim group, per column g. The score MFMAs
+    // of a group start from -128 Qs (the offset of the 128 + code operands), and one more
+    // MFMA per row set adds b0 Qs0 + b1 Qs1 (k-slots 0..3 of lane group 0: Qs split into
+    // bf16 hi and lo parts times the row's bias pair). The output corrections
+    // sum_p (P b_grp - 128 P'_grp) accumulate in cb[grp] by two MFMAs per group and tile;
+    // every row of cb[grp] holds the column's value.
+    float qs0 = 0.f, qs1 = 0.f;
+    f32x4 cb[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    u32x4 qbias = {0u, 0u, 0u, 0u};
     if (kI4) {
       for (int s = 0; s < 4; ++s) {
         const u32x4 w = __builtin_bit_cast(u32x4, qop[s]);
@@ -684,44 +780,154 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       qs0 += __shfl_xor(qs0, 32, 64);
       qs1 += __shfl_xor(qs1, 16, 64);
       qs1 += __shfl_xor(qs1, 32, 64);
+      if (c == 0) {
+        const uint32_t h0 = f32_to_bf16_bits(qs0), h1 = f32_to_bf16_bits(qs1);
+        qbias[0] = h0 | (f32_to_bf16_bits(qs0 - bf16_lo(h0)) << 16);
+        qbias[1] = h1 | (f32_to_bf16_bits(qs1 - bf16_lo(h1)) << 16);
+      }
     }
+    const f32x4 ainit0 = {-128.f * qs0, -128.f * qs0, -128.f * qs0, -128.f * qs0};
+    const f32x4 ainit1 = {-128.f * qs1, -128.f * qs1, -128.f * qs1, -128.f * qs1};
+    const u32x4 neg128 = {0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u};  // bf16 -128
     // int4 V: lane m and lane m ^ 8 swap half words, so that nibble j of a lane's word is
     // dim 64 (j / 4) + 8 (m % 8) + 4 (m / 8) + j % 4 and the first four nibbles are group 0
     const uint32_t vsel = m < 8 ? 0x05040100u : 0x03020706u;
 
+    // int4 scores of tile `tile` from registers t into x (position p0 + 8c + k <-> x[k]);
+    // in a segment's last tile, positions past L (stale rows) are masked and their V
+    // parameters (possibly not finite) zeroed.
+    auto i4_scores = [&](I4Tile& t, int tile, float* x) __attribute__((always_inline)) {
+      const int p0 = tile * kTile;
+      if (kFused && owner && tile == w_tile) {
+        // the stored form of row w (LDS), into the registers that loaded it
+        const uint32_t* nw = (const uint32_t*)&new_kv[0][0];
+        for (int r = 0; r < 2; ++r)
+          if (p0 + krow0 + 4 * r == w_row) {
+            for (int i = 0; i < 2; ++i) t.k[r][i] = u32x2{nw[8 * i + 2 * c], nw[8 * i + 2 * c + 1]};
+            t.kb[r] = nw[33];
+          }
+        for (int kk = 0; kk < 8; ++kk)
+          if (p0 + 8 * c + kk == w_row) t.v[kk] = nw[16 + m];
+        for (int h = 0; h < 2; ++h)
+          for (int e = 0; e < 4; ++e)
+            if (p0 + 8 * c + 4 * h + e == w_row) {
+              t.ks[h][e] = nw[32];
+              t.vs[h][e] = nw[34];
+              t.vb[h][e] = nw[35];
+            }
+      }
+      // C row 4c + i of set r is position p0 + 8c + 4r + i
+      for (int r = 0; r < 2; ++r) {
+        f32x4 acc0 = ainit0, acc1 = ainit1;
+        acc0 = mfma16(i4_kop(t.k[r][0][0]), qop[0], acc0);
+        acc0 = mfma16(i4_kop(t.k[r][0][1]), qop[1], acc0);
+        acc1 = mfma16(i4_kop(t.k[r][1][0]), qop[2], acc1);
+        acc1 = mfma16(i4_kop(t.k[r][1][1]), qop[3], acc1);
+        u32x4 ab;
+        ab[0] = __builtin_amdgcn_perm(t.kb[r], t.kb[r], 0x01000100u);  // (b0, b0)
+        ab[1] = __builtin_amdgcn_perm(t.kb[r], t.kb[r], 0x03020302u);  // (b1, b1)
+        ab[2] = ab[0];
+        ab[3] = ab[1];
+        const f32x4 accb = mfma16(as_bf16x8(ab), as_bf16x8(qbias), f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int i = 0; i < 4; ++i)
+          x[4 * r + i] = __builtin_fmaf(bf16_lo(t.ks[r][i]), acc0[i], __builtin_fmaf(bf16_hi(t.ks[r][i]), acc1[i], accb[i]));
+      }
+      if (p0 + kTile > L)
+        for (int k = 0; k < 8; ++k)
+          if (p0 + 8 * c + k >= L) {
+            x[k] = -INFINITY;
+            t.vs[k >> 2][k & 3] = 0u;
+            t.vb[k >> 2][k & 3] = 0u;
+          }
+    };
+    // int4 PV of one tile: probabilities x (position p0 + 8c + k <-> x[k]) against the
+    // codes and parameters in t
+    auto i4_pv = [&](const I4Tile& t, const float* x) __attribute__((always_inline)) {
+      uint32_t cw[8];
+      for (int kk = 0; kk < 8; ++kk) {
+        const uint32_t pw = (uint32_t)__builtin_amdgcn_mov_dpp((int)t.v[kk], 0x128, 0xF, 0xF, false);  // row_ror:8
+        cw[kk] = __builtin_amdgcn_perm(pw, t.v[kk], vsel);
+      }
+      // B operands P'_grp = bf16(P s_grp) and bf16(P), A operands of the bias rows; k = 2e,
+      // 2e + 1 <-> positions p0 + 8c + 2e, +1
+      u32x4 pw0, pw1, pb, ab0, ab1;
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t s_lo = t.vs[e >> 1][2 * (e & 1)], s_hi = t.vs[e >> 1][2 * (e & 1) + 1];
+        const uint32_t b_lo = t.vb[e >> 1][2 * (e & 1)], b_hi = t.vb[e >> 1][2 * (e & 1) + 1];
+        pw0[e] = pack_bf16x2(x[2 * e] * bf16_lo(s_lo), x[2 * e + 1] * bf16_lo(s_hi));
+        pw1[e] = pack_bf16x2(x[2 * e] * bf16_hi(s_lo), x[2 * e + 1] * bf16_hi(s_hi));
+        pb[e] = pack_bf16x2(x[2 * e], x[2 * e + 1]);
+        ab0[e] = __builtin_amdgcn_perm(b_hi, b_lo, 0x05040100u);  // (b0 of 2e, b0 of 2e + 1)
+        ab1[e] = __builtin_amdgcn_perm(b_hi, b_lo, 0x07060302u);  // (b1 of 2e, b1 of 2e + 1)
+      }
+      const bf16x8 pop0 = as_bf16x8(pw0), pop1 = as_bf16x8(pw1);
+      cb[0] = mfma16(as_bf16x8(ab0), as_bf16x8(pb), cb[0]);
+      cb[0] = mfma16(as_bf16x8(neg128), pop0, cb[0]);
+      cb[1] = mfma16(as_bf16x8(ab1), as_bf16x8(pb), cb[1]);
+      cb[1] = mfma16(as_bf16x8(neg128), pop1, cb[1]);
+      // A operand of dim slot j: row m, k-slots (2tt, 2tt + 1) = nibble j of the words of
+      // positions p0 + 8c + 2tt, +1 (byte j / 2 of both gathered by one v_perm)
+      for (int bb = 0; bb < 4; ++bb) {
+        u32x4 a0, a1;
+        for (int tt = 0; tt < 4; ++tt) {
+          const uint32_t w2 = __builtin_amdgcn_perm(cw[2 * tt + 1], cw[2 * tt], 0x0C000C00u | (uint32_t)bb | ((4u + bb) << 16));
+          a0[tt] = and_or(w2, 0x000F000Fu, 0x43004300u);
+          a1[tt] = and_or(w2 >> 4, 0x000F000Fu, 0x43004300u);
+        }
+        o[2 * bb] = mfma16(as_bf16x8(a0), bb < 2 ? pop0 : pop1, o[2 * bb]);
+        o[2 * bb + 1] = mfma16(as_bf16x8(a1), bb < 2 ? pop0 : pop1, o[2 * bb + 1]);
+      }
+    };
+
+    if constexpr (kI4) {
+      // slot si holds this tile; the tile two ahead goes into the slot read last
+      int si = 0;
+      for (int tile = first; tile < tile1; tile += kWaves) {
+        if (tile + 2 * kWaves < tile1) {
+          i4_dma(tile + 2 * kWaves, si == 0 ? 2 : si - 1);
+          wait_vm<16>();  // this tile's 8 loads have landed, the 16 after them may not
+        } else if (tile + kWaves < tile1) {
+          wait_vm<8>();
+        } else {
+          wait_vm<0>();
+        }
+        I4Tile t;
+        i4_read(si, t);
+        float x[8];
+        i4_scores(t, tile, x);
+        float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+        mx = max_over_rows(mx);
+        const float m_new = fmaxf(m_run, mx * a.qk_scale);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        const bool grew = __any(m_new > m_run);
+        float psum = 0.f;
+        for (int e = 0; e < 8; ++e) {
+          x[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a.qk_scale, -m_new));
+          psum += x[e];
+        }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (grew) {
+          // rescale only when some column's maximum grew (alpha is exactly 1 elsewhere)
+          for (int j = 0; j < 8; ++j) o[j] *= alpha;
+          cb[0] *= alpha;
+          cb[1] *= alpha;
+        }
+        i4_pv(t, x);
+        si = si == 2 ? 0 : si + 1;
+      }
+    }
+    if constexpr (!kI4)
     for (int tile = first; tile < tile1; tile += kWaves) {
       const bool more = tile + kWaves < tile1;
-      if (kI4) {
-        if (more) load_tile4(tile + kWaves, k4n, v4n, mkn, mvn);
-      } else if (kFp8) {
+      if (kFp8) {
         if (more) load_tile8(tile + kWaves, k8n, v8n, ken, ven);
         decode_tile8();
       } else if (more) {
         load_tile(tile + kWaves, kn, vn);
       }
       const int p0 = tile * kTile;
-      if (kI4 && kFused && owner && tile == w_tile) {
-        // the stored form of row w (LDS), into the registers that loaded it
-        const uint32_t* nw = (const uint32_t*)&new_kv[0][0];
-        for (int r = 0; r < 2; ++r) {
-          const int p = p0 + krow0 + 4 * r;
-          if ((p < L ? p : L - 1) == w_row)
-            for (int i = 0; i < 2; ++i) k4[r][i] = u32x2{nw[8 * i + 2 * c], nw[8 * i + 2 * c + 1]};
-        }
-        for (int kk = 0; kk < 8; ++kk) {
-          const int p = p0 + 8 * c + kk;
-          if ((p < L ? p : L - 1) == w_row) v4[kk] = nw[16 + m];
-        }
-        for (int h = 0; h < 2; ++h)
-          for (int e = 0; e < 4; ++e)
-            if (p0 + 8 * c + 4 * h + e == w_row) {
-              mk[0][h][e] = nw[32];
-              mk[1][h][e] = nw[33];
-              mv[0][h][e] = nw[34];
-              mv[1][h][e] = nw[35];
-            }
-      }
-      if (!kI4 && kFused && owner && tile == w_tile) {
+      if (kFused && owner && tile == w_tile) {
         // rows whose (clamped) load position is w
         for (int r = 0; r < 2; ++r) {
           const int p = p0 + krow0 + 4 * r;
@@ -735,26 +941,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
 
       f32x4 sc[2];
-      if (kI4) {
-        for (int r = 0; r < 2; ++r) {
-          f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-          acc0 = mfma16(i4_kop(k4[r][0][0]), qop[0], acc0);
-          acc0 = mfma16(i4_kop(k4[r][0][1]), qop[1], acc0);
-          acc1 = mfma16(i4_kop(k4[r][1][0]), qop[2], acc1);
-          acc1 = mfma16(i4_kop(k4[r][1][1]), qop[3], acc1);
-          // C row 4c + i of set r is position p0 + 8c + 4r + i: meta word [r][i]
-          for (int i = 0; i < 4; ++i) {
-            const float s0 = bf16_lo(mk[0][r][i]), s1 = bf16_hi(mk[0][r][i]);
-            const float b0 = bf16_lo(mk[1][r][i]), b1 = bf16_hi(mk[1][r][i]);
-            sc[r][i] = s0 * acc0[i] + s1 * acc1[i] + (b0 - 128.f * s0) * qs0 + (b1 - 128.f * s1) * qs1;
-          }
-        }
-      } else {
-        for (int r = 0; r < 2; ++r) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          for (int s = 0; s < 4; ++s) acc = mfma16(as_bf16x8(kc[r][s]), qop[s], acc);
-          sc[r] = acc;
-        }
+      for (int r = 0; r < 2; ++r) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 4; ++s) acc = mfma16(as_bf16x8(kc[r][s]), qop[s], acc);
+        sc[r] = acc;
       }
       // running max on raw scores (scale > 0), exponent as one fma
       float x[8];
@@ -766,11 +956,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           x[4 * r + i] = v;
           mx = fmaxf(mx, v);
         }
-      mx = wave_max_xor(mx, 16);
-      mx = wave_max_xor(mx, 32);
+      mx = max_over_rows(mx);
       const float m_new = fmaxf(m_run, mx * a.qk_scale);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      const float m_run_prev = m_run;
       float psum = 0.f;
       for (int e = 0; e < 8; ++e) {
         x[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a.qk_scale, -m_new));
@@ -778,77 +966,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       l_run = l_run * alpha + psum;
       m_run = m_new;
-      if (!kI4) {
-        for (int j = 0; j < 8; ++j) o[j] *= alpha;
-      } else if (__any(m_new > m_run_prev)) {
-        // int4 is VALU-bound: rescale only when some column's maximum grew (alpha is
-        // exactly 1 elsewhere)
-        for (int j = 0; j < 8; ++j) o[j] *= alpha;
-        cor0 *= alpha;
-        cor1 *= alpha;
-      }
-
-      if (kI4) {
-        uint32_t cw[8];
-        for (int kk = 0; kk < 8; ++kk) {
-          const uint32_t pw = (uint32_t)__builtin_amdgcn_mov_dpp((int)v4[kk], 0x128, 0xF, 0xF, false);  // row_ror:8
-          cw[kk] = __builtin_amdgcn_perm(pw, v4[kk], vsel);
-        }
-        // B operands P'_grp = bf16(P s_grp), k = 4h + e <-> position p0 + 8c + k; in the
-        // segment's last tile the parameters of positions past L (stale, possibly not
-        // finite) are zeroed first
-        if (p0 + kTile > L)
-          for (int k = 0; k < 8; ++k)
-            if (p0 + 8 * c + k >= L) {
-              mv[0][k >> 2][k & 3] = 0u;
-              mv[1][k >> 2][k & 3] = 0u;
-            }
-        float pv0[8], pv1[8];
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t sw = mv[0][k >> 2][k & 3];
-          const uint32_t bw = mv[1][k >> 2][k & 3];
-          pv0[k] = x[k] * bf16_lo(sw);
-          pv1[k] = x[k] * bf16_hi(sw);
-          cor0 += x[k] * bf16_lo(bw);
-          cor1 += x[k] * bf16_hi(bw);
-        }
-        // the offset's share uses the rounded operands themselves: sum of each bf16 pair
-        // by a dot product with (1, 1)
-        u32x4 pw0, pw1;
-        float t0 = 0.f, t1 = 0.f;
-        for (int e = 0; e < 4; ++e) {
-          pw0[e] = pack_bf16x2(pv0[2 * e], pv0[2 * e + 1]);
-          pw1[e] = pack_bf16x2(pv1[2 * e], pv1[2 * e + 1]);
-          t0 = dot2_bf16(pw0[e], 0x3F803F80u, t0);
-          t1 = dot2_bf16(pw1[e], 0x3F803F80u, t1);
-        }
-        cor0 = __builtin_fmaf(-128.f, t0, cor0);
-        cor1 = __builtin_fmaf(-128.f, t1, cor1);
-        const bf16x8 pop0 = as_bf16x8(pw0), pop1 = as_bf16x8(pw1);
-        // A operand of dim slot j: row m, k-slots (2tt, 2tt + 1) = nibble j of the words of
-        // positions p0 + 8c + 2tt, +1 (byte j / 2 of both gathered by one v_perm)
-        for (int bb = 0; bb < 4; ++bb) {
-          u32x4 a0, a1;
-          for (int tt = 0; tt < 4; ++tt) {
-            const uint32_t t = __builtin_amdgcn_perm(cw[2 * tt + 1], cw[2 * tt], 0x0C000C00u | (uint32_t)bb | ((4u + bb) << 16));
-            a0[tt] = and_or(t, 0x000F000Fu, 0x43004300u);
-            a1[tt] = and_or(t >> 4, 0x000F000Fu, 0x43004300u);
-          }
-          o[2 * bb] = mfma16(as_bf16x8(a0), bb < 2 ? pop0 : pop1, o[2 * bb]);
-          o[2 * bb + 1] = mfma16(as_bf16x8(a1), bb < 2 ? pop0 : pop1, o[2 * bb + 1]);
-        }
-        if (more) {
-          for (int r = 0; r < 2; ++r)
-            for (int i = 0; i < 2; ++i) k4[r][i] = k4n[r][i];
-          for (int kk = 0; kk < 8; ++kk) v4[kk] = v4n[kk];
-          for (int h = 0; h < 2; ++h)
-            for (int q = 0; q < 2; ++q) {
-              mk[q][h] = mkn[q][h];
-              mv[q][h] = mvn[q][h];
-            }
-        }
-        continue;
-      }
+      for (int j = 0; j < 8; ++j) o[j] *= alpha;
 
       // P^T B operand: k = 4r + i <-> position p0 + 8c + k
       u32x4 pw;
@@ -896,18 +1014,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (kI4) {
       // add the corrections of the column; row 4c + i of slot j is dim
       // 64 (j / 4) + 32 (c % 2) + 8i + 4 (c / 2) + j % 4
-      cor0 += __shfl_xor(cor0, 16, 64);
-      cor0 += __shfl_xor(cor0, 32, 64);
-      cor1 += __shfl_xor(cor1, 16, 64);
-      cor1 += __shfl_xor(cor1, 32, 64);
+      const float cor0 = cb[0][0], cor1 = cb[1][0];
       for (int i = 0; i < 4; ++i) {
-        float* dst = &cmb.o[wave][g][32 * (c & 1) + 8 * i + 4 * (c >> 1)];
+        float* dst = (float*)&wave_lds[wave][0] + g * kD + 32 * (c & 1) + 8 * i + 4 * (c >> 1);
         *(f32x4*)dst = f32x4{o[0][i] + cor0, o[1][i] + cor0, o[2][i] + cor0, o[3][i] + cor0};
         *(f32x4*)(dst + 64) = f32x4{o[4][i] + cor1, o[5][i] + cor1, o[6][i] + cor1, o[7][i] + cor1};
       }
     } else {
       for (int i = 0; i < 4; ++i) {
-        float* dst = &cmb.o[wave][g][32 * c + 8 * i];
+        float* dst = (float*)&wave_lds[wave][0] + g * kD + 32 * c + 8 * i;
         *(f32x4*)dst = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
         *(f32x4*)(dst + 4) = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
       }
@@ -926,7 +1041,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int ww = 0; ww < kWaves; ++ww) {
         const float sc = __builtin_amdgcn_exp2f(cmb.m[ww][gg] - M);  // idle waves: m = -inf -> 0
         Lsum += sc * cmb.l[ww][gg];
-        acc += sc * cmb.o[ww][gg][d];
+        acc += sc * ((const float*)&wave_lds[ww][0])[gg * kD + d];
       }
       if (single) {
         a.out[((int64_t)b * a.Hq + (int64_t)kh * a.G + gg) * kD + d] = (uint16_t)f32_to_bf16_bits(acc / Lsum);
