@@ -11,6 +11,12 @@
 // weight row n (lowest bits first), s and b the per-group scale and bias, all of x, s,
 // b and y in one activation type (bf16 or f16).
 //
+// Two regimes, as in MLX, whose quantized matmul takes vector kernels for a few rows of x
+// and, for many, kernels that dequantise weight tiles into the activation type first:
+// - up to 32 rows (and the streaming fallback): exact products, below;
+// - more than 32 rows with K a multiple of 64: qgemm_dq_kernel, on weights dequantised
+//   into bf16 / f16 (one rounding each) in LDS.
+//
 // Exact products. The MFMA's B operand is not the dequantised weight (which would have to
 // be rounded to bf16) but C + q, with the field's bits dropped into the mantissa of the
 // constant C (bf16 2^7 or f16 2^10: one and-or per pair of weights), which is exact; an
@@ -29,9 +35,9 @@
 // N / 16 workgroups, so a decode-sized projection (M <= 32) spreads over the whole chip
 // and streams every weight once; each lane keeps up to 8 groups of loads in flight,
 // issued in the order they are consumed (vmcnt counts in order), and a wave's groups
-// past its range read zeros out of bounds instead of branching. For larger M the row
-// tiles of one weight tile are dispatched together on one XCD, so its L2 serves the
-// re-reads.
+// past its range read zeros out of bounds instead of branching. For larger M (when the
+// dequantising GEMM does not apply) the row tiles of one weight tile are dispatched
+// together on one XCD, so its L2 serves the re-reads.
 #include "ema_common.hpp"
 
 namespace ema {
@@ -746,205 +752,217 @@ int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, const QmvPlan&
   }
 }
 
-// ---------------------------------------------------------------- tiled GEMM (M > 32)
-// A workgroup of eight waves computes a 128 x 128 tile of y (128 rows of x, 128 weight
-// rows); wave (wm, wn) = (wave & 1, wave >> 1) owns rows 64 wm .. + 64 (four 16-row tiles)
-// and columns 32 wn .. + 32 (two 16-column tiles), so each unpacked B operand serves four
-// row tiles and each x tile in LDS four column waves. K is walked in chunks of KC (64, or
-// 128 for group 128) through a ring of NB = 2 LDS buffers filled by LDS-DMA, chunk c + 1
-// issued as chunk c starts (into the buffer chunk c - 1 freed); all scales and biases of
-// the 128 rows are staged first. Products are exact as in qmv_kernel (C + q in the
-// mantissa, per-group f32 epilogue). LDS layout in 16-byte units:
-//   x        row block rb = row / 8 (16, padded by 128 bytes), unit u of the chunk, row % 8
-//   weights  unit u of the chunk, then row (128): (u, row) <- row, chunk bytes [16 u, +16)
-//   scales   (g / 8, row) <- row, groups [g, g + 8); biases likewise
-struct QgemmPlan {
-  int KC, NC, NB;
-  uint32_t x_rb;               // one x row block plus padding
-  uint32_t buf;                // bytes of one buffer (x then weights)
-  uint32_t w_off;              // weights within a buffer
-  uint32_t nX, nW, nS;         // DMA instructions per chunk (x, weights) and for the scales
-  uint32_t s_off, b_off, bytes;
-  int ntiles;                  // 128-column tiles
-  int remap;
+// ---------------------------------------------------------------- dequantising GEMM (M > 32)
+// MLX's quantized matmul for many rows (its qmm kernels) dequantises each weight tile into
+// the activation type in threadgroup memory and multiplies that. Here likewise: a workgroup
+// of eight waves owns a 256 x 128 tile of y (256 rows of x, 128 weight rows) and walks K in
+// chunks of 64. Per chunk, x arrives in LDS by LDS-DMA, and every thread dequantises 16
+// weights of one weight row, w = round(fma(s, q, b)) in f32 then to bf16 / f16 (the
+// rounding of MLX's dequantise, parity unpinned as to one rounding or two), into LDS; then
+// wave (wm, wn) = (wave % 4, wave / 4) multiplies its 64 x 64 block as 4 x 4 16x16x32
+// MFMA tiles, two k-steps per chunk. Two LDS buffers: the next chunk's x and weights are
+// staged while this chunk is multiplied, one barrier per chunk.
+// LDS per buffer: x rows (128 bytes of a chunk each), then weight rows; the 16-byte units of
+// a row are swizzled, unit u at u ^ ((row >> 1) & 7), so that the 16 rows an MFMA operand
+// read touches at one unit land on 16 different bank groups (rows are 128 bytes: two per
+// 256-byte bank cycle).
+// Workgroup order: with the tile grid split into eight regions of whole rows and columns
+// of tiles, consecutive workgroups (which the dispatcher spreads over the eight XCDs) take
+// the same place in different regions, so each XCD works through one region and its L2
+// holds that region's x rows and weight rows.
+constexpr int kDqBM = 256, kDqBN = 128, kDqKC = 64, kDqWaves = 8;
+constexpr uint32_t kDqXBytes = kDqBM * 128, kDqBuf = kDqXBytes + kDqBN * 128;
+constexpr uint32_t kDqLds = 2 * kDqBuf;  // 96 KB: one workgroup per CU
+
+struct DqPlan {
+  int mtiles, ntiles;
+  int rm, rn;  // tile rows / columns per region (regions: mtiles / rm x ntiles / rn = 8), or 0
 };
 
-constexpr int kGemmWaves = 8;
-constexpr int kGemmBN = 128;
+// byte I of x as f32 (v_cvt_f32_ubyteI)
+template <int I>
+__device__ __forceinline__ float ubyte_f32(uint32_t x) { return (float)((x >> (8 * I)) & 0xFFu); }
+__device__ __forceinline__ uint32_t dq_unit(uint32_t row, uint32_t u) { return row * 8 + (u ^ ((row >> 1) & 7)); }
 
 template <int BITS, int GS, bool F16>
-__global__ __launch_bounds__(64 * kGemmWaves) void qgemm_kernel(QmmArgs a, QgemmPlan p) {
-  using F = Fields<BITS, F16>;
-  constexpr int kSteps = GS / 32;
-  constexpr int kWDw = GS * BITS / 128;
-  constexpr uint32_t kWBytes = GS * BITS / 8;
+__global__ __launch_bounds__(64 * kDqWaves) void qgemm_dq_kernel(QmmArgs a, DqPlan p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
-
-  int tile = blockIdx.x;
-  if (p.remap) tile = (tile % 8) * (gridDim.x / 8) + tile / 8;
-  const int m0 = (tile / p.ntiles) * 128, n0 = (tile % p.ntiles) * kGemmBN;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rows_n = min(kGemmBN, a.N - n0), rows_m = min(128, a.M - m0);
-  const uint32_t wrow = (uint32_t)a.K * BITS / 8;
-  const uint32_t xrow = (uint32_t)a.ldx * 2;
-  const uint32_t G2 = (uint32_t)a.G * 2;
+  int mt, nt;
+  if (p.rm > 0) {
+    const int x8 = blockIdx.x % 8, l = blockIdx.x / 8;
+    const int rgm = p.mtiles / p.rm;  // regions along M
+    mt = (x8 % rgm) * p.rm + l % p.rm;
+    nt = (x8 / rgm) * p.rn + l / p.rm;
+  } else {
+    mt = blockIdx.x / p.ntiles;
+    nt = blockIdx.x % p.ntiles;
+  }
+  const int m0 = mt * kDqBM, n0 = nt * kDqBN;
+  const int rows_m = min(kDqBM, a.M - m0), rows_n = min(kDqBN, a.N - n0);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t xrow = (uint32_t)a.ldx * 2, wrow = (uint32_t)a.K * BITS / 8, G2 = (uint32_t)a.G * 2;
   const u32x4 X = rsrc4(a.x + (int64_t)m0 * xrow, (rows_m - 1) * xrow + (uint32_t)a.K * 2);
-  const u32x4 W = rsrc4(a.w + (int64_t)n0 * wrow, rows_n * wrow);
-  const u32x4 S = rsrc4(a.s + (int64_t)n0 * G2, rows_n * G2);
-  const u32x4 B = rsrc4(a.b + (int64_t)n0 * G2, rows_n * G2);
-  const uint32_t ux = (uint32_t)p.KC / 8;             // x units per row per chunk
-  const uint32_t uw = (uint32_t)p.KC * BITS / 128;    // weight units per row per chunk
+  const auto W = rsrc(a.w + (int64_t)n0 * wrow, rows_n * wrow);
+  const auto S = rsrc(a.s + (int64_t)n0 * G2, rows_n * G2);
+  const auto Bi = rsrc(a.b + (int64_t)n0 * G2, rows_n * G2);
 
-  auto mine = [&](uint32_t n) -> uint32_t {
-    return n > (uint32_t)wave ? (n - wave + kGemmWaves - 1) / kGemmWaves : 0;
-  };
-  const uint32_t per_chunk = mine(p.nX) + mine(p.nW);
-  auto issue = [&](int c) {
-    const uint32_t bb = lds0 + (uint32_t)(c % p.NB) * p.buf;
-    const uint32_t kb = (uint32_t)c * p.KC;
-    for (uint32_t i = wave; i < p.nX + p.nW; i += kGemmWaves) {
-      if (i < p.nX) {
-        // 64 units of one x row block: 8 units u of each of its 8 rows (8 ux is a multiple of 64)
-        const uint32_t rb = (64 * i) / (8 * ux), first = 64 * i - rb * 8 * ux, rem = first + lane;
-        const uint32_t row = rb * 8 + (rem & 7), u = rem >> 3;
-        dma16(X, row < (uint32_t)rows_m ? row * xrow + 2 * kb + 16 * u : kOffRow,
-              __builtin_amdgcn_readfirstlane(bb + rb * p.x_rb + 16 * first));
-      } else {
-        const uint32_t j = i - p.nX, q = 64 * j + lane, u = q / kGemmBN, row = q % kGemmBN;
-        dma16(W, row < (uint32_t)rows_n && u < uw ? row * wrow + kb * BITS / 8 + 16 * u : kOffRow,
-              __builtin_amdgcn_readfirstlane(bb + p.w_off + 1024 * j));
-      }
+  // x: 2048 units per chunk, four DMA instructions per wave; LDS unit U holds row U / 8,
+  // chunk unit (U % 8) ^ ((row >> 1) & 7)
+  auto issue_x = [&](int c, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t blk = 4 * wave + i, U = 64 * blk + lane, row = U >> 3, u = (U & 7) ^ ((row >> 1) & 7);
+      dma16(X, row < (uint32_t)rows_m ? row * xrow + (uint32_t)c * (2 * kDqKC) + 16 * u : kOffRow,
+            __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)buf * kDqBuf + 1024 * blk));
     }
   };
-  for (uint32_t i = wave; i < 2 * p.nS; i += kGemmWaves) {
-    const uint32_t jj = i % p.nS, q = 64 * jj + lane, g8 = q / kGemmBN, row = q % kGemmBN;
-    const bool ok = row < (uint32_t)rows_n && 8 * g8 < (uint32_t)a.G;
-    dma16(i < p.nS ? S : B, ok ? row * G2 + 16 * g8 : kOffRow,
-          __builtin_amdgcn_readfirstlane(lds0 + (i < p.nS ? p.s_off : p.b_off) + 1024 * jj));
-  }
-  const int pre = p.NB - 1 < p.NC ? p.NB - 1 : p.NC;
-  for (int c = 0; c < pre; ++c) issue(c);
+  // weights: thread t dequantises k 16 (t % 4) .. +15 of the chunk for weight row t / 4
+  constexpr int kWd = BITS / 2;  // words of 16 fields
+  const uint32_t wn_row = (uint32_t)tid >> 2, kp = (uint32_t)tid & 3;
+  const bool w_in = wn_row < (uint32_t)rows_n;
+  auto load_w = [&](int c, uint32_t (&wr)[kWd], uint32_t& sr, uint32_t& br) __attribute__((always_inline)) {
+    const uint32_t k0 = (uint32_t)c * kDqKC + 16 * kp;
+    const uint32_t wo = w_in ? wn_row * wrow + k0 * BITS / 8 : kOffRow;
+    if constexpr (kWd == 2) {
+      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(W, wo, 0, 0));
+      wr[0] = v[0];
+      wr[1] = v[1];
+    } else {
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, 0, 0));
+      for (int e = 0; e < 4; ++e) wr[e] = v[e];
+    }
+    const uint32_t so = w_in ? wn_row * G2 + 2 * (k0 / GS) : kOffRow;
+    sr = __builtin_amdgcn_raw_buffer_load_b16(S, so, 0, 0);
+    br = __builtin_amdgcn_raw_buffer_load_b16(Bi, so, 0, 0);
+  };
+  auto dq_w = [&](const uint32_t (&wr)[kWd], uint32_t sr, uint32_t br, int buf) __attribute__((always_inline)) {
+    const float sc = act_to_f32<F16>(sr), bc = act_to_f32<F16>(br);
+    float q[16];
+    if constexpr (BITS == 4) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t lo = wr[e] & 0x0F0F0F0Fu, hi = (wr[e] >> 4) & 0x0F0F0F0Fu;  // fields 2i, 2i + 1 as bytes
+        q[8 * e + 0] = ubyte_f32<0>(lo);
+        q[8 * e + 1] = ubyte_f32<0>(hi);
+        q[8 * e + 2] = ubyte_f32<1>(lo);
+        q[8 * e + 3] = ubyte_f32<1>(hi);
+        q[8 * e + 4] = ubyte_f32<2>(lo);
+        q[8 * e + 5] = ubyte_f32<2>(hi);
+        q[8 * e + 6] = ubyte_f32<3>(lo);
+        q[8 * e + 7] = ubyte_f32<3>(hi);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        q[4 * e + 0] = ubyte_f32<0>(wr[e]);
+        q[4 * e + 1] = ubyte_f32<1>(wr[e]);
+        q[4 * e + 2] = ubyte_f32<2>(wr[e]);
+        q[4 * e + 3] = ubyte_f32<3>(wr[e]);
+      }
+    }
+    u32x4 o0, o1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o0[e] = (uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[2 * e], bc)) |
+              ((uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[2 * e + 1], bc)) << 16);
+      o1[e] = (uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[8 + 2 * e], bc)) |
+              ((uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[8 + 2 * e + 1], bc)) << 16);
+    }
+    uint8_t* const wb = smem + (uint32_t)buf * kDqBuf + kDqXBytes;
+    *reinterpret_cast<u32x4*>(wb + 16 * dq_unit(wn_row, 2 * kp)) = o0;
+    *reinterpret_cast<u32x4*>(wb + 16 * dq_unit(wn_row, 2 * kp + 1)) = o1;
+  };
 
-  const int wm = wave & 1, wn = wave >> 1;
-  const int c16 = lane & 15, j = lane >> 4;
-  const u32x4 ones = {F::kOnes, F::kOnes, F::kOnes, F::kOnes};
-  f32x4 tot[4][2];
+  const int wm = wave & 3, wn = wave >> 2;
+  const uint32_t r16 = (uint32_t)lane & 15, j = (uint32_t)lane >> 4;
+  f32x4 acc[4][4];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) tot[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int GC = p.KC / GS;  // groups per chunk
+    for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int c = 0; c < p.NC; ++c) {
-    if (c + p.NB - 1 < p.NC) issue(c + p.NB - 1);  // its buffer held chunk c - 1
-    const int later = min(p.NB - 1, p.NC - 1 - c);
-    wait_vmcnt((uint32_t)later * per_chunk);
-    __syncthreads();
-    const uint8_t* xb = smem + (uint32_t)(c % p.NB) * p.buf;
-    const uint8_t* wb = xb + p.w_off;
-    for (int g = 0; g < GC; ++g) {
-      const int gg = c * GC + g;
-      float sc[2], bc[2];
-      uint32_t wd[2][kWDw];
+  const int NC = a.K / kDqKC;
+  uint32_t wr[kWd], sr, br;
+  issue_x(0, 0);
+  load_w(0, wr, sr, br);
+  dq_w(wr, sr, br, 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's x DMA has landed
+  __syncthreads();
+  for (int c = 0; c < NC; ++c) {
+    const int buf = c & 1;
+    const bool next = c + 1 < NC;
+    if (next) {
+      issue_x(c + 1, buf ^ 1);
+      load_w(c + 1, wr, sr, br);
+    }
+    const uint8_t* const xb = smem + (uint32_t)buf * kDqBuf;
+    const uint8_t* const wb = xb + kDqXBytes;
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int row = 32 * wn + 16 * ct + c16;
-        const uint32_t so = 16 * ((gg >> 3) * kGemmBN + row) + 2 * (gg & 7);
-        sc[ct] = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.s_off + so));
-        bc[ct] = act_to_f32<F16>(*reinterpret_cast<const uint16_t*>(smem + p.b_off + so)) - F::kOff * sc[ct];
-        const uint32_t bo = g * kWBytes + j * (kWBytes / 4);  // byte of the row within the chunk
+    for (int ks = 0; ks < 2; ++ks) {
+      const uint32_t u = 4 * ks + j;
+      u32x4 A[4], B[4];
 #pragma unroll
-        for (int e = 0; e < kWDw; ++e) {
-          const uint32_t be = bo + 4 * e;
-          wd[ct][e] = *reinterpret_cast<const uint32_t*>(wb + 16 * ((be >> 4) * kGemmBN + row) + (be & 15));
-        }
-      }
-      f32x4 aq[4][2], a1[4];
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        a1[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) aq[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) {
-        const u32x4 Bw0 = F::weights(wd[0], st), Bw1 = F::weights(wd[1], st);
-        const uint32_t u = (g * GS + j * (GS / 4) + 8 * st) >> 3;  // x unit of this step
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-          const int row = 64 * wm + 16 * rt + c16;
-          const u32x4 xv = *reinterpret_cast<const u32x4*>(xb + (row >> 3) * p.x_rb + 16 * (u * 8 + (row & 7)));
-          const uint32_t xd[4] = {xv[0], xv[1], xv[2], xv[3]};
-          const u32x4 A = F::acts(xd);
-          aq[rt][0] = mma<F16>(A, Bw0, aq[rt][0]);
-          aq[rt][1] = mma<F16>(A, Bw1, aq[rt][1]);
-          a1[rt] = mma<F16>(A, ones, a1[rt]);
-        }
+      for (int t = 0; t < 4; ++t) {
+        A[t] = *reinterpret_cast<const u32x4*>(xb + 16 * dq_unit(64 * wm + 16 * t + r16, u));
+        B[t] = *reinterpret_cast<const u32x4*>(wb + 16 * dq_unit(64 * wn + 16 * t + r16, u));
       }
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            tot[rt][ct][q] = fmaf(sc[ct], aq[rt][ct][q], fmaf(bc[ct], a1[rt][q], tot[rt][ct][q]));
+        for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = mma<F16>(A[rt], B[ct], acc[rt][ct]);
     }
-    __syncthreads();  // the buffer is refilled at the next turn
+    if (next) dq_w(wr, sr, br, buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
   }
 
+  // lane (r16, j) of tile (rt, ct) holds rows 4j .. 4j + 3 of column r16
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
+    for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int m = 64 * wm + 16 * rt + 4 * j + q, n = 32 * wn + 16 * ct + c16;
+        const int m = 64 * wm + 16 * rt + 4 * (int)j + q, n = 64 * wn + 16 * ct + (int)r16;
         if (m < rows_m && n < rows_n)
-          reinterpret_cast<uint16_t*>(a.y)[(int64_t)(m0 + m) * a.ldy + n0 + n] = f32_to_act<F16>(tot[rt][ct][q]);
+          reinterpret_cast<uint16_t*>(a.y)[(int64_t)(m0 + m) * a.ldy + n0 + n] = f32_to_act<F16>(acc[rt][ct][q]);
       }
 }
 
-// Plan of the tiled GEMM, or NC = 0 when it does not apply (K a multiple of the chunk,
-// K / gs a multiple of 8, everything within the LDS budget with at least two buffers).
-QgemmPlan plan_qgemm(int M, int N, int K, int gs, int bits) {
-  QgemmPlan p{};
-  p.NC = 0;
-  const int kc = gs > 64 ? gs : 64;
-  if (K % kc || (K / gs) % 8) return p;
-  const int G = K / gs;
-  p.KC = kc;
-  p.x_rb = (uint32_t)kc / 8 * 128 + 128;
-  p.nX = 16 * ((uint32_t)kc / 8) * 8 / 64;
-  const uint32_t uw = (uint32_t)kc * bits / 128;
-  p.nW = (uint32_t)kGemmBN * uw / 64;
-  p.w_off = 16 * p.x_rb;
-  p.buf = p.w_off + 1024 * p.nW;
-  p.nS = ((uint32_t)kGemmBN * (G / 8) + 63) / 64;
-  // two buffers: at most ~75 KB, so two workgroups (four waves per SIMD) share a CU,
-  // which hides the LDS and DMA latency better than a deeper ring at one workgroup
-  const int nb = 2;
-  p.NC = K / kc;
-  p.NB = nb < p.NC ? nb : (p.NC < 2 ? 2 : p.NC);
-  p.s_off = p.NB * p.buf;
-  p.b_off = p.s_off + 1024 * p.nS;
-  p.bytes = p.b_off + 1024 * p.nS;
-  p.ntiles = (N + kGemmBN - 1) / kGemmBN;
-  const int64_t tiles = (int64_t)p.ntiles * ((M + 127) / 128);
-  p.remap = tiles % 8 == 0;
-  if (p.bytes > kQmvMaxLds) p.NC = 0;
-  return p;
+// Plan of the dequantising GEMM: K a multiple of the chunk and of the group, x within one
+// buffer range per tile. Regions: 2 x 4, 4 x 2, 1 x 8 or 8 x 1 whole tile rows and columns,
+// the one with the least bytes per region, when the grid divides into them.
+bool plan_dq(int M, int N, int K, int gs, int bits, int64_t ldx, DqPlan* p) {
+  if (K % kDqKC || K % gs || (int64_t)kDqBM * ldx * 2 + (int64_t)K * 2 >= ((int64_t)1 << 31)) return false;
+  p->mtiles = (M + kDqBM - 1) / kDqBM;
+  p->ntiles = (N + kDqBN - 1) / kDqBN;
+  p->rm = p->rn = 0;
+  const double xb = (double)kDqBM * K * 2, wb = (double)kDqBN * K * (bits / 8.0 + 4.0 / gs);
+  double best = 0;
+  for (int gm = 1; gm <= 8; gm *= 2) {  // regions along M
+    const int gn = 8 / gm;
+    if (p->mtiles % gm || p->ntiles % gn) continue;
+    const int rm = p->mtiles / gm, rn = p->ntiles / gn;
+    const double bytes = rm * xb + rn * wb;
+    if (p->rm == 0 || bytes < best) {
+      best = bytes;
+      p->rm = rm;
+      p->rn = rn;
+    }
+  }
+  return true;
 }
 
 template <int BITS, int GS, bool F16>
-int32_t launch_qgemm(hipStream_t st, const QmmArgs& a, const QgemmPlan& p) {
+int32_t launch_dq(hipStream_t st, const QmmArgs& a, const DqPlan& p) {
   static std::atomic<uint64_t> lds_set{0};  // this instantiation's LDS above 64 KB, per device
-  const int32_t rc = allow_lds_once((const void*)qgemm_kernel<BITS, GS, F16>, kQmvMaxLds, &lds_set,
+  const int32_t rc = allow_lds_once((const void*)qgemm_dq_kernel<BITS, GS, F16>, kDqLds, &lds_set,
                                     "quantized_matmul: LDS attribute");
   if (rc) return rc;
-  const unsigned tiles = (unsigned)(p.ntiles * ((a.M + 127) / 128));
-  hipLaunchKernelGGL((qgemm_kernel<BITS, GS, F16>), dim3(tiles), dim3(64 * kGemmWaves), p.bytes, st, a, p);
+  hipLaunchKernelGGL((qgemm_dq_kernel<BITS, GS, F16>), dim3((unsigned)(p.mtiles * p.ntiles)), dim3(64 * kDqWaves),
+                     kDqLds, st, a, p);
   return check_hip(hipGetLastError(), "quantized_matmul launch");
 }
 
@@ -1109,8 +1127,8 @@ int32_t launch_t(hipStream_t st, QmmArgs a) {
     }
     if (p.NC > 0) return launch_qmv_rows<BITS, GS, F16>(st, a, mx, p);
   } else {
-    const QgemmPlan p = plan_qgemm(a.M, a.N, a.K, GS, BITS);
-    if (p.NC > 0) return launch_qgemm<BITS, GS, F16>(st, a, p);
+    DqPlan dp;
+    if (plan_dq(a.M, a.N, a.K, GS, BITS, a.ldx, &dp)) return launch_dq<BITS, GS, F16>(st, a, dp);
   }
   const int mr = a.M <= 16 ? 1 : 2;
   a.mtiles = (a.M + 16 * mr - 1) / (16 * mr);

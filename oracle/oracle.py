@@ -382,6 +382,26 @@ def dequantize(wq, scales, biases, gs: int, bits: int) -> np.ndarray:
     return out
 
 
+def dequantize_act(wq, scales, biases, gs: int, bits: int, dtype: str = "bf16") -> np.ndarray:
+    """The weights as MLX's quantized matmul for many rows of x (its qmm kernels) multiplies
+    them: dequantised into the activation type first. w = round_T(s * q + b) with s * q + b
+    formed in f32 (s * q is exact there, so the sum is rounded once, as by an fma) and one
+    round-to-nearest-even to T = bf16 / f16. Returns the f32 values [N, K]. Whether MLX
+    rounds once or twice (s * q, then + b, in T) is parity unpinned; this one-rounding
+    reading is the one the GPU's large-M path implements."""
+    wq = _c(np.asarray(wq), np.uint32)
+    N = wq.shape[0]
+    K = wq.shape[1] * 32 // bits
+    G = K // gs
+    q = dequantize(wq, np.ones((N, G), np.float32), np.zeros((N, G), np.float32), gs, bits).astype(np.float32)
+    s = np.repeat(np.asarray(scales, dtype=np.float32), gs, axis=1)
+    b = np.repeat(np.asarray(biases, dtype=np.float32), gs, axis=1)
+    w = (s * q).astype(np.float32) + b  # f32 ops: the product is exact, the sum rounds once
+    if dtype == "bf16":
+        return f32_from_bf16(bf16_from_f32(w))
+    return w.astype(np.float16).astype(np.float32)
+
+
 def qmatmul(x, wq, scales, biases, gs: int, bits: int) -> np.ndarray:
     """MLX quantized_matmul(x, w, scales, biases, transpose=true, gs, bits, "affine")
     (transform.rs:77-88; qmatmul, crates/ops/src/quant.rs:57-76) in float64: x [..., K]

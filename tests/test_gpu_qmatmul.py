@@ -2,9 +2,13 @@
 with transpose=true as called by crates/ops/src/quant.rs:57-76) against the oracle's f64
 restatement (oracle.qmatmul), through the C ABI.
 
-Bars. The kernel multiplies exactly and accumulates in f32, so every output is within
-one rounding of the exact sum: |y - ref| <= 2^-8 |ref| (bf16; 2^-10 for f16) plus
-4e-5 * sum_k |x_k w_k| for the f32 accumulation; at the Qwen3-8B decode shape also the
+Bars. For up to 32 rows of x the kernels multiply exactly and accumulate in f32, so every
+output is within one rounding of the exact sum: |y - ref| <= 2^-8 |ref| (bf16; 2^-10 for
+f16) plus 4e-5 * sum_k |x_k w_k| for the f32 accumulation. For more rows (K a multiple of
+64) the weights are dequantised into the activation type first, as MLX's qmm kernels do
+(oracle.dequantize_act), and the same bar holds against x times those weights; against the
+exact sum they add at most half an ulp of the type per weight (2^-8 sum |x w| for bf16;
+2^-11 for f16, plus 2^-25 sum |x| below f16's normal range); at the Qwen3-8B decode shape also the
 bf16 bar of the other parity tests (max-abs 2e-2, mean-abs 2e-3). Separate q, k and v
 calls into one q|k|v row (ldy > N) and the fused call are each within one rounding of the
 oracle, so within two of each other: the property the reference checks at 1e-3
@@ -47,11 +51,25 @@ def make(ora, seed, M, N, K, gs, bits, dtype="bf16", wstd=0.02):
     return d, (hx, wq, hs, hb)
 
 
+def dq_path(M, K):
+    """Whether ema_quantized_matmul takes the dequantising GEMM (more than 32 rows, K a
+    multiple of its 64-wide chunks)."""
+    return M > 32 and K % 64 == 0
+
+
 def check(ora, y, h, gs, bits, what, dtype="bf16", bar=False):
     hx, wq, hs, hb = h
-    ref = ora.qmatmul(hx, wq, hs, hb, gs, bits)
     W = ora.dequantize(wq, hs, hb, gs, bits)
     mag = np.abs(hx).astype(np.float64) @ np.abs(W).T
+    if dq_path(*hx.shape):
+        Wt = ora.dequantize_act(wq, hs, hb, gs, bits, dtype).astype(np.float64)
+        ref = hx.astype(np.float64) @ Wt.T
+        exact = ora.qmatmul(hx, wq, hs, hb, gs, bits)
+        half_ulp, floor = (2.0**-8, 0.0) if dtype == "bf16" else (2.0**-11, 2.0**-25)
+        xs = np.abs(hx).astype(np.float64).sum(axis=1, keepdims=True)
+        assert np.all(np.abs(ref - exact) <= (half_ulp * mag + floor * xs) * (1 + 1e-6)), f"{what}: dequantised weights"
+    else:
+        ref = ora.qmatmul(hx, wq, hs, hb, gs, bits)
     got = y.float().cpu().numpy().astype(np.float64)
     assert got.shape == ref.shape and np.all(np.isfinite(got)), what
     rel = 2.0**-8 if dtype == "bf16" else 2.0**-10
@@ -106,8 +124,11 @@ def test_qmatmul_8bit_wide_rows_x_in_registers(ema, ora, M, gs, dtype):
     (500, 70, 1024, 128, 8, "f16"),
     (96, 80, 512, 32, 8, "bf16"),
     (2048, 256, 2048, 64, 4, "bf16"),   # a prefill chunk's rows
-    (40, 48, 320, 32, 4, "bf16"),       # K / gs = 10: the streaming kernel
+    (40, 48, 320, 32, 4, "bf16"),       # K / gs = 10
     (70, 64, 320, 32, 8, "f16"),
+    (40, 48, 288, 32, 4, "bf16"),       # K not a multiple of 64: the streaming kernel
+    (70, 64, 288, 32, 8, "f16"),
+    (257, 129, 512, 32, 4, "f16"),      # ragged tiles in both directions
 ])
 def test_qmatmul_prefill_rows(ema, ora, M, N, K, gs, bits, dtype):
     say(f"qmatmul prefill rows M={M} N={N} K={K} gs={gs} bits={bits} {dtype}")
@@ -203,14 +224,15 @@ def test_qmatmul_strided_rows_and_determinism(ema, ora):
     check(ora, y1, h, gs, bits, "strided")
 
 
-def test_qmatmul_extreme_fields_and_groups(ema, ora):
+@pytest.mark.parametrize("M", [4, 64])
+def test_qmatmul_extreme_fields_and_groups(ema, ora, M):
     # all-zero and all-max fields, zero and negative scales, large biases: the C + q
-    # offset and the bias term cancel exactly
+    # offset and the bias term cancel exactly (4 rows); dequantised into bf16 (64 rows)
     import torch
 
-    M, N, K, gs = 4, 32, 512, 64
+    N, K, gs = 32, 512, 64
     for bits in (4, 8):
-        say(f"qmatmul extreme fields bits={bits}")
+        say(f"qmatmul extreme fields bits={bits} M={M}")
         rng = np.random.default_rng(bits)
         q = np.where(rng.random((N, K)) < 0.5, 0, (1 << bits) - 1).astype(np.uint32)
         wq = ora.pack_bits(q, bits)

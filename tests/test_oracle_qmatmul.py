@@ -124,3 +124,32 @@ def test_minmax_quantize_round_trip(bits):
     lo = w.reshape(N, K // gs, gs).min(-1)
     slack = np.repeat(s * (0.5 + ((1 << bits) - 1) * 2.0**-8) + np.abs(lo - b) + 1e-7, gs, axis=1)
     assert np.all(np.abs(W - w) <= slack)
+
+
+def test_dequantize_act_rounds_each_weight_once_to_nearest_even():
+    # the large-M weights: round_T(s q + b). Pinned against torch's own bf16 / f16 rounding
+    # of the exact value (exact in f64 for bf16 s and b and fields below 256), ties to even
+    # at hand-built halfway points, and exactness where the value is representable
+    import torch
+
+    rng = np.random.default_rng(7)
+    for bits in (4, 8):
+        N, K, gs = 6, 128, 32
+        q, wq, s, b = _rand_q(rng, N, K, gs, bits)
+        exact = oracle.dequantize(wq, s, b, gs, bits)  # f64, exact here
+        for dtype, td in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+            got = oracle.dequantize_act(wq, s, b, gs, bits, dtype)
+            want = torch.from_numpy(exact.astype(np.float32)).to(td).float().numpy()
+            assert np.array_equal(got, want), (bits, dtype)
+    one = np.ones((1, 1), np.float32)
+    # 1 + 2^-8 is halfway between bf16 1 and 1 + 2^-7: even is 1; 1 + 3 2^-8 rounds up to
+    # 1 + 2^-6; f16 (10 fraction bits) keeps both
+    w = oracle.pack_bits(np.array([[1, 3] + [0] * 30], np.uint32), 4)
+    s = np.full((1, 1), 2.0**-8, np.float32)
+    assert oracle.dequantize_act(w, s, one, 32, 4, "bf16")[0, :2].tolist() == [1.0, 1.0 + 2.0**-6]
+    assert oracle.dequantize_act(w, s, one, 32, 4, "f16")[0, :2].tolist() == [1.0 + 2.0**-8, 1.0 + 3 * 2.0**-8]
+    # representable values pass unchanged
+    q = np.arange(16, dtype=np.uint32)[None, :].repeat(2, axis=1)
+    w = oracle.pack_bits(q, 4)
+    got = oracle.dequantize_act(w, np.full((1, 1), 0.5, np.float32), np.full((1, 1), -3.0, np.float32), 32, 4)
+    assert got[0].tolist() == (0.5 * q[0] - 3.0).tolist()
