@@ -755,13 +755,18 @@ int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, const QmvPlan&
 // ---------------------------------------------------------------- dequantising GEMM (M > 32)
 // MLX's quantized matmul for many rows (its qmm kernels) dequantises each weight tile into
 // the activation type in threadgroup memory and multiplies that. Here likewise: a workgroup
-// of eight waves owns a 256 x 128 tile of y (256 rows of x, 128 weight rows) and walks K in
-// chunks of 64. Per chunk, x arrives in LDS by LDS-DMA, and every thread dequantises 16
-// weights of one weight row, w = round(fma(s, q, b)) in f32 then to bf16 / f16 (the
-// rounding of MLX's dequantise, parity unpinned as to one rounding or two), into LDS; then
-// wave (wm, wn) = (wave % 4, wave / 4) multiplies its 64 x 64 block as 4 x 4 16x16x32
-// MFMA tiles, two k-steps per chunk. Two LDS buffers: the next chunk's x and weights are
-// staged while this chunk is multiplied, one barrier per chunk.
+// owns a 256 x 128 tile of y (256 rows of x, 128 weight rows) and walks K in chunks of 64,
+// with two roles:
+// - eight compute waves, wave (wm, wn) = (wave % 4, wave / 4) multiplying its 64 x 64 block
+//   as 4 x 4 16x16x32 MFMA tiles, two k-steps per chunk, from LDS only;
+// - eight loader waves, which load each chunk's x, packed weights, scales and biases three
+//   chunks ahead into registers (three sets in turn), then write x into LDS and dequantise
+//   the weights into it, w = round(fma(s, q, b)) in f32 then to bf16 / f16 (the rounding
+//   of MLX's dequantise, parity unpinned as to one rounding or two).
+// Two LDS buffers: the loaders fill chunk c + 1's while the compute waves multiply chunk
+// c's, one barrier per chunk. The loaders issue every load on every path (a chunk past the
+// end loads at offsets past the ranges: zeros, no memory access), so the compiler's waits
+// count exactly the chunk they need.
 // LDS per buffer: x rows (128 bytes of a chunk each), then weight rows; the 16-byte units of
 // a row are swizzled, unit u at u ^ ((row >> 1) & 7), so that the 16 rows an MFMA operand
 // read touches at one unit land on 16 different bank groups (rows are 128 bytes: two per
@@ -770,7 +775,7 @@ int32_t launch_qmv_rows(hipStream_t st, const QmmArgs& a, int mx, const QmvPlan&
 // of tiles, consecutive workgroups (which the dispatcher spreads over the eight XCDs) take
 // the same place in different regions, so each XCD works through one region and its L2
 // holds that region's x rows and weight rows.
-constexpr int kDqBM = 256, kDqBN = 128, kDqKC = 64, kDqWaves = 8;
+constexpr int kDqBM = 256, kDqBN = 128, kDqKC = 64, kDqCompute = 8, kDqLoaders = 8;
 constexpr uint32_t kDqXBytes = kDqBM * 128, kDqBuf = kDqXBytes + kDqBN * 128;
 constexpr uint32_t kDqLds = 2 * kDqBuf;  // 96 KB: one workgroup per CU
 
@@ -783,11 +788,29 @@ struct DqPlan {
 template <int I>
 __device__ __forceinline__ float ubyte_f32(uint32_t x) { return (float)((x >> (8 * I)) & 0xFFu); }
 __device__ __forceinline__ uint32_t dq_unit(uint32_t row, uint32_t u) { return row * 8 + (u ^ ((row >> 1) & 7)); }
+// Buffer loads issued as asm, untracked by the compiler: the loader waits for them with
+// explicit vmcnt counts (a wait that takes the loaded registers as operands, so that no use
+// of them moves above it). With compiler-tracked loads, register reuse across the rotating
+// register sets made it wait for the loads just issued.
+__device__ __forceinline__ u32x4 ld128(u32x4 rs, uint32_t off) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(off), "s"(rs));
+  return v;
+}
+__device__ __forceinline__ u32x2 ld64(u32x4 rs, uint32_t off) {
+  u32x2 v;
+  asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen" : "=v"(v) : "v"(off), "s"(rs));
+  return v;
+}
+__device__ __forceinline__ uint32_t ld16u(u32x4 rs, uint32_t off) {
+  uint32_t v;
+  asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(v) : "v"(off), "s"(rs));
+  return v;
+}
 
 template <int BITS, int GS, bool F16>
-__global__ __launch_bounds__(64 * kDqWaves) void qgemm_dq_kernel(QmmArgs a, DqPlan p) {
+__global__ __launch_bounds__(64 * (kDqCompute + kDqLoaders)) void qgemm_dq_kernel(QmmArgs a, DqPlan p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
   int mt, nt;
   if (p.rm > 0) {
     const int x8 = blockIdx.x % 8, l = blockIdx.x / 8;
@@ -802,79 +825,121 @@ __global__ __launch_bounds__(64 * kDqWaves) void qgemm_dq_kernel(QmmArgs a, DqPl
   const int rows_m = min(kDqBM, a.M - m0), rows_n = min(kDqBN, a.N - n0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t xrow = (uint32_t)a.ldx * 2, wrow = (uint32_t)a.K * BITS / 8, G2 = (uint32_t)a.G * 2;
-  const u32x4 X = rsrc4(a.x + (int64_t)m0 * xrow, (rows_m - 1) * xrow + (uint32_t)a.K * 2);
-  const auto W = rsrc(a.w + (int64_t)n0 * wrow, rows_n * wrow);
-  const auto S = rsrc(a.s + (int64_t)n0 * G2, rows_n * G2);
-  const auto Bi = rsrc(a.b + (int64_t)n0 * G2, rows_n * G2);
+  const int NC = a.K / kDqKC;
 
-  // x: 2048 units per chunk, four DMA instructions per wave; LDS unit U holds row U / 8,
-  // chunk unit (U % 8) ^ ((row >> 1) & 7)
-  auto issue_x = [&](int c, int buf) __attribute__((always_inline)) {
+  if (wave >= kDqCompute) {
+    // ---- loader: lane ll of the eight loader waves
+    const uint32_t ll = (uint32_t)(tid - 64 * kDqCompute);
+    const uint32_t xrow = (uint32_t)a.ldx * 2, wrow = (uint32_t)a.K * BITS / 8, G2 = (uint32_t)a.G * 2;
+    const u32x4 Xr = rsrc4(a.x + (int64_t)m0 * xrow, (rows_m - 1) * xrow + (uint32_t)a.K * 2);
+    const u32x4 W = rsrc4(a.w + (int64_t)n0 * wrow, rows_n * wrow);
+    const u32x4 S = rsrc4(a.s + (int64_t)n0 * G2, rows_n * G2);
+    const u32x4 Bi = rsrc4(a.b + (int64_t)n0 * G2, rows_n * G2);
+    // x: unit u = ll % 8 of rows ll / 8 + 64 i (one load instruction covers 8 whole rows)
+    const uint32_t xu = ll & 7, xr0 = ll >> 3;
+    uint32_t x_off[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t blk = 4 * wave + i, U = 64 * blk + lane, row = U >> 3, u = (U & 7) ^ ((row >> 1) & 7);
-      dma16(X, row < (uint32_t)rows_m ? row * xrow + (uint32_t)c * (2 * kDqKC) + 16 * u : kOffRow,
-            __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)buf * kDqBuf + 1024 * blk));
+      const uint32_t row = xr0 + 64 * i;
+      x_off[i] = row < (uint32_t)rows_m ? row * xrow + 16 * xu : kOffRow;
     }
-  };
-  // weights: thread t dequantises k 16 (t % 4) .. +15 of the chunk for weight row t / 4
-  constexpr int kWd = BITS / 2;  // words of 16 fields
-  const uint32_t wn_row = (uint32_t)tid >> 2, kp = (uint32_t)tid & 3;
-  const bool w_in = wn_row < (uint32_t)rows_n;
-  auto load_w = [&](int c, uint32_t (&wr)[kWd], uint32_t& sr, uint32_t& br) __attribute__((always_inline)) {
-    const uint32_t k0 = (uint32_t)c * kDqKC + 16 * kp;
-    const uint32_t wo = w_in ? wn_row * wrow + k0 * BITS / 8 : kOffRow;
-    if constexpr (kWd == 2) {
-      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(W, wo, 0, 0));
-      wr[0] = v[0];
-      wr[1] = v[1];
-    } else {
-      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, 0, 0));
-      for (int e = 0; e < 4; ++e) wr[e] = v[e];
-    }
-    const uint32_t so = w_in ? wn_row * G2 + 2 * (k0 / GS) : kOffRow;
-    sr = __builtin_amdgcn_raw_buffer_load_b16(S, so, 0, 0);
-    br = __builtin_amdgcn_raw_buffer_load_b16(Bi, so, 0, 0);
-  };
-  auto dq_w = [&](const uint32_t (&wr)[kWd], uint32_t sr, uint32_t br, int buf) __attribute__((always_inline)) {
-    const float sc = act_to_f32<F16>(sr), bc = act_to_f32<F16>(br);
-    float q[16];
-    if constexpr (BITS == 4) {
+    // weights: k 16 h .. 16 h + 15 of the chunk (h = ll % 4, LDS units 2 h, 2 h + 1) for
+    // weight row ll / 4
+    constexpr int kWq = BITS / 2;  // words of 16 fields
+    const uint32_t wr_row = ll >> 2, wh = ll & 3;
+    const bool w_in = wr_row < (uint32_t)rows_n;
+    typedef uint32_t wv_t __attribute__((ext_vector_type(kWq)));
+    struct Regs {
+      u32x4 x[4];
+      wv_t w;
+      uint32_t s, b;
+    };
+    auto load = [&](int c, Regs& r) __attribute__((always_inline)) {
+      const bool real = c < NC;
+      const uint32_t cc = real ? (uint32_t)c : 0u, no = real ? 0u : kOffRow;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t lo = wr[e] & 0x0F0F0F0Fu, hi = (wr[e] >> 4) & 0x0F0F0F0Fu;  // fields 2i, 2i + 1 as bytes
-        q[8 * e + 0] = ubyte_f32<0>(lo);
-        q[8 * e + 1] = ubyte_f32<0>(hi);
-        q[8 * e + 2] = ubyte_f32<1>(lo);
-        q[8 * e + 3] = ubyte_f32<1>(hi);
-        q[8 * e + 4] = ubyte_f32<2>(lo);
-        q[8 * e + 5] = ubyte_f32<2>(hi);
-        q[8 * e + 6] = ubyte_f32<3>(lo);
-        q[8 * e + 7] = ubyte_f32<3>(hi);
+      for (int i = 0; i < 4; ++i) r.x[i] = ld128(Xr, (x_off[i] | no) + cc * (2 * kDqKC));
+      const uint32_t k0 = cc * kDqKC + 16 * wh;
+      const uint32_t wo = (w_in ? wr_row * wrow + k0 * BITS / 8 : kOffRow) | no;
+      if constexpr (kWq == 2) r.w = ld64(W, wo);
+      else r.w = ld128(W, wo);
+      const uint32_t so = (w_in ? wr_row * G2 + 2 * (k0 / GS) : kOffRow) | no;
+      r.s = ld16u(S, so);
+      r.b = ld16u(Bi, so);
+    };
+    // loads per chunk: 4 of x, 1 of weights, 2 of scales and biases; staging a set waits
+    // for it with the two later sets' loads still in flight
+    auto wait_set = [&](Regs& r) __attribute__((always_inline)) {
+      asm volatile("s_waitcnt vmcnt(14)"
+                   : "+v"(r.x[0]), "+v"(r.x[1]), "+v"(r.x[2]), "+v"(r.x[3]), "+v"(r.w), "+v"(r.s), "+v"(r.b)
+                   :
+                   : "memory");
+    };
+    auto stage = [&](Regs& r, int buf) __attribute__((always_inline)) {
+      wait_set(r);
+      uint8_t* const xb = smem + (uint32_t)buf * kDqBuf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(xb + 16 * dq_unit(xr0 + 64 * i, xu)) = r.x[i];
+      const float sc = act_to_f32<F16>(r.s), bc = act_to_f32<F16>(r.b);
+      uint8_t* const wb = xb + kDqXBytes;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {  // unit 2 wh + u: k 8 u .. 8 u + 7 of the quarter
+        float q[8];
+        if constexpr (BITS == 4) {
+          const uint32_t wd = r.w[u], lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;  // fields 2i, 2i + 1
+          q[0] = ubyte_f32<0>(lo);
+          q[1] = ubyte_f32<0>(hi);
+          q[2] = ubyte_f32<1>(lo);
+          q[3] = ubyte_f32<1>(hi);
+          q[4] = ubyte_f32<2>(lo);
+          q[5] = ubyte_f32<2>(hi);
+          q[6] = ubyte_f32<3>(lo);
+          q[7] = ubyte_f32<3>(hi);
+        } else {
+          q[0] = ubyte_f32<0>(r.w[2 * u]);
+          q[1] = ubyte_f32<1>(r.w[2 * u]);
+          q[2] = ubyte_f32<2>(r.w[2 * u]);
+          q[3] = ubyte_f32<3>(r.w[2 * u]);
+          q[4] = ubyte_f32<0>(r.w[2 * u + 1]);
+          q[5] = ubyte_f32<1>(r.w[2 * u + 1]);
+          q[6] = ubyte_f32<2>(r.w[2 * u + 1]);
+          q[7] = ubyte_f32<3>(r.w[2 * u + 1]);
+        }
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = (uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[2 * e], bc)) |
+                 ((uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[2 * e + 1], bc)) << 16);
+        *reinterpret_cast<u32x4*>(wb + 16 * dq_unit(wr_row, 2 * wh + u)) = o;
       }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        q[4 * e + 0] = ubyte_f32<0>(wr[e]);
-        q[4 * e + 1] = ubyte_f32<1>(wr[e]);
-        q[4 * e + 2] = ubyte_f32<2>(wr[e]);
-        q[4 * e + 3] = ubyte_f32<3>(wr[e]);
-      }
+    };
+    // chunk k in register set k % 3: at iteration c, chunk c + 3 is loaded into the set
+    // chunk c left (staged at iteration c - 1) and chunk c + 1 is staged
+    Regs r0, r1, r2;
+    load(0, r0);
+    load(1, r1);
+    load(2, r2);
+    stage(r0, 0);
+    __syncthreads();
+    for (int c = 0; c < NC;) {
+      load(c + 3, r0);
+      if (c + 1 < NC) stage(r1, (c + 1) & 1);
+      __syncthreads();
+      if (++c >= NC) break;
+      load(c + 3, r1);
+      if (c + 1 < NC) stage(r2, (c + 1) & 1);
+      __syncthreads();
+      if (++c >= NC) break;
+      load(c + 3, r2);
+      if (c + 1 < NC) stage(r0, (c + 1) & 1);
+      __syncthreads();
+      ++c;
     }
-    u32x4 o0, o1;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      o0[e] = (uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[2 * e], bc)) |
-              ((uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[2 * e + 1], bc)) << 16);
-      o1[e] = (uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[8 + 2 * e], bc)) |
-              ((uint32_t)f32_to_act<F16>(__builtin_fmaf(sc, q[8 + 2 * e + 1], bc)) << 16);
-    }
-    uint8_t* const wb = smem + (uint32_t)buf * kDqBuf + kDqXBytes;
-    *reinterpret_cast<u32x4*>(wb + 16 * dq_unit(wn_row, 2 * kp)) = o0;
-    *reinterpret_cast<u32x4*>(wb + 16 * dq_unit(wn_row, 2 * kp + 1)) = o1;
-  };
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // the loads past the end (zeros)
+    return;
+  }
 
+  // ---- compute
   const int wm = wave & 3, wn = wave >> 2;
   const uint32_t r16 = (uint32_t)lane & 15, j = (uint32_t)lane >> 4;
   f32x4 acc[4][4];
@@ -882,22 +947,9 @@ __global__ __launch_bounds__(64 * kDqWaves) void qgemm_dq_kernel(QmmArgs a, DqPl
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int NC = a.K / kDqKC;
-  uint32_t wr[kWd], sr, br;
-  issue_x(0, 0);
-  load_w(0, wr, sr, br);
-  dq_w(wr, sr, br, 0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's x DMA has landed
-  __syncthreads();
+  __syncthreads();  // chunk 0 staged
   for (int c = 0; c < NC; ++c) {
-    const int buf = c & 1;
-    const bool next = c + 1 < NC;
-    if (next) {
-      issue_x(c + 1, buf ^ 1);
-      load_w(c + 1, wr, sr, br);
-    }
-    const uint8_t* const xb = smem + (uint32_t)buf * kDqBuf;
+    const uint8_t* const xb = smem + (uint32_t)(c & 1) * kDqBuf;
     const uint8_t* const wb = xb + kDqXBytes;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -913,8 +965,6 @@ __global__ __launch_bounds__(64 * kDqWaves) void qgemm_dq_kernel(QmmArgs a, DqPl
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = mma<F16>(A[rt], B[ct], acc[rt][ct]);
     }
-    if (next) dq_w(wr, sr, br, buf ^ 1);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
   }
 
@@ -961,7 +1011,8 @@ int32_t launch_dq(hipStream_t st, const QmmArgs& a, const DqPlan& p) {
   const int32_t rc = allow_lds_once((const void*)qgemm_dq_kernel<BITS, GS, F16>, kDqLds, &lds_set,
                                     "quantized_matmul: LDS attribute");
   if (rc) return rc;
-  hipLaunchKernelGGL((qgemm_dq_kernel<BITS, GS, F16>), dim3((unsigned)(p.mtiles * p.ntiles)), dim3(64 * kDqWaves),
+  hipLaunchKernelGGL((qgemm_dq_kernel<BITS, GS, F16>), dim3((unsigned)(p.mtiles * p.ntiles)),
+                     dim3(64 * (kDqCompute + kDqLoaders)),
                      kDqLds, st, a, p);
   return check_hip(hipGetLastError(), "quantized_matmul launch");
 }
