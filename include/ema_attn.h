@@ -379,7 +379,10 @@ EMA_API int32_t ema_gdn_scan_ws(ema_stream_t stream, const void* q, const void* 
  *   y:      [M, ldy] in `dtype`; columns [0, N) of each row written, the rest untouched
  *           (ldy > N writes one piece of a wider row: the separate q, k and v projections
  *           of run_qkv land in one q|k|v row without a concatenation)
- * Products are exact and accumulate in f32; y is rounded once (RNE) to `dtype`.
+ * Up to 32 rows (and K not a multiple of 64): products are exact and accumulate in f32.
+ * More than 32 rows with K a multiple of 64: as MLX's quantized matmul for many rows, the
+ * weights are first dequantised into `dtype`, w = round(fma_f32(scale, q, bias)), and
+ * x * w accumulates in f32. Either way y is rounded once (RNE) to `dtype`.
  * dtype: EMA_DTYPE_BF16 or EMA_DTYPE_F16. bits: 4 or 8; group_size: 32, 64 or 128; K a
  * multiple of group_size; ldx >= K, ldy >= N. x and w 16-byte aligned, ldx a multiple
  * of 8; scales, biases and y element-aligned. M = 0 is a no-op. */
