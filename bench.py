@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "decode_b1", "prefill_chunk", "fp8",
-                                       "int4", "gdn", "gdn_step", "qmm", "prefill_1p7b"],
+                                       "int4", "gdn", "gdn_step", "qmm", "prefill_1p7b", "pre"],
                    default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -550,8 +550,9 @@ def main():
         secondary.append(bench_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_qwen3_8b", 1, 32, 8, 128, 4096, 2048, 0))
     if args.only in ("all", "prefill_1p7b"):
         secondary.append(bench_prefill(ctx, ema, "prefill_causal_T2048_16q8kv_qwen3_1p7b", 1, 16, 8, 128, 4096, 2048, 0))
-    if args.only == "all":
+    if args.only in ("all", "pre"):
         secondary.append(bench_pre(ctx, ema, "pre_attention_T2048_16q8kv", 2048, 16, 8, 128, 4096))
+    if args.only == "all":
         secondary.append(bench_decode_pair(ctx, ema, "decode_B32_32q8kv_unfused_pre_attention_plus_attention"))
     if args.only in ("all", "decode_b1"):
         secondary.append(bench_decode(ctx, ema, "decode_B1_16q8kv_L1024_cap4096", 1, 16, 8, 128, 4096, [1024]))

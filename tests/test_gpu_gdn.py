@@ -253,6 +253,44 @@ def test_gdn_wy_segments_are_bit_identical(ema):
         assert torch.equal(y.view(torch.int16), outs[0][0].view(torch.int16))
 
 
+def test_gdn_wy_graph_replay(ema):
+    # a WY scan in segments (a workspace of two chunks) and a whole one, each captured in a
+    # graph and replayed with eager work between the replays: every replay gives the eager
+    # call's bits
+    import torch
+
+    B, T, Hk, Hv, Dk, Dv = 1, 500, 2, 4, 128, 64
+    say(f"gdn WY graph replay T={T}")
+    (dq, dk_, dv_, dg, db, dS), _ = make_inputs(71, B, T, Hk, Hv, Dk, Dv, "bf16")
+    full = ema.gdn_scan_workspace_size(B, T, Hk, Hv, Dk, Dv)
+    per_chunk = full // ((T + 31) // 32)
+    ws = ema.gdn_workspace(B, T, Hk, Hv, Dk, Dv)
+    S0 = dS.clone()
+    y0 = ema.gdn_scan(dq, dk_, dv_, dg, db, S0, workspace=ws)
+    S1 = dS.clone()
+    y1 = ema.gdn_scan(dq, dk_, dv_, dg, db, S1, workspace=torch.empty(2 * per_chunk, dtype=torch.uint8, device="cuda"))
+    torch.cuda.synchronize()
+    assert torch.equal(S1, S0) and torch.equal(y1.view(torch.int16), y0.view(torch.int16))
+    for wsx in (ws, torch.empty(2 * per_chunk, dtype=torch.uint8, device="cuda")):
+        Sg = dS.clone()
+        yg = torch.empty_like(y0)
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(st):
+            with torch.cuda.graph(g, stream=st):
+                ema.gdn_scan(dq, dk_, dv_, dg, db, Sg, y=yg, workspace=wsx, stream=st)
+        torch.cuda.synchronize()
+        for i in range(3):
+            Sg.copy_(dS)
+            yg.fill_(float(i + 2))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(Sg, S0), f"replay {i}: state"
+            assert torch.equal(yg.view(torch.int16), y0.view(torch.int16)), f"replay {i}: y"
+
+
 def test_gdn_wy_gate_extremes(ema, ora):
     B, T, Hk, Hv, Dk, Dv = 1, 96, 1, 2, 128, 32
     say(f"gdn WY gate extremes T={T}")
