@@ -68,6 +68,11 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // compile-time choice of the softmax step's masking code
 struct MaskOn { static constexpr bool value = true; };
 struct MaskOff { static constexpr bool value = false; };
+// the segment of a block stream that a step's block lies in, when the caller knows it
+// (paired workgroups: segment A, the light rows, then segment B, the heavy rows)
+struct SegAny { static constexpr int value = 0; };
+struct SegA { static constexpr int value = 1; };
+struct SegB { static constexpr int value = 2; };
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Raw buffer resource (V#) over `bytes` bytes from `base`: stride 0, gfx9 dword3 with a
@@ -109,7 +114,16 @@ __device__ __forceinline__ uint32_t pk_max3_f16(uint32_t a, uint32_t b, uint32_t
 // [base, q_off + T) with base = max(0, q_off + T - cap), position p in row p % cap; the
 // kernel works on key indices c = p - base (q_off is taken relative to base), so all its
 // causal and range logic is that of a static cache, and only the loads map c to its row.
-template <bool kRot>
+//
+// kPair: the workgroup owns a heavy query block and a light one of the same head (the
+// light block's key range is a prefix of the heavy block's). Group 0 streams the light
+// rows over all their key blocks and then the heavy rows over the first key blocks of
+// the heavy range; group 1 streams the heavy rows over the rest, so both groups take
+// half of the pair's key blocks in one pipeline each: one prologue and one merge per
+// workgroup instead of two, and no refill of the pipeline between the blocks. The light
+// rows are complete when group 0 leaves them; group 0 stores them on its own. A middle
+// block paired with itself (odd block count) runs as a heavy block with no light rows.
+template <bool kRot, bool kPair>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
 
@@ -122,9 +136,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // blocks first, and with two workgroups' worth of query blocks or more per CU a pair
   // per workgroup -- the heavy block nqb-1-p, then the light one p of the same head --
   // which balances the causal work per workgroup and pays one launch per pair.
-  const PrefillItem item = prefill_item(blockIdx.x, gridDim.x, a.B, a.Hkv, a.G, a.nqb, a.paired);
-  const int qb_first = item.qb_first;
-  const int qb_second = item.qb_second;  // == qb_first: no second
+  const PrefillItem item = prefill_item(blockIdx.x, gridDim.x, a.B, a.Hkv, a.G, a.nqb, kPair ? 1 : 0);
   const int b = item.b;
   const int h = item.h;
   const int kh = item.kh;
@@ -137,32 +149,53 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     key_base = key_base < 0 ? 0 : key_base;
     q_off -= key_base;
   }
-  auto run_block = [&](const int qb) __attribute__((always_inline)) {
   int kv_len = q_off + a.T;
   kv_len = kv_len > a.cap ? a.cap : kv_len;
   const bool causal = a.flags & EMA_PREFILL_CAUSAL;
   int kv_begin = (a.flags & EMA_PREFILL_CHUNK_ONLY) ? q_off : 0;
   kv_begin = kv_begin > kv_len ? kv_len : kv_begin;
-
-  const int row0 = qb * kBM;                      // first query row of the workgroup
-  int wg_end = kv_len;
-  if (causal) {
-    const int lim = q_off + row0 + kBM;           // last row sees keys < lim
-    wg_end = lim < wg_end ? lim : wg_end;
-  }
   const int blk_begin = kv_begin / kBN;
-  const int blk_end = (wg_end + kBN - 1) / kBN;
-  const int nblk = blk_end > blk_begin ? blk_end - blk_begin : 0;
-  const int n0 = (nblk + 1) / 2;                  // group 0: the first half of the blocks
-  const int gb0 = blk_begin + (g ? n0 : 0);       // this group's first block
-  const int ng = g ? nblk - n0 : n0;              // and its block count
+  // 64-key blocks attended by query block qb: [blk_begin, blk_begin + blocks_of(qb))
+  auto blocks_of = [&](int qb) __attribute__((always_inline)) {
+    int wg_end = kv_len;
+    if (causal) {
+      const int lim = q_off + qb * kBM + kBM;     // its last row sees keys < lim
+      wg_end = lim < wg_end ? lim : wg_end;
+    }
+    const int blk_end = (wg_end + kBN - 1) / kBN;
+    return blk_end > blk_begin ? blk_end - blk_begin : 0;
+  };
 
-  // this lane's query row
-  const int qr = row0 + 32 * wq + (lane & 31);
-  const int q_abs = q_off + qr;                   // causal limit: key <= q_abs
-  const int wave_first_abs = q_off + row0 + 32 * wq;
-  const int wave_last_abs = wave_first_abs + 31;
+  // The wave's block stream: segment A (group 0 of a pair: the light rows over all their
+  // blocks), then segment B (the heavy rows: the first n0 - n1 of their blocks in group 0,
+  // the rest in group 1). Without a light block group 0 takes the first half.
+  const int qb_h = item.qb_first;
+  const bool has_light = kPair && item.qb_second != qb_h;
+  const int qb_l = has_light ? item.qb_second : qb_h;
+  const int nblk_h = blocks_of(qb_h);
+  const int nblk_l = has_light ? blocks_of(qb_l) : 0;   // <= nblk_h
+  const int n0 = (nblk_l + nblk_h + 1) / 2;               // blocks of group 0
+  const int nh0 = n0 - nblk_l;                            // heavy blocks of group 0
+  const int n1 = kPair && g == 0 ? nblk_l : 0;            // segment A
+  const int gbA = blk_begin;
+  const int gbB = blk_begin + (g ? nh0 : 0);              // first block of segment B
+  const int nB = g ? nblk_h - nh0 : nh0;
+  const int ng = n1 + nB;                                 // blocks of this wave's stream
+  // stream block j: in segment A (tag SegAny: decided from j), and its absolute block index
+  auto in_a = [&](int j, auto seg) __attribute__((always_inline)) {
+    constexpr int kSeg = decltype(seg)::value;
+    return kSeg == 1 || (kSeg == 0 && kPair && j < n1);
+  };
+  const int offB = gbB - n1;
+  auto blk_of = [&](int j) __attribute__((always_inline)) { return j + (in_a(j, SegAny{}) ? gbA : offB); };
+
+  const int row0 = qb_h * kBM;                    // first query row of the heavy block
+  const int row0A = qb_l * kBM;                   // and of the light block
   const int hh = lane >> 5;                       // which half of the k slots
+  // the wave's first query row in either segment; lane row: + (lane & 31), causal limit
+  // key <= that
+  const int wfaB = q_off + row0 + 32 * wq, wfaA = q_off + row0A + 32 * wq;
+  auto wfa_of = [&](int j, auto seg) __attribute__((always_inline)) { return in_a(j, seg) ? wfaA : wfaB; };
 
   uint16_t* const Ks = lds + g * kGroupElems;     // this group's K tiles: buffer i at Ks + i * kTile
   uint16_t* const Vs = Ks + 2 * kTile;            // and V tiles
@@ -205,11 +238,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // number of its rows before the ring's end (rows past it are cap rows back).
   auto blk_off = [&](int j) __attribute__((always_inline)) {
     if (j >= ng) return kNoRow;
-    if (kRot) return (uint32_t)((key_base + (gb0 + j) * kBN) % a.cap) * row_bytes;
-    return (uint32_t)((gb0 + j) * kBN) * row_bytes;
+    if (kRot) return (uint32_t)((key_base + blk_of(j) * kBN) % a.cap) * row_bytes;
+    return (uint32_t)(blk_of(j) * kBN) * row_bytes;
   };
   auto wrap_rows = [&](int j) __attribute__((always_inline)) {
-    return kRot && j < ng ? a.cap - (key_base + (gb0 + j) * kBN) % a.cap : kBN;
+    return kRot && j < ng ? a.cap - (key_base + blk_of(j) * kBN) % a.cap : kBN;
   };
   const uint32_t ring_bytes = (uint32_t)a.cap * row_bytes;
   auto tile_dst = [&](const uint16_t* tile) __attribute__((always_inline)) {
@@ -242,7 +275,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t ob = blk_off(j), dst = tile_dst(tile);
     const u32x4 r = kRot ? tensor_r : tile_rsrc(tensor, ob);
     const int wrap = wrap_rows(j);
-    const int base = (gb0 + j) * kBN;
+    const int base = blk_of(j) * kBN;
     if (j < ng && base < kv_begin) {
       // first block of a chunk-only window: rows before kv_begin are outside the
       // attended range; an out-of-range offset makes them arrive as zeros, so whatever
@@ -297,19 +330,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   int v_col[4];
   for (int dt = 0; dt < 4; ++dt) v_col[dt] = tr_row * kD + 16 * (grp & 1) + 4 * (s16 & 3) + 32 * (dt ^ (s16 >> 2));
 
-  auto active = [&](int j) __attribute__((always_inline)) { return !causal || (gb0 + j) * kBN <= wave_last_abs; };
-  // Block j holds keys outside [kv_begin, kv_len) or above the causal limit of some row
-  // of this wave. For j >= 1 this holds exactly from block j_mask on.
-  auto need_mask = [&](int j) __attribute__((always_inline)) {
-    const int kbase = (gb0 + j) * kBN;
-    return kbase < kv_begin || kbase + kBN > kv_len || (causal && kbase + kBN - 1 > wave_first_abs);
+  // Some row of the wave attends to a key of block j (the last row's limit is the first's + 31).
+  auto active = [&](int j, auto seg) __attribute__((always_inline)) {
+    return !causal || (j + (in_a(j, seg) ? gbA : offB)) * kBN <= wfa_of(j, seg) + 31;
   };
-  int j_mask = kv_len / kBN - gb0;  // first block reaching past kv_len
-  if (causal) {
-    const int jc = (wave_first_abs + 1) / kBN - gb0;  // first block reaching past row 0's limit
-    j_mask = jc < j_mask ? jc : j_mask;
-  }
-  j_mask = j_mask < 1 ? 1 : j_mask;
+  // Block j holds keys outside [kv_begin, kv_len) or above the causal limit of some row
+  // of this wave. Inside a segment, for its blocks after the first, this holds exactly
+  // from the segment's block j_mask on.
+  auto need_mask = [&](int j, auto seg) __attribute__((always_inline)) {
+    const int kbase = (j + (in_a(j, seg) ? gbA : offB)) * kBN;
+    return kbase < kv_begin || kbase + kBN > kv_len || (causal && kbase + kBN - 1 > wfa_of(j, seg));
+  };
+  // first block of a segment (starting at absolute block gb, rows from wave_first) that
+  // needs a mask, at least 1; and the blocks of its n that the wave attends to
+  auto seg_mask = [&](int gb, int wave_first) __attribute__((always_inline)) {
+    int jm = kv_len / kBN - gb;  // first block reaching past kv_len
+    if (causal) {
+      const int jc = (wave_first + 1) / kBN - gb;  // first block reaching past row 0's limit
+      jm = jc < jm ? jc : jm;
+    }
+    return jm < 1 ? 1 : jm;
+  };
+  auto seg_act = [&](int gb, int wave_first, int n) __attribute__((always_inline)) {
+    if (!causal) return n;
+    const int last = (wave_first + 31) / kBN - gb + 1;
+    return last < 0 ? 0 : (last < n ? last : n);
+  };
 
   // Matrix step j: O += V^T P^T for block j-1, then S^T = K Q^T - m_use for block j. A base
   // change of the softmax step before is applied to o first.
@@ -374,10 +420,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   };
   // general matrix step (first and last steps, causal-inactive blocks)
-  auto mstep = [&](int j) __attribute__((always_inline)) {
+  auto mstep = [&](int j, auto seg) __attribute__((always_inline)) {
     apply_rescale();
-    const bool do_pv = j >= 1 && j - 1 < ng && active(j - 1);
-    const bool do_qk = j < ng && active(j);
+    const bool do_pv = j >= 1 && j - 1 < ng && active(j - 1, seg);
+    const bool do_qk = j < ng && active(j, seg);
     __builtin_amdgcn_s_setprio(1);
     if (do_pv) pv(j - 1);
     if (do_qk) qk(j);
@@ -397,13 +443,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // buffer held K of block j, last read by the matrix step just before) and of V for
   // block j+1 (its buffer held V of block j-1, last read by that same matrix step).
   // With kMask false the block is known to need no mask (the steady-state loop).
-  auto vstep = [&](int j, auto mask_tag) __attribute__((always_inline)) {
+  auto vstep = [&](int j, auto mask_tag, auto seg) __attribute__((always_inline)) {
     constexpr bool kMask = decltype(mask_tag)::value;
     if (j < 0 || j >= ng) return;
-    if (active(j)) {
-      const int kbase = (gb0 + j) * kBN;
+    if (active(j, seg)) {
+      const int kbase = blk_of(j) * kBN;
       // key of slot i in sub-tile kt: kbase + 32kt + (i%4) + 8(i/4) + 4hh
-      if (kMask && need_mask(j)) {
+      if (kMask && need_mask(j, seg)) {
+        const int q_abs = wfa_of(j, seg) + (lane & 31);
         int hi = causal && q_abs < kv_len - 1 ? q_abs : kv_len - 1;
         hi -= kbase + 4 * hh;
         const int lo = kv_begin - kbase - 4 * hh;
@@ -492,6 +539,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       dma16<0>(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
     }
   }
+  // The light rows' Q (pairs): rows 0-63 in group 0's second V tile, rows 64-127 in group
+  // 1's, swizzled as the heavy rows; those tiles are first loaded by the groups' first
+  // softmax steps, after group 0 has read its Q^T operand from them.
+  auto light_q = [&](int r) __attribute__((always_inline)) { return lds + (r >> 6) * kGroupElems + 3 * kTile + (r & 63) * kD; };
+  if (has_light && nblk_l > 0) {
+    const int qrows = a.T - row0A < kBM ? a.T - row0A : kBM;
+    const u32x4 r = buffer_rsrc(a.q + (((int64_t)b * a.Hq + h) * a.T + row0A) * kD, (uint32_t)qrows * kD * 2);
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)light_q(16 * wave);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = (uint32_t)(16 * wave + 4 * i + r4);
+      dma16<0>(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
+    }
+  }
   if (ng > 0) {
     load_k(0);
     load_v(0);
@@ -503,53 +563,104 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // Q^T as B operand: step s covers dims 16s + 8*hh .. +7 of row 32wq + (lane & 31). Q is
   // scaled by scale*log2(e) and rounded to bf16 here, so the scores come out of the
   // MFMA in the log2 domain and the softmax needs no multiply per score.
-  {
+  auto scale_q = [&](const u32x4 raw) __attribute__((always_inline)) {
+    u32x4 w;
+    for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(bf16_lo(raw[e]) * a.qk_scale, bf16_hi(raw[e]) * a.qk_scale);
+    return as_bf16x8(w);
+  };
+  // Segment B's rows: Q^T of the heavy rows from LDS, and a fresh softmax state (o and
+  // the row sums are cleared where segment A's output leaves).
+  auto start_b = [&]() __attribute__((always_inline)) {
     const uint16_t* qp = Qs + 32 * wq * kD + k_lane;
-    for (int s = 0; s < 8; ++s) {
-      const u32x4 raw = *(const u32x4*)(qp + (k_x ^ (16 * s)));
-      u32x4 w;
-      for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf16x2(bf16_lo(raw[e]) * a.qk_scale, bf16_hi(raw[e]) * a.qk_scale);
-      qop[s] = as_bf16x8(w);
+    for (int s = 0; s < 8; ++s) qop[s] = scale_q(*(const u32x4*)(qp + (k_x ^ (16 * s))));
+    m_use = 0.f;
+    seen = false;
+    all_seen = false;
+  };
+  // Segment A's rows are complete (the PV of their last block ran in the matrix step
+  // before): normalise, stage the wave's 32 rows in its own rows of the Q area (whose heavy
+  // Q^T it has read), store them as whole 256-byte rows, and clear o and the row sums.
+  auto finish_a = [&]() __attribute__((always_inline)) {
+    const float l_lo = __shfl(lsum[0], lane & 15, 64), l_hi = __shfl(lsum[1], lane & 15, 64);
+    const float l_run = (lane & 16) ? l_hi : l_lo;
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    const int rr = 32 * wq + (lane & 31);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int dt = 0; dt < 4; ++dt)
+      for (int i4 = 0; i4 < 4; ++i4) {
+        // lane holds O[rr][32dt + (i%4) + 8(i/4) + 4hh]: chunk 4dt + i4, half hh
+        u32x2 wv;
+        wv[0] = pack_bf16x2(o[dt][4 * i4] * inv, o[dt][4 * i4 + 1] * inv);
+        wv[1] = pack_bf16x2(o[dt][4 * i4 + 2] * inv, o[dt][4 * i4 + 3] * inv);
+        const int c = 4 * dt + i4;
+        *(u32x2*)(Qs + rr * kD + 8 * (c ^ (rr & 15)) + 4 * hh) = wv;
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads what its lanes wrote
+    for (int it = 0; it < 8; ++it) {
+      const int n = it * 64 + lane;
+      const int r = 32 * wq + (n >> 4), c = n & 15;
+      const u32x4 v = *(const u32x4*)(Qs + r * kD + 8 * (c ^ (r & 15)));
+      if (row0A + r < a.T) *(u32x4*)(a.out + (((int64_t)b * a.T + row0A + r) * a.Hq + h) * kD + 8 * c) = v;
     }
-  }
+    for (int dt = 0; dt < 4; ++dt)
+      for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+    lsum = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
 
   // Phase 2t + half: group 0 runs matrix step t then softmax step t; group 1 runs
   // softmax step t-1 then matrix step t, so the groups always sit in opposite halves.
-  // Every wave passes the same number of barriers. Matrix steps 1 .. jm-1 of a wave have
-  // both halves active and run in a loop of their own with the scheduled full step.
-  int j_act = ng;  // blocks this wave attends to (causal: up to its last row)
-  if (causal) {
-    const int last = wave_last_abs / kBN - gb0 + 1;
-    j_act = last < 0 ? 0 : (last < ng ? last : ng);
-  }
-  // The steady-state loop also runs only over softmax steps of blocks that need no mask
-  // (blocks 1 .. j_mask-1), so its softmax step carries no masking code.
-  const int jm = j_act;
+  // Every wave passes the same number of barriers (n0 + 1 phase pairs). Matrix steps whose
+  // two halves are both active and inside one segment run in loops of their own with the
+  // scheduled full step; those loops also run only over softmax steps of blocks that need
+  // no mask, so their softmax step carries no masking code.
   const MaskOn mask_on;
   const MaskOff mask_off;
+  const int actB = seg_act(gbB, wfaB, nB), maskB = seg_mask(gbB, wfaB);
   if (g == 0) {
-    auto half0 = [&](int t, bool full, auto mask_tag) __attribute__((always_inline)) {
+    auto half0 = [&](int t, bool full, auto mask_tag, auto seg, bool switch_rows) __attribute__((always_inline)) {
       if (full) mstep_full(t);
-      else mstep(t);
+      else mstep(t, seg);
       __syncthreads();
-      vstep(t, mask_tag);
+      vstep(t, mask_tag, seg);
+      if (switch_rows) start_b();
       __syncthreads();
     };
-    const int t_full = jm < j_mask ? jm : j_mask;
     int t = 0;
-    for (; t <= n0 && t < 1; ++t) half0(t, false, mask_on);
-    for (; t < t_full; ++t) half0(t, true, mask_off);
-    for (; t <= n0; ++t) half0(t, false, mask_on);
+    if (kPair && n1 > 0) {
+      // segment A: blocks 0 .. n1-1, the last one followed by the switch of the Q operand
+      const uint16_t* qp = light_q(32 * wq) + k_lane;
+      for (int s = 0; s < 8; ++s) qop[s] = scale_q(*(const u32x4*)(qp + (k_x ^ (16 * s))));
+      const int actA = seg_act(gbA, wfaA, n1), maskA = seg_mask(gbA, wfaA);
+      const int tfA = actA < maskA ? actA : maskA;
+      for (; t < n1 - 1 && t < 1; ++t) half0(t, false, mask_on, SegA{}, false);
+      for (; t < n1 - 1 && t < tfA; ++t) half0(t, true, mask_off, SegA{}, false);
+      for (; t < n1 - 1; ++t) half0(t, false, mask_on, SegA{}, false);
+      half0(t, false, mask_on, SegA{}, true);
+      ++t;
+    } else {
+      start_b();
+    }
+    // step n1: the PV of segment A's last block beside the QK of segment B's first; segment
+    // A's rows leave in the softmax half
+    mstep(t, SegAny{});
+    __syncthreads();
+    vstep(t, mask_on, SegB{});
+    if (has_light) finish_a();
+    __syncthreads();
+    ++t;
+    const int tfB = n1 + (actB < maskB ? actB : maskB);
+    for (; t < tfB; ++t) half0(t, true, mask_off, SegB{}, false);
+    for (; t <= n0; ++t) half0(t, false, mask_on, SegB{}, false);
   } else {
+    start_b();
     auto half1 = [&](int t, bool full, auto mask_tag) __attribute__((always_inline)) {
-      vstep(t - 1, mask_tag);
+      vstep(t - 1, mask_tag, SegB{});
       __syncthreads();
       if (full) mstep_full(t);
-      else mstep(t);
+      else mstep(t, SegB{});
       __syncthreads();
     };
-    const int t_full = jm < j_mask + 1 ? jm : j_mask + 1;
+    const int t_full = actB < maskB + 1 ? actB : maskB + 1;
     int t = 0;
     for (; t <= n0 && t < 2; ++t) half1(t, false, mask_on);
     for (; t < t_full; ++t) half1(t, true, mask_off);
@@ -629,13 +740,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       if (row0 + r < a.T) *(u32x4*)(a.out + (((int64_t)b * a.T + row0 + r) * a.Hq + h) * kD + 8 * c) = v;
     }
   }
-  };
-
-  run_block(qb_first);
-  if (qb_second != qb_first) {
-    __syncthreads();  // the staging tile is read before the next block's Q lands there
-    run_block(qb_second);
-  }
 }
 
 }  // namespace
@@ -650,12 +754,13 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
     return set_error(EMA_ERR_UNSUPPORTED,
                      "ema_prefill_attention: capacity %d x stride_pos %lld exceeds the 2 GiB per-head range",
                      c.capacity, (long long)c.stride_pos);
-  static std::atomic<uint64_t> lds_set[2];  // per instantiation, one bit per device
-  int32_t rc = allow_lds_once((const void*)prefill_kernel<false>, kLdsBytes, &lds_set[0],
-                              "ema_prefill_attention: LDS attribute");
-  if (rc) return rc;
-  rc = allow_lds_once((const void*)prefill_kernel<true>, kLdsBytes, &lds_set[1], "ema_prefill_attention: LDS attribute");
-  if (rc) return rc;
+  static std::atomic<uint64_t> lds_set[4];  // per instantiation, one bit per device
+  const void* kernels[4] = {(const void*)prefill_kernel<false, false>, (const void*)prefill_kernel<true, false>,
+                            (const void*)prefill_kernel<false, true>, (const void*)prefill_kernel<true, true>};
+  for (int i = 0; i < 4; ++i) {
+    const int32_t rc = allow_lds_once(kernels[i], kLdsBytes, &lds_set[i], "ema_prefill_attention: LDS attribute");
+    if (rc) return rc;
+  }
   PrefillArgs a;
   a.q = (const uint16_t*)q;
   a.k = (const uint16_t*)c.k;
@@ -680,10 +785,15 @@ int32_t launch_prefill(hipStream_t s, const void* q, const ema_kvcache_desc& c,
   a.paired = a.nqb >= 2 && items >= 2 * (int64_t)cus;
   const int64_t blocks = prefill_grid(c.batch, Hq, a.nqb, a.paired);
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_prefill_attention: grid too large");
-  if (c.flags & EMA_KV_ROTATING)
-    hipLaunchKernelGGL(prefill_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
+  const bool rot = c.flags & EMA_KV_ROTATING;
+  if (rot && a.paired)
+    hipLaunchKernelGGL((prefill_kernel<true, true>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
+  else if (rot)
+    hipLaunchKernelGGL((prefill_kernel<true, false>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
+  else if (a.paired)
+    hipLaunchKernelGGL((prefill_kernel<false, true>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
   else
-    hipLaunchKernelGGL(prefill_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
+    hipLaunchKernelGGL((prefill_kernel<false, false>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s, a);
   return check_hip(hipGetLastError(), "ema_prefill_attention launch");
 }
 
