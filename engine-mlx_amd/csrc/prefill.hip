@@ -140,9 +140,37 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int b = item.b;
   const int h = item.h;
   const int kh = item.kh;
+  const int q_off_arg = a.q_off[b];  // (a scalar load, waited for after the Q loads are issued)
+  const int qb_h = item.qb_first;
+  const bool has_light = kPair && item.qb_second != qb_h;
+  const int qb_l = has_light ? item.qb_second : qb_h;
+  const int row0 = qb_h * kBM;                    // first query row of the heavy block
+  const int row0A = qb_l * kBM;                   // and of the light block
 
-  int q_off = a.q_off[b];
-  q_off = q_off < 0 ? 0 : q_off;
+  // Prologue, part 1: the workgroup's Q rows go to LDS before anything depends on q_off.
+  // Global -> LDS without registers (buffer_load_dwordx4 ... lds): one instruction moves
+  // 1 KB, lane l's 16 bytes landing at byte 16l of the destination, i.e. 4 rows of 256 B;
+  // wave w moves rows 16w .. 16w+15, chunk p of row r from chunk p ^ (r & 15). Rows past
+  // T arrive as zeros.
+  const int r4 = lane >> 4, p16 = lane & 15;  // row within the 4, chunk position in the row
+  auto load_q = [&](int qrow0, uint32_t dst) __attribute__((always_inline)) {
+    const int qrows = a.T - qrow0 < kBM ? a.T - qrow0 : kBM;
+    const u32x4 r = buffer_rsrc(a.q + (((int64_t)b * a.Hq + h) * a.T + qrow0) * kD, (uint32_t)qrows * kD * 2);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = (uint32_t)(16 * wave + 4 * i + r4);
+      dma16<0>(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
+    }
+  };
+  // The heavy rows in the Q area for the whole stream. The light rows' Q (pairs): rows
+  // 0-63 in group 0's second V tile, rows 64-127 in group 1's; those tiles are first
+  // loaded by the groups' first softmax steps, after group 0 has read its Q^T operand
+  // from them.
+  uint16_t* const Qs = lds + 2 * kGroupElems;
+  auto light_q = [&](int r) __attribute__((always_inline)) { return lds + (r >> 6) * kGroupElems + 3 * kTile + (r & 63) * kD; };
+  load_q(row0, (uint32_t)(uintptr_t)(lds_void*)(Qs + 16 * wave * kD));
+  if (has_light) load_q(row0A, (uint32_t)(uintptr_t)(lds_void*)light_q(16 * wave));
+
+  int q_off = q_off_arg < 0 ? 0 : q_off_arg;
   int key_base = 0;  // absolute position of key index 0 (rotating cache; n_tokens <= cap)
   if (kRot) {
     key_base = q_off + a.T - a.cap;
@@ -169,9 +197,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // The wave's block stream: segment A (group 0 of a pair: the light rows over all their
   // blocks), then segment B (the heavy rows: the first n0 - n1 of their blocks in group 0,
   // the rest in group 1). Without a light block group 0 takes the first half.
-  const int qb_h = item.qb_first;
-  const bool has_light = kPair && item.qb_second != qb_h;
-  const int qb_l = has_light ? item.qb_second : qb_h;
   const int nblk_h = blocks_of(qb_h);
   const int nblk_l = has_light ? blocks_of(qb_l) : 0;   // <= nblk_h
   const int n0 = (nblk_l + nblk_h + 1) / 2;               // blocks of group 0
@@ -189,8 +214,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int offB = gbB - n1;
   auto blk_of = [&](int j) __attribute__((always_inline)) { return j + (in_a(j, SegAny{}) ? gbA : offB); };
 
-  const int row0 = qb_h * kBM;                    // first query row of the heavy block
-  const int row0A = qb_l * kBM;                   // and of the light block
   const int hh = lane >> 5;                       // which half of the k slots
   // the wave's first query row in either segment; lane row: + (lane & 31), causal limit
   // key <= that
@@ -225,7 +248,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // at instruction offset 1024 i); the per-lane source offsets below apply the swizzle,
   // have that instruction offset taken out (row >= 4i and row_bytes >= 256 keep them
   // non-negative) and stay the same for every block.
-  const int r4 = lane >> 4, p16 = lane & 15;  // row within the 4, chunk position in the row
   uint32_t koff[4], voff[4];
   for (int i = 0; i < 4; ++i) {
     const uint32_t row = (uint32_t)(16 * wq + 4 * i + r4);
@@ -525,39 +547,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
   };
 
-  // Prologue: the workgroup's 128 Q rows (wave w moves rows 16w .. 16w+15, swizzled as
-  // the K tiles) and this group's first tiles go to LDS together, so their memory
-  // latencies overlap; rows past T and past kv_len arrive as zeros (every tile row is
-  // written on every load, so no stale LDS content is ever read).
-  uint16_t* const Qs = lds + 2 * kGroupElems;
-  {
-    const int qrows = a.T - row0 < kBM ? a.T - row0 : kBM;
-    const u32x4 r = buffer_rsrc(a.q + (((int64_t)b * a.Hq + h) * a.T + row0) * kD, (uint32_t)qrows * kD * 2);
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)(Qs + 16 * wave * kD);
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t row = (uint32_t)(16 * wave + 4 * i + r4);
-      dma16<0>(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
-    }
-  }
-  // The light rows' Q (pairs): rows 0-63 in group 0's second V tile, rows 64-127 in group
-  // 1's, swizzled as the heavy rows; those tiles are first loaded by the groups' first
-  // softmax steps, after group 0 has read its Q^T operand from them.
-  auto light_q = [&](int r) __attribute__((always_inline)) { return lds + (r >> 6) * kGroupElems + 3 * kTile + (r & 63) * kD; };
-  if (has_light && nblk_l > 0) {
-    const int qrows = a.T - row0A < kBM ? a.T - row0A : kBM;
-    const u32x4 r = buffer_rsrc(a.q + (((int64_t)b * a.Hq + h) * a.T + row0A) * kD, (uint32_t)qrows * kD * 2);
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void*)light_q(16 * wave);
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t row = (uint32_t)(16 * wave + 4 * i + r4);
-      dma16<0>(r, row * kD * 2 + (uint32_t)((p16 ^ (4 * i + r4)) * 16), dst + 4 * i * kD * 2);
-    }
-  }
-  if (ng > 0) {
-    load_k(0);
-    load_v(0);
-    load_k(1);
-  }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  // Prologue, part 2: this group's first tiles (K of blocks 0 and 1, V of block 0; zero
+  // fills past the stream, so the count is fixed). The first matrix step reads Q and K of
+  // block 0 only: the wait leaves the last 8 loads in flight, and the first softmax step's
+  // wait (before the barrier that precedes the second matrix step) covers them.
+  load_k(0);
+  load_v(0);
+  load_k(1);
+  __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
   __syncthreads();
 
   // Q^T as B operand: step s covers dims 16s + 8*hh .. +7 of row 32wq + (lane & 31). Q is
