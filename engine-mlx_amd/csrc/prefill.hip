@@ -94,9 +94,10 @@ __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
 // at each barrier and before each LDS read.
 template <int I>
 __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+  // lds_addr is wave-uniform; readfirstlane keeps it in a scalar register for M0
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen offset:%3 lds"
                :
-               : "v"(voff), "s"(rsrc), "s"(lds_addr), "i"(1024 * I)
+               : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "i"(1024 * I)
                : "memory", "m0");
 }
 // Block offset that no buffer range reaches (ranges stay below 2^31 bytes, and a per-lane
@@ -314,8 +315,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto load_v = [&](int j) __attribute__((always_inline)) { dma(Vg, v_rsrc, j, voff, Vs + (j & 1) * kTile); };
 
   // Online softmax state of this lane's row, in the log2 domain. The accumulators hold
-  // o and l relative to the base m_use (p = 2^(s - m_use)); the score MFMA starts from
-  // -m_use, so it yields s - m_use directly. m_use only changes on the slow path of the
+  // o and l relative to the base m_use (p = 2^(s - m_use)); the score MFMA chains start
+  // from -m_use (each softmax step leaves it in the score registers once it has read the
+  // scores), so they yield s - m_use directly. m_use only changes on the slow path of the
   // softmax step.
   float m_use = 0.f;
   bool seen = false;      // m_use is this row's running max (some score was finite)
@@ -400,14 +402,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   };
   auto qk = [&](int jb) __attribute__((always_inline)) {
-    f32x16 neg_m;  // the chains start from -m_use, so the scores come out relative to it
-    for (int i = 0; i < 16; ++i) neg_m[i] = -m_use;
     const uint16_t* kp = Ks + (jb & 1) * kTile + k_lane;
     // two independent accumulation chains (sub-tiles kt = 0, 1), interleaved
     for (int s = 0; s < 8; ++s) {
       const uint16_t* ks = kp + (k_x ^ (16 * s));
       for (int kt = 0; kt < 2; ++kt)
-        sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(ks + kt * 32 * kD)), qop[s], s == 0 ? neg_m : sc[kt]);
+        sc[kt] = mfma32(as_bf16x8(*(const u32x4*)(ks + kt * 32 * kD)), qop[s], sc[kt]);
     }
   };
   // Issue order of the steady-state matrix step (one wave runs it alone on its SIMD, so
@@ -541,6 +541,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       load_k(j + 2);
       load_v(j + 1);
     }
+    // the score chains of the next matrix step start from -m_use
+    for (int kt = 0; kt < 2; ++kt)
+      for (int i = 0; i < 16; ++i) sc[kt][i] = -m_use;
     // the loads of the previous softmax step (K of block j+1, V of block j) are read by
     // the next matrix step: wait for them, leaving this step's own 8 loads in flight
     // (loads complete in issue order); step 0's predecessors were waited for up front
@@ -573,6 +576,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     m_use = 0.f;
     seen = false;
     all_seen = false;
+    for (int kt = 0; kt < 2; ++kt)
+      for (int i = 0; i < 16; ++i) sc[kt][i] = 0.f;
   };
   // Segment A's rows are complete (the PV of their last block ran in the matrix step
   // before): normalise, stage the wave's 32 rows in its own rows of the Q area (whose heavy
