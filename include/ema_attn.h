@@ -75,7 +75,7 @@ extern "C" {
  * reference's FP8 cache (crates/ops/src/fp8.rs:71-92: exp = ceil(log2(amax / 448)),
  * amax = max(1e-4, max |x|) over the block, round to nearest even, saturate at 448; the
  * whole head is quantised, i.e. n_rot = 0). Decoded exactly to bf16 by the readers.
- * head_dim 128 only. Values must be finite. */
+ * head_dim 128 only, static or rotating (EMA_KV_ROTATING) caches. Values must be finite. */
 #define EMA_DTYPE_FP8_E4M3 2
 /* 4-bit affine codes (MLX "affine" quantisation, group 64, the layout of the reference's
  * int4 KV buffers, crates/serve/src/engine_ext.rs:92-129): per row of head_dim values,

@@ -212,6 +212,66 @@ def test_rotating_fp8_prefill_equals_bf16_ring(ema, ora, q_off, T, W, chunk):
     assert_close(host(o8), ora.sdpa(q, kd, vd, L, scale_of(D), True, kv_begin=lo), f"rotating fp8 prefill W={W}")
 
 
+def _fp8_ring(ema, ora, totals, W, D, seed, B=3, Hkv=4):
+    """FP8 ring over the oracle's quantisation of a chronological cache of totals.max()
+    positions; unheld rows hold code 0x7F (NaN in E4M3FN). Returns (cache, decoded K, V)."""
+    from test_gpu_fp8 import quantized_pair
+
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, int(totals.max()), D), seed=seed)
+    cache = ema.StaticCache(B, Hkv, W, D, dtype="fp8", rotating=True,
+                            k=dev(ring_any(ora, kc, totals, W, 0x7F)), v=dev(ring_any(ora, vc, totals, W, 0x7F)),
+                            k_exp=dev(ring_any(ora, ke, totals, W, 0)), v_exp=dev(ring_any(ora, ve, totals, W, 0)))
+    return cache, kd, vd
+
+
+@pytest.mark.parametrize("W", [64, 96])
+def test_rotating_fp8_decode_attends_the_window(ema, ora, W):
+    """Decode over a rotating FP8 cache attends its min(length, W) held rows, decoded
+    exactly; a read of an unheld row (NaN codes) would show."""
+    import torch
+
+    B, Hq, Hkv, D = 3, 16, 4, 128
+    N = np.array([W - 5, W + 37, 3 * W + 1], np.int32)  # tokens seen
+    say(f"rotating fp8 decode W={W} N={N.tolist()}")
+    cache, kd, vd = _fp8_ring(ema, ora, N, W, D, seed=W + 40, B=B, Hkv=Hkv)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=W + 42)
+    out = ema.decode_attention(dev(q), cache, dev(N), W)
+    torch.cuda.synchronize()
+    ref = ora.sdpa(q, kd, vd, N, scale_of(D), False, kv_begin=np.maximum(N - W, 0))
+    assert_close(host(out), ref, f"rotating fp8 decode W={W}")
+
+
+def test_rotating_fp8_fused_step_writes_the_ring_row(ema, ora):
+    """The fused step on an FP8 ring writes row offset % W (quantised as pre-attention's)
+    and attends the window: it equals pre-attention + decode attention on the same ring,
+    and only that row changes."""
+    import torch
+
+    B, Hq, Hkv, D, W = 3, 16, 4, 128, 64
+    off = np.array([W - 1, W + 10, 2 * W + 63], np.int32)
+    say(f"rotating fp8 fused step W={W} off={off.tolist()}")
+    qkv = ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=53)
+    qw = ora.normal_bf16(D, seed=54, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=55, mean=1.0, std=0.02)
+    c_f, _, _ = _fp8_ring(ema, ora, off, W, D, seed=51, B=B, Hkv=Hkv)
+    c_p, _, _ = _fp8_ring(ema, ora, off, W, D, seed=51, B=B, Hkv=Hkv)
+    before = [host(t).copy() for t in (c_f.k, c_f.k_exp, c_f.v, c_f.v_exp)]
+    fused = ema.decode_step(dev(qkv), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c_f, W)
+    q = ema.pre_attention(dev(qkv.reshape(B, 1, -1)), dev(qw), dev(kw), 1e-6, 1e6, dev(off), Hq, c_p)
+    pair = ema.decode_attention(q, c_p, dev(off + 1), W)
+    torch.cuda.synchronize()
+    after = [host(t) for t in (c_f.k, c_f.k_exp, c_f.v, c_f.v_exp)]
+    for x, y in zip(after, [host(t) for t in (c_p.k, c_p.k_exp, c_p.v, c_p.v_exp)]):
+        assert np.array_equal(x, y), "fused and pre-attention write the same ring rows"
+    assert_close(host(fused), host(pair), "fp8 ring fused vs pair", max_abs=1e-2, mean_abs=1e-4)
+    for b in range(B):
+        r = int(off[b]) % W
+        others = np.r_[0:r, r + 1:W]
+        for x, y in zip(before, after):
+            assert np.array_equal(x[b][:, others], y[b][:, others]), "rows other than offset % W"
+        assert not np.array_equal(before[2][b][:, r], after[2][b][:, r]), "the ring row was written"
+
+
 def _int4_ring(ema, ora, big_bf16, totals, W):
     """int4 ring over the oracle's quantisation of a chronological bf16 cache; unheld rows
     hold all-ones code words, NaN scales and +inf biases. Returns (cache, MLX-dequantized
