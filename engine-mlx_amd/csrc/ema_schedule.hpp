@@ -61,6 +61,33 @@ EMA_HD int64_t prefill_grid(int B, int Hq, int nqb, int paired) {
   return (int64_t)(paired ? (nqb + 1) / 2 : nqb) * B * Hq;
 }
 
+// Block streams of a prefill workgroup's two wave groups. A query block attends the
+// 64-key blocks [blk_begin, blk_begin + n) of its key range; the heavy block has nblk_h
+// of them, the light block of a pair nblk_l <= nblk_h (0 without a light block: a single
+// block, or an empty range). Group 0 streams segment A, the light rows over all their
+// blocks [0, n1), then segment B, the heavy rows over [gbB, gbB + nB) = [0, nh0); group 1
+// streams segment B only, the heavy rows over the rest [nh0, nblk_h). Group 0 thus takes
+// prefill_group0_blocks of the pair's blocks and group 1 the others (as many, or one
+// fewer), and the heavy rows' two partial states meet in the merge. Block indices are
+// relative to blk_begin.
+struct PrefillStream {
+  int n1;   // segment A's blocks (group 0 of a pair only)
+  int gbB;  // segment B's first block
+  int nB;   // segment B's blocks
+};
+
+EMA_HD int prefill_group0_blocks(int nblk_h, int nblk_l) { return (nblk_l + nblk_h + 1) / 2; }
+
+EMA_HD PrefillStream prefill_stream(int g, int nblk_h, int nblk_l) {
+  const int n0 = prefill_group0_blocks(nblk_h, nblk_l);
+  const int nh0 = n0 - nblk_l;  // heavy blocks of group 0
+  PrefillStream s;
+  s.n1 = g == 0 ? nblk_l : 0;
+  s.gbB = g == 0 ? 0 : nh0;
+  s.nB = g == 0 ? nh0 : nblk_h - nh0;
+  return s;
+}
+
 // ------------------------------------------------------------------ decode split
 // The valid rows of every (sequence b, kv head kh) pair form a segment of ceil(len/32)
 // tiles; segments are laid end to end (sequence-major, then kv head) and the flattened

@@ -200,12 +200,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // the rest in group 1). Without a light block group 0 takes the first half.
   const int nblk_h = blocks_of(qb_h);
   const int nblk_l = has_light ? blocks_of(qb_l) : 0;   // <= nblk_h
-  const int n0 = (nblk_l + nblk_h + 1) / 2;               // blocks of group 0
-  const int nh0 = n0 - nblk_l;                            // heavy blocks of group 0
-  const int n1 = kPair && g == 0 ? nblk_l : 0;            // segment A
+  const int n0 = prefill_group0_blocks(nblk_h, nblk_l);   // blocks of group 0
+  const PrefillStream ps = prefill_stream(g, nblk_h, nblk_l);
+  const int n1 = kPair ? ps.n1 : 0;                       // segment A
   const int gbA = blk_begin;
-  const int gbB = blk_begin + (g ? nh0 : 0);              // first block of segment B
-  const int nB = g ? nblk_h - nh0 : nh0;
+  const int gbB = blk_begin + ps.gbB;                     // first block of segment B
+  const int nB = ps.nB;
   const int ng = n1 + nB;                                 // blocks of this wave's stream
   // stream block j: in segment A (tag SegAny: decided from j), and its absolute block index
   auto in_a = [&](int j, auto seg) __attribute__((always_inline)) {

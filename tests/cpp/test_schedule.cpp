@@ -3,7 +3,8 @@
 //  - prefill: every (sequence, query head, query block) is run by exactly one workgroup,
 //    paired or not, with and without the XCD grouping; the heavy block of a pair runs
 //    first; with the XCD grouping every item of a (sequence, kv head) group lands on the
-//    group's XCD; ranks run heaviest first;
+//    group's XCD; ranks run heaviest first; inside a workgroup the two wave groups' block
+//    streams see each (row set, key block) once and stay balanced;
 //  - decode split: the worker slices tile [0, total) exactly once, split_worker_of
 //    inverts split_begin, the merge's slot range [w0, w1] of every segment is exactly the
 //    set of slices that intersect it, and the partial-state slots (w + segment) of split
@@ -152,8 +153,39 @@ static void test_decode() {
               cases);
 }
 
+// The two wave groups' block streams of a prefill workgroup (prefill_stream): the light
+// rows see each of their blocks once (group 0), the heavy rows each of theirs once (group
+// 0's head, group 1's tail, no block twice or missed), group 0 runs
+// prefill_group0_blocks of them and group 1 as many or one fewer, so both groups run the
+// same number of matrix steps.
+static void test_prefill_streams() {
+  int cases = 0;
+  for (int nh = 0; nh <= 80; ++nh)
+    for (int nl = 0; nl <= nh; ++nl) {
+      const int n0 = prefill_group0_blocks(nh, nl);
+      const PrefillStream s0 = prefill_stream(0, nh, nl), s1 = prefill_stream(1, nh, nl);
+      CHECK(s0.n1 == nl && s1.n1 == 0, "nh=%d nl=%d: segment A (%d, %d)", nh, nl, s0.n1, s1.n1);
+      CHECK(s0.n1 + s0.nB == n0, "nh=%d nl=%d: group 0 runs %d blocks, not %d", nh, nl, s0.n1 + s0.nB, n0);
+      CHECK(s1.nB >= 0 && s0.nB >= 0, "nh=%d nl=%d: negative segment", nh, nl);
+      CHECK(s1.nB == n0 || s1.nB == n0 - 1 || (nh + nl == 0 && s1.nB == 0),
+            "nh=%d nl=%d: group 1 runs %d blocks against %d", nh, nl, s1.nB, n0);
+      std::vector<int> heavy(nh, 0);
+      for (int j = 0; j < s0.nB; ++j) ++heavy[s0.gbB + j];
+      for (int j = 0; j < s1.nB; ++j) {
+        CHECK(s1.gbB + j < nh, "nh=%d nl=%d: group 1 block %d past the range", nh, nl, s1.gbB + j);
+        ++heavy[s1.gbB + j];
+      }
+      for (int j = 0; j < nh; ++j) CHECK(heavy[j] == 1, "nh=%d nl=%d: heavy block %d seen %d times", nh, nl, j, heavy[j]);
+      CHECK(s0.gbB == 0 && s1.gbB == s0.nB, "nh=%d nl=%d: segment B bounds", nh, nl);
+      ++cases;
+    }
+  std::printf("prefill streams: %d (heavy, light) block counts: each block of each row set once, groups balanced\n",
+              cases);
+}
+
 int main() {
   test_prefill();
+  test_prefill_streams();
   test_decode();
   std::printf("%d checks passed\n", g_checks);
   return 0;
