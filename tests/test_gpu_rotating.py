@@ -153,6 +153,33 @@ def test_rotating_prefill_window(ema, ora, q_off, T, W, chunk):
     assert_close(host(out), ref, f"prefill W={W}")
 
 
+@pytest.mark.parametrize("q_off,chunk", [
+    ((0, 300, 1500, 2100), False),  # one sequence without a wrap, three wrapping
+    ((100, 1200, 40, 2500), True),  # chunk-only keys
+])
+def test_rotating_prefill_paired(ema, ora, q_off, chunk):
+    """A rotating-cache prefill large enough for the paired grid (B 4 x 16 query heads x 8
+    query blocks = 512 blocks, two per CU on MI355X): each workgroup streams a light and a
+    heavy query block over ring rows."""
+    import torch
+
+    B, Hq, Hkv, D, T, W = 4, 16, 4, 128, 1000, 1024
+    qo = np.asarray(q_off, np.int32)
+    L = qo + T
+    say(f"rotating paired prefill W={W} q_off={qo.tolist()} T={T} chunk_only={chunk}")
+    big_k = ora.normal_bf16((B, Hkv, int(L.max()), D), seed=71)
+    big_v = ora.normal_bf16((B, Hkv, int(L.max()), D), seed=72)
+    q = ora.normal_bf16((B, Hq, T, D), seed=73)
+    cache = ring_cache(ema, ring_from(ora, big_k, L, W), ring_from(ora, big_v, L, W))
+    out = ema.prefill_attention(dev(q), cache, dev(qo), causal=True, chunk_only=chunk)
+    torch.cuda.synchronize()
+    lo = np.maximum(L - W, 0)
+    if chunk:
+        lo = np.maximum(lo, qo)
+    ref = ora.sdpa(q, big_k, big_v, L, scale_of(D), True, kv_begin=lo)
+    assert_close(host(out), ref, f"paired rotating prefill chunk_only={chunk}")
+
+
 def test_rotating_prefill_without_wrap_equals_static(ema, ora):
     import torch
 
