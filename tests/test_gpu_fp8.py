@@ -322,3 +322,26 @@ def test_fp8_prefill_equals_bf16_prefill_of_decoded_cache(ema, ora, T, q_off, ca
     kb = qo if chunk else None
     ref = ora.sdpa(q, kd, vd, kv_len, scale_of(D), causal, kv_begin=kb)
     assert_close(host(o8), ref, "fp8 prefill vs oracle")
+
+
+def test_fp8_prefill_paired(ema, ora):
+    """The FP8 prefill at a paired grid (B 4 x 16 query heads x 8 query blocks = 512 blocks,
+    two per CU on MI355X): the paired kernel over the decoded rows in the workspace, whose
+    row count (max_kv_len) differs from the cache's capacity. Bit-identical to the bf16
+    cache of the decoded values, within the bf16 tolerance of the oracle."""
+    import torch
+
+    B, Hkv, G, D, cap, T = 4, 4, 4, 128, 2048, 1000
+    Hq = G * Hkv
+    qo = np.array([0, 300, 48, 1000], np.int32)
+    say(f"fp8 paired prefill B={B} Hq={Hq} T={T} q_off={qo.tolist()}")
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, cap, D), seed=881)
+    q = ora.normal_bf16((B, Hq, T, D), seed=883)
+    c8 = fp8_cache(ema, kc, ke, vc, ve)
+    c16 = ema.StaticCache(B, Hkv, cap, D, k=dev(kd), v=dev(vd))
+    o8 = ema.prefill_attention(dev(q), c8, dev(qo), causal=True, max_kv_len=int((qo + T).max()))
+    o16 = ema.prefill_attention(dev(q), c16, dev(qo), causal=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(o8), host(o16)), "decoded fp8 rows == the bf16 cache"
+    ref = ora.sdpa(q, kd, vd, (qo + T).astype(np.int32), scale_of(D), True)
+    assert_close(host(o8), ref, "fp8 paired prefill vs oracle")
