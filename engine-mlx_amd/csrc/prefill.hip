@@ -13,8 +13,9 @@
 // 32 rows, each group streaming its own 64-key K/V blocks through its own
 // double-buffered LDS. The two partial (o, m, l) states of a row meet in LDS at the end.
 // Halving the key range halves the longest causal work item, and workgroups are
-// dispatched heaviest first, so the short ones fill in behind the long ones (or, with
-// two or more query blocks per CU, each workgroup runs a heavy and a light block).
+// dispatched heaviest first, so the short ones fill in behind the long ones. With two or
+// more query blocks per CU, each workgroup owns a heavy and a light block of one head and
+// runs them as one block stream per group (prefill_kernel<*, true>, described there).
 //
 // Both contractions run on MFMA 32x32x16 (bf16 in, f32 accumulate), in the transposed
 // form that keeps the softmax lane-local:
