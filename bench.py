@@ -207,28 +207,72 @@ def cpu_baseline(state, seconds):
     }
 
 
+def cpu_baseline_b1(seconds):
+    """The oracle's f32 SDPA (OpenMP) on the batch-1 Qwen3-1.7B-shape decode attention:
+    16 query / 8 kv heads, head_dim 128, cache capacity 4096 with 1024 valid positions,
+    q/K/V ~ N(0,1) from seeds, scale 1/sqrt(128)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    B, Hq, Hkv, D, cap, L = 1, 16, 8, 128, 4096, 1024
+    q = oracle.normal_bf16((B, Hq, 1, D), seed=11)
+    kc = oracle.normal_bf16((B, Hkv, cap, D), seed=12)
+    vc = oracle.normal_bf16((B, Hkv, cap, D), seed=13)
+    lens = np.full(B, L, np.int32)
+    by = decode_bytes([L], Hq, Hkv, D)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t = time.perf_counter()
+        oracle.sdpa(q, kc, vc, lens, 1.0 / math.sqrt(D), False, precision=1)
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() > t_end or len(times) >= 2000:
+            break
+    med = statistics.median(times)
+    return {
+        "value": by / med / 1e9, "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
+        "us_per_call": med * 1e6, "workload": "decode_B1_16q8kv_L1024_cap4096",
+        "sample": f"the batch-1 decode attention, L 1024 of cap 4096 ({len(times)} runs, median "
+                  f"{med*1e6:.0f} us): oracle f32 SDPA, bf16 inputs, OpenMP over (sequence, kv head)",
+    }
+
+
 # ------------------------------------------------------------- secondary
 def prefill_flops(Hq, D, T, off):
     return 4 * Hq * D * (T * off + T * (T + 1) // 2)
 
 
-# Counter readings of prefill_kernel (rocprofv3 --pmc runs of this script's prefill
-# workloads; the commands and raw figures are in profiles/prefill_causal_T2048_32q8kv.md):
-# matrix-pipe busy fraction at 2.4 GHz, executed MFMA flops over algorithmic flops, and
-# HBM bytes per call (FETCH_SIZE x 2 + WRITE_SIZE, the copy-kernel calibration).
-PREFILL_COUNTERS = {
-    "prefill_causal_T2048_32q8kv_qwen3_8b": {"mfma_busy": 0.327, "executed_over_algorithmic": 1.095,
-                                             "traffic": 58315366},
-    "prefill_chunk_off14336_T2048_64q8kv": {"mfma_busy": 0.507, "executed_over_algorithmic": 1.065,
-                                            "traffic": 354643046},
-}
+def profiled_counters():
+    """Counter readings of the kernels as profiled (rocprofv3 runs of this script's
+    workloads, recorded in profiles/*.md as `bench_counters: {json}` lines, one per
+    workload): matrix-pipe busy fraction at 2.4 GHz, executed MFMA flops over algorithmic
+    flops, and HBM bytes per call (FETCH_SIZE x 2 + WRITE_SIZE, the copy-kernel
+    calibration). Keyed by workload name; each entry names its profile file."""
+    found = {}
+    pdir = os.path.join(ROOT, "profiles")
+    try:
+        names = sorted(os.listdir(pdir))
+    except OSError:
+        return found
+    for name in names:
+        if not name.endswith(".md"):
+            continue
+        for line in open(os.path.join(pdir, name)):
+            if line.startswith("bench_counters:"):
+                rec = json.loads(line.split(":", 1)[1])
+                rec["counter_source"] = "profiles/" + name
+                found[rec.pop("workload")] = rec
+    return found
 
 
 def prefill_roofline(name, tf, fl):
     roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops_per_call": fl}
-    if name in PREFILL_COUNTERS:
-        roof.update(PREFILL_COUNTERS[name], counter_source="profiles/prefill_causal_T2048_32q8kv.md")
+    rec = profiled_counters().get(name)
+    if rec:
+        roof.update(rec)
     return roof
 
 
@@ -588,11 +632,14 @@ def main():
         secondary.append(bench_qmm(ctx, ema, "qmatmul_qkv_M32_K4096_N6144_8bit_g64", 32, 6144, 4096, bits=8))
         secondary.append(bench_qmm(ctx, ema, "qmatmul_qkv_prefill_M2048_K2048_N4096_4bit_g64", 2048, 4096, 2048,
                                    steps=8))
-    cpu = None
+    cpu = cpu_b1 = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle f32 SDPA on the host)")
         cpu = cpu_baseline(state, args.cpu_seconds)
         log(f"[bench] CPU baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+        cpu_b1 = cpu_baseline_b1(min(args.cpu_seconds, 3.0))
+        log(f"[bench] CPU baseline, batch-1 decode: {cpu_b1['us_per_call']:.0f} us per call, "
+            f"{cpu_b1['value']:.2f} GB/s on {cpu_b1['cores']} threads")
     line = {
         "metric": METRIC,
         "value": round(res["step_gbs"], 2),
@@ -619,6 +666,7 @@ def main():
             "call_us": round(res["call_ms"] * 1e3, 2), "call_bytes": res["step_bytes"],
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_decode_b1": cpu_b1,
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
