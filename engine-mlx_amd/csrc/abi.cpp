@@ -105,8 +105,12 @@ int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
 // states), one copy per device, held until the process ends. In host code `scratch` is only
 // a stand-in for the symbol: its device address comes from hipGetSymbolAddress, looked up
 // once per device with that device current, and only that address is passed to kernels.
-// The decode kernels write every byte they later read, so nothing needs clearing; calls
-// that overlap on one device share the array and race.
+// Its first EMA_DECODE_COUNTER_BYTES hold the split's arrival counters, which must read
+// zero when a call starts: a __device__ array is zero when the library is loaded, and every
+// call returns each counter it uses to zero before it ends (the last workgroup to arrive at
+// a counter resets it). The rest (the tile prefix and the partial states) is written before
+// it is read within each call, so it needs no clearing. Calls that overlap on one device
+// share the array and race.
 __device__ __align__(256) unsigned char scratch[EMA_NOALLOC_SCRATCH_BYTES];
 std::atomic<void*> g_scratch_addr[kMaxDevices];
 std::mutex g_scratch_mu;
@@ -466,9 +470,16 @@ static int32_t check_prefill(const char* op, const void* q, const ema_kvcache_de
   return EMA_OK;
 }
 
+// Rows of the bf16 copy an FP8 prefill decodes into: max_kv_len for a static cache (rows at
+// or past it are not attended); the whole ring for a rotating cache, whose positions sit at
+// row p % capacity once they wrap, so a copy with fewer rows would put them elsewhere.
+static int32_t prefill_copy_rows(const ema_kvcache_desc* c, int32_t max_kv_len) {
+  return (c->flags & EMA_KV_ROTATING) ? c->capacity : max_kv_len;
+}
+
 static uint64_t prefill_ws_bytes(const ema_kvcache_desc* c, int32_t max_kv_len) {
   if (c->dtype != EMA_DTYPE_FP8_E4M3) return 0;
-  return 2ull * (uint64_t)c->batch * c->n_kv_heads * (uint64_t)max_kv_len * c->head_dim * 2ull;
+  return 2ull * (uint64_t)c->batch * c->n_kv_heads * (uint64_t)prefill_copy_rows(c, max_kv_len) * c->head_dim * 2ull;
 }
 
 int32_t ema_prefill_workspace_size(const ema_kvcache_desc* cache, int32_t max_kv_len, uint64_t* bytes) {
@@ -504,23 +515,24 @@ int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_k
   if (!aligned16(workspace)) return set_error(EMA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", op);
   if ((int64_t)cache->batch * cache->n_kv_heads > 65535)
     return set_error(EMA_ERR_UNSUPPORTED, "%s: batch * n_kv_heads exceeds 65535", op);
-  rc = launch_fp8_to_bf16((hipStream_t)stream, *cache, q_offsets, n_tokens, flags, max_kv_len, workspace);
+  const int32_t rows = prefill_copy_rows(cache, max_kv_len);
+  rc = launch_fp8_to_bf16((hipStream_t)stream, *cache, q_offsets, n_tokens, flags, rows, workspace);
   if (rc) return rc;
-  // the bf16 copy: [B, Hkv, max_kv_len, D] K then V
+  // the bf16 copy: [B, Hkv, rows, D] K then V
   ema_kvcache_desc w{};
-  const int64_t per = (int64_t)cache->batch * cache->n_kv_heads * max_kv_len * cache->head_dim;
+  const int64_t per = (int64_t)cache->batch * cache->n_kv_heads * rows * cache->head_dim;
   w.k = workspace;
   w.v = (uint16_t*)workspace + per;
   w.batch = cache->batch;
   w.n_kv_heads = cache->n_kv_heads;
-  w.capacity = max_kv_len;
+  w.capacity = rows;
   w.head_dim = cache->head_dim;
   w.stride_pos = cache->head_dim;
-  w.stride_head = (int64_t)max_kv_len * cache->head_dim;
-  w.stride_batch = (int64_t)cache->n_kv_heads * max_kv_len * cache->head_dim;
+  w.stride_head = (int64_t)rows * cache->head_dim;
+  w.stride_batch = (int64_t)cache->n_kv_heads * rows * cache->head_dim;
   w.dtype = EMA_DTYPE_BF16;
-  // a ring stays a ring: the copy holds the cache's rows at the same row indices (all
-  // max_kv_len of them, which is the capacity once positions wrap)
+  // a ring stays a ring: the copy holds the cache's rows at the same row indices (the
+  // whole ring, so wrapped positions land where the cache holds them)
   w.flags = cache->flags & EMA_KV_ROTATING;
   return launch_prefill((hipStream_t)stream, q, w, q_offsets, n_tokens, n_heads, scale, flags, out);
 }

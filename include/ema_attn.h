@@ -119,7 +119,11 @@ extern "C" {
  * sequence that reached the capacity stays there and the caller can see it. This is the
  * reference's per-token bookkeeping (crates/serve/src/decode_compiled.rs:49,
  * `self.offset += 1` after each step) kept on the device, so that one captured graph of
- * N steps decodes N tokens per sequence with no host work in between. */
+ * N steps decodes N tokens per sequence with no host work in between. The reference keeps
+ * one offset for the whole model, shared by every layer of a token: when the layers of a
+ * model share one offsets array, only the last layer's step of each token carries this
+ * flag (an earlier layer's advance would move the later layers' write row and length);
+ * otherwise each layer needs an offsets array of its own. */
 #define EMA_STEP_ADVANCE 4u
 
 /* ema_prefill_attention flags */
@@ -310,7 +314,10 @@ EMA_API int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const 
                               float scale, uint32_t flags, void* out);
 
 /* Workspace (bytes) ema_prefill_attention_ws needs: 0 for a bf16 cache; for an FP8 cache
- * a bf16 copy of the attended rows, 2 * batch * n_kv_heads * max_kv_len * head_dim * 2. */
+ * a bf16 copy of the attended rows, 2 * batch * n_kv_heads * rows * head_dim * 2, where rows
+ * is max_kv_len for a static cache and the capacity for a rotating (EMA_KV_ROTATING) one:
+ * a ring's positions sit at row p % capacity once they wrap, so its copy holds the whole
+ * ring whatever max_kv_len says. */
 EMA_API int32_t ema_prefill_workspace_size(const ema_kvcache_desc* cache, int32_t max_kv_len,
                                            uint64_t* bytes);
 /* ema_prefill_attention for either cache format (the prefill over the reference's FP8
@@ -318,8 +325,9 @@ EMA_API int32_t ema_prefill_workspace_size(const ema_kvcache_desc* cache, int32_
  * FP8 cache's attended rows are decoded exactly into bf16 in the workspace, and the bf16
  * prefill runs over that copy, so the result equals that of a bf16 cache holding the
  * decoded values. max_kv_len: host upper bound of q_offsets[b] + n_tokens (<= capacity;
- * rows at or past it are not attended). The workspace needs no initialisation; calls that
- * share one must not overlap. */
+ * rows at or past it are not attended); for a rotating cache it only has to lie in
+ * [n_tokens, capacity], and every held row of the ring is decoded. The workspace needs no
+ * initialisation; calls that share one must not overlap. */
 EMA_API int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                                          const int32_t* q_offsets, int32_t n_tokens, int32_t n_heads,
                                          float scale, uint32_t flags, void* out, int32_t max_kv_len,

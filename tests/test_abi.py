@@ -330,6 +330,16 @@ def test_rotating_flag_is_validated(ema):
     # workspace, before any launch)
     rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d8), g, 8, 16, 0.088, 1, g, 48, g, 16)
     assert rc == ema.EMA_ERR_WORKSPACE, ema.last_error()
+    # the bf16 copy of a ring holds the whole ring whatever max_kv_len says (wrapped positions
+    # sit at row p % capacity); a static fp8 cache's copy holds max_kv_len rows
+    assert L.ema_prefill_workspace_size(ctypes.byref(d8), 48, ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 8 * 64 * 128 * 2
+    need = n.value
+    rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d8), g, 8, 16, 0.088, 1, g, 48, g, need - 16)
+    assert rc == ema.EMA_ERR_WORKSPACE and str(need) in ema.last_error()
+    d8.flags = 0
+    assert L.ema_prefill_workspace_size(ctypes.byref(d8), 48, ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 8 * 48 * 128 * 2
 
 
 def test_quantized_matmul_argument_errors(ema):

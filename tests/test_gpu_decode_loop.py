@@ -166,3 +166,131 @@ def test_rotating_loop_wraps(ema, ora):
         cur = cur + 1
     assert np.array_equal(host(off_d), cur)
     assert np.array_equal(host(cache.v), ring_from(ora, big_v, cur, W))
+
+
+def oracle_step_inplace(ora, qkv, qw, kw, kr, vr, off, Hq, Hkv, D, cap):
+    """One step of the static decode loop on the host, writing into kr / vr in place
+    (views of one sequence are contiguous, so nothing is copied). Returns the output and
+    which sequences wrote their row."""
+    B = kr.shape[0]
+    q = np.zeros((B, Hq, 1, D), np.uint16)
+    wrote = np.zeros(B, bool)
+    for b in range(B):
+        if 0 <= off[b] < cap:
+            q[b:b + 1] = ora.pre_attention(qkv[b:b + 1, None].copy(), qw, kw, 1e-6, 1e6, off[b:b + 1], Hq, Hkv,
+                                           kr[b:b + 1], vr[b:b + 1])
+            wrote[b] = True
+        else:
+            x = ora.rms_norm(qkv[b, :Hq * D].reshape(Hq, D).copy(), qw, 1e-6)
+            q[b] = ora.rope(x, np.full(Hq, off[b], np.int32), 1e6).reshape(Hq, 1, D)
+    L = np.clip(off + 1, 0, cap).astype(np.int32)
+    return ora.sdpa(q, kr, vr, L, scale_of(D), False), wrote
+
+
+def test_graph_loop_qwen3_8b_batched_shape(ema, ora):
+    """The batch-32 Qwen3-8B decode shape as a loop: 32q/8kv, capacity 8192, lengths
+    uniform in [512, 8192] (seed 1234, the bench's), one sequence two rows below the
+    capacity (it stops there mid-loop), one at it and one twelve rows below; eight steps captured in one HIP graph with EMA_STEP_ADVANCE
+    and replayed once equal the oracle's loop step by step, the offsets stop at the
+    capacity, and only the written rows change."""
+    import torch
+
+    B, Hq, Hkv, D, cap, n = 32, 32, 8, 128, 8192, 8
+    off = (np.random.default_rng(1234).integers(512, cap + 1, size=B) - 1).astype(np.int32)
+    off[[3, 17, 29]] = [cap - 12, cap - 2, cap]
+    say(f"decode loop graph at the 8B batched shape: B={B} cap={cap} steps={n} sum(L)={int((off + 1).sum())}")
+    qkvs = [ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=1900 + i) for i in range(n)]
+    qw = ora.normal_bf16(D, seed=1950, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=1951, mean=1.0, std=0.02)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=1952)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=1953)
+
+    cache = ema.StaticCache(B, Hkv, cap, D, k=dev(kc), v=dev(vc))
+    qkv_d = dev(np.stack(qkvs))
+    qw_d, kw_d, off_d = dev(qw), dev(kw), dev(off)
+    outs = torch.zeros((n, B, Hq * D), dtype=torch.bfloat16, device="cuda")
+    ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                ema.decode_step(qkv_d[i], qw_d, kw_d, 1e-6, 1e6, off_d, Hq, cache, cap, out=outs[i], workspace=ws,
+                                flags=ema.EMA_STEP_ADVANCE)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    got = host(outs)
+    gk, gv = host(cache.k), host(cache.v)
+
+    kr, vr, cur = kc.copy(), vc.copy(), off.copy()
+    for i in range(n):
+        ref, wrote = oracle_step_inplace(ora, qkvs[i], qw, kw, kr, vr, cur, Hq, Hkv, D, cap)
+        assert_close(got[i], ref, f"step {i}")
+        cur = np.where(wrote, cur + 1, cur).astype(np.int32)
+    assert np.array_equal(host(off_d), cur), "offsets after the loop"
+    assert cur[29] == cap and cur[17] == cap and cur[3] == cap - 12 + n
+    assert np.array_equal(gv, vr), "V rows: bit copies at each step's offset, the rest untouched"
+    rows = np.zeros((B, cap), bool)
+    for b in range(B):
+        rows[b, off[b]:cur[b]] = True
+    assert np.array_equal(gk[~rows[:, None, :].repeat(Hkv, 1)], kc[~rows[:, None, :].repeat(Hkv, 1)]), \
+        "K rows that no step wrote are untouched"
+    wk = rows[:, None, :].repeat(Hkv, 1)
+    assert_close(gk[wk][None], kr[wk][None], "written K rows")
+
+
+def test_two_layers_share_one_offsets_array(ema, ora):
+    """Two layers whose steps share one offsets array, the reference's one model-wide
+    offset (crates/serve/src/decode_compiled.rs:49): EMA_STEP_ADVANCE on the second
+    layer's step only. Six tokens captured in one graph (layer 0, layer 1 per token)
+    equal the oracle's loop layer by layer: both layers write their row at the same
+    offset and attend the same length, and the offset moves once per token."""
+    import torch
+
+    B, Hq, Hkv, D, cap, n = 4, 16, 8, 128, 512, 6
+    off = np.array([0, 17, cap - 3, 300], np.int32)
+    say(f"two layers, one offsets array: B={B} cap={cap} tokens={n}")
+    layers = []
+    for li in range(2):
+        qkvs = [ora.normal_bf16((B, (Hq + 2 * Hkv) * D), seed=2000 + 100 * li + i) for i in range(n)]
+        qw = ora.normal_bf16(D, seed=2050 + 100 * li, mean=1.0, std=0.02)
+        kw = ora.normal_bf16(D, seed=2051 + 100 * li, mean=1.0, std=0.02)
+        kc = ora.normal_bf16((B, Hkv, cap, D), seed=2052 + 100 * li)
+        vc = ora.normal_bf16((B, Hkv, cap, D), seed=2053 + 100 * li)
+        layers.append(dict(qkvs=qkvs, qw=qw, kw=kw, kc=kc, vc=vc,
+                           cache=ema.StaticCache(B, Hkv, cap, D, k=dev(kc), v=dev(vc)),
+                           qkv_d=dev(np.stack(qkvs)), qw_d=dev(qw), kw_d=dev(kw),
+                           ws=ema.decode_workspace(B, Hq, Hkv, D, cap),
+                           outs=torch.zeros((n, B, Hq * D), dtype=torch.bfloat16, device="cuda")))
+    off_d = dev(off)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                for li, ly in enumerate(layers):
+                    ema.decode_step(ly["qkv_d"][i], ly["qw_d"], ly["kw_d"], 1e-6, 1e6, off_d, Hq, ly["cache"], cap,
+                                    out=ly["outs"][i], workspace=ly["ws"],
+                                    flags=ema.EMA_STEP_ADVANCE if li == 1 else 0)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+
+    state = [(ly["kc"].copy(), ly["vc"].copy()) for ly in layers]
+    cur = off.copy()
+    for i in range(n):
+        wrote_all = None
+        for li, ly in enumerate(layers):
+            kr, vr = state[li]
+            ref, wrote = oracle_step_inplace(ora, ly["qkvs"][i], ly["qw"], ly["kw"], kr, vr, cur, Hq, Hkv, D, cap)
+            assert_close(host(ly["outs"][i]), ref, f"token {i} layer {li}")
+            wrote_all = wrote
+        cur = np.where(wrote_all, cur + 1, cur).astype(np.int32)
+    assert np.array_equal(host(off_d), cur), "the shared offsets moved once per token"
+    for li, ly in enumerate(layers):
+        assert np.array_equal(host(ly["cache"].v), state[li][1]), f"layer {li} V rows"

@@ -395,7 +395,8 @@ def test_prefill_paired_blocks(ema, ora, B, Hq, Hkv, T, q_off, causal, chunk):
 
 def test_prefill_chunk_on_existing_cache_every_block(ema, ora):
     """64q/8kv, 14336 cached + 2048 new (16384 capacity): all 64 heads at the first and
-    last four rows of every 128-row query block."""
+    last four rows of every 128-row query block, and every row of the first, a middle and
+    the last query block."""
     import torch
 
     B, Hq, Hkv, D, cap, T, off = 1, 64, 8, 128, 16384, 2048, 14336
@@ -413,6 +414,11 @@ def test_prefill_chunk_on_existing_cache_every_block(ema, ora):
             # r0 + i the keys <= off + r0 + i
             ref = ora.sdpa(q[:, :, r0:r0 + 4].copy(), kc, vc, [off + r0 + 4], scale_of(D), True)
             assert_close(out[r0:r0 + 4][None], ref, f"rows {r0}..{r0 + 3}")
+    for qb in (0, 8, 15):  # whole query blocks: the pair partners 0/15 and a middle one
+        r0 = qb * 128
+        say(f"prefill chunked: every row of query block {qb}")
+        ref = ora.sdpa(q[:, :, r0:r0 + 128].copy(), kc, vc, [off + r0 + 128], scale_of(D), True)
+        assert_close(out[r0:r0 + 128][None], ref, f"query block {qb}")
 
 
 @pytest.mark.parametrize("causal,chunk,q_off", [(True, True, 100), (True, True, 64), (False, True, 37),
