@@ -5,11 +5,15 @@
 //!   constant, the `ema_kvcache_desc` layout);
 //! - [`hip`]: the few HIP runtime calls the safe layer needs (device memory and copies);
 //! - the safe layer, in the shape of the reference's crates: the `KvCache` trait
-//!   (`crates/kvcache/src/lib.rs:52-76`), a static pre-allocated cache (the serve crate's
-//!   `kv_bufs` + `static_offsets`, `crates/serve/src/engine_ext.rs:266-306`),
+//!   (`crates/kvcache/src/lib.rs:52-76`) and `HipKvCache`, the caches the kernels work on
+//!   in place: a static pre-allocated cache (the serve crate's `kv_bufs` +
+//!   `static_offsets`, `crates/serve/src/engine_ext.rs:266-306`), `RotatingCache`
+//!   (`crates/kvcache/src/rotating.rs`, as a ring) and `Fp8Cache`
+//!   (`crates/kvcache/src/fp8.rs`, stored as codes + block exponents);
 //!   `QuantWeights` (`crates/ops/src/quant.rs:16-40`), `GqaConfig` / `GqaWeights` /
 //!   `gqa_attention` (`crates/attention/src/gqa.rs:27-107`) and
-//!   `sliding_window_attention` (`crates/attention/src/sliding_window.rs:40-50`).
+//!   `sliding_window_attention` (`crates/attention/src/sliding_window.rs:40-50`), both
+//!   generic over the cache as the reference's are.
 //!
 //! Arrays are device buffers ([`DeviceArray`]) instead of `mlx_array` handles, and the
 //! context ([`HipCtx`]) carries the HIP stream and a caller-sized device arena instead of
@@ -133,6 +137,9 @@ pub mod sys {
                                       head_dim: i32) -> i32;
         pub fn ema_kvcache_quantize_int4(stream: EmaStream, src: *const EmaKvCacheDesc, src_row: i32,
                                          dst: *const EmaKvCacheDesc, dst_row: i32, n_rows: i32) -> i32;
+        pub fn ema_kvcache_convert(stream: EmaStream, src: *const EmaKvCacheDesc, src_row: i32,
+                                   dst: *const EmaKvCacheDesc, dst_row: i32, n_rows: i32) -> i32;
+        pub fn ema_position_write(stream: EmaStream, slot: *mut i32, value: i32) -> i32;
         pub fn ema_kvcache_free(desc: *mut EmaKvCacheDesc) -> i32;
         pub fn ema_kvcache_memory_bytes(desc: *const EmaKvCacheDesc, bytes: *mut u64) -> i32;
         pub fn ema_pre_attention(stream: EmaStream, qkv: *const c_void, q_norm_w: *const c_void,
@@ -284,6 +291,100 @@ pub trait KvCache: Send {
     fn memory_bytes(&self) -> usize;
 }
 
+/// A [`KvCache`] the kernels read and write in place: the generic parameter of the layer
+/// functions, as the reference's `gqa_attention<C: KvCache>` (`crates/attention/src/gqa.rs:62-69`)
+/// takes any cache (its documented uses pass an `Fp8Cache` or a `RotatingCache`,
+/// `crates/attention/src/lib.rs:22-27`). The kernels write a call's new rows through the
+/// descriptor and read the first new token's position from device memory.
+pub trait HipKvCache: KvCache {
+    /// The descriptor the kernels take: buffers, strides, dtype, `EMA_KV_ROTATING`.
+    fn desc(&self) -> &sys::EmaKvCacheDesc;
+    /// Device pointer to an int32 holding `p`, valid for work enqueued on `ctx.stream`
+    /// after this call (a static cache: 0 <= p <= capacity).
+    fn position(&self, ctx: &HipCtx, p: i64) -> Result<*const i32>;
+    /// The cache now holds the tokens [0, n) (a ring: the last `capacity` of them).
+    fn set_len(&mut self, n: i64) -> Result<()>;
+    fn rotating(&self) -> bool {
+        self.desc().flags & sys::EMA_KV_ROTATING != 0
+    }
+    fn capacity(&self) -> i32 {
+        self.desc().capacity
+    }
+    fn n_kv_heads(&self) -> i32 {
+        self.desc().n_kv_heads
+    }
+    fn head_dim(&self) -> i32 {
+        self.desc().head_dim
+    }
+}
+
+/// Device table of the int32 values 0, 1, ..., n: the analogue of the pre-built
+/// `static_offsets` scalars (`crates/serve/src/engine_ext.rs:293-299`), so a step passes its
+/// offset without a host-to-device copy.
+struct PositionTable {
+    table: *mut i32,
+    n: i32,
+}
+
+impl PositionTable {
+    fn new(n: i32) -> Result<Self> {
+        if n < 0 {
+            bail!("PositionTable: negative size {}", n);
+        }
+        let values: Vec<i32> = (0..=n).collect();
+        let bytes = values.len() * std::mem::size_of::<i32>();
+        let mut p: *mut c_void = std::ptr::null_mut();
+        check_hip(unsafe { hip::hipMalloc(&mut p, bytes) }, "position table")?;
+        let table = PositionTable { table: p as *mut i32, n }; // freed by Drop on the error path
+        check_hip(
+            unsafe { hip::hipMemcpy(p, values.as_ptr() as *const c_void, bytes, hip::HIP_MEMCPY_HOST_TO_DEVICE) },
+            "position table upload",
+        )?;
+        Ok(table)
+    }
+
+    /// Device pointer to the value p, 0 <= p <= n (`cap` names the cache in the error).
+    fn at(&self, p: i64, cap: i32) -> Result<*const i32> {
+        if p < 0 || p > self.n as i64 {
+            bail!("static KV overflow offset={} cap={}", p, cap);
+        }
+        Ok(unsafe { self.table.add(p as usize) } as *const i32)
+    }
+}
+
+impl Drop for PositionTable {
+    fn drop(&mut self) {
+        if !self.table.is_null() {
+            unsafe { hip::hipFree(self.table as *mut c_void) };
+        }
+    }
+}
+
+/// Checks k and v of an append: contiguous [1, n_kv_heads, seq, head_dim], equal lengths.
+/// Returns seq.
+fn append_len(desc: &sys::EmaKvCacheDesc, k: &DeviceArray, v: &DeviceArray, op: &str) -> Result<i64> {
+    let hkv = desc.n_kv_heads as i64;
+    let d = desc.head_dim as i64;
+    for a in [k, v] {
+        if a.data.is_null() {
+            bail!("{}: null k/v", op);
+        }
+        if a.shape.len() != 4 || a.shape[0] != 1 || a.shape[1] != hkv || a.shape[3] != d || !a.strides.is_empty() {
+            bail!("{}: expected contiguous [1, {}, seq, {}], got {:?}", op, hkv, d, a.shape);
+        }
+    }
+    if k.shape[2] != v.shape[2] {
+        bail!("{}: k/v lengths differ", op);
+    }
+    Ok(k.shape[2])
+}
+
+fn memory_bytes_of(desc: &sys::EmaKvCacheDesc) -> usize {
+    let mut b: u64 = 0;
+    unsafe { sys::ema_kvcache_memory_bytes(desc, &mut b) };
+    b as usize
+}
+
 /// Static pre-allocated bf16 cache of one layer, [1, Hkv, capacity, head_dim], allocated
 /// zeroed once and reused (`alloc_kv_static`, `crates/serve/src/engine_ext.rs:266-306`):
 /// `reset` rewinds the length only. It also holds the device table 0..=capacity, the
@@ -292,93 +393,36 @@ pub trait KvCache: Send {
 pub struct StaticCache {
     desc: sys::EmaKvCacheDesc,
     offset: i32,
-    positions: *mut i32,
+    positions: PositionTable,
 }
 
 unsafe impl Send for StaticCache {}
 
 impl StaticCache {
     pub fn new(n_kv_heads: i32, capacity: i32, head_dim: i32) -> Result<Self> {
+        let positions = PositionTable::new(capacity.max(0))?;
         let mut desc = sys::EmaKvCacheDesc::default();
         check(unsafe { sys::ema_kvcache_alloc(&mut desc, 1, n_kv_heads, capacity, head_dim) }, "kvcache_alloc")?;
-        let table: Vec<i32> = (0..=capacity).collect();
-        let bytes = table.len() * std::mem::size_of::<i32>();
-        let mut p: *mut c_void = std::ptr::null_mut();
-        let rc = unsafe { hip::hipMalloc(&mut p, bytes) };
-        let rc = if rc == hip::HIP_SUCCESS {
-            unsafe { hip::hipMemcpy(p, table.as_ptr() as *const c_void, bytes, hip::HIP_MEMCPY_HOST_TO_DEVICE) }
-        } else {
-            rc
-        };
-        if rc != hip::HIP_SUCCESS {
-            unsafe {
-                if !p.is_null() {
-                    hip::hipFree(p);
-                }
-                sys::ema_kvcache_free(&mut desc);
-            }
-            check_hip(rc, "StaticCache: positions")?;
-        }
-        Ok(StaticCache { desc, offset: 0, positions: p as *mut i32 })
-    }
-
-    pub fn capacity(&self) -> i32 {
-        self.desc.capacity
-    }
-    pub fn n_kv_heads(&self) -> i32 {
-        self.desc.n_kv_heads
-    }
-    pub fn head_dim(&self) -> i32 {
-        self.desc.head_dim
-    }
-    pub fn desc(&self) -> &sys::EmaKvCacheDesc {
-        &self.desc
+        Ok(StaticCache { desc, offset: 0, positions })
     }
 
     /// Device pointer to the int32 value p, 0 <= p <= capacity.
     pub fn device_position(&self, p: i32) -> Result<*const i32> {
-        if p < 0 || p > self.desc.capacity {
-            bail!("static KV overflow offset={} cap={}", p, self.desc.capacity);
-        }
-        Ok(unsafe { self.positions.add(p as usize) } as *const i32)
-    }
-
-    fn set_len(&mut self, n: i64) -> Result<()> {
-        if n < 0 || n > self.desc.capacity as i64 {
-            bail!("static KV overflow offset={} cap={}", n, self.desc.capacity);
-        }
-        self.offset = n as i32;
-        Ok(())
+        self.positions.at(p as i64, self.desc.capacity)
     }
 }
 
 impl Drop for StaticCache {
     fn drop(&mut self) {
-        unsafe {
-            sys::ema_kvcache_free(&mut self.desc);
-            if !self.positions.is_null() {
-                hip::hipFree(self.positions as *mut c_void);
-            }
-        }
+        unsafe { sys::ema_kvcache_free(&mut self.desc) };
     }
 }
 
 impl KvCache for StaticCache {
     fn append(&mut self, ctx: &HipCtx, k: &DeviceArray, v: &DeviceArray) -> Result<()> {
-        let hkv = self.desc.n_kv_heads as i64;
+        let t = append_len(&self.desc, k, v, "StaticCache::append")?;
+        let hkv = self.desc.n_kv_heads as usize;
         let d = self.desc.head_dim as i64;
-        for a in [k, v] {
-            if a.data.is_null() {
-                bail!("StaticCache::append: null k/v");
-            }
-            if a.shape.len() != 4 || a.shape[0] != 1 || a.shape[1] != hkv || a.shape[3] != d || !a.strides.is_empty() {
-                bail!("StaticCache::append: expected contiguous [1, {}, seq, {}], got {:?}", hkv, d, a.shape);
-            }
-        }
-        if k.shape[2] != v.shape[2] {
-            bail!("StaticCache::append: k/v lengths differ");
-        }
-        let t = k.shape[2];
         if self.offset as i64 + t > self.desc.capacity as i64 {
             bail!("static KV overflow offset={} cap={}", self.offset as i64 + t, self.desc.capacity);
         }
@@ -389,7 +433,7 @@ impl KvCache for StaticCache {
             check_hip(
                 unsafe {
                     hip::hipMemcpy2DAsync(at as *mut c_void, self.desc.stride_head as usize * 2, src, width, width,
-                                          hkv as usize, hip::HIP_MEMCPY_DEVICE_TO_DEVICE, ctx.stream)
+                                          hkv, hip::HIP_MEMCPY_DEVICE_TO_DEVICE, ctx.stream)
                 },
                 "StaticCache::append copy",
             )?;
@@ -419,9 +463,306 @@ impl KvCache for StaticCache {
     }
 
     fn memory_bytes(&self) -> usize {
-        let mut b: u64 = 0;
-        unsafe { sys::ema_kvcache_memory_bytes(&self.desc, &mut b) };
-        b as usize
+        memory_bytes_of(&self.desc)
+    }
+}
+
+impl HipKvCache for StaticCache {
+    fn desc(&self) -> &sys::EmaKvCacheDesc {
+        &self.desc
+    }
+    fn position(&self, _ctx: &HipCtx, p: i64) -> Result<*const i32> {
+        self.positions.at(p, self.desc.capacity)
+    }
+    fn set_len(&mut self, n: i64) -> Result<()> {
+        if n < 0 || n > self.desc.capacity as i64 {
+            bail!("static KV overflow offset={} cap={}", n, self.desc.capacity);
+        }
+        self.offset = n as i32;
+        Ok(())
+    }
+}
+
+/// Rotating (sliding-window) bf16 cache of one layer: the reference's `RotatingCache`
+/// (`crates/kvcache/src/rotating.rs:22-122`), which keeps the last `window_size` tokens,
+/// held as a ring [1, Hkv, window_size, head_dim] (`EMA_KV_ROTATING`): the token at
+/// position p lives in row p % window_size, so an append writes rows in place instead of
+/// concatenating and slicing. `len()` = min(tokens seen, window_size) (rotating.rs:108-110).
+/// The layer calls write the ring rows themselves and attend the window.
+pub struct RotatingCache {
+    desc: sys::EmaKvCacheDesc,
+    total: i64,
+    slot: *mut i32,
+}
+
+unsafe impl Send for RotatingCache {}
+
+impl RotatingCache {
+    /// `RotatingCache::new(window_size, n_kv_heads, head_dim)` (rotating.rs:41-51); the
+    /// ring is allocated zeroed here.
+    pub fn new(window_size: usize, n_kv_heads: usize, head_dim: usize) -> Result<Self> {
+        let w = i32::try_from(window_size)?;
+        let hkv = i32::try_from(n_kv_heads)?;
+        let hd = i32::try_from(head_dim)?;
+        let mut slot: *mut c_void = std::ptr::null_mut();
+        check_hip(unsafe { hip::hipMalloc(&mut slot, std::mem::size_of::<i32>()) }, "RotatingCache: position slot")?;
+        let mut cache = RotatingCache { desc: sys::EmaKvCacheDesc::default(), total: 0, slot: slot as *mut i32 };
+        check(unsafe { sys::ema_kvcache_alloc(&mut cache.desc, 1, hkv, w, hd) }, "kvcache_alloc")?;
+        cache.desc.flags = sys::EMA_KV_ROTATING;
+        Ok(cache)
+    }
+
+    pub fn window_size(&self) -> usize {
+        self.desc.capacity as usize
+    }
+
+    /// Tokens seen since the last reset (may exceed the window).
+    pub fn total_len(&self) -> i64 {
+        self.total
+    }
+}
+
+impl Drop for RotatingCache {
+    fn drop(&mut self) {
+        unsafe {
+            sys::ema_kvcache_free(&mut self.desc);
+            if !self.slot.is_null() {
+                hip::hipFree(self.slot as *mut c_void);
+            }
+        }
+    }
+}
+
+impl KvCache for RotatingCache {
+    /// Appends at positions [total, total + T); with T > window_size only the last
+    /// window_size tokens are kept (rotating.rs:81-92).
+    fn append(&mut self, ctx: &HipCtx, k: &DeviceArray, v: &DeviceArray) -> Result<()> {
+        let t_all = append_len(&self.desc, k, v, "RotatingCache::append")?;
+        let hkv = self.desc.n_kv_heads as usize;
+        let d = self.desc.head_dim as i64;
+        let w = self.desc.capacity as i64;
+        // tokens [skip, T) at positions total + t: one or two runs of consecutive ring rows
+        let mut t = if t_all > w { t_all - w } else { 0 };
+        while t < t_all {
+            let row = (self.total + t) % w;
+            let n = (t_all - t).min(w - row);
+            let width = (n * d * 2) as usize;
+            for (dst, src) in [(self.desc.k, k.data), (self.desc.v, v.data)] {
+                let at = unsafe { (dst as *mut u8).add(row as usize * self.desc.stride_pos as usize * 2) };
+                let from = unsafe { (src as *const u8).add((t * d * 2) as usize) };
+                check_hip(
+                    unsafe {
+                        hip::hipMemcpy2DAsync(at as *mut c_void, self.desc.stride_head as usize * 2,
+                                              from as *const c_void, (t_all * d * 2) as usize, width, hkv,
+                                              hip::HIP_MEMCPY_DEVICE_TO_DEVICE, ctx.stream)
+                    },
+                    "RotatingCache::append copy",
+                )?;
+            }
+            t += n;
+        }
+        self.total += t_all;
+        Ok(())
+    }
+
+    /// The held tokens in order, [1, Hkv, len, head_dim]: the ring itself until it wraps,
+    /// then a rotated copy in `ctx`'s arena (2 * Hkv * window * head_dim * 2 bytes; valid
+    /// until the next call that uses the arena).
+    fn get(&self, ctx: &HipCtx) -> Result<(DeviceArray, DeviceArray)> {
+        if self.total == 0 {
+            bail!("Rotating KV cache is empty");
+        }
+        let hkv = self.desc.n_kv_heads as i64;
+        let d = self.desc.head_dim as i64;
+        let w = self.desc.capacity as i64;
+        let shape = vec![1, hkv, self.len() as i64, d];
+        if self.total <= w {
+            let strides = vec![self.desc.stride_batch, self.desc.stride_head, self.desc.stride_pos, 1];
+            return Ok((
+                DeviceArray { data: self.desc.k, shape: shape.clone(), strides: strides.clone() },
+                DeviceArray { data: self.desc.v, shape, strides },
+            ));
+        }
+        // wrapped: the oldest token is in row total % W; copy rows [start, W), then [0, start)
+        let mut arena = Arena::new(ctx);
+        let half = (hkv * w * d * 2) as usize;
+        let buf = arena.take(2 * half) as *mut u8;
+        arena.check("RotatingCache::get")?;
+        let start = self.total % w;
+        let pitch_src = self.desc.stride_head as usize * 2;
+        let pitch_dst = (w * d * 2) as usize;
+        for (i, src) in [self.desc.k, self.desc.v].into_iter().enumerate() {
+            let dst = buf.wrapping_add(i * half);
+            let src = src as *const u8;
+            check_hip(
+                unsafe {
+                    hip::hipMemcpy2DAsync(dst as *mut c_void, pitch_dst,
+                                          src.wrapping_add(start as usize * self.desc.stride_pos as usize * 2)
+                                              as *const c_void,
+                                          pitch_src, ((w - start) * d * 2) as usize, hkv as usize,
+                                          hip::HIP_MEMCPY_DEVICE_TO_DEVICE, ctx.stream)
+                },
+                "RotatingCache::get copy",
+            )?;
+            if start > 0 {
+                check_hip(
+                    unsafe {
+                        hip::hipMemcpy2DAsync(dst.wrapping_add(((w - start) * d * 2) as usize) as *mut c_void,
+                                              pitch_dst, src as *const c_void, pitch_src, (start * d * 2) as usize,
+                                              hkv as usize, hip::HIP_MEMCPY_DEVICE_TO_DEVICE, ctx.stream)
+                    },
+                    "RotatingCache::get copy",
+                )?;
+            }
+        }
+        Ok((
+            DeviceArray::new(buf as *mut c_void, &shape),
+            DeviceArray::new(buf.wrapping_add(half) as *mut c_void, &shape),
+        ))
+    }
+
+    fn len(&self) -> usize {
+        self.total.min(self.desc.capacity as i64) as usize
+    }
+
+    fn reset(&mut self) {
+        self.total = 0;
+    }
+
+    fn memory_bytes(&self) -> usize {
+        memory_bytes_of(&self.desc)
+    }
+}
+
+impl HipKvCache for RotatingCache {
+    fn desc(&self) -> &sys::EmaKvCacheDesc {
+        &self.desc
+    }
+    /// The cache's one device slot, rewritten with `p` on `ctx.stream`
+    /// (`ema_position_write`: stream-ordered, so a later call rewrites it only after the
+    /// work that read it).
+    fn position(&self, ctx: &HipCtx, p: i64) -> Result<*const i32> {
+        if p < 0 || p > i32::MAX as i64 {
+            bail!("rotating KV position {} out of range", p);
+        }
+        check(unsafe { sys::ema_position_write(ctx.stream, self.slot, p as i32) }, "position_write")?;
+        Ok(self.slot as *const i32)
+    }
+    fn set_len(&mut self, n: i64) -> Result<()> {
+        if n < 0 {
+            bail!("rotating KV length {} out of range", n);
+        }
+        self.total = n;
+        Ok(())
+    }
+}
+
+/// FP8 E4M3FN cache of one layer: the reference's `Fp8Cache` (`crates/kvcache/src/fp8.rs:27-91`,
+/// which keeps the E4M3FN round trip of every 64-value block of each K/V row), stored as one
+/// code byte per value plus one exponent byte per block (`ema_kvcache_alloc_fp8`), allocated
+/// zeroed once with a static capacity; `reset` rewinds the length only. The layer calls
+/// quantise the rows they write and attend the decoded values. `n_rot` (the reference's
+/// unquantised RoPE tail of each head) must be 0; head_dim 128.
+pub struct Fp8Cache {
+    desc: sys::EmaKvCacheDesc,
+    offset: i32,
+    positions: PositionTable,
+}
+
+unsafe impl Send for Fp8Cache {}
+
+impl Fp8Cache {
+    pub fn new(n_kv_heads: i32, capacity: i32, head_dim: i32, n_rot: i32) -> Result<Self> {
+        if n_rot != 0 {
+            bail!("Fp8Cache: n_rot {} (an unquantised RoPE tail) is not supported; the whole head is quantised",
+                  n_rot);
+        }
+        let positions = PositionTable::new(capacity.max(0))?;
+        let mut desc = sys::EmaKvCacheDesc::default();
+        check(unsafe { sys::ema_kvcache_alloc_fp8(&mut desc, 1, n_kv_heads, capacity, head_dim) },
+              "kvcache_alloc_fp8")?;
+        Ok(Fp8Cache { desc, offset: 0, positions })
+    }
+}
+
+impl Drop for Fp8Cache {
+    fn drop(&mut self) {
+        unsafe { sys::ema_kvcache_free(&mut self.desc) };
+    }
+}
+
+impl KvCache for Fp8Cache {
+    /// Quantises K and V [1, Hkv, T, head_dim] bf16 into rows [len, len + T)
+    /// (`fp8_round_trip` per 64-value block, `crates/kvcache/src/fp8.rs:47-68`).
+    fn append(&mut self, ctx: &HipCtx, k: &DeviceArray, v: &DeviceArray) -> Result<()> {
+        let t = append_len(&self.desc, k, v, "Fp8Cache::append")?;
+        if self.offset as i64 + t > self.desc.capacity as i64 {
+            bail!("static KV overflow offset={} cap={}", self.offset as i64 + t, self.desc.capacity);
+        }
+        if t == 0 {
+            return Ok(());
+        }
+        // the new rows as a bf16 cache of T rows, quantised into rows [offset, offset + T)
+        let mut src = sys::EmaKvCacheDesc::default();
+        check(
+            unsafe {
+                sys::ema_kvcache_init(&mut src, k.data, v.data, 1, self.desc.n_kv_heads, t as i32, self.desc.head_dim)
+            },
+            "kvcache_init",
+        )?;
+        check(unsafe { sys::ema_kvcache_convert(ctx.stream, &src, 0, &self.desc, self.offset, t as i32) },
+              "kvcache_convert")?;
+        self.offset += t as i32;
+        Ok(())
+    }
+
+    /// The held rows decoded to bf16 (exactly the values the reference keeps),
+    /// [1, Hkv, len, head_dim] each, in `ctx`'s arena (valid until the next call that uses it).
+    fn get(&self, ctx: &HipCtx) -> Result<(DeviceArray, DeviceArray)> {
+        if self.offset == 0 {
+            bail!("FP8 KV cache is empty");
+        }
+        let hkv = self.desc.n_kv_heads;
+        let d = self.desc.head_dim;
+        let n = self.offset;
+        let bytes = hkv as usize * n as usize * d as usize * 2;
+        let mut arena = Arena::new(ctx);
+        let kb = arena.take(bytes);
+        let vb = arena.take(bytes);
+        arena.check("Fp8Cache::get")?;
+        let mut dst = sys::EmaKvCacheDesc::default();
+        check(unsafe { sys::ema_kvcache_init(&mut dst, kb, vb, 1, hkv, n, d) }, "kvcache_init")?;
+        check(unsafe { sys::ema_kvcache_convert(ctx.stream, &self.desc, 0, &dst, 0, n) }, "kvcache_convert")?;
+        let shape = [1, hkv as i64, n as i64, d as i64];
+        Ok((DeviceArray::new(kb, &shape), DeviceArray::new(vb, &shape)))
+    }
+
+    fn len(&self) -> usize {
+        self.offset as usize
+    }
+
+    fn reset(&mut self) {
+        self.offset = 0;
+    }
+
+    fn memory_bytes(&self) -> usize {
+        memory_bytes_of(&self.desc)
+    }
+}
+
+impl HipKvCache for Fp8Cache {
+    fn desc(&self) -> &sys::EmaKvCacheDesc {
+        &self.desc
+    }
+    fn position(&self, _ctx: &HipCtx, p: i64) -> Result<*const i32> {
+        self.positions.at(p, self.desc.capacity)
+    }
+    fn set_len(&mut self, n: i64) -> Result<()> {
+        if n < 0 || n > self.desc.capacity as i64 {
+            bail!("static KV overflow offset={} cap={}", n, self.desc.capacity);
+        }
+        self.offset = n as i32;
+        Ok(())
     }
 }
 
@@ -495,8 +836,8 @@ fn decode_ws_bytes(c: &GqaConfig, capacity: i32) -> Result<usize> {
 }
 
 /// Arena bytes `gqa_attention` needs for up to `max_seq_len` tokens of `hidden_size`
-/// over a cache of `capacity` rows: q|k|v rows, o_proj output, q, attention output and
-/// the decode split state.
+/// over a bf16 cache of `capacity` rows: q|k|v rows, o_proj output, q, attention output
+/// and the decode split state. [`gqa_workspace_bytes_for`] covers any cache.
 pub fn gqa_workspace_bytes(config: &GqaConfig, hidden_size: i64, max_seq_len: i32, capacity: i32) -> Result<usize> {
     let t = max_seq_len.max(1) as usize;
     let hd = (config.n_heads * config.head_dim) as usize;
@@ -506,6 +847,32 @@ pub fn gqa_workspace_bytes(config: &GqaConfig, hidden_size: i64, max_seq_len: i3
         + aligned(hd * t * 2)
         + aligned(t * hd * 2)
         + aligned(decode_ws_bytes(config, capacity)?))
+}
+
+/// [`gqa_workspace_bytes`] for `cache`: an FP8 cache's prefill also needs the bf16 copy of
+/// the rows it attends (`ema_prefill_workspace_size` over the whole capacity).
+pub fn gqa_workspace_bytes_for<C: HipKvCache>(config: &GqaConfig, hidden_size: i64, max_seq_len: i32, cache: &C)
+                                             -> Result<usize> {
+    let desc = cache.desc();
+    let mut bytes = gqa_workspace_bytes(config, hidden_size, max_seq_len, desc.capacity)?;
+    if max_seq_len > 1 && desc.dtype != sys::EMA_DTYPE_BF16 {
+        bytes += aligned(prefill_ws_bytes(desc, desc.capacity)?);
+    }
+    Ok(bytes)
+}
+
+/// Rows a prefill call attends: the ring for a rotating cache, else [0, offset + T).
+fn prefill_rows(desc: &sys::EmaKvCacheDesc, offset: i64, t: i32) -> i32 {
+    if desc.flags & sys::EMA_KV_ROTATING != 0 {
+        return desc.capacity;
+    }
+    (offset + t as i64).min(desc.capacity as i64) as i32
+}
+
+fn prefill_ws_bytes(desc: &sys::EmaKvCacheDesc, rows: i32) -> Result<usize> {
+    let mut need: u64 = 0;
+    check(unsafe { sys::ema_prefill_workspace_size(desc, rows, &mut need) }, "prefill_workspace_size")?;
+    Ok(need as usize)
 }
 
 /// Carves a call's temporaries out of the arena, in order. The decode counters stay at
@@ -572,19 +939,26 @@ fn project(ctx: &HipCtx, x: *const c_void, ldx: i64, w: &QuantWeights, m: i32, n
     )
 }
 
-/// Full GQA attention layer (`crates/attention/src/gqa.rs:62-107`) over a static cache.
+/// Full GQA attention layer (`crates/attention/src/gqa.rs:62-107`), generic over the cache
+/// backend like the reference's (`StaticCache`, `RotatingCache`, `Fp8Cache`).
 ///
 /// - `x`: hidden state [1, seq_len, hidden] bf16
 /// - `offset`: position of the first new token
 ///
 /// Returns [1, seq_len, hidden] bf16 in `ctx`'s arena. The q, k and v projections land in
 /// one q|k|v row (`run_qkv`'s separate pieces without the concatenation); q/k norms,
-/// RoPE and the cache write follow (`ema_pre_attention`), then causal attention over
-/// [0, offset + T) for T > 1 (`is_prefill`, gqa.rs:78), or for T == 1 the fused decode
-/// step over offset + 1 rows; then o_proj. The cache length becomes offset + T.
-pub fn gqa_attention(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache: &mut StaticCache,
-                     config: &GqaConfig, offset: i32) -> Result<DeviceArray> {
-    let op = "gqa_attention";
+/// RoPE and the cache write follow (`ema_pre_attention`: ring rows for a rotating cache,
+/// quantised rows for an FP8 one), then causal attention over the cache for T > 1
+/// (`is_prefill`, gqa.rs:78; a ring attends its window), or for T == 1 the fused decode
+/// step over min(offset + 1, capacity) rows; then o_proj. The cache length becomes
+/// offset + T.
+pub fn gqa_attention<C: HipKvCache>(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache: &mut C,
+                                    config: &GqaConfig, offset: i32) -> Result<DeviceArray> {
+    gqa_layer(ctx, x, weights, cache, config, offset, "gqa_attention")
+}
+
+fn gqa_layer<C: HipKvCache>(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache: &mut C,
+                            config: &GqaConfig, offset: i32, op: &str) -> Result<DeviceArray> {
     let (hq, hkv, d) = (config.n_heads, config.n_kv_heads, config.head_dim);
     if hq <= 0 || hkv <= 0 || d <= 0 || hq % hkv != 0 {
         bail!("{}: bad head config n_heads={} n_kv_heads={} head_dim={}", op, hq, hkv, d);
@@ -600,14 +974,18 @@ pub fn gqa_attention(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache:
     let t = x.shape[1] as i32;
     let hidden = x.shape[2] as i32;
     let cap = cache.capacity();
-    if offset < 0 || offset as i64 + t as i64 > cap as i64 {
+    if !cache.rotating() && (offset < 0 || offset as i64 + t as i64 > cap as i64) {
         bail!("static KV overflow offset={} cap={}", offset as i64 + t as i64 - 1, cap);
+    }
+    if cache.rotating() && (offset < 0 || t > cap) {
+        bail!("{}: {} tokens exceed the window {}", op, t, cap);
     }
     check_proj(&weights.q_proj, hq * d, hidden, op, "q_proj")?;
     check_proj(&weights.k_proj, hkv * d, hidden, op, "k_proj")?;
     check_proj(&weights.v_proj, hkv * d, hidden, op, "v_proj")?;
     check_proj(&weights.o_proj, hidden, hq * d, op, "o_proj")?;
 
+    let desc = *cache.desc();
     let f = ((hq + 2 * hkv) * d) as i64;
     let hd = (hq * d) as usize;
     let mut arena = Arena::new(ctx);
@@ -617,6 +995,11 @@ pub fn gqa_attention(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache:
     let y = arena.take(t as usize * hidden as usize * 2);
     let q = if t > 1 { arena.take(hd * t as usize * 2) } else { std::ptr::null_mut() };
     let attn = arena.take(t as usize * hd * 2);
+    // an FP8 cache's prefill attends a bf16 copy of its rows
+    let quantised = desc.dtype != sys::EMA_DTYPE_BF16;
+    let rows = prefill_rows(&desc, offset as i64, t);
+    let pws_bytes = if t > 1 && quantised { prefill_ws_bytes(&desc, rows)? } else { 0 };
+    let pws = if pws_bytes > 0 { arena.take(pws_bytes) } else { std::ptr::null_mut() };
     arena.check(op)?;
 
     // 1. q|k|v projections (project_qkv, crates/ops/src/attention.rs:31-51)
@@ -641,28 +1024,38 @@ pub fn gqa_attention(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache:
     let qw = weights.q_norm.as_ref().map_or(std::ptr::null(), |a| a.data as *const c_void);
     let kw = weights.k_norm.as_ref().map_or(std::ptr::null(), |a| a.data as *const c_void);
     let scale = 1.0f32 / (d as f32).sqrt();
-    let pos = cache.device_position(offset)?;
+    let pos = cache.position(ctx, offset as i64)?;
     if t > 1 {
         check(
             unsafe {
                 sys::ema_pre_attention(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, t, hq,
-                                       hkv, d, flags, q, cache.desc())
+                                       hkv, d, flags, q, &desc)
             },
             "pre_attention",
         )?;
-        check(
-            unsafe {
-                sys::ema_prefill_attention(ctx.stream, q, cache.desc(), pos, t, hq, scale, sys::EMA_PREFILL_CAUSAL,
-                                           attn)
-            },
-            "prefill_attention",
-        )?;
+        if quantised {
+            check(
+                unsafe {
+                    sys::ema_prefill_attention_ws(ctx.stream, q, &desc, pos, t, hq, scale, sys::EMA_PREFILL_CAUSAL,
+                                                  attn, rows, pws, pws_bytes as u64)
+                },
+                "prefill_attention_ws",
+            )?;
+        } else {
+            check(
+                unsafe {
+                    sys::ema_prefill_attention(ctx.stream, q, &desc, pos, t, hq, scale, sys::EMA_PREFILL_CAUSAL,
+                                               attn)
+                },
+                "prefill_attention",
+            )?;
+        }
     } else {
         let max_len = (offset + 1).min(cap);
         check(
             unsafe {
                 sys::ema_decode_step(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos as *mut i32,
-                                     max_len, hq, flags, scale, cache.desc(), attn, ws, ws_bytes as u64)
+                                     max_len, hq, flags, scale, &desc, attn, ws, ws_bytes as u64)
             },
             "decode_step",
         )?;
@@ -675,8 +1068,15 @@ pub fn gqa_attention(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache:
 }
 
 /// `crates/attention/src/sliding_window.rs:40-50`: the reference delegates to
-/// `gqa_attention` and leaves the window to the cache backend.
-pub fn sliding_window_attention(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache: &mut StaticCache,
-                                config: &SlidingWindowConfig, offset: i32) -> Result<DeviceArray> {
-    gqa_attention(ctx, x, weights, cache, &config.gqa, offset)
+/// `gqa_attention` and leaves the window to the cache backend. A `RotatingCache` is that
+/// window here (its ring of `window_size` rows), so a ring whose size differs from
+/// `config.window_size` is an error; any other cache attends all its rows, as in the
+/// reference.
+pub fn sliding_window_attention<C: HipKvCache>(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights, cache: &mut C,
+                                               config: &SlidingWindowConfig, offset: i32) -> Result<DeviceArray> {
+    if cache.rotating() && config.window_size != cache.capacity() as usize {
+        bail!("sliding_window_attention: window_size {} differs from the cache's {}", config.window_size,
+              cache.capacity());
+    }
+    gqa_layer(ctx, x, weights, cache, &config.gqa, offset, "sliding_window_attention")
 }

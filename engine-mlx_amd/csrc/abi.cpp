@@ -65,6 +65,12 @@ namespace {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ema_position_write: one lane stores the value (a vector store; the address depends on
+// the lane index, so the compiler does not turn it into a scalar store).
+__global__ void position_write_kernel(int32_t* dst, int32_t v) {
+  if (threadIdx.x < 1) dst[threadIdx.x] = v;
+}
+
 int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
   if (!c) return set_error(EMA_ERR_INVALID_ARG, "%s: cache descriptor is null", op);
   if (!c->k || !c->v) return set_error(EMA_ERR_INVALID_ARG, "%s: KV cache is empty (null K/V buffer)", op);
@@ -303,6 +309,41 @@ int32_t ema_kvcache_quantize_int4(ema_stream_t stream, const ema_kvcache_desc* s
                      dst->capacity);
   if (n_rows == 0) return EMA_OK;
   return launch_quantize_int4((hipStream_t)stream, *src, src_row, *dst, dst_row, n_rows);
+}
+
+int32_t ema_kvcache_convert(ema_stream_t stream, const ema_kvcache_desc* src, int32_t src_row,
+                            const ema_kvcache_desc* dst, int32_t dst_row, int32_t n_rows) {
+  const char* op = "ema_kvcache_convert";
+  int32_t rc = check_cache(op, src);
+  if (rc) return rc;
+  if ((rc = check_cache(op, dst))) return rc;
+  const bool to_int4 = src->dtype == EMA_DTYPE_BF16 && dst->dtype == EMA_DTYPE_INT4_AFFINE;
+  const bool to_fp8 = src->dtype == EMA_DTYPE_BF16 && dst->dtype == EMA_DTYPE_FP8_E4M3;
+  const bool from_fp8 = src->dtype == EMA_DTYPE_FP8_E4M3 && dst->dtype == EMA_DTYPE_BF16;
+  if (!to_int4 && !to_fp8 && !from_fp8)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: converts bf16 -> fp8, fp8 -> bf16 and bf16 -> int4 rows (dtypes %d -> %d)",
+                     op, src->dtype, dst->dtype);
+  if (src->batch != dst->batch || src->n_kv_heads != dst->n_kv_heads || src->head_dim != dst->head_dim)
+    return set_error(EMA_ERR_SHAPE, "%s: source (%d, %d, %d) and destination (%d, %d, %d) shapes differ", op,
+                     src->batch, src->n_kv_heads, src->head_dim, dst->batch, dst->n_kv_heads, dst->head_dim);
+  if (n_rows < 0 || src_row < 0 || dst_row < 0 || (int64_t)src_row + n_rows > src->capacity ||
+      (int64_t)dst_row + n_rows > dst->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: rows [%d, +%d) of the source (capacity %d) or [%d, +%d) of the "
+                     "destination (capacity %d) out of range", op, src_row, n_rows, src->capacity, dst_row, n_rows,
+                     dst->capacity);
+  if ((src->dtype == EMA_DTYPE_BF16 && (src->stride_pos % 8 || src->stride_head % 8 || src->stride_batch % 8)) ||
+      (dst->dtype == EMA_DTYPE_BF16 && (dst->stride_pos % 8 || dst->stride_head % 8 || dst->stride_batch % 8)))
+    return set_error(EMA_ERR_SHAPE, "%s: bf16 strides must be multiples of 8 elements", op);
+  if (n_rows == 0) return EMA_OK;
+  if (to_int4) return launch_quantize_int4((hipStream_t)stream, *src, src_row, *dst, dst_row, n_rows);
+  return launch_fp8_convert((hipStream_t)stream, *src, src_row, *dst, dst_row, n_rows);
+}
+
+int32_t ema_position_write(ema_stream_t stream, int32_t* slot, int32_t value) {
+  if (!slot) return set_error(EMA_ERR_INVALID_ARG, "ema_position_write: slot is null");
+  if (((uintptr_t)slot & 3u) != 0) return set_error(EMA_ERR_INVALID_ARG, "ema_position_write: slot is not 4-byte aligned");
+  hipLaunchKernelGGL(position_write_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, slot, value);
+  return check_hip(hipGetLastError(), "ema_position_write launch");
 }
 
 int32_t ema_kvcache_free(ema_kvcache_desc* d) {

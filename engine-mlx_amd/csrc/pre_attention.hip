@@ -107,37 +107,6 @@ struct PreArgs {
   int rot;  // rotating cache: position p lives in row p % cap
 };
 
-// Scale exponent of one 64-element block from this lane's share (amax over the 8 lanes
-// of the head): ceil(log2(amax / 448)) with amax = max(1e-4, max |x|). The logarithm is
-// taken in double and rounded to f32 before the ceiling, which reproduces an f32 log2
-// rounded to nearest (the reference's f32::log2) also just above powers of two.
-__device__ __forceinline__ int fp8_block_exp(float amax_lane) {
-  float amax = fmaxf(amax_lane, 1.0e-4f);
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-  return (int)ceilf((float)log2((double)(amax / 448.0f)));
-}
-
-// 8 values (bf16 bits) -> 8 E4M3FN codes of v * 2^-e: clamp to +-448 (NaN -> +448, as
-// the reference's f32::min does), round to nearest even; -0 is stored as +0.
-__device__ __forceinline__ u32x2 fp8_encode8(const uint16_t* x, int e) {
-  const float inv = ldexpf(1.0f, -e);
-  float y[8];
-  for (int i = 0; i < 8; ++i) {
-    float t = bf16_to_f32(x[i]) * inv;
-    t = t != t ? 448.0f : fminf(fmaxf(t, -448.0f), 448.0f);
-    y[i] = t + 0.0f;
-  }
-  u32x2 w;
-  for (int h = 0; h < 2; ++h) {
-    int d = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h], y[4 * h + 1], 0, false);
-    d = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h + 2], y[4 * h + 3], d, true);
-    w[h] = (uint32_t)d;
-  }
-  return w;
-}
-
 template <int D, bool kFp8, bool kI4 = false>
 __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
   constexpr int HALF = D / 2;

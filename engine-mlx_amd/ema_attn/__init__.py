@@ -44,7 +44,7 @@ EMA_PREFILL_CHUNK_ONLY = 2
 EXPORTED = (
     "ema_last_error", "ema_version", "ema_kvcache_init", "ema_kvcache_alloc", "ema_kvcache_free",
     "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8", "ema_kvcache_init_int4", "ema_kvcache_alloc_int4",
-    "ema_kvcache_quantize_int4",
+    "ema_kvcache_quantize_int4", "ema_kvcache_convert", "ema_position_write",
     "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
     "ema_decode_attention", "ema_decode_step", "ema_decode_step_noalloc", "ema_prefill_attention", "ema_prefill_workspace_size",
     "ema_prefill_attention_ws", "ema_gdn_scan", "ema_gdn_scan_workspace_size", "ema_gdn_scan_ws",
@@ -95,6 +95,8 @@ def lib() -> ctypes.CDLL:
             "ema_kvcache_init_int4": (i32, [D, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
             "ema_kvcache_alloc_int4": (i32, [D, i32, i32, i32, i32]),
             "ema_kvcache_quantize_int4": (i32, [vp, D, i32, D, i32, i32]),
+            "ema_kvcache_convert": (i32, [vp, D, i32, D, i32, i32]),
+            "ema_position_write": (i32, [vp, vp, i32]),
             "ema_kvcache_free": (i32, [D]),
             "ema_kvcache_memory_bytes": (i32, [D, ctypes.POINTER(u64)]),
             "ema_pre_attention": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, i32, i32, i32, u32, vp, D]),
@@ -237,6 +239,20 @@ def quantize_int4(src: StaticCache, dst: StaticCache, n_rows: int, src_row: int 
     crates/serve/src/engine_ext.rs:158-210)."""
     _check(lib().ema_kvcache_quantize_int4(_stream(stream), ctypes.byref(src.desc), src_row, ctypes.byref(dst.desc),
                                            dst_row, n_rows), "ema_kvcache_quantize_int4")
+
+
+def kvcache_convert(src: StaticCache, dst: StaticCache, n_rows: int, src_row: int = 0, dst_row: int = 0,
+                    stream=None) -> None:
+    """Rows [src_row, src_row + n_rows) of ``src`` converted into rows [dst_row, ...) of
+    ``dst``: bf16 -> FP8 (Fp8Cache::append's quantisation, crates/kvcache/src/fp8.rs:47-68),
+    FP8 -> bf16 (the decoded values Fp8Cache::get returns) or bf16 -> int4."""
+    _check(lib().ema_kvcache_convert(_stream(stream), ctypes.byref(src.desc), src_row, ctypes.byref(dst.desc),
+                                     dst_row, n_rows), "ema_kvcache_convert")
+
+
+def position_write(slot, value: int, stream=None) -> None:
+    """Stream-ordered write of ``value`` into the device int32 tensor element ``slot``."""
+    _check(lib().ema_position_write(_stream(stream), _ptr(slot), int(value)), "ema_position_write")
 
 
 def pre_attention(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: StaticCache, flags=0,

@@ -63,12 +63,6 @@ class Arena {
   const char* op_;
 };
 
-// Writes v into *dst on the stream: the rotating cache's position slot. The address
-// depends on the lane, so the store is a vector store.
-__global__ void set_slot_kernel(int32_t* dst, int32_t v) {
-  if (threadIdx.x < 1) dst[threadIdx.x] = v;
-}
-
 std::string shape_str(const std::vector<int64_t>& s) {
   std::string r = "[";
   for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
@@ -81,25 +75,29 @@ int64_t Array::numel() const {
   return std::accumulate(shape.begin(), shape.end(), (int64_t)1, [](int64_t a, int64_t b) { return a * b; });
 }
 
-StaticCache::StaticCache(int32_t n_kv_heads, int32_t capacity, int32_t head_dim) {
-  check(ema_kvcache_alloc(&desc_, 1, n_kv_heads, capacity, head_dim), "kvcache_alloc");
-  std::vector<int32_t> pos((size_t)capacity + 1);
+PositionTable::PositionTable(int32_t n) {
+  if (n < 0) throw Error(EMA_ERR_SHAPE, "PositionTable: negative size");
+  std::vector<int32_t> pos((size_t)n + 1);
   std::iota(pos.begin(), pos.end(), 0);
-  try {
-    check_hip(hipMalloc((void**)&positions_, pos.size() * sizeof(int32_t)), "StaticCache: positions");
-    check_hip(hipMemcpy(positions_, pos.data(), pos.size() * sizeof(int32_t), hipMemcpyHostToDevice),
-              "StaticCache: positions upload");
-  } catch (...) {
-    if (positions_) (void)hipFree(positions_);
-    ema_kvcache_free(&desc_);
-    throw;
+  check_hip(hipMalloc((void**)&table_, pos.size() * sizeof(int32_t)), "position table");
+  const hipError_t e = hipMemcpy(table_, pos.data(), pos.size() * sizeof(int32_t), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(table_);
+    table_ = nullptr;
+    check_hip(e, "position table upload");
   }
 }
 
-StaticCache::~StaticCache() {
-  ema_kvcache_free(&desc_);
-  if (positions_) (void)hipFree(positions_);
+PositionTable::~PositionTable() {
+  if (table_) (void)hipFree(table_);
 }
+
+StaticCache::StaticCache(int32_t n_kv_heads, int32_t capacity, int32_t head_dim)
+    : positions_(capacity > 0 ? capacity : 0) {
+  check(ema_kvcache_alloc(&desc_, 1, n_kv_heads, capacity, head_dim), "kvcache_alloc");
+}
+
+StaticCache::~StaticCache() { ema_kvcache_free(&desc_); }
 
 size_t StaticCache::memory_bytes() const {
   uint64_t b = 0;
@@ -111,7 +109,14 @@ const int32_t* StaticCache::device_position(int32_t p) const {
   if (p < 0 || p > desc_.capacity)
     throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string(p) + " cap=" +
                                       std::to_string(desc_.capacity));
-  return positions_ + p;
+  return positions_.at(p);
+}
+
+const int32_t* StaticCache::position(const Ctx&, int64_t p) const {
+  if (p < 0 || p > desc_.capacity)
+    throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string(p) + " cap=" +
+                                      std::to_string(desc_.capacity));
+  return positions_.at((int32_t)p);
 }
 
 void StaticCache::advance(int32_t n) {
@@ -187,8 +192,7 @@ size_t RotatingCache::memory_bytes() const {
 
 const int32_t* RotatingCache::position(const Ctx& ctx, int64_t p) const {
   if (p < 0 || p >= ((int64_t)1 << 31)) throw Error(EMA_ERR_CAPACITY, "rotating KV position " + std::to_string(p));
-  hipLaunchKernelGGL(set_slot_kernel, dim3(1), dim3(64), 0, (hipStream_t)ctx.stream, slot_, (int32_t)p);
-  check_hip(hipGetLastError(), "RotatingCache: position slot");
+  check(ema_position_write(ctx.stream, slot_, (int32_t)p), "position_write");
   return slot_;
 }
 
@@ -255,6 +259,74 @@ std::pair<Array, Array> RotatingCache::get(const Ctx& ctx) const {
   return {k, v};
 }
 
+Fp8Cache::Fp8Cache(int32_t n_kv_heads, int32_t capacity, int32_t head_dim, int32_t n_rot)
+    : positions_(capacity > 0 ? capacity : 0) {
+  if (n_rot != 0)
+    throw Error(EMA_ERR_UNSUPPORTED, "Fp8Cache: n_rot " + std::to_string(n_rot) +
+                                         " (an unquantised RoPE tail) is not supported; the whole head is quantised");
+  check(ema_kvcache_alloc_fp8(&desc_, 1, n_kv_heads, capacity, head_dim), "kvcache_alloc_fp8");
+}
+
+Fp8Cache::~Fp8Cache() { ema_kvcache_free(&desc_); }
+
+size_t Fp8Cache::memory_bytes() const {
+  uint64_t b = 0;
+  check(ema_kvcache_memory_bytes(&desc_, &b), "kvcache_memory_bytes");
+  return (size_t)b;
+}
+
+const int32_t* Fp8Cache::position(const Ctx&, int64_t p) const {
+  if (p < 0 || p > desc_.capacity)
+    throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string(p) + " cap=" +
+                                      std::to_string(desc_.capacity));
+  return positions_.at((int32_t)p);
+}
+
+void Fp8Cache::set_len(int64_t n) {
+  if (n < 0 || n > desc_.capacity)
+    throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string(n) + " cap=" +
+                                      std::to_string(desc_.capacity));
+  offset_ = (int32_t)n;
+}
+
+void Fp8Cache::append(const Ctx& ctx, const Array& k, const Array& v) {
+  const int64_t Hkv = desc_.n_kv_heads, D = desc_.head_dim;
+  for (const Array* a : {&k, &v}) {
+    if (!a->data) throw Error(EMA_ERR_INVALID_ARG, "Fp8Cache::append: null k/v");
+    if (a->shape.size() != 4 || a->shape[0] != 1 || a->shape[1] != Hkv || a->shape[3] != D || !a->strides.empty())
+      throw Error(EMA_ERR_SHAPE, "Fp8Cache::append: expected contiguous [1, " + std::to_string(Hkv) + ", seq, " +
+                                     std::to_string(D) + "], got " + shape_str(a->shape));
+  }
+  if (k.shape[2] != v.shape[2]) throw Error(EMA_ERR_SHAPE, "Fp8Cache::append: k/v lengths differ");
+  const int64_t T = k.shape[2];
+  if (offset_ + T > desc_.capacity)
+    throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string(offset_ + T) + " cap=" +
+                                      std::to_string(desc_.capacity));
+  if (T == 0) return;
+  // the new rows as a bf16 cache of T rows, quantised into rows [offset, offset + T)
+  ema_kvcache_desc src{};
+  check(ema_kvcache_init(&src, k.data, v.data, 1, (int32_t)Hkv, (int32_t)T, (int32_t)D), "kvcache_init");
+  check(ema_kvcache_convert(ctx.stream, &src, 0, &desc_, offset_, (int32_t)T), "kvcache_convert");
+  offset_ += (int32_t)T;
+}
+
+std::pair<Array, Array> Fp8Cache::get(const Ctx& ctx) const {
+  if (offset_ == 0) throw Error(EMA_ERR_INVALID_ARG, "FP8 KV cache is empty");
+  const int64_t Hkv = desc_.n_kv_heads, D = desc_.head_dim, n = offset_;
+  Arena arena(ctx, "Fp8Cache::get");
+  char* kb = (char*)arena.take((size_t)Hkv * n * D * 2);
+  char* vb = (char*)arena.take((size_t)Hkv * n * D * 2);
+  arena.check();
+  ema_kvcache_desc dst{};
+  check(ema_kvcache_init(&dst, kb, vb, 1, (int32_t)Hkv, (int32_t)n, (int32_t)D), "kvcache_init");
+  check(ema_kvcache_convert(ctx.stream, &desc_, 0, &dst, 0, (int32_t)n), "kvcache_convert");
+  Array k, v;
+  k.data = kb;
+  v.data = vb;
+  k.shape = v.shape = {1, Hkv, n, D};
+  return {k, v};
+}
+
 namespace {
 
 void check_config(const GqaConfig& c, const std::string& op) {
@@ -270,45 +342,67 @@ uint64_t decode_ws_bytes(const GqaConfig& c, int32_t capacity) {
   return need;
 }
 
-// Temporaries of the attention core, carved in this order: q (prefill only), the
-// attention output, the decode split state (decode only).
+// Temporaries of the attention core, carved in this order: the decode split state (decode
+// only, at the start of the arena), q (prefill only), the attention output, and an FP8
+// cache's prefill workspace (the bf16 copy of the attended rows).
 struct CoreBuffers {
   void* q = nullptr;
   void* attn = nullptr;
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
+  void* pws = nullptr;
+  uint64_t pws_bytes = 0;
 };
 
+// Rows the prefill of a call attends to: the ring for a rotating cache, else [0, offset + T).
+int32_t prefill_rows(const ema_kvcache_desc& d, int64_t offset, int32_t T) {
+  if (d.flags & EMA_KV_ROTATING) return d.capacity;
+  const int64_t n = offset + T;
+  return (int32_t)(n < d.capacity ? n : d.capacity);
+}
+
+uint64_t prefill_ws_bytes(const ema_kvcache_desc& d, int32_t rows) {
+  uint64_t need = 0;
+  check(ema_prefill_workspace_size(&d, rows, &need), "prefill_workspace_size");
+  return need;
+}
+
 // Carved first (the decode workspace must start the arena).
-CoreBuffers take_core(Arena& arena, const GqaConfig& c, int32_t T, int32_t capacity) {
+CoreBuffers take_core(Arena& arena, const GqaConfig& c, int32_t T, const ema_kvcache_desc& d, int32_t offset) {
   CoreBuffers b;
   const size_t HD = (size_t)c.n_heads * c.head_dim;
   if (T == 1) {
-    b.ws_bytes = decode_ws_bytes(c, capacity);
+    b.ws_bytes = decode_ws_bytes(c, d.capacity);
     b.ws = arena.take_decode_workspace((size_t)b.ws_bytes);
   }
   if (T > 1) b.q = arena.take(HD * T * 2);
   b.attn = arena.take((size_t)T * HD * 2);
+  if (T > 1 && d.dtype != EMA_DTYPE_BF16) {
+    b.pws_bytes = prefill_ws_bytes(d, prefill_rows(d, offset, T));
+    b.pws = arena.take((size_t)b.pws_bytes);
+  }
   return b;
 }
 
-// The attention layer over either cache, on q|k|v rows already in device memory:
-// pre-attention writes the chunk's K/V (ring rows for a rotating cache) and causal
-// prefill attends (T > 1, gqa.rs:78), or the fused decode step does both (T == 1).
-void check_range(int32_t cap, int32_t offset, int32_t T, bool rotating, const std::string& name) {
-  if (!rotating && (offset < 0 || (int64_t)offset + T > cap))
+// The attention layer over any cache, on q|k|v rows already in device memory:
+// pre-attention writes the chunk's K/V (quantised for an FP8 cache, ring rows for a
+// rotating one) and causal prefill attends (T > 1, gqa.rs:78), or the fused decode step
+// does both (T == 1).
+void check_range(const HipKvCache& cache, int32_t offset, int32_t T, const std::string& name) {
+  const int32_t cap = cache.capacity();
+  if (!cache.rotating() && (offset < 0 || (int64_t)offset + T > cap))
     throw Error(EMA_ERR_CAPACITY, "static KV overflow offset=" + std::to_string((int64_t)offset + T - 1) +
                                       " cap=" + std::to_string(cap));
-  if (rotating && (offset < 0 || T > cap))
+  if (cache.rotating() && (offset < 0 || T > cap))
     throw Error(EMA_ERR_CAPACITY, name + ": " + std::to_string(T) + " tokens exceed the window " + std::to_string(cap));
 }
 
-template <class Cache>
 void attend(const Ctx& ctx, const void* qkv, int32_t T, const std::optional<Array>& q_norm,
-            const std::optional<Array>& k_norm, Cache& cache, const GqaConfig& config, int32_t offset,
+            const std::optional<Array>& k_norm, HipKvCache& cache, const GqaConfig& config, int32_t offset,
             const CoreBuffers& buf) {
   const int32_t Hq = config.n_heads, Hkv = config.n_kv_heads, D = config.head_dim;
-  const int32_t cap = cache.desc().capacity;
+  const ema_kvcache_desc& d = cache.desc();
+  const int32_t cap = d.capacity;
   // optional_qk_norm (crates/ops/src/attention.rs:57-76): each norm on its own
   uint32_t flags = 0;
   if (!q_norm) flags |= EMA_PRE_NO_Q_NORM;
@@ -320,21 +414,25 @@ void attend(const Ctx& ctx, const void* qkv, int32_t T, const std::optional<Arra
   const int32_t* pos = cache.position(ctx, offset);
   if (T > 1) {  // is_prefill (gqa.rs:78): causal over the cache
     check(ema_pre_attention(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, T, Hq, Hkv, D, flags,
-                            buf.q, &cache.desc()),
+                            buf.q, &d),
           "pre_attention");
-    check(ema_prefill_attention(ctx.stream, buf.q, &cache.desc(), pos, T, Hq, scale, EMA_PREFILL_CAUSAL, buf.attn),
-          "prefill_attention");
+    if (d.dtype == EMA_DTYPE_BF16)
+      check(ema_prefill_attention(ctx.stream, buf.q, &d, pos, T, Hq, scale, EMA_PREFILL_CAUSAL, buf.attn),
+            "prefill_attention");
+    else
+      check(ema_prefill_attention_ws(ctx.stream, buf.q, &d, pos, T, Hq, scale, EMA_PREFILL_CAUSAL, buf.attn,
+                                     prefill_rows(d, offset, T), buf.pws, buf.pws_bytes),
+            "prefill_attention_ws");
   } else {  // the decode step writes the row at the offset and attends offset + 1 rows
     const int32_t max_len = offset + 1 < cap ? offset + 1 : cap;
     check(ema_decode_step(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, const_cast<int32_t*>(pos),
-                          max_len, Hq, flags, scale, &cache.desc(), buf.attn, buf.ws, buf.ws_bytes),
+                          max_len, Hq, flags, scale, &d, buf.attn, buf.ws, buf.ws_bytes),
           "decode_step");
   }
   cache.set_len((int64_t)offset + T);
 }
 
-template <class Cache>
-void check_cache_config(const Cache& cache, const GqaConfig& config, const std::string& name) {
+void check_cache_config(const HipKvCache& cache, const GqaConfig& config, const std::string& name) {
   check_config(config, name);
   if (config.n_kv_heads != cache.n_kv_heads() || config.head_dim != cache.head_dim())
     throw Error(EMA_ERR_SHAPE, name + ": config does not match the cache");
@@ -348,15 +446,14 @@ int32_t seq_len_of(const Array& a, int64_t width, const std::string& name, const
   return (int32_t)a.shape[1];
 }
 
-template <class Cache>
 Array qkv_layer(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
-                const std::optional<Array>& k_norm, Cache& cache, const GqaConfig& config, int32_t offset,
-                bool rotating, const std::string& name) {
+                const std::optional<Array>& k_norm, HipKvCache& cache, const GqaConfig& config, int32_t offset,
+                const std::string& name) {
   check_cache_config(cache, config, name);
   const int32_t T = seq_len_of(qkv, (int64_t)(config.n_heads + 2 * config.n_kv_heads) * config.head_dim, name, "qkv");
-  check_range(cache.desc().capacity, offset, T, rotating, name);
+  check_range(cache, offset, T, name);
   Arena arena(ctx, name.c_str());
-  const CoreBuffers buf = take_core(arena, config, T, cache.desc().capacity);
+  const CoreBuffers buf = take_core(arena, config, T, cache.desc(), offset);
   arena.check();
   attend(ctx, qkv.data, T, q_norm, k_norm, cache, config, offset, buf);
   Array r;
@@ -395,9 +492,8 @@ void project(const Ctx& ctx, const void* x, int64_t ldx, const QuantWeights& w, 
 // gqa.rs:62-107: project q, k, v into one q|k|v row (run_qkv's separate pieces without
 // the concatenation, crates/serve/src/forward/projection.rs:105-128), attend, o_proj
 // (attend_and_project, crates/ops/src/attention.rs:162-177).
-template <class Cache>
-Array gqa_layer(const Ctx& ctx, const Array& x, const GqaWeights& w, Cache& cache, const GqaConfig& config,
-                int32_t offset, bool rotating, const std::string& name) {
+Array gqa_layer(const Ctx& ctx, const Array& x, const GqaWeights& w, HipKvCache& cache, const GqaConfig& config,
+                int32_t offset, const std::string& name) {
   check_cache_config(cache, config, name);
   if (!x.data || x.shape.size() != 3 || x.shape[2] <= 0)
     throw Error(EMA_ERR_SHAPE, name + ": x must be contiguous [1, seq, hidden], got " + shape_str(x.shape));
@@ -406,14 +502,14 @@ Array gqa_layer(const Ctx& ctx, const Array& x, const GqaWeights& w, Cache& cach
   const int32_t T = seq_len_of(x, hidden, name, "x");
   const int32_t Hq = config.n_heads, Hkv = config.n_kv_heads, D = config.head_dim;
   const int64_t F = (int64_t)(Hq + 2 * Hkv) * D;
-  check_range(cache.desc().capacity, offset, T, rotating, name);
+  check_range(cache, offset, T, name);
   const int32_t K = (int32_t)hidden;
   check_proj(w.q_proj, Hq * D, K, name, "q_proj");
   check_proj(w.k_proj, Hkv * D, K, name, "k_proj");
   check_proj(w.v_proj, Hkv * D, K, name, "v_proj");
   check_proj(w.o_proj, K, Hq * D, name, "o_proj");
   Arena arena(ctx, name.c_str());
-  const CoreBuffers buf = take_core(arena, config, T, cache.desc().capacity);
+  const CoreBuffers buf = take_core(arena, config, T, cache.desc(), offset);
   void* qkv = arena.take((size_t)T * F * 2);
   void* y = arena.take((size_t)T * hidden * 2);
   arena.check();
@@ -436,6 +532,13 @@ size_t qkv_attention_workspace_bytes(const GqaConfig& config, int32_t max_seq_le
   return aligned(HD * T * 2) + aligned(T * HD * 2) + aligned((size_t)decode_ws_bytes(config, capacity));
 }
 
+size_t qkv_attention_workspace_bytes(const GqaConfig& config, int32_t max_seq_len, const HipKvCache& cache) {
+  const ema_kvcache_desc& d = cache.desc();
+  size_t bytes = qkv_attention_workspace_bytes(config, max_seq_len, d.capacity);
+  if (max_seq_len > 1 && d.dtype != EMA_DTYPE_BF16) bytes += aligned((size_t)prefill_ws_bytes(d, d.capacity));
+  return bytes;
+}
+
 size_t gqa_workspace_bytes(const GqaConfig& config, int64_t hidden_size, int32_t max_seq_len, int32_t capacity) {
   const size_t T = (size_t)(max_seq_len > 1 ? max_seq_len : 1);
   const size_t F = (size_t)(config.n_heads + 2 * config.n_kv_heads) * config.head_dim;
@@ -443,35 +546,32 @@ size_t gqa_workspace_bytes(const GqaConfig& config, int64_t hidden_size, int32_t
          qkv_attention_workspace_bytes(config, max_seq_len, capacity);
 }
 
-Array gqa_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, StaticCache& cache,
+size_t gqa_workspace_bytes(const GqaConfig& config, int64_t hidden_size, int32_t max_seq_len,
+                           const HipKvCache& cache) {
+  const size_t T = (size_t)(max_seq_len > 1 ? max_seq_len : 1);
+  const size_t F = (size_t)(config.n_heads + 2 * config.n_kv_heads) * config.head_dim;
+  return aligned(T * F * 2) + aligned(T * (size_t)hidden_size * 2) +
+         qkv_attention_workspace_bytes(config, max_seq_len, cache);
+}
+
+Array gqa_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, HipKvCache& cache,
                     const GqaConfig& config, int32_t offset) {
-  return gqa_layer(ctx, x, weights, cache, config, offset, false, "gqa_attention");
+  return gqa_layer(ctx, x, weights, cache, config, offset, "gqa_attention");
 }
 
-Array sliding_window_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, StaticCache& cache,
+Array sliding_window_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, HipKvCache& cache,
                                const SlidingWindowConfig& config, int32_t offset) {
-  // The reference delegates to gqa_attention and leaves the window to the
-  // cache backend (crates/attention/src/sliding_window.rs:40-50).
-  return gqa_attention(ctx, x, weights, cache, config.gqa, offset);
-}
-
-Array sliding_window_attention(const Ctx& ctx, const Array& x, const GqaWeights& weights, RotatingCache& cache,
-                               const SlidingWindowConfig& config, int32_t offset) {
-  if (config.window_size != (size_t)cache.window_size())
+  // The reference delegates to gqa_attention and leaves the window to the cache backend
+  // (crates/attention/src/sliding_window.rs:40-50): a ring enforces it.
+  if (cache.rotating() && config.window_size != (size_t)cache.capacity())
     throw Error(EMA_ERR_SHAPE, "sliding_window_attention: window_size " + std::to_string(config.window_size) +
-                                   " differs from the cache's " + std::to_string(cache.window_size()));
-  return gqa_layer(ctx, x, weights, cache, config.gqa, offset, true, "sliding_window_attention");
+                                   " differs from the cache's " + std::to_string(cache.capacity()));
+  return gqa_layer(ctx, x, weights, cache, config.gqa, offset, "sliding_window_attention");
 }
 
 Array qkv_attention(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
-                    const std::optional<Array>& k_norm, StaticCache& cache, const GqaConfig& config, int32_t offset) {
-  return qkv_layer(ctx, qkv, q_norm, k_norm, cache, config, offset, false, "qkv_attention");
-}
-
-Array qkv_attention(const Ctx& ctx, const Array& qkv, const std::optional<Array>& q_norm,
-                    const std::optional<Array>& k_norm, RotatingCache& cache, const GqaConfig& config,
-                    int32_t offset) {
-  return qkv_layer(ctx, qkv, q_norm, k_norm, cache, config, offset, true, "qkv_attention");
+                    const std::optional<Array>& k_norm, HipKvCache& cache, const GqaConfig& config, int32_t offset) {
+  return qkv_layer(ctx, qkv, q_norm, k_norm, cache, config, offset, "qkv_attention");
 }
 
 }  // namespace ema

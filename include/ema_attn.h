@@ -207,6 +207,20 @@ EMA_API int32_t ema_kvcache_alloc_int4(ema_kvcache_desc* out, int32_t batch, int
  * error (EMA_ERR_CAPACITY). */
 EMA_API int32_t ema_kvcache_quantize_int4(ema_stream_t stream, const ema_kvcache_desc* src, int32_t src_row,
                                           const ema_kvcache_desc* dst, int32_t dst_row, int32_t n_rows);
+/* Convert rows [src_row, src_row + n_rows) of every (sequence, kv head) of `src` into rows
+ * [dst_row, dst_row + n_rows) of `dst` (same batch, heads and head_dim; rows outside either
+ * capacity are EMA_ERR_CAPACITY; ring rows are plain rows here):
+ *   bf16 -> FP8   the quantisation of Fp8Cache::append (crates/kvcache/src/fp8.rs:47-68,
+ *                 crates/ops/src/fp8.rs:71-92), as ema_pre_attention writes rows;
+ *   FP8 -> bf16   the exact decoded values, what Fp8Cache::get hands SDPA (fp8.rs:60-68);
+ *   bf16 -> int4  as ema_kvcache_quantize_int4.
+ * Other pairs are EMA_ERR_UNSUPPORTED. */
+EMA_API int32_t ema_kvcache_convert(ema_stream_t stream, const ema_kvcache_desc* src, int32_t src_row,
+                                    const ema_kvcache_desc* dst, int32_t dst_row, int32_t n_rows);
+/* Write `value` into the device int32 at `slot` on `stream` (a one-lane kernel, stream
+ * ordered): the position a rotating cache's layer call passes as its offset, without a
+ * host-to-device copy. No counterpart in the reference (MLX builds a scalar array). */
+EMA_API int32_t ema_position_write(ema_stream_t stream, int32_t* slot, int32_t value);
 /* Free buffers obtained from ema_kvcache_alloc, _alloc_fp8 or _alloc_int4 and clear the descriptor. */
 EMA_API int32_t ema_kvcache_free(ema_kvcache_desc* desc);
 /* Bytes held by K and V, exponents or scales and biases included (KvCache::memory_bytes,

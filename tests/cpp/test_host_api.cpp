@@ -3,7 +3,7 @@
 //   crates/kvcache/tests/lib.rs     (KvCache trait contract, InMemoryCache)
 //   crates/kvcache/tests/concat.rs  (new_is_empty, reset, get bails when empty)
 //   crates/attention/tests/gqa.rs   (GqaConfig constructible, gqa_attention errors)
-// plus GPU checks of StaticCache, RotatingCache, gqa_attention (projections, norms, RoPE,
+// plus GPU checks of StaticCache, RotatingCache, Fp8Cache, gqa_attention (projections, norms, RoPE,
 // cache write, attention, o_proj), sliding_window_attention and qkv_attention against
 // the CPU oracle chain ora_qmatmul -> ora_pre_attention -> ora_sdpa -> ora_qmatmul.
 //
@@ -194,6 +194,55 @@ struct DevQW {
   }
 };
 
+// Equal as values (+0 and -0 alike), element by element.
+static bool same_values(const std::vector<uint16_t>& a, const std::vector<uint16_t>& b) {
+  if (a.size() != b.size()) return false;
+  for (size_t i = 0; i < a.size(); ++i)
+    if (ora_bf16_to_f32(a[i]) != ora_bf16_to_f32(b[i])) return false;
+  return true;
+}
+
+// Rows [r0, r0 + n) of each head of a [H, cap, D] bf16 cache replaced by their FP8 round
+// trip (exact in bf16: a 4-bit significand times a power of two).
+static void fp8_round_trip_rows(std::vector<uint16_t>& c, int H, int cap, int D, int r0, int n) {
+  std::vector<float> f((size_t)n * D);
+  for (int h = 0; h < H; ++h) {
+    uint16_t* rows = &c[((size_t)h * cap + r0) * D];
+    ora_bf16_to_f32_array(rows, f.data(), f.size());
+    ora_fp8_round_trip(f.data(), n, D, 0);
+    for (size_t i = 0; i < f.size(); ++i) rows[i] = ora_f32_to_bf16(f[i]);
+  }
+}
+
+// Checks that `held` ([H, n, D] decoded FP8 rows) is the oracle's round-tripped cache `ref`
+// ([H, cap, D], rows [0, n)) to within one FP8 step: |held - ref| <= |ref| / 4 + 2^-7 s,
+// with s = the block scale 2^ceil(log2(amax / 448)) of the oracle's 64-value block (a
+// neighbouring code, or the block's scale one step up), on at most `max_frac` of the
+// values. Then copies `held` into `ref`.
+static void adopt_fp8_rows(std::vector<uint16_t>& ref, const std::vector<uint16_t>& held, int H, int cap, int n, int D,
+                           const char* what, double max_frac) {
+  size_t differ = 0, total = (size_t)H * n * D;
+  double worst = 0;
+  for (int h = 0; h < H; ++h)
+    for (int r = 0; r < n; ++r)
+      for (int b = 0; b < D; b += 64) {
+        const uint16_t* want = &ref[((size_t)h * cap + r) * D + b];
+        const uint16_t* got = &held[((size_t)h * n + r) * D + b];
+        float amax = 1e-4f;
+        for (int i = 0; i < 64; ++i) amax = std::max(amax, std::fabs(ora_bf16_to_f32(want[i])));
+        const float s = std::ldexp(1.0f, (int)std::ceil(std::log2(amax / 448.0f)));
+        for (int i = 0; i < 64; ++i) {
+          const float w = ora_bf16_to_f32(want[i]), g = ora_bf16_to_f32(got[i]);
+          if (g == w) continue;
+          ++differ;
+          worst = std::max(worst, (double)std::fabs(g - w) / (std::fabs(w) / 4 + s / 128));
+        }
+      }
+  std::printf("     %s: %zu of %zu values on another FP8 code, worst/bound=%.3f\n", what, differ, total, worst);
+  EXPECT(worst <= 1.0 && (double)differ <= max_frac * (double)total);
+  for (int h = 0; h < H; ++h) std::copy_n(&held[(size_t)h * n * D], (size_t)n * D, &ref[(size_t)h * cap * D]);
+}
+
 // The reference layer on the host (gqa.rs:62-107 with the oracle's ops): q|k|v
 // projections, norms (null = absent), RoPE and the cache write at `off`, SDPA over
 // [begin, off + T) (causal for T > 1), o_proj. kref/vref are the chronological caches.
@@ -201,6 +250,13 @@ struct OracleLayer {
   HostQW q, k, v, o;
   int Hq, Hkv, D, cap;
   std::vector<uint16_t> kref, vref;
+  bool fp8 = false;  // the cache keeps the FP8 round trip of each written row (fp8.rs:71-92)
+  // FP8 caches: the rows the device cache holds after the call ([Hkv, off + T, D], decoded),
+  // which replace the oracle's rows. The device's projected k/v differ from the oracle's
+  // within the projection's bf16 tolerance, and one FP8 step is 2^5 bf16 steps, so the
+  // caller pins these rows otherwise (as the FP8 round trip of the rows a bf16 cache gets).
+  const std::vector<uint16_t>* k_held = nullptr;
+  const std::vector<uint16_t>* v_held = nullptr;
   OracleLayer(int hidden, int Hq_, int Hkv_, int D_, int cap_, uint64_t seed)
       : q(random_qw(Hq_ * D_, hidden, seed, 0.0068f)), k(random_qw(Hkv_ * D_, hidden, seed + 1, 0.0068f)),
         v(random_qw(Hkv_ * D_, hidden, seed + 2, 0.0068f)), o(random_qw(hidden, Hq_ * D_, seed + 3, 0.0034f)),
@@ -221,6 +277,14 @@ struct OracleLayer {
     if (ora_pre_attention(qkv.data(), qw, kw, 1e-6f, 1e6f, &o32, 1, T, Hq, Hkv, D, flags, qh.data(), kref.data(),
                           vref.data(), cap) != 0)
       throw std::runtime_error("oracle overflow");
+    if (fp8) {
+      fp8_round_trip_rows(kref, Hkv, cap, D, off, T);
+      fp8_round_trip_rows(vref, Hkv, cap, D, off, T);
+      for (auto [held, c] : {std::pair{k_held, &kref}, std::pair{v_held, &vref}})
+        if (held)
+          for (int h = 0; h < Hkv; ++h)
+            std::copy_n(&(*held)[(size_t)h * (off + T) * D], (size_t)(off + T) * D, &(*c)[(size_t)h * cap * D]);
+    }
     ora_sdpa(qh.data(), kref.data(), vref.data(), &len, &b32, 1, Hq, Hkv, T, D, cap, 1.0f / std::sqrt((float)D),
              T > 1 ? 1 : 0, 0, attn.data());
     return ora_project(attn, T, o);
@@ -478,6 +542,170 @@ static void gpu_tests() {
       expect_close(download(out.data, ref.size()), ref, t > 1 ? "ring prefill" : "ring decode");
       (void)hipFree(dqkv);
     }
+  });
+  // ---- Fp8Cache (crates/kvcache/src/fp8.rs:27-91; the layer over it, crates/attention/src/lib.rs:22-27)
+  run("fp8_cache_new_is_empty", [&] {
+    Fp8Cache c(Hkv, 64, D);
+    EXPECT(c.len() == 0 && c.is_empty() && c.n_rot() == 0);
+    EXPECT(c.memory_bytes() == (size_t)2 * Hkv * 64 * (D + D / 64));
+    EXPECT(error_of([&] { c.get(ctx); }).find("empty") != std::string::npos);
+    try {
+      Fp8Cache bad(Hkv, 64, D, 64);
+      EXPECT(false);
+    } catch (const Error& e) {
+      EXPECT(e.code() == EMA_ERR_UNSUPPORTED);
+    }
+  });
+  run("fp8_cache_append_then_get_is_the_round_trip", [&] {
+    const int cap8 = 64, T1 = 5, T2 = 3;
+    Fp8Cache c(Hkv, cap8, D);
+    // values spread over several binades, so the block exponents differ between blocks
+    auto k1 = normal((size_t)Hkv * T1 * D, 31, 0.f, 3.f), v1 = normal((size_t)Hkv * T1 * D, 32, 0.f, 0.01f);
+    auto k2 = normal((size_t)Hkv * T2 * D, 33, 0.f, 200.f), v2 = normal((size_t)Hkv * T2 * D, 34);
+    void *dk1 = upload(k1), *dv1 = upload(v1), *dk2 = upload(k2), *dv2 = upload(v2);
+    c.append(ctx, Array{dk1, {1, Hkv, T1, D}, {}}, Array{dv1, {1, Hkv, T1, D}, {}});
+    c.append(ctx, Array{dk2, {1, Hkv, T2, D}, {}}, Array{dv2, {1, Hkv, T2, D}, {}});
+    EXPECT(c.len() == T1 + T2);
+    auto kv = c.get(ctx);
+    (void)hipDeviceSynchronize();
+    EXPECT(kv.first.shape == std::vector<int64_t>({1, Hkv, T1 + T2, D}));
+    auto gk = download(kv.first.data, (size_t)Hkv * (T1 + T2) * D);
+    auto gv = download(kv.second.data, gk.size());
+    // the expected cache: the chronological rows, round-tripped per row as the oracle does
+    auto expect = [&](const std::vector<uint16_t>& a, const std::vector<uint16_t>& b) {
+      std::vector<uint16_t> e((size_t)Hkv * (T1 + T2) * D);
+      for (int h = 0; h < Hkv; ++h)
+        for (int t = 0; t < T1 + T2; ++t)
+          for (int d = 0; d < D; ++d)
+            e[((size_t)h * (T1 + T2) + t) * D + d] =
+                t < T1 ? a[((size_t)h * T1 + t) * D + d] : b[((size_t)h * T2 + t - T1) * D + d];
+      fp8_round_trip_rows(e, 1, Hkv * (T1 + T2), D, 0, Hkv * (T1 + T2));
+      return e;
+    };
+    EXPECT(same_values(gk, expect(k1, k2)));
+    EXPECT(same_values(gv, expect(v1, v2)));
+    // the stored codes and exponents are the oracle's quantisation of the same rows
+    std::vector<float> f((size_t)T1 * D);
+    std::vector<uint8_t> codes((size_t)T1 * D), got_codes((size_t)T1 * D);
+    std::vector<int8_t> exps((size_t)T1 * D / 64), got_exps(exps.size());
+    ora_bf16_to_f32_array(k1.data(), f.data(), f.size());  // head 0, rows [0, T1)
+    ora_fp8_quantize_rows(f.data(), T1, D, codes.data(), exps.data());
+    EXPECT(hipMemcpy(got_codes.data(), c.desc().k, got_codes.size(), hipMemcpyDeviceToHost) == hipSuccess);
+    EXPECT(hipMemcpy(got_exps.data(), c.desc().k_exp, got_exps.size(), hipMemcpyDeviceToHost) == hipSuccess);
+    for (auto* c : {&codes, &got_codes})  // -0 (0x80) and +0 (0x00) are the same value
+      for (auto& b : *c) b = b == 0x80 ? 0 : b;
+    EXPECT(got_codes == codes && got_exps == exps);
+    std::string e = error_of([&] {
+      auto big = normal((size_t)Hkv * 60 * D, 35);
+      void* db = upload(big);
+      try {
+        c.append(ctx, Array{db, {1, Hkv, 60, D}, {}}, Array{db, {1, Hkv, 60, D}, {}});
+      } catch (...) {
+        (void)hipFree(db);
+        throw;
+      }
+      (void)hipFree(db);
+    });
+    EXPECT(e.find("static KV overflow") != std::string::npos && c.len() == T1 + T2);
+    c.reset();
+    EXPECT(c.is_empty());
+    for (void* p : {dk1, dv1, dk2, dv2}) (void)hipFree(p);
+  });
+  run("gqa_attention_over_fp8_cache_matches_oracle", [&] {
+    Fp8Cache c(Hkv, cap, D);
+    Ctx fctx;
+    fctx.workspace_bytes = gqa_workspace_bytes(cfg, hidden, 64, c);
+    EXPECT(fctx.workspace_bytes > gqa_workspace_bytes(cfg, hidden, 64, cap));  // + the prefill's bf16 copy
+    EXPECT(hipMalloc(&fctx.workspace, fctx.workspace_bytes) == hipSuccess &&
+           hipMemset(fctx.workspace, 0, fctx.workspace_bytes) == hipSuccess);
+    OracleLayer ref(hidden, Hq, Hkv, D, cap, 6000);
+    ref.fp8 = true;
+    DevQW dq(ref.q), dk(ref.k), dv(ref.v), dout(ref.o);
+    auto qw = normal(D, 60, 1.f, 0.02f), kw = normal(D, 61, 1.f, 0.02f);
+    void *dqw = upload(qw), *dkw = upload(kw);
+    GqaWeights w{dq.qw, dk.qw, dv.qw, dout.qw, Array{dqw, {D}, {}}, Array{dkw, {D}, {}}};
+    int step = 0;
+    std::vector<uint16_t> kh, vh;
+    ref.k_held = &kh;
+    ref.v_held = &vh;
+    // The same layer over a bf16 cache: its rows (held to the oracle by the bf16 layer tests)
+    // are what the FP8 layer quantises, so the FP8 rows must be their round trip exactly.
+    StaticCache c16(Hkv, cap, D);
+    auto layer = [&](const Ctx& cx, const Array& x, HipKvCache& cache, int off, bool window) {
+      SlidingWindowConfig sw{cfg, 8};
+      return window ? sliding_window_attention(cx, x, w, cache, sw, off) : gqa_attention(cx, x, w, cache, cfg, off);
+    };
+    auto rows_of = [&](const void* base, int n) {  // rows [0, n) of a [Hkv, cap, D] cache
+      auto all = download(base, (size_t)Hkv * cap * D);
+      std::vector<uint16_t> r((size_t)Hkv * n * D);
+      for (int h = 0; h < Hkv; ++h) std::copy_n(&all[(size_t)h * cap * D], (size_t)n * D, &r[(size_t)h * n * D]);
+      return r;
+    };
+    // one layer call; then the output, and the held rows (get() reuses the arena after it)
+    auto call = [&](int off, int t, uint64_t seed, bool window) {
+      auto x = normal((size_t)t * hidden, seed);
+      void* dx = upload(x);
+      Array y = layer(fctx, Array{dx, {1, t, hidden}, {}}, c, off, window);
+      (void)hipDeviceSynchronize();
+      EXPECT(c.len() == (size_t)(off + t));
+      auto got = download(y.data, (size_t)t * hidden);
+      (void)layer(ctx, Array{dx, {1, t, hidden}, {}}, c16, off, window);
+      auto kv = c.get(fctx);
+      (void)hipDeviceSynchronize();
+      kh = download(kv.first.data, (size_t)Hkv * (off + t) * D);
+      vh = download(kv.second.data, kh.size());
+      auto k16 = rows_of(c16.desc().k, off + t), v16 = rows_of(c16.desc().v, off + t);
+      fp8_round_trip_rows(k16, 1, Hkv * (off + t), D, 0, Hkv * (off + t));
+      fp8_round_trip_rows(v16, 1, Hkv * (off + t), D, 0, Hkv * (off + t));
+      EXPECT(same_values(kh, k16) && same_values(vh, v16));
+      auto want = ref.run(x, t, off, 0, qw.data(), kw.data());
+      expect_close_out(got, want, window ? "fp8 window step (whole cache)"
+                                         : t > 1 ? "fp8 layer prefill" : "fp8 layer decode");
+      (void)hipFree(dx);
+    };
+    // prefill 37, 3 decode steps, a 20-token chunk over the cache, one more step
+    for (auto [off, t] : std::vector<std::pair<int, int>>{{0, 37}, {37, 1}, {38, 1}, {39, 1}, {40, 20}, {60, 1}})
+      call(off, t, 700 + step++, false);
+    // a window layer over a non-rotating cache attends the whole cache (sliding_window.rs:40-50)
+    call(61, 1, 799, true);
+    (void)hipFree(dqw);
+    (void)hipFree(dkw);
+    (void)hipFree(fctx.workspace);
+  });
+  run("qkv_attention_over_fp8_cache_matches_oracle", [&] {
+    Fp8Cache c(Hkv, 128, D);
+    Ctx fctx;
+    fctx.workspace_bytes = qkv_attention_workspace_bytes(cfg, 64, c);
+    EXPECT(hipMalloc(&fctx.workspace, fctx.workspace_bytes) == hipSuccess &&
+           hipMemset(fctx.workspace, 0, fctx.workspace_bytes) == hipSuccess);
+    std::vector<uint16_t> kref((size_t)Hkv * 128 * D, 0), vref((size_t)Hkv * 128 * D, 0);
+    const float scale = 1.0f / std::sqrt((float)D);
+    int step = 0;
+    for (auto [off, t] : std::vector<std::pair<int, int>>{{0, 50}, {50, 1}, {51, 64}, {115, 1}}) {
+      auto qkv = normal((size_t)t * F, 900 + step++);
+      void* dqkv = upload(qkv);
+      Array out = qkv_attention(fctx, Array{dqkv, {1, t, F}, {}}, std::nullopt, std::nullopt, c, cfg, off);
+      (void)hipDeviceSynchronize();
+      std::vector<uint16_t> q((size_t)Hq * t * D), ref((size_t)t * Hq * D);
+      int32_t o32 = off, len = off + t;
+      EXPECT(ora_pre_attention(qkv.data(), nullptr, nullptr, 1e-6f, 1e6f, &o32, 1, t, Hq, Hkv, D, ORA_FLAG_NO_NORM,
+                               q.data(), kref.data(), vref.data(), 128) == 0);
+      fp8_round_trip_rows(kref, Hkv, 128, D, off, t);
+      fp8_round_trip_rows(vref, Hkv, 128, D, off, t);
+      ora_sdpa(q.data(), kref.data(), vref.data(), &len, nullptr, 1, Hq, Hkv, t, D, 128, scale, t > 1 ? 1 : 0, 0,
+               ref.data());
+      expect_close(download(out.data, ref.size()), ref, t > 1 ? "fp8 prefill" : "fp8 decode");
+      (void)hipFree(dqkv);
+    }
+    // V rows (written as given) decode to the oracle's round trip exactly; K rows (after
+    // RoPE, whose bf16 rounding may differ by one step) to within one FP8 step
+    auto kv = c.get(fctx);
+    (void)hipDeviceSynchronize();
+    std::vector<uint16_t> vwant((size_t)Hkv * 116 * D);
+    for (int h = 0; h < Hkv; ++h) std::copy_n(&vref[(size_t)h * 128 * D], (size_t)116 * D, &vwant[(size_t)h * 116 * D]);
+    EXPECT(same_values(download(kv.second.data, vwant.size()), vwant));
+    adopt_fp8_rows(kref, download(kv.first.data, vwant.size()), Hkv, 128, 116, D, "K rows", 0.01);
+    (void)hipFree(fctx.workspace);
   });
   (void)hipFree(ctx.workspace);
 }

@@ -400,3 +400,43 @@ def test_int4_cache_descriptor_and_errors(ema):
     s2 = ema.KvCacheDesc()
     assert L.ema_kvcache_init(ctypes.byref(s2), a, a, 2, 4, 40, 128) == 0
     assert L.ema_kvcache_quantize_int4(None, ctypes.byref(s2), 0, ctypes.byref(d), 0, 8) == ema.EMA_ERR_SHAPE
+
+
+def test_kvcache_convert_argument_errors(ema):
+    L = ema.lib()
+    a = 0x40000  # 16-byte aligned stand-ins; no call below reaches HIP
+    bf = ema.KvCacheDesc()
+    assert L.ema_kvcache_init(ctypes.byref(bf), a, a, 2, 8, 40, 128) == 0
+    f8 = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_fp8(ctypes.byref(f8), a, a, a, a, 2, 8, 64, 128) == 0
+    i4 = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_int4(ctypes.byref(i4), a, a, a, a, a, a, 2, 8, 64, 128) == 0
+    # zero rows of every supported pair is a no-op
+    for s, d in ((bf, f8), (f8, bf), (bf, i4)):
+        assert L.ema_kvcache_convert(None, ctypes.byref(s), 0, ctypes.byref(d), 0, 0) == 0
+    # unsupported pairs: same dtype, fp8 <-> int4, int4 -> bf16
+    for s, d in ((bf, bf), (f8, f8), (f8, i4), (i4, bf), (i4, f8)):
+        assert L.ema_kvcache_convert(None, ctypes.byref(s), 0, ctypes.byref(d), 0, 4) == ema.EMA_ERR_UNSUPPORTED
+    assert "converts" in ema.last_error()
+    # rows outside either capacity, negative rows
+    assert L.ema_kvcache_convert(None, ctypes.byref(bf), 0, ctypes.byref(f8), 30, 41) == ema.EMA_ERR_CAPACITY
+    assert L.ema_kvcache_convert(None, ctypes.byref(bf), 8, ctypes.byref(f8), 0, 33) == ema.EMA_ERR_CAPACITY
+    assert L.ema_kvcache_convert(None, ctypes.byref(f8), 60, ctypes.byref(bf), 0, 8) == ema.EMA_ERR_CAPACITY
+    assert L.ema_kvcache_convert(None, ctypes.byref(bf), -1, ctypes.byref(f8), 0, 4) == ema.EMA_ERR_CAPACITY
+    assert L.ema_kvcache_convert(None, ctypes.byref(bf), 0, ctypes.byref(f8), 0, -4) == ema.EMA_ERR_CAPACITY
+    # shapes must agree; null or empty descriptors are rejected
+    b4 = ema.KvCacheDesc()
+    assert L.ema_kvcache_init(ctypes.byref(b4), a, a, 2, 4, 40, 128) == 0
+    assert L.ema_kvcache_convert(None, ctypes.byref(b4), 0, ctypes.byref(f8), 0, 4) == ema.EMA_ERR_SHAPE
+    assert "shapes differ" in ema.last_error()
+    assert L.ema_kvcache_convert(None, None, 0, ctypes.byref(f8), 0, 4) == ema.EMA_ERR_INVALID_ARG
+    empty = ema.KvCacheDesc()
+    assert L.ema_kvcache_convert(None, ctypes.byref(bf), 0, ctypes.byref(empty), 0, 4) == ema.EMA_ERR_INVALID_ARG
+
+
+def test_position_write_argument_errors(ema):
+    L = ema.lib()
+    assert L.ema_position_write(None, None, 5) == ema.EMA_ERR_INVALID_ARG
+    assert "null" in ema.last_error()
+    assert L.ema_position_write(None, 0x40002, 5) == ema.EMA_ERR_INVALID_ARG
+    assert "aligned" in ema.last_error()

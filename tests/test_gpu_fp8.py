@@ -345,3 +345,50 @@ def test_fp8_prefill_paired(ema, ora):
     assert np.array_equal(host(o8), host(o16)), "decoded fp8 rows == the bf16 cache"
     ref = ora.sdpa(q, kd, vd, (qo + T).astype(np.int32), scale_of(D), True)
     assert_close(host(o8), ref, "fp8 paired prefill vs oracle")
+
+
+# ------------------------------------------------------------------ row conversion
+def test_fp8_convert_quantises_and_decodes_rows(ema, ora):
+    """ema_kvcache_convert bf16 -> FP8 writes the oracle's codes and exponents for the
+    copied rows only (Fp8Cache::append, crates/kvcache/src/fp8.rs:47-68); FP8 -> bf16
+    gives the exact decoded values (what Fp8Cache::get hands SDPA)."""
+    import torch
+
+    B, Hkv, D = 2, 3, 128
+    say("fp8 convert: bf16 rows [5, 38) -> fp8 rows [20, 53), then back")
+    x = ora.normal_f32((B, Hkv, 40, D), seed=901, std=4.0)
+    x[0, 1, 7, :64] *= 1e-3  # one small block
+    xb = ora.bf16_from_f32(x)
+    src = ema.StaticCache(B, Hkv, 40, D, k=dev(xb), v=dev(xb[:, ::-1].copy()))
+    dst = ema.StaticCache(B, Hkv, 64, D, dtype="fp8")
+    ema.kvcache_convert(src, dst, 33, src_row=5, dst_row=20)
+    torch.cuda.synchronize()
+    for name, rows, codes, exps in (("k", xb, dst.k, dst.k_exp), ("v", xb[:, ::-1], dst.v, dst.v_exp)):
+        rc, re = ora.fp8_quantize(ora.f32_from_bf16(np.ascontiguousarray(rows[:, :, 5:38])))
+        gc, ge = host(codes), host(exps)
+        assert np.array_equal(canon(gc[:, :, 20:53]), canon(rc)), f"{name} codes"
+        assert np.array_equal(ge[:, :, 20:53], re), f"{name} exponents"
+        assert not gc[:, :, :20].any() and not gc[:, :, 53:].any() and not ge[:, :, 53:].any()
+    # FP8 -> bf16 of random codes (every finite code, exponents -8 / -7) into rows [3, 51)
+    (kc, ke, kd), (vc, ve, vd) = random_fp8_pair(ora, (B, Hkv, 64, D), seed=907)
+    c8 = fp8_cache(ema, kc, ke, vc, ve)
+    out = ema.StaticCache(B, Hkv, 56, D)
+    ema.kvcache_convert(c8, out, 48, src_row=10, dst_row=3)
+    torch.cuda.synchronize()
+    for name, got, want in (("k", out.k, kd), ("v", out.v, vd)):
+        g = ora.f32_from_bf16(host(got))
+        assert np.array_equal(g[:, :, 3:51], ora.f32_from_bf16(want[:, :, 10:58])), f"{name} decoded"
+        assert not g[:, :, :3].any() and not g[:, :, 51:].any()
+
+
+def test_position_write_is_stream_ordered(ema):
+    import torch
+
+    say("position_write")
+    t = torch.full((4,), -1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+    for v in (7, 11, 123456):
+        ema.position_write(t[2:], v, stream=s)
+        t[0] = t[2]  # a later op on the same stream reads the written value
+    torch.cuda.synchronize()
+    assert t.cpu().tolist() == [123456, -1, 123456, -1]

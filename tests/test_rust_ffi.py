@@ -160,6 +160,33 @@ def test_crate_links_the_library_and_mirrors_the_reference_api(rust):
     for item in ("pub trait KvCache: Send", "fn append(&mut self, ctx: &HipCtx", "fn get(&self, ctx: &HipCtx)",
                  "fn len(&self) -> usize", "fn reset(&mut self)", "fn memory_bytes(&self) -> usize",
                  "impl KvCache for StaticCache", "pub struct QuantWeights", "pub struct GqaWeights",
-                 "pub struct GqaConfig", "pub fn gqa_attention(", "pub fn sliding_window_attention(",
-                 "pub q_norm: Option<DeviceArray>"):
+                 "pub struct GqaConfig", "pub q_norm: Option<DeviceArray>",
+                 # the layer functions are generic over the cache, as gqa.rs:62-69 is
+                 "pub trait HipKvCache: KvCache", "fn desc(&self) -> &sys::EmaKvCacheDesc",
+                 "fn position(&self, ctx: &HipCtx, p: i64) -> Result<*const i32>",
+                 "pub fn gqa_attention<C: HipKvCache>(", "pub fn sliding_window_attention<C: HipKvCache>(",
+                 "pub fn gqa_workspace_bytes_for<C: HipKvCache>("):
         assert item in rust, item
+    for cache in ("StaticCache", "RotatingCache", "Fp8Cache"):
+        assert f"impl KvCache for {cache}" in rust and f"impl HipKvCache for {cache}" in rust, cache
+        assert f"unsafe impl Send for {cache}" in rust, cache
+    # the ring flag, the slot write and the FP8 conversions are what the types rest on
+    assert "cache.desc.flags = sys::EMA_KV_ROTATING" in rust
+    assert "sys::ema_position_write(ctx.stream, self.slot" in rust
+    assert rust.count("sys::ema_kvcache_convert(") == 2
+    assert "sys::ema_kvcache_alloc_fp8(" in rust and "sys::ema_prefill_attention_ws(" in rust
+
+
+def test_crate_source_is_balanced(rust):
+    """No Rust toolchain here: at least the delimiters of the crate source pair up."""
+    text = re.sub(r'"(\\.|[^"\\])*"', '""', rust)  # string literals
+    text = re.sub(r"'(\\.|[^'\\])'", "' '", text)  # char literals
+    stack = []
+    pairs = {")": "(", "]": "[", "}": "{"}
+    for i, ch in enumerate(text):
+        if ch in "([{":
+            stack.append((ch, i))
+        elif ch in pairs:
+            assert stack and stack[-1][0] == pairs[ch], f"unbalanced {ch} at {i}: {text[max(0, i - 80):i + 1]}"
+            stack.pop()
+    assert not stack, stack[-1]
