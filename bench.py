@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "decode_b1", "prefill_chunk", "fp8",
-                                       "int4", "gdn", "gdn_step", "qmm", "prefill_1p7b", "pre"],
+                                      "fp8_tail", "int4", "gdn", "gdn_step", "qmm", "prefill_1p7b", "pre"],
                    default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -334,36 +334,45 @@ def bench_decode_pair(ctx, ema, name, steps=20):
             "attn_gbs": by / (ms_attn * 1e-3) / 1e9, "frac_of_peak": by / (ms_attn * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-def fp8_cache(ctx, ema, B, Hkv, cap, D):
+def fp8_cache(ctx, ema, B, Hkv, cap, D, n_rot=0):
     """FP8 cache of random finite E4M3FN codes with block exponents in {-8, -7} (values of
-    N(0,1) size)."""
+    N(0,1) size); with n_rot = 64 the last 64 dims of each row are N(0,1) bf16 values."""
     torch = ctx.torch
 
     def codes():
-        c = torch.randint(0, 254, (B, Hkv, cap, D), generator=ctx.gen, device=ctx.dev, dtype=torch.int32)
-        return (c + (c >= 0x7F).to(torch.int32)).to(torch.uint8)  # no NaN codes
+        c = torch.randint(0, 254, (B, Hkv, cap, D - n_rot), generator=ctx.gen, device=ctx.dev, dtype=torch.int32)
+        c = (c + (c >= 0x7F).to(torch.int32)).to(torch.uint8)  # no NaN codes
+        if not n_rot:
+            return c
+        tail = ctx.randn((B, Hkv, cap, n_rot)).view(torch.uint8)
+        return torch.cat([c, tail], dim=-1).contiguous()
 
     def exps():
-        return torch.randint(-8, -6, (B, Hkv, cap, D // 64), generator=ctx.gen, device=ctx.dev,
-                             dtype=torch.int32).to(torch.int8)
+        e = torch.randint(-8, -6, (B, Hkv, cap, D // 64), generator=ctx.gen, device=ctx.dev,
+                          dtype=torch.int32).to(torch.int8)
+        if n_rot:
+            e[..., 1] = 0
+        return e
 
-    return ema.StaticCache(B, Hkv, cap, D, dtype="fp8", k=codes(), v=codes(), k_exp=exps(), v_exp=exps())
+    return ema.StaticCache(B, Hkv, cap, D, dtype="fp8", n_rot=n_rot, k=codes(), v=codes(), k_exp=exps(),
+                           v_exp=exps())
 
 
-def fp8_decode_bytes(lengths, Hq, Hkv, D):
-    """K and V codes + block exponents of the valid rows, q in, out."""
+def fp8_decode_bytes(lengths, Hq, Hkv, D, n_rot=0):
+    """K and V rows (codes, and the bf16 tail with n_rot) + block exponents of the valid
+    rows, q in, out."""
     B = len(lengths)
-    return sum(2 * Hkv * int(L) * (D + D // 64) for L in lengths) + 2 * B * Hq * D * 2
+    return sum(2 * Hkv * int(L) * (D + n_rot + D // 64) for L in lengths) + 2 * B * Hq * D * 2
 
 
-def bench_fp8_step(ctx, ema, name, steps=20):
+def bench_fp8_step(ctx, ema, name, steps=20, n_rot=0):
     """The batch-32 Qwen3-8B-shape decode step (fused ema_decode_step) over an FP8 cache."""
     import numpy as np
 
     torch = ctx.torch
     B, Hq, Hkv, D, cap = 32, 32, 8, 128, 8192
     lengths = np.random.default_rng(1234).integers(512, 8193, size=B)
-    cache = fp8_cache(ctx, ema, B, Hkv, cap, D)
+    cache = fp8_cache(ctx, ema, B, Hkv, cap, D, n_rot)
     qkv = ctx.randn((B, (Hq + 2 * Hkv) * D))
     qw, kw = ctx.randn((D,), 1.0, 0.02), ctx.randn((D,), 1.0, 0.02)
     off_d = ctx.i32(lengths - 1)
@@ -371,22 +380,23 @@ def bench_fp8_step(ctx, ema, name, steps=20):
     ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
     ms = time_calls(torch, lambda: ema.decode_step(qkv, qw, kw, 1e-6, 1e6, off_d, Hq, cache, cap, out=out,
                                                    workspace=ws), steps, 5)
-    by = fp8_decode_bytes(lengths, Hq, Hkv, D) + B * (Hq + 2 * Hkv) * D * 2 + B * Hkv * 2 * (D + D // 64)
+    by = (fp8_decode_bytes(lengths, Hq, Hkv, D, n_rot) + B * (Hq + 2 * Hkv) * D * 2
+          + B * Hkv * 2 * (D + n_rot + D // 64))
     gbs = by / (ms * 1e-3) / 1e9
     log(f"[bench] {name}: step {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM)")
     return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
 
 
-def bench_fp8_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20):
+def bench_fp8_decode(ctx, ema, name, B, Hq, Hkv, D, cap, lengths, steps=20, n_rot=0):
     torch = ctx.torch
-    cache = fp8_cache(ctx, ema, B, Hkv, cap, D)
+    cache = fp8_cache(ctx, ema, B, Hkv, cap, D, n_rot)
     q = ctx.randn((B, Hq, D))
     ld = ctx.i32(lengths)
     out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
     ws = ema.decode_workspace(B, Hq, Hkv, D, cap)
     ms = time_calls(torch, lambda: ema.decode_attention(q, cache, ld, int(max(lengths)), out=out, workspace=ws),
                     steps, 5)
-    by = fp8_decode_bytes(lengths, Hq, Hkv, D)
+    by = fp8_decode_bytes(lengths, Hq, Hkv, D, n_rot)
     gbs = by / (ms * 1e-3) / 1e9
     log(f"[bench] {name}: {ms*1e3:.1f} us, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM)")
     return {"workload": name, "us": ms * 1e3, "gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "bytes": by}
@@ -611,6 +621,11 @@ def main():
                                           [32768] * 8))
         secondary.append(bench_fp8_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_fp8_cache", 1, 32, 8, 128, 4096,
                                            2048, 0))
+    if args.only in ("all", "fp8", "fp8_tail"):
+        # Fp8Cache::new(128, 64): dims 64..127 of each row kept as bf16
+        secondary.append(bench_fp8_step(ctx, ema, "decode_step_B32_32q8kv_fp8_cache_rope_tail64", n_rot=64))
+        secondary.append(bench_fp8_decode(ctx, ema, "decode_B8_32q4kv_L32768_fp8_cache_rope_tail64", 8, 32, 4, 128,
+                                          32768, [32768] * 8, n_rot=64))
     if args.only in ("all", "int4"):
         secondary.append(bench_int4_step(ctx, ema, "decode_step_B32_32q8kv_int4_cache"))
         secondary.append(bench_int4_decode(ctx, ema, "decode_B8_32q4kv_L32768_int4_cache", 8, 32, 4, 128, 32768,

@@ -90,6 +90,7 @@ pub mod sys {
         pub k_biases: *mut c_void,
         pub v_scales: *mut c_void,
         pub v_biases: *mut c_void,
+        pub n_rot: i32,
     }
 
     impl Default for EmaKvCacheDesc {
@@ -113,6 +114,7 @@ pub mod sys {
                 k_biases: null,
                 v_scales: null,
                 v_biases: null,
+                n_rot: 0,
             }
         }
     }
@@ -126,9 +128,9 @@ pub mod sys {
                                  head_dim: i32) -> i32;
         pub fn ema_kvcache_init_fp8(desc: *mut EmaKvCacheDesc, k: *mut c_void, v: *mut c_void,
                                     k_exp: *mut c_void, v_exp: *mut c_void, batch: i32, n_kv_heads: i32,
-                                    capacity: i32, head_dim: i32) -> i32;
+                                    capacity: i32, head_dim: i32, n_rot: i32) -> i32;
         pub fn ema_kvcache_alloc_fp8(out: *mut EmaKvCacheDesc, batch: i32, n_kv_heads: i32, capacity: i32,
-                                     head_dim: i32) -> i32;
+                                     head_dim: i32, n_rot: i32) -> i32;
         pub fn ema_kvcache_init_int4(desc: *mut EmaKvCacheDesc, k: *mut c_void, v: *mut c_void,
                                      k_scales: *mut c_void, k_biases: *mut c_void, v_scales: *mut c_void,
                                      v_biases: *mut c_void, batch: i32, n_kv_heads: i32, capacity: i32,
@@ -661,8 +663,9 @@ impl HipKvCache for RotatingCache {
 /// which keeps the E4M3FN round trip of every 64-value block of each K/V row), stored as one
 /// code byte per value plus one exponent byte per block (`ema_kvcache_alloc_fp8`), allocated
 /// zeroed once with a static capacity; `reset` rewinds the length only. The layer calls
-/// quantise the rows they write and attend the decoded values. `n_rot` (the reference's
-/// unquantised RoPE tail of each head) must be 0; head_dim 128.
+/// quantise the rows they write and attend the decoded values. `n_rot` is the reference's
+/// unquantised RoPE tail of each head (`Fp8Cache::new(head_dim, n_rot)`, fp8.rs:38-54): 0 or
+/// 64, whose dims 64..127 are stored as bf16; head_dim 128.
 pub struct Fp8Cache {
     desc: sys::EmaKvCacheDesc,
     offset: i32,
@@ -673,15 +676,16 @@ unsafe impl Send for Fp8Cache {}
 
 impl Fp8Cache {
     pub fn new(n_kv_heads: i32, capacity: i32, head_dim: i32, n_rot: i32) -> Result<Self> {
-        if n_rot != 0 {
-            bail!("Fp8Cache: n_rot {} (an unquantised RoPE tail) is not supported; the whole head is quantised",
-                  n_rot);
-        }
         let positions = PositionTable::new(capacity.max(0))?;
         let mut desc = sys::EmaKvCacheDesc::default();
-        check(unsafe { sys::ema_kvcache_alloc_fp8(&mut desc, 1, n_kv_heads, capacity, head_dim) },
+        check(unsafe { sys::ema_kvcache_alloc_fp8(&mut desc, 1, n_kv_heads, capacity, head_dim, n_rot) },
               "kvcache_alloc_fp8")?;
         Ok(Fp8Cache { desc, offset: 0, positions })
+    }
+
+    /// Dims at the end of each head kept unquantised (bf16).
+    pub fn n_rot(&self) -> i32 {
+        self.desc.n_rot
     }
 }
 

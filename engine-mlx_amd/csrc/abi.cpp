@@ -82,6 +82,13 @@ int32_t check_cache(const char* op, const ema_kvcache_desc* c) {
       return set_error(EMA_ERR_UNSUPPORTED, "%s: fp8 cache with head_dim %d not supported (128)", op, c->head_dim);
     if (c->stride_pos % 16 || c->stride_head % 16 || c->stride_batch % 16)
       return set_error(EMA_ERR_SHAPE, "%s: fp8 cache strides must be multiples of 16 bytes", op);
+    if (c->n_rot != 0 && c->n_rot != 64)
+      return set_error(EMA_ERR_UNSUPPORTED, "%s: fp8 cache n_rot %d not supported (0 or 64)", op, c->n_rot);
+    if (c->stride_pos < (int64_t)c->head_dim + c->n_rot)
+      return set_error(EMA_ERR_SHAPE, "%s: fp8 cache rows with n_rot %d need stride_pos >= %d bytes", op, c->n_rot,
+                       c->head_dim + c->n_rot);
+  } else if (c->n_rot != 0) {
+    return set_error(EMA_ERR_INVALID_ARG, "%s: n_rot %d is an fp8 cache field (0 for other dtypes)", op, c->n_rot);
   }
   if (c->dtype == EMA_DTYPE_INT4_AFFINE) {
     if (!c->k_scales || !c->k_biases || !c->v_scales || !c->v_biases)
@@ -198,7 +205,7 @@ int32_t ema_kvcache_alloc(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_hea
 }
 
 int32_t ema_kvcache_init_fp8(ema_kvcache_desc* d, void* k, void* v, void* k_exp, void* v_exp, int32_t batch,
-                             int32_t n_kv_heads, int32_t capacity, int32_t head_dim) {
+                             int32_t n_kv_heads, int32_t capacity, int32_t head_dim, int32_t n_rot) {
   if (!d) return set_error(EMA_ERR_INVALID_ARG, "ema_kvcache_init_fp8: descriptor is null");
   memset(d, 0, sizeof(*d));
   d->k = k;
@@ -209,15 +216,18 @@ int32_t ema_kvcache_init_fp8(ema_kvcache_desc* d, void* k, void* v, void* k_exp,
   d->n_kv_heads = n_kv_heads;
   d->capacity = capacity;
   d->head_dim = head_dim;
-  d->stride_pos = head_dim;
-  d->stride_head = (int64_t)capacity * head_dim;
-  d->stride_batch = (int64_t)n_kv_heads * capacity * head_dim;
+  d->n_rot = n_rot;
+  // a row: head_dim - n_rot code bytes, then n_rot bf16 values
+  const int64_t row = (int64_t)head_dim + n_rot;
+  d->stride_pos = row;
+  d->stride_head = (int64_t)capacity * row;
+  d->stride_batch = (int64_t)n_kv_heads * capacity * row;
   d->dtype = EMA_DTYPE_FP8_E4M3;
   return check_cache("ema_kvcache_init_fp8", d);
 }
 
 int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads, int32_t capacity,
-                              int32_t head_dim) {
+                              int32_t head_dim, int32_t n_rot) {
   const char* op = "ema_kvcache_alloc_fp8";
   if (!out) return set_error(EMA_ERR_INVALID_ARG, "%s: descriptor is null", op);
   memset(out, 0, sizeof(*out));
@@ -225,8 +235,10 @@ int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv
     return set_error(head_dim != 128 && head_dim > 0 ? EMA_ERR_UNSUPPORTED : EMA_ERR_SHAPE,
                      "%s: bad dims (batch=%d n_kv_heads=%d capacity=%d head_dim=%d; fp8 needs head_dim 128)", op,
                      batch, n_kv_heads, capacity, head_dim);
+  if (n_rot != 0 && n_rot != 64)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: n_rot %d not supported (0 or 64)", op, n_rot);
   const size_t rows = (size_t)batch * n_kv_heads * capacity;
-  const size_t code_bytes = rows * head_dim, exp_bytes = rows * (head_dim / 64);
+  const size_t code_bytes = rows * (head_dim + n_rot), exp_bytes = rows * (head_dim / 64);
   void* p[4] = {nullptr, nullptr, nullptr, nullptr};
   const size_t sz[4] = {code_bytes, code_bytes, exp_bytes, exp_bytes};
   int32_t rc = EMA_OK;
@@ -239,7 +251,7 @@ int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv
       if (p[i]) (void)hipFree(p[i]);
     return rc;
   }
-  return ema_kvcache_init_fp8(out, p[0], p[1], p[2], p[3], batch, n_kv_heads, capacity, head_dim);
+  return ema_kvcache_init_fp8(out, p[0], p[1], p[2], p[3], batch, n_kv_heads, capacity, head_dim, n_rot);
 }
 
 int32_t ema_kvcache_init_int4(ema_kvcache_desc* d, void* k, void* v, void* k_scales, void* k_biases,
@@ -364,7 +376,7 @@ int32_t ema_kvcache_memory_bytes(const ema_kvcache_desc* d, uint64_t* bytes) {
   int32_t rc = check_cache("ema_kvcache_memory_bytes", d);
   if (rc) return rc;
   const uint64_t rows = 2ull * d->batch * d->n_kv_heads * d->capacity;  // K and V
-  if (d->dtype == EMA_DTYPE_FP8_E4M3) *bytes = rows * (d->head_dim + d->head_dim / 64);
+  if (d->dtype == EMA_DTYPE_FP8_E4M3) *bytes = rows * (d->head_dim + d->n_rot + d->head_dim / 64);
   else if (d->dtype == EMA_DTYPE_INT4_AFFINE) *bytes = rows * (d->head_dim / 2 + 4ull * (d->head_dim / 64));
   else *bytes = rows * d->head_dim * 2ull;
   return EMA_OK;

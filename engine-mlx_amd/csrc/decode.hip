@@ -42,7 +42,9 @@
 // FP8 E4M3FN cache: a lane loads the same row pieces as 8 codes (8 bytes) instead of
 // 8 bf16 values, plus the row's two block exponents, and turns them into the same bf16
 // operands just before use (code value times 2^exp is exact in bf16). Half the bytes,
-// identical arithmetic after the decode step.
+// identical arithmetic after the decode step. With an unquantised RoPE tail (n_rot = 64:
+// a row is 64 codes, then dims 64..127 as bf16) the pieces of dims >= 64 are loaded as
+// bf16 and used as they are.
 #include "ema_common.hpp"
 #include "ema_schedule.hpp"
 
@@ -409,8 +411,11 @@ __device__ void merge_segment(const DecodeArgs& a, int b, int kh, int64_t s, int
   for (int e = threadIdx.x; e < a.G * kD; e += blockDim.x) merge_element<true>(a, b, kh, s, w0, w1, e / kD, e % kD);
 }
 
-template <bool kFused, bool kFp8, bool kI4 = false>
+template <bool kFused, bool kFp8, bool kI4 = false, bool kRot = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
+  // kRot: FP8 rows with the RoPE tail, read only (the fused step over them is the
+  // pre-attention kernel followed by this kernel, see launch_decode)
+  static_assert(!kRot || (kFp8 && !kFused), "the RoPE-tail reader is the unfused FP8 decode");
   constexpr bool kNarrow = kFp8 || kI4;  // the fp8 head-dim order (kdim)
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
@@ -480,31 +485,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint16_t* const Ve = kFp8 ? (const uint16_t*)a.vexp + erow : nullptr;
     u32x2 k8[2][4], v8[8], k8n[2][4], v8n[8];
     uint32_t ke[2], ve[8], ken[2], ven[8];
-    auto load_tile8 = [&](int tile, u32x2 (&kr)[2][4], u32x2 (&vr)[8], uint32_t (&kx)[2], uint32_t (&vx)[8]) {
+    // RoPE tail (kRot): the bf16 K pieces of steps 2, 3 and one aligned 16-byte V load per
+    // position: for lanes m < 8 the codes of dims 8(m & ~1) .. +15 (its own 8 are words
+    // 2(m & 1), +1), for m >= 8 the bf16 dims 8m .. 8m+7
+    u32x4 kt[2][2], ktn[2][2], vw[8], vwn[8];
+    auto load_k8 = [&](int tile, u32x2 (&kr)[2][4], uint32_t (&kx)[2], u32x4 (&ktr)[2][2]) {
       const int p0 = tile * kTile;
       for (int r = 0; r < 2; ++r) {
         int p = p0 + krow0 + 4 * r;
         p = p < L ? p : L - 1;
         const uint8_t* row = Kb8 + (int64_t)p * a.sp;
-        for (int i = 0; i < 2; ++i) {  // steps 2i, 2i+1: one 16-byte load
+        for (int i = 0; i < (kRot ? 1 : 2); ++i) {  // steps 2i, 2i+1: one 16-byte load
           const u32x4 w = __builtin_nontemporal_load((const u32x4*)(row + kdim<true>(2 * i, c)));
           kr[r][2 * i] = u32x2{w[0], w[1]};
           kr[r][2 * i + 1] = u32x2{w[2], w[3]};
         }
+        if (kRot) {  // dims 64 + 16c .. +15 as bf16: bytes 64 + 32c .. +31 of the row
+          ktr[r][0] = __builtin_nontemporal_load((const u32x4*)(row + 64 + 32 * c));
+          ktr[r][1] = __builtin_nontemporal_load((const u32x4*)(row + 64 + 32 * c + 16));
+        }
         kx[r] = Ke[p];
       }
+    };
+    auto load_v8 = [&](int tile, u32x2 (&vr)[8], uint32_t (&vx)[8], u32x4 (&vwr)[8]) {
+      const int p0 = tile * kTile;
       for (int kk = 0; kk < 8; ++kk) {
         int p = p0 + 8 * c + kk;
         p = p < L ? p : L - 1;
-        vr[kk] = ld8_stream(Vb8 + (int64_t)p * a.sp + 8 * m);
+        if (kRot)
+          vwr[kk] = __builtin_nontemporal_load(
+              (const u32x4*)(Vb8 + (int64_t)p * a.sp + (m < 8 ? 16 * (m >> 1) : 16 * m - 64)));
+        else
+          vr[kk] = ld8_stream(Vb8 + (int64_t)p * a.sp + 8 * m);
         vx[kk] = Ve[p];
       }
+    };
+    auto load_tile8 = [&](int tile, u32x2 (&kr)[2][4], u32x2 (&vr)[8], uint32_t (&kx)[2], uint32_t (&vx)[8],
+                          u32x4 (&ktr)[2][2], u32x4 (&vwr)[8]) {
+      load_k8(tile, kr, kx, ktr);
+      load_v8(tile, vr, vx, vwr);
     };
     u32x4 kc[2][4], vc[8], kn[2][4], vn[8];
     auto decode_tile8 = [&]() {
       for (int r = 0; r < 2; ++r)
-        for (int s = 0; s < 4; ++s) kc[r][s] = fp8_decode8(k8[r][s], (int)(int8_t)(ke[r] >> (s >= 2 ? 8 : 0)));
-      for (int kk = 0; kk < 8; ++kk) vc[kk] = fp8_decode8(v8[kk], (int)(int8_t)(ve[kk] >> (m >= 8 ? 8 : 0)));
+        for (int s = 0; s < 4; ++s)
+          kc[r][s] = kRot && s >= 2 ? kt[r][s - 2] : fp8_decode8(k8[r][s], (int)(int8_t)(ke[r] >> (s >= 2 ? 8 : 0)));
+      for (int kk = 0; kk < 8; ++kk) {
+        if (kRot) {
+          const u32x2 w = (m & 1) ? u32x2{vw[kk][2], vw[kk][3]} : u32x2{vw[kk][0], vw[kk][1]};
+          const u32x4 d = fp8_decode8(w, (int)(int8_t)ve[kk]);
+          vc[kk] = m < 8 ? d : vw[kk];
+        } else {
+          vc[kk] = fp8_decode8(v8[kk], (int)(int8_t)(ve[kk] >> (m >= 8 ? 8 : 0)));
+        }
+      }
     };
     auto load_tile = [&](int tile, u32x4 (&kr)[2][4], u32x4 (&vr)[8]) {
       const int p0 = tile * kTile;
@@ -614,7 +648,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           if (first + kWaves < tile1) i4_dma(first + kWaves, 1);
         }
       } else if (kFp8) {
-        load_tile8(first, k8, v8, ke, ve);
+        load_tile8(first, k8, v8, ke, ve, kt, vw);
       } else {
         load_tile(first, kc, vc);
       }
@@ -920,8 +954,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if constexpr (!kI4)
     for (int tile = first; tile < tile1; tile += kWaves) {
       const bool more = tile + kWaves < tile1;
-      if (kFp8) {
-        if (more) load_tile8(tile + kWaves, k8n, v8n, ken, ven);
+      if (kFp8 && kRot) {
+        // decoded first, so that the raw tile dies before the next one's registers are
+        // claimed; the next V rows are requested after the score MFMAs, once kc is dead
+        decode_tile8();
+        if (more) load_k8(tile + kWaves, k8n, ken, ktn);
+      } else if (kFp8) {
+        if (more) load_tile8(tile + kWaves, k8n, v8n, ken, ven, ktn, vwn);
         decode_tile8();
       } else if (more) {
         load_tile(tile + kWaves, kn, vn);
@@ -946,6 +985,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int s = 0; s < 4; ++s) acc = mfma16(as_bf16x8(kc[r][s]), qop[s], acc);
         sc[r] = acc;
       }
+      if (kFp8 && kRot && more) load_v8(tile + kWaves, v8n, ven, vwn);
       // running max on raw scores (scale > 0), exponent as one fma
       float x[8];
       float mx = -INFINITY;
@@ -989,10 +1029,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (kFp8) {
           for (int r = 0; r < 2; ++r) {
             for (int s = 0; s < 4; ++s) k8[r][s] = k8n[r][s];
+            if (kRot) kt[r][0] = ktn[r][0], kt[r][1] = ktn[r][1];
             ke[r] = ken[r];
           }
           for (int kk = 0; kk < 8; ++kk) {
             v8[kk] = v8n[kk];
+            if (kRot) vw[kk] = vwn[kk];
             ve[kk] = ven[kk];
           }
         } else {
@@ -1178,11 +1220,28 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.vb = (uint32_t*)c.v_biases;
   const bool fp8 = c.dtype == EMA_DTYPE_FP8_E4M3;
   const bool i4 = c.dtype == EMA_DTYPE_INT4_AFFINE;
+  const bool tail = fp8 && c.n_rot != 0;
   const dim3 grid(plan.workers), block(kWaves * 64);
-  if (a.fused && i4) hipLaunchKernelGGL((decode_kernel<true, false, true>), grid, block, 0, s, a);
+  if (a.fused && tail) {
+    // The fused step over FP8 rows with a RoPE tail runs as two kernels: the fused kernel
+    // has no registers to spare for the tail's wider rows (it spilled and ran at 155 us
+    // against 69 us at the batch-32 shape). The pre-attention kernel writes the new row and
+    // puts q in `out` (q [B, Hq, 1, D] and out [B, Hq * D] share one layout); the decode
+    // kernel then reads q there and takes its lengths from the offsets (a.fused). Every
+    // workgroup reads the q of a (sequence, kv head) segment before it arrives, and out of
+    // that segment is written only after the last arrival (or by decode_merge_kernel), so
+    // no q is overwritten before it is read.
+    int32_t rc = launch_pre_attention(s, fused->qkv, fused->q_norm_w, fused->k_norm_w, fused->eps, fused->theta,
+                                      fused->offsets, c.batch, 1, Hq, c.n_kv_heads, kD,
+                                      fused->flags & ~(uint32_t)EMA_STEP_ADVANCE, out, c);
+    if (rc) return rc;
+    a.q = (const uint16_t*)out;
+    hipLaunchKernelGGL((decode_kernel<false, true, false, true>), grid, block, 0, s, a);
+  } else if (a.fused && i4) hipLaunchKernelGGL((decode_kernel<true, false, true>), grid, block, 0, s, a);
   else if (i4) hipLaunchKernelGGL((decode_kernel<false, false, true>), grid, block, 0, s, a);
   else if (a.fused && fp8) hipLaunchKernelGGL((decode_kernel<true, true>), grid, block, 0, s, a);
   else if (a.fused) hipLaunchKernelGGL((decode_kernel<true, false>), grid, block, 0, s, a);
+  else if (tail) hipLaunchKernelGGL((decode_kernel<false, true, false, true>), grid, block, 0, s, a);
   else if (fp8) hipLaunchKernelGGL((decode_kernel<false, true>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((decode_kernel<false, false>), grid, block, 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");

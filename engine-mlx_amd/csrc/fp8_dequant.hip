@@ -9,7 +9,8 @@
 // written per row of K or V, small next to the prefill's matrix work.
 //
 // Mapping: 8 threads per 128-dim row, 16 codes (one 16-byte load) each, 32 rows per
-// 256-thread workgroup pass; blockIdx.y = (batch, kv head). Rows [lo, hi) of a sequence
+// 256-thread workgroup pass; blockIdx.y = (batch, kv head). With an unquantised RoPE
+// tail (n_rot = 64) the threads of dims 64..127 copy their 16 bf16 values. Rows [lo, hi) of a sequence
 // are decoded, hi = min(q_off + T, rows), lo = q_off with EMA_PREFILL_CHUNK_ONLY (0
 // otherwise) -- exactly the rows the prefill kernel reads. A rotating cache (position p in
 // row p % cap) has every held row decoded, lo = 0 (a chunk's rows may wrap the ring).
@@ -32,6 +33,7 @@ struct DequantArgs {
   int Hkv, cap, R, T;
   uint32_t flags;
   int rot;
+  int nrot;  // dims 64..127 stored as bf16 after the 64 codes of a row
 };
 
 __global__ __launch_bounds__(256) void fp8_to_bf16_kernel(DequantArgs a) {
@@ -51,6 +53,13 @@ __global__ __launch_bounds__(256) void fp8_to_bf16_kernel(DequantArgs a) {
   const int64_t erow = (int64_t)bh * a.cap + row;
   const int64_t dst = ((int64_t)bh * a.R + row) * kD + 16 * t8;
   for (int kv = 0; kv < 2; ++kv) {
+    if (a.nrot && t8 >= 4) {  // dims 16 t8 .. +15: bf16 at bytes 64 + 2 (16 t8 - 64)
+      const uint8_t* tail = (kv ? a.v : a.k) + (src - 16 * t8) + 32 * t8 - 64;
+      uint16_t* const out = (kv ? a.wv : a.wk) + dst;
+      *(u32x4*)out = *(const u32x4*)tail;
+      *(u32x4*)(out + 8) = *(const u32x4*)(tail + 16);
+      continue;
+    }
     const u32x4 codes = *(const u32x4*)((kv ? a.v : a.k) + src);
     const uint32_t ex = (kv ? a.vexp : a.kexp)[erow];
     const int e = (int)(int8_t)(ex >> (t8 >= 4 ? 8 : 0));  // dims < 64: block 0
@@ -73,7 +82,8 @@ __global__ __launch_bounds__(256) void fp8_to_bf16_kernel(DequantArgs a) {
 // crates/kvcache/src/fp8.rs:47-68, as ema_pre_attention writes it) or FP8 -> bf16 (the
 // exact decoded values, what Fp8Cache::get hands SDPA: fp8.rs:60-68). 8 lanes per 128-value
 // row, lane j with values 8j .. 8j+7 and 64+8j .. 64+8j+7 (one 64-value block each), 32
-// rows per 256-thread workgroup. HBM-bound.
+// rows per 256-thread workgroup. HBM-bound. With an unquantised RoPE tail (the FP8
+// side's n_rot = 64) the second block is copied as bf16 and its exponent written as 0.
 struct ConvArgs {
   const uint8_t* sk;  // source K / V (bytes; element strides below)
   const uint8_t* sv;
@@ -87,6 +97,7 @@ struct ConvArgs {
   int64_t dsb, dsh, dsp;  // destination strides (elements)
   int Hkv, scap, dcap, src_row, dst_row, n;
   int64_t total;  // B * Hkv * n rows
+  int nrot;       // the FP8 side keeps dims 64..127 as bf16
 };
 
 template <bool kToFp8>
@@ -115,17 +126,20 @@ __global__ __launch_bounds__(256) void fp8_convert_kernel(ConvArgs a) {
         m0 = fmaxf(m0, fabsf(bf16_to_f32(x[e])));
         m1 = fmaxf(m1, fabsf(bf16_to_f32(x[8 + e])));
       }
-      const int e0 = fp8_block_exp(m0), e1 = fp8_block_exp(m1);
+      const int e0 = fp8_block_exp(m0);
+      const int e1 = a.nrot ? 0 : fp8_block_exp(m1);  // (uniform over the 8 lanes)
       uint8_t* codes = (kv ? a.dv : a.dk) + drow;
       *(u32x2*)(codes + 8 * lane8) = fp8_encode8(x, e0);
-      *(u32x2*)(codes + 64 + 8 * lane8) = fp8_encode8(x + 8, e1);
+      if (a.nrot) *(u32x4*)(codes + 64 + 16 * lane8) = hi;
+      else *(u32x2*)(codes + 64 + 8 * lane8) = fp8_encode8(x + 8, e1);
       if (lane8 == 0)
         (kv ? a.dvexp : a.dkexp)[bh * a.dcap + a.dst_row + r] = (uint16_t)((uint8_t)e0 | ((uint32_t)(uint8_t)e1 << 8));
     } else {
       const uint8_t* codes = (kv ? a.sv : a.sk) + srow;
       const uint32_t ex = (kv ? a.svexp : a.skexp)[bh * a.scap + a.src_row + r];
       uint16_t* dst = (uint16_t*)(kv ? a.dv : a.dk) + drow;
-      for (int h = 0; h < 2; ++h) {
+      if (a.nrot) *(u32x4*)(dst + 64 + 8 * lane8) = *(const u32x4*)(codes + 64 + 16 * lane8);
+      for (int h = 0; h < (a.nrot ? 1 : 2); ++h) {
         const u32x2 w = *(const u32x2*)(codes + 64 * h + 8 * lane8);
         const float sc = __uint_as_float((uint32_t)((int)(int8_t)(ex >> (8 * h)) + 127) << 23);
         u32x4 o4;
@@ -165,6 +179,7 @@ int32_t launch_fp8_convert(hipStream_t s, const ema_kvcache_desc& src, int src_r
   a.dst_row = dst_row;
   a.n = n_rows;
   a.total = (int64_t)dst.batch * dst.n_kv_heads * n_rows;
+  a.nrot = (dst.dtype == EMA_DTYPE_FP8_E4M3 ? dst.n_rot : src.n_rot) != 0;
   const int64_t blocks = (a.total + 31) / 32;
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_kvcache_convert: too many rows");
   const bool to_fp8 = dst.dtype == EMA_DTYPE_FP8_E4M3;
@@ -192,6 +207,7 @@ int32_t launch_fp8_to_bf16(hipStream_t s, const ema_kvcache_desc& c, const int32
   a.T = T;
   a.flags = flags;
   a.rot = (c.flags & EMA_KV_ROTATING) != 0;
+  a.nrot = c.n_rot != 0;
   const dim3 grid((unsigned)((R + 31) / 32), (unsigned)(c.batch * c.n_kv_heads));
   hipLaunchKernelGGL(fp8_to_bf16_kernel, grid, dim3(256), 0, s, a);
   return check_hip(hipGetLastError(), "ema_prefill_attention_ws: fp8 decode launch");

@@ -22,7 +22,9 @@
 // FP8 E4M3FN cache (D = 128): the two halves of a row that the 8 lanes of a head hold
 // are exactly its two 64-element blocks; each block's scale exponent comes from an
 // 8-lane max, and the lane writes its 2 x 8 codes (the quantisation of
-// crates/ops/src/fp8.rs:71-92, applied to the bf16 row as Fp8Cache::append does).
+// crates/ops/src/fp8.rs:71-92, applied to the bf16 row as Fp8Cache::append does). With
+// an unquantised RoPE tail (n_rot = 64) the second half is written as bf16 after the 64
+// codes of the first, and block 1's exponent as 0.
 #include "ema_common.hpp"
 
 namespace ema {
@@ -105,6 +107,7 @@ struct PreArgs {
   int B, T, Hq, Hkv, cap;
   uint32_t flags;
   int rot;  // rotating cache: position p lives in row p % cap
+  int nrot;  // fp8 cache: dims 64..127 kept as bf16 (n_rot = 64)
 };
 
 template <int D, bool kFp8, bool kI4 = false>
@@ -145,10 +148,12 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       m0 = fmaxf(m0, fabsf(bf16_to_f32(x[e])));
       m1 = fmaxf(m1, fabsf(bf16_to_f32(x[E + e])));
     }
-    const int e0 = fp8_block_exp(m0), e1 = fp8_block_exp(m1);
+    const int e0 = fp8_block_exp(m0);
+    const int e1 = a.nrot ? 0 : fp8_block_exp(m1);  // (uniform: all 8 lanes shuffle or none)
     uint8_t* row = (uint8_t*)codes16 + (int64_t)b_ * a.sb + (int64_t)kh * a.sh + (int64_t)p_ * a.sp;
     *(u32x2*)(row + lane8 * E) = fp8_encode8(x, e0);
-    *(u32x2*)(row + HALF + lane8 * E) = fp8_encode8(x + E, e1);
+    if (a.nrot) Vec<E>::store((uint16_t*)(row + HALF) + lane8 * E, x + E);
+    else *(u32x2*)(row + HALF + lane8 * E) = fp8_encode8(x + E, e1);
     if (lane8 == 0) {
       const int64_t r = ((int64_t)b_ * a.Hkv + kh) * a.cap + p_;
       *(uint16_t*)(exps + 2 * r) = (uint16_t)((uint8_t)e0 | ((uint32_t)(uint8_t)e1 << 8));
@@ -270,6 +275,7 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   a.cap = c.capacity;
   a.flags = flags;
   a.rot = (c.flags & EMA_KV_ROTATING) != 0;
+  a.nrot = c.dtype == EMA_DTYPE_FP8_E4M3 && c.n_rot != 0;
   const int threads = 256;
   const int64_t blocks = (int64_t)B * T;  // one workgroup per token
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many tokens");

@@ -70,6 +70,7 @@ class KvCacheDesc(ctypes.Structure):
         ("k_exp", ctypes.c_void_p), ("v_exp", ctypes.c_void_p),
         ("k_scales", ctypes.c_void_p), ("k_biases", ctypes.c_void_p),
         ("v_scales", ctypes.c_void_p), ("v_biases", ctypes.c_void_p),
+        ("n_rot", ctypes.c_int32),
     ]
 
 
@@ -90,8 +91,8 @@ def lib() -> ctypes.CDLL:
             "ema_version": (ctypes.c_char_p, []),
             "ema_kvcache_init": (i32, [D, vp, vp, i32, i32, i32, i32]),
             "ema_kvcache_alloc": (i32, [D, i32, i32, i32, i32]),
-            "ema_kvcache_init_fp8": (i32, [D, vp, vp, vp, vp, i32, i32, i32, i32]),
-            "ema_kvcache_alloc_fp8": (i32, [D, i32, i32, i32, i32]),
+            "ema_kvcache_init_fp8": (i32, [D, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+            "ema_kvcache_alloc_fp8": (i32, [D, i32, i32, i32, i32, i32]),
             "ema_kvcache_init_int4": (i32, [D, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
             "ema_kvcache_alloc_int4": (i32, [D, i32, i32, i32, i32]),
             "ema_kvcache_quantize_int4": (i32, [vp, D, i32, D, i32, i32]),
@@ -157,7 +158,9 @@ class StaticCache:
     ``dtype="fp8"``: the stored form of the reference's Fp8Cache
     (crates/kvcache/src/fp8.rs): ``k``/``v`` are uint8 E4M3FN codes and
     ``k_exp``/``v_exp`` int8 [B, Hkv, cap, D/64] block exponents
-    (value = code * 2^exp); head_dim 128.
+    (value = code * 2^exp); head_dim 128. ``n_rot=64`` (Fp8Cache::new(128, 64)): the last
+    64 dims of each row are kept as bf16, so a row of ``k``/``v`` is [B, Hkv, cap, 192]
+    bytes, 64 codes then the 64 bf16 values (block 1's exponent is 0).
 
     ``dtype="int4"``: the reference's int4 KV buffers (alloc_kv_int4,
     crates/serve/src/engine_ext.rs:92-129): ``k``/``v`` are int32 words [B, Hkv, cap, D/8]
@@ -172,7 +175,7 @@ class StaticCache:
 
     def __init__(self, batch: int, n_kv_heads: int, capacity: int, head_dim: int, device="cuda",
                  k=None, v=None, dtype="bf16", k_exp=None, v_exp=None, rotating=False, k_scales=None,
-                 k_biases=None, v_scales=None, v_biases=None):
+                 k_biases=None, v_scales=None, v_biases=None, n_rot=0):
         import torch
 
         shape = (batch, n_kv_heads, capacity, head_dim)
@@ -186,12 +189,13 @@ class StaticCache:
                                           capacity, head_dim), "ema_kvcache_init")
         elif dtype == "fp8":
             eshape = (batch, n_kv_heads, capacity, head_dim // 64)
-            self.k = k if k is not None else torch.zeros(shape, dtype=torch.uint8, device=device)
-            self.v = v if v is not None else torch.zeros(shape, dtype=torch.uint8, device=device)
+            rshape = (batch, n_kv_heads, capacity, head_dim + n_rot)
+            self.k = k if k is not None else torch.zeros(rshape, dtype=torch.uint8, device=device)
+            self.v = v if v is not None else torch.zeros(rshape, dtype=torch.uint8, device=device)
             self.k_exp = k_exp if k_exp is not None else torch.zeros(eshape, dtype=torch.int8, device=device)
             self.v_exp = v_exp if v_exp is not None else torch.zeros(eshape, dtype=torch.int8, device=device)
             _check(lib().ema_kvcache_init_fp8(ctypes.byref(self.desc), _ptr(self.k), _ptr(self.v), _ptr(self.k_exp),
-                                              _ptr(self.v_exp), batch, n_kv_heads, capacity, head_dim),
+                                              _ptr(self.v_exp), batch, n_kv_heads, capacity, head_dim, n_rot),
                    "ema_kvcache_init_fp8")
         elif dtype == "int4":
             mshape = (batch, n_kv_heads, capacity, head_dim // 64)
@@ -207,6 +211,8 @@ class StaticCache:
                    "ema_kvcache_init_int4")
         else:
             raise ValueError(f"unknown cache dtype {dtype!r} (bf16, fp8 or int4)")
+        if n_rot and dtype != "fp8":
+            raise ValueError("n_rot is an fp8 cache parameter")
         self.rotating = bool(rotating)
         if self.rotating:
             self.desc.flags = EMA_KV_ROTATING

@@ -261,10 +261,7 @@ std::pair<Array, Array> RotatingCache::get(const Ctx& ctx) const {
 
 Fp8Cache::Fp8Cache(int32_t n_kv_heads, int32_t capacity, int32_t head_dim, int32_t n_rot)
     : positions_(capacity > 0 ? capacity : 0) {
-  if (n_rot != 0)
-    throw Error(EMA_ERR_UNSUPPORTED, "Fp8Cache: n_rot " + std::to_string(n_rot) +
-                                         " (an unquantised RoPE tail) is not supported; the whole head is quantised");
-  check(ema_kvcache_alloc_fp8(&desc_, 1, n_kv_heads, capacity, head_dim), "kvcache_alloc_fp8");
+  check(ema_kvcache_alloc_fp8(&desc_, 1, n_kv_heads, capacity, head_dim, n_rot), "kvcache_alloc_fp8");
 }
 
 Fp8Cache::~Fp8Cache() { ema_kvcache_free(&desc_); }

@@ -199,8 +199,9 @@ class EMA_HOST_API RotatingCache final : public HipKvCache {
 // codes, [1, Hkv, capacity, head_dim / 64] exponents, ema_kvcache_alloc_fp8), allocated
 // zeroed once with a static capacity; reset() rewinds the length only. The layer calls
 // quantise the rows they write (ema_pre_attention / ema_decode_step) and attend the
-// decoded values. n_rot (the reference's unquantised RoPE tail of each head) must be 0:
-// other values are refused with EMA_ERR_UNSUPPORTED. head_dim 128.
+// decoded values. n_rot is the reference's unquantised RoPE tail of each head
+// (Fp8Cache::new(head_dim, n_rot), fp8.rs:38-54): 0, or 64, whose dims 64..127 are stored
+// as bf16 (other values: EMA_ERR_UNSUPPORTED). head_dim 128.
 class EMA_HOST_API Fp8Cache final : public HipKvCache {
  public:
   Fp8Cache(int32_t n_kv_heads, int32_t capacity, int32_t head_dim, int32_t n_rot = 0);
@@ -220,7 +221,7 @@ class EMA_HOST_API Fp8Cache final : public HipKvCache {
   const ema_kvcache_desc& desc() const override { return desc_; }
   const int32_t* position(const Ctx&, int64_t p) const override;
   void set_len(int64_t n) override;
-  int32_t n_rot() const { return 0; }
+  int32_t n_rot() const { return desc_.n_rot; }
 
  private:
   ema_kvcache_desc desc_{};

@@ -73,9 +73,11 @@ extern "C" {
 /* FP8 E4M3FN codes (one byte per element) plus one int8 exponent per 64-element block
  * of a row: element = e4m3(code) * 2^exp. Written with the quantisation of the
  * reference's FP8 cache (crates/ops/src/fp8.rs:71-92: exp = ceil(log2(amax / 448)),
- * amax = max(1e-4, max |x|) over the block, round to nearest even, saturate at 448; the
- * whole head is quantised, i.e. n_rot = 0). Decoded exactly to bf16 by the readers.
- * head_dim 128 only, static or rotating (EMA_KV_ROTATING) caches. Values must be finite. */
+ * amax = max(1e-4, max |x|) over the block, round to nearest even, saturate at 448).
+ * Decoded exactly to bf16 by the readers. head_dim 128 only, static or rotating
+ * (EMA_KV_ROTATING) caches. Values must be finite. With n_rot = 64 (the descriptor's
+ * field; Fp8Cache::new(128, 64), crates/kvcache/src/fp8.rs:38-54) the last 64 dims of each
+ * row are the RoPE tail that the reference leaves unquantised: they are stored as bf16. */
 #define EMA_DTYPE_FP8_E4M3 2
 /* 4-bit affine codes (MLX "affine" quantisation, group 64, the layout of the reference's
  * int4 KV buffers, crates/serve/src/engine_ext.rs:92-129): per row of head_dim values,
@@ -146,7 +148,8 @@ typedef void* ema_stream_t; /* hipStream_t */
  * crates/serve/src/engine_ext.rs:266-306, and reuses them across requests).
  * FP8: k/v hold the codes (strides in elements = bytes, multiples of 16) and
  * k_exp/v_exp the block exponents, int8 [batch, n_kv_heads, capacity, head_dim / 64],
- * contiguous.
+ * contiguous. With n_rot = 64 a row is 64 code bytes (dims 0..63, block 0) followed by
+ * the 64 bf16 values of dims 64..127 (stride_pos >= 192 bytes); block 1's exponent is 0.
  * INT4: k/v hold the packed words (strides in 4-bit elements, multiples of 32, i.e. 16
  * bytes) and k_scales/k_biases/v_scales/v_biases the bf16 group parameters
  * [batch, n_kv_heads, capacity, head_dim / 64], contiguous. */
@@ -168,6 +171,7 @@ typedef struct ema_kvcache_desc {
   void* k_biases;
   void* v_scales;
   void* v_biases;
+  int32_t n_rot;        /* EMA_DTYPE_FP8_E4M3: dims at the end of each row kept as bf16 (0 or 64; else 0) */
 } ema_kvcache_desc;
 
 /* Thread-local message of the last failed call on this thread ("" if none). */
@@ -182,13 +186,17 @@ EMA_API int32_t ema_kvcache_init(ema_kvcache_desc* desc, void* k, void* v, int32
  * crates/serve/src/engine_ext.rs:273-278). Not for the hot path. */
 EMA_API int32_t ema_kvcache_alloc(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads,
                           int32_t capacity, int32_t head_dim);
-/* FP8 E4M3FN cache over caller-owned codes [batch, n_kv_heads, capacity, head_dim] (uint8)
- * and exponents [batch, n_kv_heads, capacity, head_dim / 64] (int8), all contiguous. */
+/* FP8 E4M3FN cache over caller-owned rows [batch, n_kv_heads, capacity, head_dim + n_rot]
+ * (bytes: head_dim - n_rot codes, then n_rot bf16 values) and exponents
+ * [batch, n_kv_heads, capacity, head_dim / 64] (int8), all contiguous. n_rot is the
+ * reference's Fp8Cache::new(head_dim, n_rot) argument: 0 or 64 (EMA_ERR_UNSUPPORTED
+ * otherwise). */
 EMA_API int32_t ema_kvcache_init_fp8(ema_kvcache_desc* desc, void* k, void* v, void* k_exp, void* v_exp,
-                                     int32_t batch, int32_t n_kv_heads, int32_t capacity, int32_t head_dim);
-/* Allocate a zeroed FP8 cache (codes and exponents). Not for the hot path. */
+                                     int32_t batch, int32_t n_kv_heads, int32_t capacity, int32_t head_dim,
+                                     int32_t n_rot);
+/* Allocate a zeroed FP8 cache (rows and exponents). Not for the hot path. */
 EMA_API int32_t ema_kvcache_alloc_fp8(ema_kvcache_desc* out, int32_t batch, int32_t n_kv_heads,
-                                      int32_t capacity, int32_t head_dim);
+                                      int32_t capacity, int32_t head_dim, int32_t n_rot);
 /* int4 affine cache over caller-owned words [batch, n_kv_heads, capacity, head_dim / 8]
  * (uint32) and scales/biases [batch, n_kv_heads, capacity, head_dim / 64] (bf16), all
  * contiguous: the six buffers of alloc_kv_int4 (crates/serve/src/engine_ext.rs:92-129). */

@@ -203,13 +203,14 @@ static bool same_values(const std::vector<uint16_t>& a, const std::vector<uint16
 }
 
 // Rows [r0, r0 + n) of each head of a [H, cap, D] bf16 cache replaced by their FP8 round
-// trip (exact in bf16: a 4-bit significand times a power of two).
-static void fp8_round_trip_rows(std::vector<uint16_t>& c, int H, int cap, int D, int r0, int n) {
+// trip (exact in bf16: a 4-bit significand times a power of two), the last n_rot dims of
+// each row passing through (fp8.rs:69-92).
+static void fp8_round_trip_rows(std::vector<uint16_t>& c, int H, int cap, int D, int r0, int n, int n_rot = 0) {
   std::vector<float> f((size_t)n * D);
   for (int h = 0; h < H; ++h) {
     uint16_t* rows = &c[((size_t)h * cap + r0) * D];
     ora_bf16_to_f32_array(rows, f.data(), f.size());
-    ora_fp8_round_trip(f.data(), n, D, 0);
+    ora_fp8_round_trip(f.data(), n, D, n_rot);
     for (size_t i = 0; i < f.size(); ++i) rows[i] = ora_f32_to_bf16(f[i]);
   }
 }
@@ -251,6 +252,7 @@ struct OracleLayer {
   int Hq, Hkv, D, cap;
   std::vector<uint16_t> kref, vref;
   bool fp8 = false;  // the cache keeps the FP8 round trip of each written row (fp8.rs:71-92)
+  int n_rot = 0;     // ... with this unquantised RoPE tail
   // FP8 caches: the rows the device cache holds after the call ([Hkv, off + T, D], decoded),
   // which replace the oracle's rows. The device's projected k/v differ from the oracle's
   // within the projection's bf16 tolerance, and one FP8 step is 2^5 bf16 steps, so the
@@ -278,8 +280,8 @@ struct OracleLayer {
                           vref.data(), cap) != 0)
       throw std::runtime_error("oracle overflow");
     if (fp8) {
-      fp8_round_trip_rows(kref, Hkv, cap, D, off, T);
-      fp8_round_trip_rows(vref, Hkv, cap, D, off, T);
+      fp8_round_trip_rows(kref, Hkv, cap, D, off, T, n_rot);
+      fp8_round_trip_rows(vref, Hkv, cap, D, off, T, n_rot);
       for (auto [held, c] : {std::pair{k_held, &kref}, std::pair{v_held, &vref}})
         if (held)
           for (int h = 0; h < Hkv; ++h)
@@ -549,16 +551,19 @@ static void gpu_tests() {
     EXPECT(c.len() == 0 && c.is_empty() && c.n_rot() == 0);
     EXPECT(c.memory_bytes() == (size_t)2 * Hkv * 64 * (D + D / 64));
     EXPECT(error_of([&] { c.get(ctx); }).find("empty") != std::string::npos);
+    Fp8Cache rot(Hkv, 64, D, 64);  // Fp8Cache::new(128, 64): dims 64..127 kept as bf16
+    EXPECT(rot.n_rot() == 64 && rot.memory_bytes() == (size_t)2 * Hkv * 64 * (D + 64 + D / 64));
     try {
-      Fp8Cache bad(Hkv, 64, D, 64);
+      Fp8Cache bad(Hkv, 64, D, 32);
       EXPECT(false);
     } catch (const Error& e) {
       EXPECT(e.code() == EMA_ERR_UNSUPPORTED);
     }
   });
-  run("fp8_cache_append_then_get_is_the_round_trip", [&] {
+  for (const int nr : {0, 64})
+  run(nr ? "fp8_cache_append_then_get_is_the_round_trip_rope_tail_64" : "fp8_cache_append_then_get_is_the_round_trip", [&] {
     const int cap8 = 64, T1 = 5, T2 = 3;
-    Fp8Cache c(Hkv, cap8, D);
+    Fp8Cache c(Hkv, cap8, D, nr);
     // values spread over several binades, so the block exponents differ between blocks
     auto k1 = normal((size_t)Hkv * T1 * D, 31, 0.f, 3.f), v1 = normal((size_t)Hkv * T1 * D, 32, 0.f, 0.01f);
     auto k2 = normal((size_t)Hkv * T2 * D, 33, 0.f, 200.f), v2 = normal((size_t)Hkv * T2 * D, 34);
@@ -579,22 +584,31 @@ static void gpu_tests() {
           for (int d = 0; d < D; ++d)
             e[((size_t)h * (T1 + T2) + t) * D + d] =
                 t < T1 ? a[((size_t)h * T1 + t) * D + d] : b[((size_t)h * T2 + t - T1) * D + d];
-      fp8_round_trip_rows(e, 1, Hkv * (T1 + T2), D, 0, Hkv * (T1 + T2));
+      fp8_round_trip_rows(e, 1, Hkv * (T1 + T2), D, 0, Hkv * (T1 + T2), nr);
       return e;
     };
     EXPECT(same_values(gk, expect(k1, k2)));
     EXPECT(same_values(gv, expect(v1, v2)));
-    // the stored codes and exponents are the oracle's quantisation of the same rows
-    std::vector<float> f((size_t)T1 * D);
-    std::vector<uint8_t> codes((size_t)T1 * D), got_codes((size_t)T1 * D);
-    std::vector<int8_t> exps((size_t)T1 * D / 64), got_exps(exps.size());
-    ora_bf16_to_f32_array(k1.data(), f.data(), f.size());  // head 0, rows [0, T1)
-    ora_fp8_quantize_rows(f.data(), T1, D, codes.data(), exps.data());
-    EXPECT(hipMemcpy(got_codes.data(), c.desc().k, got_codes.size(), hipMemcpyDeviceToHost) == hipSuccess);
+    // the stored codes and exponents are the oracle's quantisation of the same rows (head
+    // 0, rows [0, T1)); with the tail, a row is 64 codes then the 64 tail values as bf16
+    const int R = D + nr, nq = D - nr;  // bytes per stored row, quantised dims
+    std::vector<float> f((size_t)T1 * D), fq((size_t)T1 * nq);
+    std::vector<uint8_t> codes((size_t)T1 * nq), got_rows((size_t)T1 * R), got_codes;
+    std::vector<int8_t> exps((size_t)T1 * nq / 64), got_exps((size_t)T1 * D / 64), want_exps;
+    ora_bf16_to_f32_array(k1.data(), f.data(), f.size());
+    for (int t = 0; t < T1; ++t) std::copy_n(&f[(size_t)t * D], nq, &fq[(size_t)t * nq]);
+    ora_fp8_quantize_rows(fq.data(), T1, nq, codes.data(), exps.data());
+    EXPECT(hipMemcpy(got_rows.data(), c.desc().k, got_rows.size(), hipMemcpyDeviceToHost) == hipSuccess);
     EXPECT(hipMemcpy(got_exps.data(), c.desc().k_exp, got_exps.size(), hipMemcpyDeviceToHost) == hipSuccess);
+    for (int t = 0; t < T1; ++t) {
+      got_codes.insert(got_codes.end(), &got_rows[(size_t)t * R], &got_rows[(size_t)t * R + nq]);
+      for (int b = 0; b < D / 64; ++b) want_exps.push_back(b < nq / 64 ? exps[(size_t)t * (nq / 64) + b] : 0);
+      // the tail: the bf16 bytes of the appended values
+      EXPECT(std::memcmp(&got_rows[(size_t)t * R + nq], &k1[(size_t)t * D + nq], (size_t)nr * 2) == 0);
+    }
     for (auto* c : {&codes, &got_codes})  // -0 (0x80) and +0 (0x00) are the same value
       for (auto& b : *c) b = b == 0x80 ? 0 : b;
-    EXPECT(got_codes == codes && got_exps == exps);
+    EXPECT(got_codes == codes && got_exps == want_exps);
     std::string e = error_of([&] {
       auto big = normal((size_t)Hkv * 60 * D, 35);
       void* db = upload(big);
@@ -611,15 +625,17 @@ static void gpu_tests() {
     EXPECT(c.is_empty());
     for (void* p : {dk1, dv1, dk2, dv2}) (void)hipFree(p);
   });
-  run("gqa_attention_over_fp8_cache_matches_oracle", [&] {
-    Fp8Cache c(Hkv, cap, D);
+  for (const int nr : {0, 64})
+  run(nr ? "gqa_attention_over_fp8_cache_rope_tail_64_matches_oracle" : "gqa_attention_over_fp8_cache_matches_oracle", [&] {
+    Fp8Cache c(Hkv, cap, D, nr);
     Ctx fctx;
     fctx.workspace_bytes = gqa_workspace_bytes(cfg, hidden, 64, c);
     EXPECT(fctx.workspace_bytes > gqa_workspace_bytes(cfg, hidden, 64, cap));  // + the prefill's bf16 copy
     EXPECT(hipMalloc(&fctx.workspace, fctx.workspace_bytes) == hipSuccess &&
            hipMemset(fctx.workspace, 0, fctx.workspace_bytes) == hipSuccess);
-    OracleLayer ref(hidden, Hq, Hkv, D, cap, 6000);
+    OracleLayer ref(hidden, Hq, Hkv, D, cap, 6000 + nr);
     ref.fp8 = true;
+    ref.n_rot = nr;
     DevQW dq(ref.q), dk(ref.k), dv(ref.v), dout(ref.o);
     auto qw = normal(D, 60, 1.f, 0.02f), kw = normal(D, 61, 1.f, 0.02f);
     void *dqw = upload(qw), *dkw = upload(kw);
@@ -655,8 +671,8 @@ static void gpu_tests() {
       kh = download(kv.first.data, (size_t)Hkv * (off + t) * D);
       vh = download(kv.second.data, kh.size());
       auto k16 = rows_of(c16.desc().k, off + t), v16 = rows_of(c16.desc().v, off + t);
-      fp8_round_trip_rows(k16, 1, Hkv * (off + t), D, 0, Hkv * (off + t));
-      fp8_round_trip_rows(v16, 1, Hkv * (off + t), D, 0, Hkv * (off + t));
+      fp8_round_trip_rows(k16, 1, Hkv * (off + t), D, 0, Hkv * (off + t), nr);
+      fp8_round_trip_rows(v16, 1, Hkv * (off + t), D, 0, Hkv * (off + t), nr);
       EXPECT(same_values(kh, k16) && same_values(vh, v16));
       auto want = ref.run(x, t, off, 0, qw.data(), kw.data());
       expect_close_out(got, want, window ? "fp8 window step (whole cache)"
@@ -672,8 +688,9 @@ static void gpu_tests() {
     (void)hipFree(dkw);
     (void)hipFree(fctx.workspace);
   });
-  run("qkv_attention_over_fp8_cache_matches_oracle", [&] {
-    Fp8Cache c(Hkv, 128, D);
+  for (const int nr : {0, 64})
+  run(nr ? "qkv_attention_over_fp8_cache_rope_tail_64_matches_oracle" : "qkv_attention_over_fp8_cache_matches_oracle", [&] {
+    Fp8Cache c(Hkv, 128, D, nr);
     Ctx fctx;
     fctx.workspace_bytes = qkv_attention_workspace_bytes(cfg, 64, c);
     EXPECT(hipMalloc(&fctx.workspace, fctx.workspace_bytes) == hipSuccess &&
@@ -690,8 +707,8 @@ static void gpu_tests() {
       int32_t o32 = off, len = off + t;
       EXPECT(ora_pre_attention(qkv.data(), nullptr, nullptr, 1e-6f, 1e6f, &o32, 1, t, Hq, Hkv, D, ORA_FLAG_NO_NORM,
                                q.data(), kref.data(), vref.data(), 128) == 0);
-      fp8_round_trip_rows(kref, Hkv, 128, D, off, t);
-      fp8_round_trip_rows(vref, Hkv, 128, D, off, t);
+      fp8_round_trip_rows(kref, Hkv, 128, D, off, t, nr);
+      fp8_round_trip_rows(vref, Hkv, 128, D, off, t, nr);
       ora_sdpa(q.data(), kref.data(), vref.data(), &len, nullptr, 1, Hq, Hkv, t, D, 128, scale, t > 1 ? 1 : 0, 0,
                ref.data());
       expect_close(download(out.data, ref.size()), ref, t > 1 ? "fp8 prefill" : "fp8 decode");

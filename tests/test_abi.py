@@ -220,23 +220,23 @@ def test_errors_are_thread_local(ema):
 def test_fp8_descriptor_and_memory_bytes(ema):
     L = ema.lib()
     d = ema.KvCacheDesc()
-    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128)
+    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128, 0)
     assert rc == ema.EMA_OK
     assert d.dtype == ema.EMA_DTYPE_FP8_E4M3 and (d.stride_pos, d.stride_head) == (128, 64 * 128)
     n = ctypes.c_uint64()
     assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
     assert n.value == 2 * 2 * 8 * 64 * (128 + 2)  # codes + one exponent byte per 64 values
     # exponents are required; head_dim 128 only
-    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, None, 0x40000, 2, 8, 64, 128)
+    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, None, 0x40000, 2, 8, 64, 128, 0)
     assert rc == ema.EMA_ERR_INVALID_ARG and "exponent" in ema.last_error()
-    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 64)
+    rc = L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 64, 0)
     assert rc == ema.EMA_ERR_UNSUPPORTED
 
 
 def test_fp8_prefill_is_unsupported(ema):
     L = ema.lib()
     d = ema.KvCacheDesc()
-    assert L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128) == 0
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128, 0) == 0
     g = 0x40000
     rc = L.ema_prefill_attention(None, g, ctypes.byref(d), g, 8, 16, 0.088, 1, g)
     assert rc == ema.EMA_ERR_UNSUPPORTED and "fp8" in ema.last_error()
@@ -255,7 +255,7 @@ def test_prefill_workspace_size_and_errors(ema):
     _, d16 = _desc(ema)
     assert L.ema_prefill_workspace_size(ctypes.byref(d16), 64, ctypes.byref(n)) == 0 and n.value == 0
     d8 = ema.KvCacheDesc()
-    assert L.ema_kvcache_init_fp8(ctypes.byref(d8), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128) == 0
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d8), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128, 0) == 0
     assert L.ema_prefill_workspace_size(ctypes.byref(d8), 48, ctypes.byref(n)) == 0
     assert n.value == 2 * 2 * 8 * 48 * 128 * 2  # bf16 K and V copies of 48 rows
     assert L.ema_prefill_workspace_size(ctypes.byref(d8), 65, ctypes.byref(n)) == ema.EMA_ERR_CAPACITY
@@ -323,7 +323,7 @@ def test_rotating_flag_is_validated(ema):
     d.flags = ema.EMA_KV_ROTATING
     assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
     d8 = ema.KvCacheDesc()
-    assert L.ema_kvcache_init_fp8(ctypes.byref(d8), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128) == 0
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d8), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128, 0) == 0
     d8.flags = ema.EMA_KV_ROTATING
     g = 0x40000
     # a rotating fp8 cache is accepted by the prefill (stopped here by the too-small
@@ -408,7 +408,7 @@ def test_kvcache_convert_argument_errors(ema):
     bf = ema.KvCacheDesc()
     assert L.ema_kvcache_init(ctypes.byref(bf), a, a, 2, 8, 40, 128) == 0
     f8 = ema.KvCacheDesc()
-    assert L.ema_kvcache_init_fp8(ctypes.byref(f8), a, a, a, a, 2, 8, 64, 128) == 0
+    assert L.ema_kvcache_init_fp8(ctypes.byref(f8), a, a, a, a, 2, 8, 64, 128, 0) == 0
     i4 = ema.KvCacheDesc()
     assert L.ema_kvcache_init_int4(ctypes.byref(i4), a, a, a, a, a, a, 2, 8, 64, 128) == 0
     # zero rows of every supported pair is a no-op
@@ -440,3 +440,29 @@ def test_position_write_argument_errors(ema):
     assert "null" in ema.last_error()
     assert L.ema_position_write(None, 0x40002, 5) == ema.EMA_ERR_INVALID_ARG
     assert "aligned" in ema.last_error()
+
+
+def test_fp8_rope_tail_descriptor(ema):
+    """n_rot = 64 (the reference's Fp8Cache::new(128, 64)): rows of 64 codes + 64 bf16."""
+    L = ema.lib()
+    a = 0x40000
+    d = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d), a, a, a, a, 2, 8, 64, 128, 64) == 0
+    assert d.n_rot == 64 and d.stride_pos == 192 and d.stride_head == 64 * 192 and d.stride_batch == 8 * 64 * 192
+    n = ctypes.c_uint64()
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 8 * 64 * (192 + 2)
+    for bad in (32, 96, 128, -64):
+        assert L.ema_kvcache_init_fp8(ctypes.byref(d), a, a, a, a, 2, 8, 64, 128, bad) == ema.EMA_ERR_UNSUPPORTED
+        assert "n_rot" in ema.last_error()
+        assert L.ema_kvcache_alloc_fp8(ctypes.byref(d), 2, 8, 64, 128, bad) == ema.EMA_ERR_UNSUPPORTED
+    # rows too short for the tail; the field on another dtype
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d), a, a, a, a, 2, 8, 64, 128, 64) == 0
+    d.stride_pos = 128
+    n2 = ctypes.c_uint64()
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(d), ctypes.byref(n2)) == ema.EMA_ERR_SHAPE
+    assert "stride_pos" in ema.last_error()
+    b = ema.KvCacheDesc()
+    assert L.ema_kvcache_init(ctypes.byref(b), a, a, 2, 8, 64, 128) == 0
+    b.n_rot = 64
+    assert L.ema_kvcache_memory_bytes(ctypes.byref(b), ctypes.byref(n2)) == ema.EMA_ERR_INVALID_ARG
