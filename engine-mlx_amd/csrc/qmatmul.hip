@@ -1026,6 +1026,9 @@ int32_t launch_dq(hipStream_t st, const QmmArgs& a, const DqPlan& p) {
 // a_1 = sum of the group's x. The row sums are reduced across the slot's lanes with xor
 // shuffles. R is chosen so the grid is about one workgroup of eight waves per CU.
 constexpr int kGemvRows = 4;  // most rows per lane
+// rows per lane for one format: two where a group of one row holds 32 dwords (8 bits,
+// group 128), whose four rows would not fit the register file beside x
+constexpr int gemv_rows(int bits, int gs) { return bits * gs / 32 >= 32 ? 2 : kGemvRows; }
 
 template <bool F16>
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -1040,6 +1043,7 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 template <int BITS, int GS, bool F16>
 __global__ __launch_bounds__(512) void qgemv1_kernel(QmmArgs a, int np, int L, int gpl) {
   using F = Fields<BITS, F16>;
+  constexpr int kRows = gemv_rows(BITS, GS);
   constexpr int kWDw = GS * BITS / 32;  // dwords of one group of one weight row
   constexpr int kXDw = GS / 2;          // dwords of one group of x
   constexpr int kBlk = GS / 8;          // blocks of 8 weights per group
@@ -1071,15 +1075,15 @@ __global__ __launch_bounds__(512) void qgemv1_kernel(QmmArgs a, int np, int L, i
       dma16(X, 1024 * i + 16 * lane, __builtin_amdgcn_readfirstlane(lds0 + 1024 * i));
   }
 
-  float y[kGemvRows];
+  float y[kRows];
 #pragma unroll
-  for (int p = 0; p < kGemvRows; ++p) y[p] = 0.0f;
+  for (int p = 0; p < kRows; ++p) y[p] = 0.0f;
   for (int i = 0; i < gpl; ++i) {
     const uint32_t g = gl + L * i;
     // weights, scale and bias of every row, in the order they are used
-    uint32_t wd[kGemvRows][kWDw], sb[kGemvRows], bb[kGemvRows];
+    uint32_t wd[kRows][kWDw], sb[kRows], bb[kRows];
 #pragma unroll
-    for (int p = 0; p < kGemvRows; ++p) {
+    for (int p = 0; p < kRows; ++p) {
       const int r = slot + slots * p;  // row within the wave's rows
       const bool ok = p < np && r < rows;
       load_dw<kWDw>(W, ok ? r * wrow + g * kWBytes : kOffRow, wd[p]);
@@ -1089,7 +1093,7 @@ __global__ __launch_bounds__(512) void qgemv1_kernel(QmmArgs a, int np, int L, i
     if (i == 0) {
       // the x DMA came before these loads: wait for it alone, then publish it
       constexpr uint32_t kPerRow = (kWDw <= 2 ? 1 : kWDw / 4) + 2;
-      wait_vmcnt(kGemvRows * kPerRow);
+      wait_vmcnt(kRows * kPerRow);
       __syncthreads();
     }
     uint32_t xd[kXDw];
@@ -1111,7 +1115,7 @@ __global__ __launch_bounds__(512) void qgemv1_kernel(QmmArgs a, int np, int L, i
       for (int e = 0; e < 4; ++e) a1 = dot2<F16>(xa[blk][e], ones[e], a1);
     }
 #pragma unroll
-    for (int p = 0; p < kGemvRows; ++p) {
+    for (int p = 0; p < kRows; ++p) {
       if (p >= np) break;
       float aq = 0.0f;
 #pragma unroll
@@ -1127,7 +1131,7 @@ __global__ __launch_bounds__(512) void qgemv1_kernel(QmmArgs a, int np, int L, i
   }
   // sum over the slot's L lanes (xor partners stay inside the slot)
 #pragma unroll
-  for (int p = 0; p < kGemvRows; ++p) {
+  for (int p = 0; p < kRows; ++p) {
     if (p >= np) break;
     float v = y[p];
     for (int m = 1; m < L; m <<= 1) v += __shfl_xor(v, m, 64);
@@ -1144,9 +1148,10 @@ bool gemv1_fits(int G, int K) { return (G % 64 == 0 || (G <= 64 && (G & (G - 1))
 template <int BITS, int GS, bool F16>
 int32_t launch_gemv1(hipStream_t st, const QmmArgs& a, int cus) {
   const int L = a.G < 64 ? a.G : 64, slots = 64 / L, gpl = a.G / L;
-  // rows per lane: about one workgroup of eight waves per CU, at most kGemvRows
+  // rows per lane: about one workgroup of eight waves per CU, at most the format's limit
   const int64_t want = ((int64_t)a.N + 8LL * cus * slots - 1) / (8LL * cus * slots);
-  const int np = (int)(want < 1 ? 1 : want > kGemvRows ? kGemvRows : want);
+  constexpr int kRows = gemv_rows(BITS, GS);
+  const int np = (int)(want < 1 ? 1 : want > kRows ? kRows : want);
   const int64_t waves = ((int64_t)a.N + slots * np - 1) / (slots * np);
   const uint32_t lds = ((uint32_t)a.K * 2 + 1023) & ~1023u;  // x, in whole DMA blocks
   hipLaunchKernelGGL((qgemv1_kernel<BITS, GS, F16>), dim3((unsigned)((waves + 7) / 8)), dim3(512), lds, st, a, np,

@@ -106,6 +106,18 @@ def test_qmatmul_qwen3_8b_qkv_decode_shape(ema, ora, M, N, bits):
     check(ora, y, h, gs, bits, "8B qkv", bar=True)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_qmatmul_one_row_8bit_group_128_many_rows(ema, ora, dtype):
+    # one row of x over 6144 weight rows at 8 bits, group 128: enough rows that the one-row
+    # kernel gives each lane its most rows (two for this format, whose 32-dword groups
+    # would not fit four to a lane)
+    M, N, K, gs, bits = 1, 6144, 2048, 128, 8
+    say(f"qmatmul one-row {dtype} bits={bits} gs={gs} N={N} K={K}")
+    d, h = make(ora, 11, M, N, K, gs, bits, dtype)
+    y = ema.quantized_matmul(*d, group_size=gs, bits=bits)
+    check(ora, y, h, gs, bits, "one row, 8-bit group 128", dtype)
+
+
 @pytest.mark.parametrize("M,gs,dtype", [(20, 128, "bf16"), (12, 64, "f16")])
 def test_qmatmul_8bit_wide_rows_x_in_registers(ema, ora, M, gs, dtype):
     # 8-bit weights of two 16-row column tiles fill most of the LDS, so x streams through
