@@ -80,6 +80,7 @@ struct DecodeArgs {
   int fused;
   int rot;  // rotating cache: the fused step's new row is row off % cap
   int inline_merge;  // merge split segments in this kernel (else decode_merge_kernel does)
+  int narrow;        // the split's products w * total stay below 2^31: 32-bit arithmetic
   // fp8 cache: block exponents [B, Hkv, cap, 2] (k, v then hold E4M3FN codes)
   const int8_t* kexp;
   const int8_t* vexp;
@@ -91,11 +92,15 @@ struct DecodeArgs {
   uint32_t* vb;
 };
 
-__device__ __forceinline__ int64_t worker_of(int64_t t, int64_t total, int W) {
-  return split_worker_of(t, total, W);
+// The split's slice bounds, in 32-bit arithmetic when the host has bounded every product
+// w * total below 2^31 (a.narrow)
+__device__ __forceinline__ int64_t worker_of(const DecodeArgs& a, int64_t t, int64_t total, int W) {
+  return a.narrow ? split_worker_of32(t, total, W) : split_worker_of(t, total, W);
 }
 __device__ __forceinline__ int active_workers(int64_t total, int W) { return split_active_workers(total, W, kWaves); }
-__device__ __forceinline__ int64_t worker_begin(int64_t w, int64_t total, int W) { return split_begin(w, total, W); }
+__device__ __forceinline__ int64_t worker_begin(const DecodeArgs& a, int64_t w, int64_t total, int W) {
+  return a.narrow ? split_begin32(w, total, W) : split_begin(w, total, W);
+}
 
 __device__ __forceinline__ int clamp_len(int L, int cap) { return L < 0 ? 0 : (L > cap ? cap : L); }
 
@@ -280,8 +285,17 @@ constexpr int kI4Slots = 3;  // the tile in use and two in flight
 constexpr int kI4SlotK = 0, kI4SlotV = kTile * 64, kI4SlotKs = 2 * kTile * 64, kI4SlotKb = kI4SlotKs + 4 * kTile,
               kI4SlotVs = kI4SlotKb + 4 * kTile, kI4SlotVb = kI4SlotVs + 4 * kTile;
 constexpr int kStateLds = 16 * kD * 4;
-template <bool kI4>
-constexpr int wave_lds_bytes() { return kI4 && kI4Slots * kI4Slot > kStateLds ? kI4Slots * kI4Slot : kStateLds; }
+// bf16 slot: the tile's K rows (32 x 256 B) and V rows (32 x 256 B)
+constexpr int kBfSlot = 2 * kTile * kD * 2;
+template <bool kI4, bool kBfDma>
+constexpr int wave_lds_bytes() {
+  return kI4 ? (kI4Slots * kI4Slot > kStateLds ? kI4Slots * kI4Slot : kStateLds) : kBfDma ? kBfSlot : kStateLds;
+}
+// bf16 K rows in the slot: row R of the tile (rows 4i .. 4i + 3 in 1 KB block i) keeps its
+// 16-byte chunk ch at unit ch ^ bf_swz(R) of the row, so that the 16 rows of one QK
+// operand read (lanes m, rows 8(m/4) + m%4 + 4r, where bf_swz(R) = m) fall on 16 distinct
+// bank groups for every chunk.
+__device__ __forceinline__ int bf_swz(int R) { return (R & 3) + 4 * ((R >> 3) & 3); }
 
 // Partial states cross XCDs, each with its own L2, without cache maintenance: they are
 // written and read with device-coherent (agent-scope) stores and loads, which go past the
@@ -411,39 +425,70 @@ __device__ void merge_segment(const DecodeArgs& a, int b, int kh, int64_t s, int
   for (int e = threadIdx.x; e < a.G * kD; e += blockDim.x) merge_element<true>(a, b, kh, s, w0, w1, e / kD, e % kD);
 }
 
-template <bool kFused, bool kFp8, bool kI4 = false, bool kRot = false>
+template <bool kFused, bool kFp8, bool kI4 = false, bool kRot = false, bool kDma = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(DecodeArgs a) {
   // kRot: FP8 rows with the RoPE tail, read only (the fused step over them is the
   // pre-attention kernel followed by this kernel, see launch_decode)
   static_assert(!kRot || (kFp8 && !kFused), "the RoPE-tail reader is the unfused FP8 decode");
+  // kDma: bf16 tiles through the wave's LDS slot by LDS-DMA (small grids, see launch_decode)
+  static_assert(!kDma || (!kFp8 && !kI4), "the LDS-DMA tiles are the bf16 cache's");
   constexpr bool kNarrow = kFp8 || kI4;  // the fp8 head-dim order (kdim)
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
-  __shared__ __attribute__((aligned(16))) uint8_t wave_lds[kWaves][wave_lds_bytes<kI4>()];
+  __shared__ __attribute__((aligned(16))) uint8_t wave_lds[kWaves][wave_lds_bytes<kI4, kDma>()];
   __shared__ float2 rope_cs[kWaves][kD / 2];  // fused: each wave's RoPE (cos, sin) table at the offset
   __shared__ __attribute__((aligned(16))) uint16_t new_kv[2][kD];  // fused: the new row, for its owner wave
-  build_prefix(a, pre);
-  if (!a.inline_merge && blockIdx.x == 0)
-    for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.hdr[i] = pre[i];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+
+  // Lengths and tile prefix. Up to 64 sequences, each wave forms them in its lanes (lane
+  // b: sequence b, scanned across lanes) into its own slice of the LDS table (lengths at
+  // 128 wave, prefix at 128 wave + 64), so no workgroup barrier stands before the first
+  // loads; larger batches scan into the workgroup's table (pre[0..B]).
+  const bool wtab = a.B <= 64;
+  int32_t* const tl = pre + 128 * wave;
+  int64_t total;
+  if (wtab) {
+    const int len_l = lane < a.B ? seq_len(a, lane) : 0;
+    const int tb = ((len_l + kTile - 1) / kTile) * a.Hkv;
+    int incl = tb;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    total = __builtin_amdgcn_readlane(incl, 63);
+    tl[lane] = len_l;
+    tl[64 + lane] = incl - tb;
+    if (!a.inline_merge && blockIdx.x == 0 && wave == 0) {
+      if (lane < a.B) a.hdr[lane] = incl - tb;
+      if (lane == 0) a.hdr[a.B] = (int32_t)total;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    build_prefix(a, pre);
+    total = pre[a.B];
+    if (!a.inline_merge && blockIdx.x == 0)
+      for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.hdr[i] = pre[i];
+  }
+  auto len_of = [&](int b) __attribute__((always_inline)) { return wtab ? tl[b] : seq_len(a, b); };
 
   // sequences with no valid position produce zeros (nothing else visits them)
   if (blockIdx.x == 0) {
     const int row_words = a.Hq * kD / 2;
     for (int b = 0; b < a.B; ++b)
-      if (seq_len(a, b) == 0)
+      if (len_of(b) == 0)
         for (int i = threadIdx.x; i < row_words; i += blockDim.x) ((uint32_t*)(a.out + (int64_t)b * a.Hq * kD))[i] = 0u;
   }
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int w = blockIdx.x;
-  const int64_t total = pre[a.B];
   const int W = active_workers(total, a.W);
   // workgroups past the active workers have no tiles (they still arrive at the grid's
   // counter below when the offsets advance)
-  int64_t t = w < W ? worker_begin(w, total, W) : 0;
-  const int64_t t_end = w < W ? worker_begin(w + 1, total, W) : 0;
+  int64_t t = w < W ? worker_begin(a, w, total, W) : 0;
+  const int64_t t_end = w < W ? worker_begin(a, w + 1, total, W) : 0;
 
   const int g = lane & 15;  // query head inside the kv group (B-operand column)
   const int c = lane >> 4;  // 16-lane group
@@ -453,19 +498,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int krow0 = 8 * (m >> 2) + (m & 3);
 
   while (t < t_end) {
-    // locate the segment containing tile t (uniform across the workgroup)
-    int lo = 0, hi = a.B;  // largest b with pre[b] <= t
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (pre[mid] <= t) lo = mid; else hi = mid;
+    // locate the segment containing tile t (uniform across the workgroup): the largest b
+    // with pre[b] <= t
+    int b;
+    int64_t pre_b;
+    if (wtab) {
+      const uint64_t le = __ballot(lane < a.B && tl[64 + lane] <= t);  // lane 0 always (pre 0)
+      b = 63 - __builtin_clzll(le);
+      pre_b = tl[64 + b];
+    } else {
+      int lo = 0, hi = a.B;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pre[mid] <= t) lo = mid; else hi = mid;
+      }
+      b = lo;
+      pre_b = pre[b];
     }
-    const int b = lo;
-    const int L = seq_len(a, b);
+    const int L = len_of(b);
     const int nb = (L + kTile - 1) / kTile;
-    const int64_t rel = t - pre[b];
-    const int kh = (int)(rel / nb);
-    const int tile0 = (int)(rel % nb);
-    const int64_t seg_first = pre[b] + (int64_t)kh * nb;
+    const uint32_t rel = (uint32_t)(t - pre_b);  // the prefix is 32-bit
+    const int kh = (int)(rel / (uint32_t)nb);
+    const int tile0 = (int)(rel % (uint32_t)nb);
+    const int64_t seg_first = pre_b + (int64_t)kh * nb;
     const int64_t seg_end = seg_first + nb;
     const int64_t piece_end = t_end < seg_end ? t_end : seg_end;
     const int tile1 = tile0 + (int)(piece_end - t);
@@ -540,6 +595,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     };
+    // bf16 tiles, two ways (positions past L clamped to row L - 1 in both, so every row read
+    // is a valid one):
+    // - straight into registers in the operands' layout, the next tile's loads in flight
+    //   during this one's work (full grids: the loads of many workgroups cover each other);
+    // - kDma (small grids): by LDS-DMA of whole rows into the wave's slot, 1 KB (four rows)
+    //   per instruction, then read out in the operands' layout. The operand layout takes 64
+    //   bytes of each of 16 K rows per load, and a CU issues those loads about 2.5 times
+    //   slower than whole rows, which a latency-bound grid pays in full (one tile's loads
+    //   per wave: 1.27 against 0.51 us in isolation). Its next tile's DMA can only refill
+    //   the slot after this one is read out, which costs full grids their overlap.
     auto load_tile = [&](int tile, u32x4 (&kr)[2][4], u32x4 (&vr)[8]) {
       const int p0 = tile * kTile;
       for (int r = 0; r < 2; ++r) {
@@ -552,6 +617,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         int p = p0 + 8 * c + kk;
         p = p < L ? p : L - 1;
         vr[kk] = ld16_stream(Vb + (int64_t)p * a.sp + 8 * m);
+      }
+    };
+    uint8_t* const bslot = &wave_lds[wave][0];
+    const uint32_t bslot_lds = (uint32_t)(uintptr_t)(lds_void*)bslot;
+    const uint32_t plane_bytes = (uint32_t)a.cap * (uint32_t)a.sp * 2u;  // bounded by the host
+    const u32x4 kbf_rs = rsrc_words(Kb, plane_bytes), vbf_rs = rsrc_words(Vb, plane_bytes);
+    auto bf_dma = [&](int tile) __attribute__((always_inline)) {
+      const int p0 = tile * kTile;
+      for (int i = 0; i < 8; ++i) {
+        const int R = 4 * i + (lane >> 4);
+        const int p = p0 + R < L ? p0 + R : L - 1;
+        const uint32_t roff = (uint32_t)p * (uint32_t)a.sp * 2u;
+        dma16(kbf_rs, roff + 16u * (uint32_t)((lane & 15) ^ bf_swz(R)), 0u, bslot_lds + 1024u * i);
+        dma16(vbf_rs, roff + 16u * (uint32_t)(lane & 15), 0u, bslot_lds + 8192u + 1024u * i);
+      }
+    };
+    auto bf_read = [&]() __attribute__((always_inline)) {
+      for (int r = 0; r < 2; ++r) {
+        const int R = krow0 + 4 * r;
+        for (int s = 0; s < 4; ++s)
+          kc[r][s] = *(const u32x4*)(bslot + 1024 * (R >> 2) + 256 * (R & 3) + 16 * ((4 * s + c) ^ bf_swz(R)));
+      }
+      for (int kk = 0; kk < 8; ++kk) {
+        const int R = 8 * c + kk;
+        vc[kk] = *(const u32x4*)(bslot + 8192 + 1024 * (R >> 2) + 256 * (R & 3) + 16 * m);
       }
     };
     // int4: the wave streams its tiles into a ring of kI4Slots LDS slots, two tiles ahead
@@ -650,7 +740,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       } else if (kFp8) {
         load_tile8(first, k8, v8, ke, ve, kt, vw);
       } else {
-        load_tile(first, kc, vc);
+        if (kDma) bf_dma(first);
+        else load_tile(first, kc, vc);
       }
     }
     bf16x8 qop[4];
@@ -962,6 +1053,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       } else if (kFp8) {
         if (more) load_tile8(tile + kWaves, k8n, v8n, ken, ven, ktn, vwn);
         decode_tile8();
+      } else if (kDma) {
+        wait_vm<0>();  // this tile's DMA has landed (and every load before it)
+        bf_read();
+        if (more) {
+          // the slot's reads are done before the next tile's DMA refills it
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          bf_dma(tile + kWaves);
+        }
       } else if (more) {
         load_tile(tile + kWaves, kn, vn);
       }
@@ -1025,22 +1124,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         o[j] = mfma16(as_bf16x8(av), pop, o[j]);
       }
-      if (more) {
-        if (kFp8) {
-          for (int r = 0; r < 2; ++r) {
-            for (int s = 0; s < 4; ++s) k8[r][s] = k8n[r][s];
-            if (kRot) kt[r][0] = ktn[r][0], kt[r][1] = ktn[r][1];
-            ke[r] = ken[r];
-          }
-          for (int kk = 0; kk < 8; ++kk) {
-            v8[kk] = v8n[kk];
-            if (kRot) vw[kk] = vwn[kk];
-            ve[kk] = ven[kk];
-          }
-        } else {
-          for (int r = 0; r < 2; ++r)
-            for (int s = 0; s < 4; ++s) kc[r][s] = kn[r][s];
-          for (int kk = 0; kk < 8; ++kk) vc[kk] = vn[kk];
+      if (!kFp8 && !kDma && more) {
+        for (int r = 0; r < 2; ++r)
+          for (int s = 0; s < 4; ++s) kc[r][s] = kn[r][s];
+        for (int kk = 0; kk < 8; ++kk) vc[kk] = vn[kk];
+      }
+      if (kFp8 && more) {
+        for (int r = 0; r < 2; ++r) {
+          for (int s = 0; s < 4; ++s) k8[r][s] = k8n[r][s];
+          if (kRot) kt[r][0] = ktn[r][0], kt[r][1] = ktn[r][1];
+          ke[r] = ken[r];
+        }
+        for (int kk = 0; kk < 8; ++kk) {
+          v8[kk] = v8n[kk];
+          if (kRot) vw[kk] = vwn[kk];
+          ve[kk] = ven[kk];
         }
       }
     }
@@ -1072,7 +1170,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
 
     // combine the four waves; thread e covers (head e / 128, dim e % 128)
-    const int64_t w0 = worker_of(seg_first, total, W), w1 = worker_of(seg_end - 1, total, W);
+    const int64_t w0 = worker_of(a, seg_first, total, W), w1 = worker_of(a, seg_end - 1, total, W);
     const bool single = w0 == w1;
     const int64_t s = (int64_t)b * a.Hkv + kh;
     for (int e = tid; e < a.G * kD; e += blockDim.x) {
@@ -1142,8 +1240,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   if (nb == 0 || total == 0) return;
   const int W = active_workers(total, a.W);
   const int64_t seg_first = a.hdr[b] + (int64_t)kh * nb;
-  const int64_t w0 = worker_of(seg_first, total, W);
-  const int64_t w1 = worker_of(seg_first + nb - 1, total, W);
+  const int64_t w0 = worker_of(a, seg_first, total, W);
+  const int64_t w1 = worker_of(a, seg_first + nb - 1, total, W);
   if (w0 == w1) return;  // written directly by decode_kernel
   merge_element<false>(a, b, kh, s, w0, w1, gg, d);
 }
@@ -1164,9 +1262,10 @@ constexpr uint64_t kHeaderBytes = ((kMaxB + 1) * sizeof(int32_t) + 255) & ~(uint
 uint64_t decode_workspace_bytes(const DecodePlan& p) { return kDecodeCounterBytes + kHeaderBytes + p.part_bytes; }
 
 // Grids of at most one workgroup per CU are latency-bound: the merge of their split
-// segments runs inside the kernel (one launch per call). Fuller grids merge in
-// decode_merge_kernel, whose launch is small beside theirs and which keeps the arrival
-// round trips out of their workgroups' slices.
+// segments runs inside the kernel (one launch per call), and a bf16 cache's tiles come by
+// LDS-DMA of whole rows (kDma). Fuller grids merge in decode_merge_kernel, whose launch is
+// small beside theirs and which keeps the arrival round trips out of their workgroups'
+// slices, and load their tiles straight into registers.
 constexpr int kInlineMergeMaxWorkers = 256;
 
 int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, const int32_t* len,
@@ -1201,6 +1300,14 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   a.G = G;
   a.cap = c.capacity;
   a.W = plan.workers;
+  // lengths are clamped to the capacity, so the tile count is at most max_tiles: the
+  // kernels keep their tile prefix in 32 bits, and the split's products w * total too when
+  // they fit
+  const int64_t max_tiles = (int64_t)c.batch * c.n_kv_heads * ((c.capacity + kTile - 1) / kTile);
+  if (max_tiles >= INT32_MAX)
+    return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: %lld tiles of %d positions exceed 2^31 - 1",
+                     (long long)max_tiles, kTile);
+  a.narrow = split_narrow(max_tiles, plan.workers);
   a.fused = fused != nullptr;
   a.rot = (c.flags & EMA_KV_ROTATING) != 0;
   a.qkv = fused ? (const uint16_t*)fused->qkv : nullptr;
@@ -1221,6 +1328,12 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   const bool fp8 = c.dtype == EMA_DTYPE_FP8_E4M3;
   const bool i4 = c.dtype == EMA_DTYPE_INT4_AFFINE;
   const bool tail = fp8 && c.n_rot != 0;
+  // the bf16 and int4 kernels address a (sequence, kv head) plane of the cache through a
+  // 32-bit buffer range
+  const int64_t plane = i4 ? (int64_t)c.capacity * (c.stride_pos / 2) : fp8 ? 0 : (int64_t)c.capacity * c.stride_pos * 2;
+  if (plane > (int64_t)UINT32_MAX)
+    return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: %lld bytes per (sequence, kv head) exceed 2^32",
+                     (long long)plane);
   const dim3 grid(plan.workers), block(kWaves * 64);
   if (a.fused && tail) {
     // The fused step over FP8 rows with a RoPE tail runs as two kernels: the fused kernel
@@ -1240,9 +1353,11 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   } else if (a.fused && i4) hipLaunchKernelGGL((decode_kernel<true, false, true>), grid, block, 0, s, a);
   else if (i4) hipLaunchKernelGGL((decode_kernel<false, false, true>), grid, block, 0, s, a);
   else if (a.fused && fp8) hipLaunchKernelGGL((decode_kernel<true, true>), grid, block, 0, s, a);
+  else if (a.fused && a.inline_merge) hipLaunchKernelGGL((decode_kernel<true, false, false, false, true>), grid, block, 0, s, a);
   else if (a.fused) hipLaunchKernelGGL((decode_kernel<true, false>), grid, block, 0, s, a);
   else if (tail) hipLaunchKernelGGL((decode_kernel<false, true, false, true>), grid, block, 0, s, a);
   else if (fp8) hipLaunchKernelGGL((decode_kernel<false, true>), grid, block, 0, s, a);
+  else if (a.inline_merge) hipLaunchKernelGGL((decode_kernel<false, false, false, false, true>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((decode_kernel<false, false>), grid, block, 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");
   if (rc || a.inline_merge || (plan.workers == 1 && !a.adv)) return rc;

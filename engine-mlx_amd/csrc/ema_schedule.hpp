@@ -117,4 +117,16 @@ EMA_HD int64_t split_begin(int64_t w, int64_t total, int W) { return w * total /
 // Slice holding tile t (the inverse of split_begin).
 EMA_HD int64_t split_worker_of(int64_t t, int64_t total, int W) { return ((t + 1) * (int64_t)W - 1) / total; }
 
+// The same two functions in 32-bit arithmetic, equal to them whenever every product
+// w * total (w <= W) stays below 2^31, which split_narrow checks for the largest tile count
+// the lengths allow. The decode kernels take these on the latency path of small grids,
+// where a 64-bit division is a long scalar emulation.
+EMA_HD bool split_narrow(int64_t max_total, int W) { return max_total * W < ((int64_t)1 << 31); }
+EMA_HD int64_t split_begin32(int64_t w, int64_t total, int W) {
+  return (int64_t)((uint32_t)w * (uint32_t)total / (uint32_t)W);
+}
+EMA_HD int64_t split_worker_of32(int64_t t, int64_t total, int W) {
+  return (int64_t)((((uint32_t)t + 1u) * (uint32_t)W - 1u) / (uint32_t)total);
+}
+
 }  // namespace ema

@@ -8,7 +8,9 @@
 //  - decode split: the worker slices tile [0, total) exactly once, split_worker_of
 //    inverts split_begin, the merge's slot range [w0, w1] of every segment is exactly the
 //    set of slices that intersect it, and the partial-state slots (w + segment) of split
-//    segments are distinct and inside the workspace the plan sizes.
+//    segments are distinct and inside the workspace the plan sizes; the 32-bit forms of
+//    split_begin / split_worker_of equal the 64-bit ones wherever split_narrow holds, up
+//    to its edge.
 // Built with g++ (no HIP), also under -fsanitize=address,undefined. Prints one line per
 // group of checks and exits non-zero on the first failure.
 #include <cstdio>
@@ -98,6 +100,13 @@ static void decode_case(const std::vector<int>& nb, int plan_workers, int waves)
       CHECK(split_worker_of(t, total, W) == w, "worker_of(%lld) = %lld, not %d", (long long)t,
             (long long)split_worker_of(t, total, W), w);
   }
+  // the 32-bit forms agree wherever the kernels take them
+  if (split_narrow(total, plan_workers)) {
+    for (int w = 0; w <= W; ++w)
+      CHECK(split_begin32(w, total, W) == split_begin(w, total, W), "begin32(%d) of %lld", w, (long long)total);
+    for (int64_t t = 0; t < total; ++t)
+      CHECK(split_worker_of32(t, total, W) == split_worker_of(t, total, W), "worker_of32(%lld)", (long long)t);
+  }
   // merge ranges and partial slots
   std::set<int64_t> slots;
   for (size_t s = 0; s < nb.size(); ++s) {
@@ -149,7 +158,18 @@ static void test_decode() {
   decode_case({256}, 64, kSplitWaves);
   decode_case(std::vector<int>(32 * 8, 256), split_plan_workers(32, 8, 8192), kSplitWaves);
   decode_case({0, 0, 5, 0, 7}, 2, kSplitWaves);
-  std::printf("decode split: %d random batches + 5 edge cases: tiles covered once, merge ranges and slots exact\n",
+  // the 32-bit forms at the edge of split_narrow: total * W just below 2^31, and just above
+  for (const int W : {1, 7, 64, 511, kSplitMaxWorkers}) {
+    const int64_t edge = (((int64_t)1 << 31) - 1) / W;
+    CHECK(split_narrow(edge, W) && !split_narrow(edge + 1, W), "split_narrow edge at W = %d", W);
+    for (int64_t w = 0; w <= W; ++w)
+      CHECK(split_begin32(w, edge, W) == split_begin(w, edge, W), "begin32 at the edge, W = %d", W);
+    for (int64_t t = 0; t < edge; t += 1 + edge / 200003)
+      CHECK(split_worker_of32(t, edge, W) == split_worker_of(t, edge, W), "worker_of32 at the edge");
+    CHECK(split_worker_of32(edge - 1, edge, W) == split_worker_of(edge - 1, edge, W), "worker_of32 of the last tile");
+  }
+  std::printf("decode split: %d random batches + 5 edge cases: tiles covered once, merge ranges and slots exact; "
+              "32-bit forms equal wherever split_narrow holds\n",
               cases);
 }
 
