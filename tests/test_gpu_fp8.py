@@ -135,6 +135,7 @@ def test_fp8_write_after_norm_rope(ema, ora, flags):
     (4, [1, 31, 32, 33, 100, 1000, 1024], 1024),
     (8, [4096, 17, 2500], 4096),
     (1, [64, 65, 3], 96),
+    (2, [203, 1, 150, 97], 203),  # capacity not a multiple of 8: exponents loaded row by row
 ])
 def test_fp8_decode_equals_bf16_decode_of_decoded_cache(ema, ora, G, lengths, cap):
     import torch
@@ -155,6 +156,35 @@ def test_fp8_decode_equals_bf16_decode_of_decoded_cache(ema, ora, G, lengths, ca
     # differ by f32 summation order only: a bf16 ulp here and there
     assert_close(host(o8), host(o16), "fp8 vs bf16 decode of the decoded cache", max_abs=2e-3, mean_abs=1e-5)
     assert_close(host(o8), ora.sdpa(q, kd, vd, L, scale_of(D), False), "fp8 decode vs oracle")
+
+
+@pytest.mark.parametrize("cap,lengths", [(1024, [1, 31, 33, 700, 1000]), (203, [1, 33, 150, 202])])
+def test_fp8_decode_stale_rows_are_never_used(ema, ora, cap, lengths):
+    """Rows at or past each length hold NaN codes and the largest exponent: the output is
+    bit-identical to that of a clean cache (16-byte exponent groups with a capacity that is
+    a multiple of 8; row-by-row exponents otherwise)."""
+    import torch
+
+    Hkv, D, G = 2, 128, 4
+    B, Hq = len(lengths), Hkv * G
+    say(f"fp8 decode stale-row poison cap={cap} lengths={lengths}")
+    (kc, ke, _), (vc, ve, _) = quantized_pair(ora, (B, Hkv, cap, D), seed=741)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=742)
+    L = np.asarray(lengths, np.int32)
+    outs = []
+    for poison in (False, True):
+        k2, e2, v2, f2 = kc.copy(), ke.copy(), vc.copy(), ve.copy()
+        if poison:
+            for b in range(B):
+                k2[b, :, L[b]:] = 0x7F  # E4M3FN NaN
+                v2[b, :, L[b]:] = 0x7F
+                e2[b, :, L[b]:] = 127
+                f2[b, :, L[b]:] = 127
+        c8 = fp8_cache(ema, k2, e2, v2, f2)
+        outs.append(host(ema.decode_attention(dev(q), c8, dev(L), cap)))
+        torch.cuda.synchronize()
+    assert np.array_equal(outs[0], outs[1]), "stale rows changed the output"
+    assert np.all(np.isfinite(ora.f32_from_bf16(outs[1])))
 
 
 def test_fp8_decode_qwen3_8b_batched_shape(ema, ora):
