@@ -287,15 +287,17 @@ constexpr int kI4SlotK = 0, kI4SlotV = kTile * 64, kI4SlotKs = 2 * kTile * 64, k
 constexpr int kStateLds = 16 * kD * 4;
 // bf16 slot: the tile's K rows (32 x 256 B) and V rows (32 x 256 B)
 constexpr int kBfSlot = 2 * kTile * kD * 2;
-template <bool kI4, bool kBfDma>
+// fp8 slot: K codes (32 x 128 B), V codes (32 x 128 B), then the K and V exponent pairs of
+// the tile's 32 rows (64 B each); two slots per wave (the tile in use and the next)
+constexpr int kF8SlotV = kTile * kD, kF8SlotKe = 2 * kTile * kD, kF8SlotVe = kF8SlotKe + 2 * kTile;
+constexpr int kF8Slot = kF8SlotVe + 2 * kTile;
+template <bool kFp8, bool kI4, bool kDma>
 constexpr int wave_lds_bytes() {
-  return kI4 ? (kI4Slots * kI4Slot > kStateLds ? kI4Slots * kI4Slot : kStateLds) : kBfDma ? kBfSlot : kStateLds;
+  return kI4 ? (kI4Slots * kI4Slot > kStateLds ? kI4Slots * kI4Slot : kStateLds)
+             : kDma ? (kFp8 ? 2 * kF8Slot : kBfSlot) : kStateLds;
 }
-// bf16 K rows in the slot: row R of the tile (rows 4i .. 4i + 3 in 1 KB block i) keeps its
-// 16-byte chunk ch at unit ch ^ bf_swz(R) of the row, so that the 16 rows of one QK
-// operand read (lanes m, rows 8(m/4) + m%4 + 4r, where bf_swz(R) = m) fall on 16 distinct
-// bank groups for every chunk.
-__device__ __forceinline__ int bf_swz(int R) { return (R & 3) + 4 * ((R >> 3) & 3); }
+// The slots' layouts (dec_krow, bf_swz, f8_swz, f8_vrow) are in ema_schedule.hpp, with the
+// CPU checks of their gathers and reads.
 
 // Partial states cross XCDs, each with its own L2, without cache maintenance: they are
 // written and read with device-coherent (agent-scope) stores and loads, which go past the
@@ -430,12 +432,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // kRot: FP8 rows with the RoPE tail, read only (the fused step over them is the
   // pre-attention kernel followed by this kernel, see launch_decode)
   static_assert(!kRot || (kFp8 && !kFused), "the RoPE-tail reader is the unfused FP8 decode");
-  // kDma: bf16 tiles through the wave's LDS slot by LDS-DMA (small grids, see launch_decode)
-  static_assert(!kDma || (!kFp8 && !kI4), "the LDS-DMA tiles are the bf16 cache's");
+  // kDma: tiles through the wave's LDS slots by LDS-DMA (bf16: small grids; fp8: capacities
+  // that are a multiple of 8; see launch_decode)
+  static_assert(!kDma || (!kI4 && !kRot), "the LDS-DMA tiles are the bf16 and plain fp8 caches'");
   constexpr bool kNarrow = kFp8 || kI4;  // the fp8 head-dim order (kdim)
   __shared__ int32_t pre[kMaxB + 1];
   __shared__ Combine cmb;
-  __shared__ __attribute__((aligned(16))) uint8_t wave_lds[kWaves][wave_lds_bytes<kI4, kDma>()];
+  __shared__ __attribute__((aligned(16))) uint8_t wave_lds[kWaves][wave_lds_bytes<kFp8, kI4, kDma>()];
   __shared__ float2 rope_cs[kWaves][kD / 2];  // fused: each wave's RoPE (cos, sin) table at the offset
   __shared__ __attribute__((aligned(16))) uint16_t new_kv[2][kD];  // fused: the new row, for its owner wave
   const int tid = threadIdx.x;
@@ -495,7 +498,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int m = lane & 15;  // A-operand row
   // K row feeding A-operand row m of MFMA set r: position 8*(m/4) + 4r + m%4,
   // so that S^T rows 4c..4c+3 of set r are positions 8c + 4r + i.
-  const int krow0 = 8 * (m >> 2) + (m & 3);
+  const int krow0 = dec_krow(m, 0);
 
   while (t < t_end) {
     // locate the segment containing tile t (uniform across the workgroup): the largest b
@@ -630,6 +633,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                           u32x4 (&ktr)[2][2], u32x4 (&vwr)[8]) {
       load_k8(tile, kr, kx, ktr);
       load_v8(tile, vr, vx, vwr);
+    };
+    // fp8 with kDma: the tile's codes and exponents by LDS-DMA into slot sl (10 instructions:
+    // four of 8 whole K rows, four of 8 whole V rows, two of the 32 exponent pairs on 4
+    // lanes), code rows past L clamped to row L - 1; the exponents of rows past L are zeroed
+    // when the tile is decoded (rows past the capacity read as zeros: the capacity is a
+    // multiple of 8, so no 16-byte piece straddles it).
+    uint8_t* const f8base = &wave_lds[wave][0];
+    const uint32_t f8lds = (uint32_t)(uintptr_t)(lds_void*)f8base;
+    const uint32_t f8plane = (uint32_t)a.cap * (uint32_t)a.sp;  // bounded by the host
+    const u32x4 k8_rs = rsrc_words(Kb8, f8plane), v8_rs = rsrc_words(Vb8, f8plane);
+    const u32x4 ke8_rs = rsrc_words(Ke, (uint32_t)a.cap * 2u), ve8_rs = rsrc_words(Ve, (uint32_t)a.cap * 2u);
+    constexpr int kF8Dma = 10;  // DMA instructions per tile
+    auto f8_dma = [&](int tile, int sl) __attribute__((always_inline)) {
+      const int p0 = tile * kTile;
+      const uint32_t dst = f8lds + (uint32_t)sl * kF8Slot;
+      for (int i = 0; i < 4; ++i) {
+        const int S = 8 * i + (lane >> 3), u = lane & 7;
+        const int pk = p0 + S < L ? p0 + S : L - 1;  // K: slot row S is row S
+        const int R = f8_vrow(S);                     // V: slot row S holds row R
+        const int pv = p0 + R < L ? p0 + R : L - 1;
+        dma16(k8_rs, (uint32_t)pk * (uint32_t)a.sp + 16u * (uint32_t)(u ^ f8_swz(S)), 0u, dst + 1024u * i);
+        dma16(v8_rs, (uint32_t)pv * (uint32_t)a.sp + 16u * (uint32_t)u, 0u, dst + kF8SlotV + 1024u * i);
+      }
+      if (lane < 4) {
+        dma16(ke8_rs, 2u * (uint32_t)p0 + 16u * lane, 0u, dst + kF8SlotKe);
+        dma16(ve8_rs, 2u * (uint32_t)p0 + 16u * lane, 0u, dst + kF8SlotVe);
+      }
+    };
+    auto f8_read = [&](int sl) __attribute__((always_inline)) {
+      const uint8_t* const sp8 = f8base + sl * kF8Slot;
+      for (int r = 0; r < 2; ++r) {
+        const int R = krow0 + 4 * r;
+        for (int i = 0; i < 2; ++i) {  // steps 2i, 2i + 1: chunk 4i + c of the row
+          const u32x4 w = *(const u32x4*)(sp8 + 128 * R + 16 * ((4 * i + c) ^ f8_swz(R)));
+          k8[r][2 * i] = u32x2{w[0], w[1]};
+          k8[r][2 * i + 1] = u32x2{w[2], w[3]};
+        }
+      }
+      for (int kk = 0; kk < 8; ++kk) {
+        const int R = 8 * c + kk;
+        v8[kk] = *(const u32x2*)(sp8 + kF8SlotV + 128 * f8_vrow(R) + 8 * m);
+      }
+      ke.g = *(const u32x4*)(sp8 + kF8SlotKe + 16 * (m >> 2));
+      ve.g = *(const u32x4*)(sp8 + kF8SlotVe + 16 * c);
     };
     u32x4 kc[2][4], vc[8], kn[2][4], vn[8];
     auto decode_tile8 = [&](int tile) {
@@ -796,6 +843,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           i4_dma(first, 0);
           if (first + kWaves < tile1) i4_dma(first + kWaves, 1);
         }
+      } else if (kFp8 && kDma) {
+        f8_dma(first, 0);
       } else if (kFp8) {
         load_tile8(first, k8, v8, ke, ve, kt, vw);
       } else {
@@ -1109,6 +1158,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // claimed; the next V rows are requested after the score MFMAs, once kc is dead
         decode_tile8(tile);
         if (more) load_k8(tile + kWaves, k8n, ken, ktn);
+      } else if (kFp8 && kDma) {
+        // two slots: the next tile's DMA goes to the other slot (read out in the previous
+        // iteration) before this tile's is waited for
+        const int sl = ((tile - first) / kWaves) & 1;
+        if (more) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          f8_dma(tile + kWaves, sl ^ 1);
+          wait_vm<kF8Dma>();
+        } else {
+          wait_vm<0>();
+        }
+        f8_read(sl);
+        decode_tile8(tile);
       } else if (kFp8) {
         if (more) load_tile8(tile + kWaves, k8n, v8n, ken, ven, ktn, vwn);
         decode_tile8(tile);
@@ -1188,7 +1250,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int s = 0; s < 4; ++s) kc[r][s] = kn[r][s];
         for (int kk = 0; kk < 8; ++kk) vc[kk] = vn[kk];
       }
-      if (kFp8 && more) {
+      if (kFp8 && !kDma && more) {
         for (int r = 0; r < 2; ++r) {
           for (int s = 0; s < 4; ++s) k8[r][s] = k8n[r][s];
           if (kRot) kt[r][0] = ktn[r][0], kt[r][1] = ktn[r][1];
@@ -1393,6 +1455,9 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   if (plane > (int64_t)UINT32_MAX)
     return set_error(EMA_ERR_UNSUPPORTED, "ema_decode_attention: %lld bytes per (sequence, kv head) exceed 2^32",
                      (long long)plane);
+  // plain fp8 rows through LDS-DMA slots: whole 16-byte exponent pieces (a capacity that is
+  // a multiple of 8) and a plane within a 32-bit buffer range; otherwise straight loads
+  const bool f8dma = fp8 && !tail && c.capacity % 8 == 0 && (int64_t)c.capacity * c.stride_pos <= (int64_t)UINT32_MAX;
   const dim3 grid(plan.workers), block(kWaves * 64);
   if (a.fused && tail) {
     // The fused step over FP8 rows with a RoPE tail runs as two kernels: the fused kernel
@@ -1411,10 +1476,12 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
     hipLaunchKernelGGL((decode_kernel<false, true, false, true>), grid, block, 0, s, a);
   } else if (a.fused && i4) hipLaunchKernelGGL((decode_kernel<true, false, true>), grid, block, 0, s, a);
   else if (i4) hipLaunchKernelGGL((decode_kernel<false, false, true>), grid, block, 0, s, a);
+  else if (a.fused && f8dma) hipLaunchKernelGGL((decode_kernel<true, true, false, false, true>), grid, block, 0, s, a);
   else if (a.fused && fp8) hipLaunchKernelGGL((decode_kernel<true, true>), grid, block, 0, s, a);
   else if (a.fused && a.inline_merge) hipLaunchKernelGGL((decode_kernel<true, false, false, false, true>), grid, block, 0, s, a);
   else if (a.fused) hipLaunchKernelGGL((decode_kernel<true, false>), grid, block, 0, s, a);
   else if (tail) hipLaunchKernelGGL((decode_kernel<false, true, false, true>), grid, block, 0, s, a);
+  else if (f8dma) hipLaunchKernelGGL((decode_kernel<false, true, false, false, true>), grid, block, 0, s, a);
   else if (fp8) hipLaunchKernelGGL((decode_kernel<false, true>), grid, block, 0, s, a);
   else if (a.inline_merge) hipLaunchKernelGGL((decode_kernel<false, false, false, false, true>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((decode_kernel<false, false>), grid, block, 0, s, a);

@@ -129,4 +129,23 @@ EMA_HD int64_t split_worker_of32(int64_t t, int64_t total, int W) {
   return (int64_t)((((uint32_t)t + 1u) * (uint32_t)W - 1u) / (uint32_t)total);
 }
 
+// ------------------------------------------------------------------ decode tile slots
+// LDS layouts of the decode kernels' tiles when they arrive by LDS-DMA: instruction i, lane l
+// writes the 16 bytes at slot byte 1024 i + 16 l, gathered from any source address; the
+// operands are then read in the MFMA layouts. The QK operand's lane (m, c) of row set r
+// reads row dec_krow(m, r) of the 32-row tile, chunk 4s + c (bf16: 16 bytes of step s) or
+// 4i + c (fp8: 16 bytes of steps 2i, 2i + 1).
+EMA_HD int dec_krow(int m, int r) { return 8 * (m >> 2) + (m & 3) + 4 * r; }
+// bf16: 256-byte rows, four per instruction (row R at byte 256 R); unit u of K row R holds
+// chunk u ^ bf_swz(R), so the 16 rows of one operand read land on 16 distinct 16-byte bank
+// groups of a 256-byte bank window (bf_swz(dec_krow(m, r)) = m).
+EMA_HD int bf_swz(int R) { return (R & 3) + 4 * ((R >> 3) & 3); }
+// fp8: 128-byte rows, eight per instruction. Unit u of K row R holds chunk u ^ f8_swz(R): the
+// row's parity picks the 128-byte half of the window and the swizzle the unit within it, so
+// again the 16 rows of a read use 16 distinct bank groups. V row R sits at slot row
+// f8_vrow(R) (an involution), so the rows 8c + kk of one read (16 lanes per row, c = 0..3)
+// alternate between the window's halves.
+EMA_HD int f8_swz(int R) { return ((R >> 1) & 1) | (((R >> 3) & 3) << 1); }
+EMA_HD int f8_vrow(int R) { return R ^ ((R >> 3) & 1); }
+
 }  // namespace ema

@@ -10,7 +10,9 @@
 //    set of slices that intersect it, and the partial-state slots (w + segment) of split
 //    segments are distinct and inside the workspace the plan sizes; the 32-bit forms of
 //    split_begin / split_worker_of equal the 64-bit ones wherever split_narrow holds, up
-//    to its edge.
+//    to its edge;
+//  - decode tile slots: the LDS-DMA gathers and the operand reads of the bf16 and fp8 slot
+//    layouts agree byte for byte, and each read spreads over distinct bank groups.
 // Built with g++ (no HIP), also under -fsanitize=address,undefined. Prints one line per
 // group of checks and exits non-zero on the first failure.
 #include <cstdio>
@@ -203,10 +205,80 @@ static void test_prefill_streams() {
               cases);
 }
 
+// Decode tile slots: an LDS-DMA instruction i writes lane l's 16 bytes at slot byte
+// 1024 i + 16 l from the source the gather chose for that lane. Simulated per byte as
+// (row, byte of the row) pairs: every operand read must find the row and chunk it wants,
+// and the 16 lanes of one K read (one V row per 16 lanes) must spread over the bank
+// groups of a 256-byte window.
+static void test_decode_slots() {
+  // bf16: K rows of 256 bytes, four per instruction; the gather puts chunk u ^ bf_swz(R) in unit u
+  {
+    std::vector<int> src(8192, -1);  // slot byte -> row * 256 + byte of the row
+    for (int i = 0; i < 8; ++i)
+      for (int l = 0; l < 64; ++l) {
+        const int R = 4 * i + (l >> 4), ch = (l & 15) ^ bf_swz(R);
+        for (int b = 0; b < 16; ++b) src[1024 * i + 16 * l + b] = R * 256 + 16 * ch + b;
+      }
+    for (int r = 0; r < 2; ++r)
+      for (int s = 0; s < 4; ++s)
+        for (int c = 0; c < 4; ++c) {
+          std::set<int> units;
+          for (int m = 0; m < 16; ++m) {
+            const int R = dec_krow(m, r), ch = 4 * s + c;
+            const int at = 1024 * (R >> 2) + 256 * (R & 3) + 16 * (ch ^ bf_swz(R));
+            for (int b = 0; b < 16; ++b)
+              CHECK(src[at + b] == R * 256 + 16 * ch + b, "bf16 slot: K row %d chunk %d byte %d", R, ch, b);
+            units.insert((at / 16) % 16);
+          }
+          CHECK(units.size() == 16, "bf16 slot: K read r=%d s=%d c=%d on %zu bank groups", r, s, c, units.size());
+        }
+  }
+  // fp8: K and V rows of 128 bytes, eight per instruction
+  {
+    std::vector<int> ksrc(4096, -1), vsrc(4096, -1);
+    for (int i = 0; i < 4; ++i)
+      for (int l = 0; l < 64; ++l) {
+        const int S = 8 * i + (l >> 3), u = l & 7;
+        for (int b = 0; b < 16; ++b) {
+          ksrc[1024 * i + 16 * l + b] = S * 128 + 16 * (u ^ f8_swz(S)) + b;
+          vsrc[1024 * i + 16 * l + b] = f8_vrow(S) * 128 + 16 * u + b;
+        }
+      }
+    for (int R = 0; R < 32; ++R) CHECK(f8_vrow(f8_vrow(R)) == R && f8_vrow(R) < 32, "f8_vrow(%d)", R);
+    for (int r = 0; r < 2; ++r)
+      for (int i = 0; i < 2; ++i)
+        for (int c = 0; c < 4; ++c) {
+          std::set<int> units;
+          for (int m = 0; m < 16; ++m) {
+            const int R = dec_krow(m, r), ch = 4 * i + c;
+            const int at = 128 * R + 16 * (ch ^ f8_swz(R));
+            for (int b = 0; b < 16; ++b)
+              CHECK(ksrc[at + b] == R * 128 + 16 * ch + b, "fp8 slot: K row %d chunk %d byte %d", R, ch, b);
+            units.insert((at / 16) % 16);
+          }
+          CHECK(units.size() == 16, "fp8 slot: K read r=%d i=%d c=%d on %zu bank groups", r, i, c, units.size());
+        }
+    for (int kk = 0; kk < 8; ++kk)
+      for (int c0 = 0; c0 < 4; c0 += 2) {
+        std::set<int> words;  // the 32 lanes of two adjacent c read 8 bytes each
+        for (int c = c0; c < c0 + 2; ++c)
+          for (int m = 0; m < 16; ++m) {
+            const int R = 8 * c + kk, at = 128 * f8_vrow(R) + 8 * m;
+            for (int b = 0; b < 8; ++b) CHECK(vsrc[at + b] == R * 128 + 8 * m + b, "fp8 slot: V row %d byte %d", R, 8 * m + b);
+            words.insert((at / 8) % 32);
+          }
+        CHECK(words.size() == 32, "fp8 slot: V read kk=%d c=%d..%d on %zu bank pairs", kk, c0, c0 + 1, words.size());
+      }
+  }
+  std::printf("decode slots: bf16 and fp8 gathers give every operand read its row and chunk; reads spread over the "
+              "bank groups\n");
+}
+
 int main() {
   test_prefill();
   test_prefill_streams();
   test_decode();
+  test_decode_slots();
   std::printf("%d checks passed\n", g_checks);
   return 0;
 }
