@@ -278,7 +278,10 @@ EMA_API int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_
  * FP8 cache: K/V rows are decoded exactly to bf16 (code value times 2^exp) and attended
  * as a bf16 cache holding those values would be.
  * int4 cache: attends the affine values scale * code + bias of every row (the reference
- * dequantizes the whole cache and runs the masked SDPA over it, decode_eager.rs:78-104). */
+ * dequantizes the whole cache and runs the masked SDPA over it, decode_eager.rs:78-104).
+ * Size limits (EMA_ERR_UNSUPPORTED beyond, also for ema_decode_step): batch * n_kv_heads *
+ * ceil(capacity / 32) below 2^31 - 1, and for bf16 and int4 caches one (sequence, kv head)
+ * plane, capacity * stride_pos bytes (int4: half that), within 4 GiB. */
 EMA_API int32_t ema_decode_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,
                              const int32_t* lengths, int32_t max_len, int32_t n_heads,
                              float scale, void* out, void* workspace, uint64_t workspace_bytes);

@@ -105,6 +105,24 @@ def test_decode_argument_errors(ema):
     assert rc == ema.EMA_ERR_INVALID_ARG
 
 
+def test_decode_size_limits(ema):
+    """Shapes past the kernels' index ranges are refused before any launch: a tile count
+    (batch * kv heads * ceil(capacity / 32)) of 2^31 - 1 or more, and a (sequence, kv head)
+    plane of a bf16 cache over 4 GiB (addressed through a 32-bit buffer range)."""
+    L = ema.lib()
+    good = 0x40000
+    # bf16, capacity 2^24 + 32: one plane is (2^24 + 32) * 256 bytes > 4 GiB
+    rc, d = _desc(ema, B=1, Hkv=1, cap=(1 << 24) + 32)
+    assert rc == ema.EMA_OK
+    rc = L.ema_decode_attention(None, good, ctypes.byref(d), good, 64, 1, 0.088, good, good, 1 << 30)
+    assert rc == ema.EMA_ERR_UNSUPPORTED and "2^32" in ema.last_error()
+    # capacity 2^31 - 32 (2^26 - 1 tiles per plane) over 40 sequence x kv-head planes
+    rc, d = _desc(ema, B=5, Hkv=8, cap=(1 << 31) - 32)
+    assert rc == ema.EMA_OK
+    rc = L.ema_decode_attention(None, good, ctypes.byref(d), good, 64, 8, 0.088, good, good, 1 << 30)
+    assert rc == ema.EMA_ERR_UNSUPPORTED and "tiles" in ema.last_error()
+
+
 def test_pre_attention_argument_errors(ema):
     L = ema.lib()
     _, d = _desc(ema)
