@@ -479,6 +479,41 @@ def bench_fp8_prefill(ctx, ema, name, B, Hq, Hkv, D, cap, T, off, steps=20):
     return {"workload": name, "us": ms * 1e3, "tflops": tf, "frac_of_peak": tf / BF16_PEAK_TFLOPS, "flops": fl}
 
 
+def bench_prefill_layer(ctx, ema, name, dtype, B, Hq, Hkv, D, cap, T, steps=20, prefill_only=False):
+    """A fresh prefill chunk (offset 0) as a layer runs it: ema_pre_attention (norms, RoPE,
+    the K/V rows written into the cache) + causal prefill. FP8 cache: ema_pre_attention_ws
+    also writes the chunk's decoded rows into the prefill's bf16 copy, and the prefill
+    (EMA_PREFILL_ROWS_DECODED, keys the chunk's own) runs no decode pass. prefill_only:
+    time the prefill call alone, with the copy filled once beforehand."""
+    torch = ctx.torch
+    fp8 = dtype == "fp8"
+    cache = ema.StaticCache(B, Hkv, cap, D, dtype=dtype)
+    qkv = ctx.randn((B, T, (Hq + 2 * Hkv) * D))
+    qw, kw = ctx.randn((D,), 1.0, 0.02), ctx.randn((D,), 1.0, 0.02)
+    off = ctx.i32([0] * B)
+    q = torch.empty((B, Hq, T, D), dtype=torch.bfloat16, device=ctx.dev)
+    out = torch.empty((B, T, Hq * D), dtype=torch.bfloat16, device=ctx.dev)
+    ws = torch.empty(ema.prefill_workspace_size(cache, T), dtype=torch.uint8, device=ctx.dev) if fp8 else None
+    pre_kw = {"prefill_workspace": ws, "max_kv_len": T} if fp8 else {}
+    att_kw = {"max_kv_len": T, "workspace": ws, "rows_decoded": True, "chunk_only": True} if fp8 else {}
+
+    def pre():
+        ema.pre_attention(qkv, qw, kw, 1e-6, 1e6, off, Hq, cache, q_out=q, **pre_kw)
+
+    def att():
+        ema.prefill_attention(q, cache, off, causal=True, out=out, **att_kw)
+
+    if prefill_only:
+        pre()
+        ms = time_calls(torch, att, steps, 5)
+    else:
+        ms = time_calls(torch, lambda: (pre(), att()), steps, 5)
+    fl = B * prefill_flops(Hq, D, T, 0)
+    tf = fl / (ms * 1e-3) / 1e12
+    log(f"[bench] {name}: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s of the attention ({tf/BF16_PEAK_TFLOPS:.1%} of bf16 peak)")
+    return {"workload": name, "us": ms * 1e3, "tflops": tf, "frac_of_peak": tf / BF16_PEAK_TFLOPS, "flops": fl}
+
+
 def gdn_bytes(B, T, Hk, Hv, Dk, Dv, act=2):
     """State read + write, q/k/v in, y out, g/beta in."""
     return 8 * B * Hv * Dv * Dk + act * B * T * (2 * Hk * Dk + 2 * Hv * Dv) + 8 * B * T * Hv
@@ -621,6 +656,12 @@ def main():
                                           [32768] * 8))
         secondary.append(bench_fp8_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_fp8_cache", 1, 32, 8, 128, 4096,
                                            2048, 0))
+        # the chunk's rows decoded by pre-attention: the prefill call runs no decode pass
+        secondary.append(bench_prefill_layer(ctx, ema, "prefill_causal_T2048_32q8kv_fp8_cache_rows_from_pre_attention",
+                                             "fp8", 1, 32, 8, 128, 4096, 2048, prefill_only=True))
+        for dt in ("bf16", "fp8"):
+            secondary.append(bench_prefill_layer(ctx, ema, f"pre_attention_plus_prefill_T2048_32q8kv_{dt}_cache", dt, 1,
+                                                 32, 8, 128, 4096, 2048))
     if args.only in ("all", "fp8", "fp8_tail"):
         # Fp8Cache::new(128, 64): dims 64..127 of each row kept as bf16
         secondary.append(bench_fp8_step(ctx, ema, "decode_step_B32_32q8kv_fp8_cache_rope_tail64", n_rot=64))

@@ -60,6 +60,7 @@ pub mod sys {
     /// `ema_prefill_attention` flags.
     pub const EMA_PREFILL_CAUSAL: u32 = 1;
     pub const EMA_PREFILL_CHUNK_ONLY: u32 = 2;
+    pub const EMA_PREFILL_ROWS_DECODED: u32 = 4;
 
     /// Arrival counters at the start of every decode workspace: zero before its first use;
     /// every call leaves them at zero.
@@ -148,6 +149,11 @@ pub mod sys {
                                  k_norm_w: *const c_void, eps: f32, theta: f32, offsets: *const i32, batch: i32,
                                  n_tokens: i32, n_heads: i32, n_kv_heads: i32, head_dim: i32, flags: u32,
                                  q_out: *mut c_void, cache: *const EmaKvCacheDesc) -> i32;
+        pub fn ema_pre_attention_ws(stream: EmaStream, qkv: *const c_void, q_norm_w: *const c_void,
+                                    k_norm_w: *const c_void, eps: f32, theta: f32, offsets: *const i32, batch: i32,
+                                    n_tokens: i32, n_heads: i32, n_kv_heads: i32, head_dim: i32, flags: u32,
+                                    q_out: *mut c_void, cache: *const EmaKvCacheDesc, max_kv_len: i32,
+                                    workspace: *mut c_void, workspace_bytes: u64) -> i32;
         pub fn ema_decode_workspace_size(batch: i32, n_heads: i32, n_kv_heads: i32, head_dim: i32, max_len: i32,
                                          bytes: *mut u64) -> i32;
         pub fn ema_decode_attention(stream: EmaStream, q: *const c_void, cache: *const EmaKvCacheDesc,
@@ -1030,22 +1036,36 @@ fn gqa_layer<C: HipKvCache>(ctx: &HipCtx, x: &DeviceArray, weights: &GqaWeights,
     let scale = 1.0f32 / (d as f32).sqrt();
     let pos = cache.position(ctx, offset as i64)?;
     if t > 1 {
-        check(
-            unsafe {
-                sys::ema_pre_attention(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, t, hq,
-                                       hkv, d, flags, q, &desc)
-            },
-            "pre_attention",
-        )?;
         if quantised {
+            // FP8: pre-attention also puts the chunk's decoded rows into the prefill's bf16
+            // copy, so the prefill decodes only earlier rows (none for a static cache's first
+            // chunk, whose keys are the chunk's own)
             check(
                 unsafe {
-                    sys::ema_prefill_attention_ws(ctx.stream, q, &desc, pos, t, hq, scale, sys::EMA_PREFILL_CAUSAL,
-                                                  attn, rows, pws, pws_bytes as u64)
+                    sys::ema_pre_attention_ws(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, t,
+                                              hq, hkv, d, flags, q, &desc, rows, pws, pws_bytes as u64)
+                },
+                "pre_attention_ws",
+            )?;
+            let mut pf = sys::EMA_PREFILL_CAUSAL | sys::EMA_PREFILL_ROWS_DECODED;
+            if offset == 0 && desc.flags & sys::EMA_KV_ROTATING == 0 {
+                pf |= sys::EMA_PREFILL_CHUNK_ONLY;
+            }
+            check(
+                unsafe {
+                    sys::ema_prefill_attention_ws(ctx.stream, q, &desc, pos, t, hq, scale, pf, attn, rows, pws,
+                                                  pws_bytes as u64)
                 },
                 "prefill_attention_ws",
             )?;
         } else {
+            check(
+                unsafe {
+                    sys::ema_pre_attention(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, t,
+                                           hq, hkv, d, flags, q, &desc)
+                },
+                "pre_attention",
+            )?;
             check(
                 unsafe {
                     sys::ema_prefill_attention(ctx.stream, q, &desc, pos, t, hq, scale, sys::EMA_PREFILL_CAUSAL,

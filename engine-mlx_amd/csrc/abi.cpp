@@ -393,11 +393,10 @@ static int32_t check_norm_weights(const char* op, const void* q_norm_w, const vo
   return EMA_OK;
 }
 
-int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
-                          float eps, float theta, const int32_t* offsets, int32_t batch, int32_t n_tokens,
-                          int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, uint32_t flags, void* q_out,
-                          const ema_kvcache_desc* cache) {
-  const char* op = "ema_pre_attention";
+static int32_t check_pre_attention(const char* op, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                   float eps, float theta, const int32_t* offsets, int32_t batch, int32_t n_tokens,
+                                   int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, uint32_t flags,
+                                   void* q_out, const ema_kvcache_desc* cache) {
   int32_t rc = check_cache(op, cache);
   if (rc) return rc;
   if (!qkv || !q_out || !offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null qkv/q_out/offsets", op);
@@ -413,8 +412,46 @@ int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_no
     return set_error(EMA_ERR_CAPACITY, "%s: static KV overflow: %d tokens exceed capacity %d", op, n_tokens, cache->capacity);
   if (!(eps >= 0.f) || !(theta > 0.f)) return set_error(EMA_ERR_INVALID_ARG, "%s: eps must be >= 0 and theta > 0", op);
   if (!aligned16(qkv) || !aligned16(q_out)) return set_error(EMA_ERR_INVALID_ARG, "%s: qkv/q_out must be 16-byte aligned", op);
+  return EMA_OK;
+}
+
+int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                          float eps, float theta, const int32_t* offsets, int32_t batch, int32_t n_tokens,
+                          int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, uint32_t flags, void* q_out,
+                          const ema_kvcache_desc* cache) {
+  int32_t rc = check_pre_attention("ema_pre_attention", qkv, q_norm_w, k_norm_w, eps, theta, offsets, batch,
+                                   n_tokens, n_heads, n_kv_heads, head_dim, flags, q_out, cache);
+  if (rc) return rc;
   return launch_pre_attention((hipStream_t)stream, qkv, q_norm_w, k_norm_w, eps, theta, offsets, batch, n_tokens,
                               n_heads, n_kv_heads, head_dim, flags, q_out, *cache);
+}
+
+// declared below, with the prefill entry points
+static int32_t prefill_copy_rows(const ema_kvcache_desc* c, int32_t max_kv_len);
+static uint64_t prefill_ws_bytes(const ema_kvcache_desc* c, int32_t max_kv_len);
+
+int32_t ema_pre_attention_ws(ema_stream_t stream, const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                             float eps, float theta, const int32_t* offsets, int32_t batch, int32_t n_tokens,
+                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, uint32_t flags, void* q_out,
+                             const ema_kvcache_desc* cache, int32_t max_kv_len, void* workspace,
+                             uint64_t workspace_bytes) {
+  const char* op = "ema_pre_attention_ws";
+  int32_t rc = check_pre_attention(op, qkv, q_norm_w, k_norm_w, eps, theta, offsets, batch, n_tokens, n_heads,
+                                   n_kv_heads, head_dim, flags, q_out, cache);
+  if (rc) return rc;
+  if (cache->dtype != EMA_DTYPE_FP8_E4M3)
+    return set_error(EMA_ERR_UNSUPPORTED, "%s: the prefill copy exists for FP8 caches only", op);
+  if (max_kv_len < n_tokens || max_kv_len > cache->capacity)
+    return set_error(EMA_ERR_CAPACITY, "%s: max_kv_len %d outside [n_tokens %d, capacity %d]", op, max_kv_len,
+                     n_tokens, cache->capacity);
+  const uint64_t need = prefill_ws_bytes(cache, max_kv_len);
+  if (!workspace || workspace_bytes < need)
+    return set_error(EMA_ERR_WORKSPACE, "%s: workspace of %llu bytes needed, %llu given", op,
+                     (unsigned long long)need, (unsigned long long)(workspace ? workspace_bytes : 0));
+  if (!aligned16(workspace)) return set_error(EMA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", op);
+  return launch_pre_attention((hipStream_t)stream, qkv, q_norm_w, k_norm_w, eps, theta, offsets, batch, n_tokens,
+                              n_heads, n_kv_heads, head_dim, flags, q_out, *cache, workspace,
+                              prefill_copy_rows(cache, max_kv_len));
 }
 
 int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
@@ -512,8 +549,10 @@ static int32_t check_prefill(const char* op, const void* q, const ema_kvcache_de
   int32_t rc = check_cache(op, cache);
   if (rc) return rc;
   if (!q || !out || !q_offsets) return set_error(EMA_ERR_INVALID_ARG, "%s: null q/out/q_offsets", op);
-  if (flags & ~(EMA_PREFILL_CAUSAL | EMA_PREFILL_CHUNK_ONLY))
+  if (flags & ~(EMA_PREFILL_CAUSAL | EMA_PREFILL_CHUNK_ONLY | EMA_PREFILL_ROWS_DECODED))
     return set_error(EMA_ERR_INVALID_ARG, "%s: unknown flags 0x%x", op, flags);
+  if ((flags & EMA_PREFILL_ROWS_DECODED) && cache->dtype != EMA_DTYPE_FP8_E4M3)
+    return set_error(EMA_ERR_INVALID_ARG, "%s: EMA_PREFILL_ROWS_DECODED applies to FP8 caches only", op);
   if ((rc = check_heads(op, n_heads, cache->n_kv_heads))) return rc;
   if (n_tokens <= 0) return set_error(EMA_ERR_SHAPE, "%s: n_tokens %d must be positive", op, n_tokens);
   if (n_tokens > cache->capacity)
@@ -587,7 +626,8 @@ int32_t ema_prefill_attention_ws(ema_stream_t stream, const void* q, const ema_k
   // a ring stays a ring: the copy holds the cache's rows at the same row indices (the
   // whole ring, so wrapped positions land where the cache holds them)
   w.flags = cache->flags & EMA_KV_ROTATING;
-  return launch_prefill((hipStream_t)stream, q, w, q_offsets, n_tokens, n_heads, scale, flags, out);
+  return launch_prefill((hipStream_t)stream, q, w, q_offsets, n_tokens, n_heads, scale,
+                        flags & ~(uint32_t)EMA_PREFILL_ROWS_DECODED, out);
 }
 
 int32_t ema_prefill_attention(ema_stream_t stream, const void* q, const ema_kvcache_desc* cache,

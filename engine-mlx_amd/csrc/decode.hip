@@ -150,16 +150,6 @@ __device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
 }
 __device__ __forceinline__ u32x2 ld8_stream(const uint8_t* p) { return __builtin_nontemporal_load((const u32x2*)p); }
 
-// 8 E4M3FN codes -> 8 bf16 values code * 2^e (exact), in the bf16 operand layout
-__device__ __forceinline__ u32x4 fp8_decode8(u32x2 w, int e) {
-  const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
-  u32x4 o;
-  o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], sc, false));
-  o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], sc, true));
-  o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], sc, false));
-  o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], sc, true));
-  return o;
-}
 
 // Quantisation of one 64-value block held one value per lane (the fused step's new row):
 // exponent ceil(log2(amax / 448)), amax = max(1e-4, max |x|) over the wave (logarithm in

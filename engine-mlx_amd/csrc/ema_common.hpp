@@ -99,6 +99,16 @@ __device__ __forceinline__ u32x2 fp8_encode8(const uint16_t* x, int e) {
   }
   return w;
 }
+// 8 E4M3FN codes -> 8 bf16 values code * 2^e (exact), value i from byte i
+__device__ __forceinline__ u32x4 fp8_decode8(u32x2 w, int e) {
+  const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
+  u32x4 o;
+  o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], sc, false));
+  o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], sc, true));
+  o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], sc, false));
+  o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], sc, true));
+  return o;
+}
 
 // ---- 4-bit affine KV rows (MLX "affine" quantisation, group 64) ----
 // Parameters of one group with minimum mn and maximum mx, as MLX's affine quantiser forms
@@ -171,10 +181,13 @@ int32_t allow_lds_once(const void* fn, int bytes, std::atomic<uint64_t>* done, c
 // Maps a HIP error to EMA_ERR_HIP with context, or returns EMA_OK.
 int32_t check_hip(hipError_t e, const char* what);
 
+// copy (fp8 cache only, else null): also write each stored K and V row, decoded to bf16,
+// into row `row` of the prefill's bf16 copy [2][B, Hkv, copy_rows, D] (rows past copy_rows
+// are not written)
 int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, const void* kw,
                              float eps, float theta, const int32_t* off, int B, int T, int Hq,
                              int Hkv, int D, uint32_t flags, void* q_out,
-                             const ema_kvcache_desc& c);
+                             const ema_kvcache_desc& c, void* copy = nullptr, int copy_rows = 0);
 
 // Arrival counters at the start of every decode workspace: one per (sequence, kv head)
 // segment, then one for the grid. The region has a fixed size, so that a workspace reused

@@ -49,6 +49,12 @@ __global__ __launch_bounds__(256) void fp8_to_bf16_kernel(DequantArgs a) {
   const int t8 = threadIdx.x & 7;  // 16-code piece of the row: dims 16 t8 .. +15
   const int row = blockIdx.x * 32 + (threadIdx.x >> 3);
   if (row < lo || row >= hi) return;
+  // EMA_PREFILL_ROWS_DECODED: the chunk's rows (positions q_off .. q_off + T - 1: rows
+  // (q_off + t) % cap of a ring, rows q_off + t of a static cache) are in the copy already
+  if (a.flags & EMA_PREFILL_ROWS_DECODED) {
+    const bool chunk = a.rot ? ((row - q_off) % a.cap + a.cap) % a.cap < a.T : row >= q_off && row - q_off < a.T;
+    if (chunk) return;
+  }
   const int64_t src = (int64_t)b * a.sb + (int64_t)kh * a.sh + (int64_t)row * a.sp + 16 * t8;
   const int64_t erow = (int64_t)bh * a.cap + row;
   const int64_t dst = ((int64_t)bh * a.R + row) * kD + 16 * t8;
@@ -190,6 +196,9 @@ int32_t launch_fp8_convert(hipStream_t s, const ema_kvcache_desc& src, int src_r
 
 int32_t launch_fp8_to_bf16(hipStream_t s, const ema_kvcache_desc& c, const int32_t* q_off, int T,
                            uint32_t flags, int R, void* ws) {
+  // the chunk's rows are decoded already and no other row is attended: nothing to do
+  if ((flags & EMA_PREFILL_ROWS_DECODED) && (flags & EMA_PREFILL_CHUNK_ONLY) && !(c.flags & EMA_KV_ROTATING))
+    return EMA_OK;
   DequantArgs a;
   a.k = (const uint8_t*)c.k;
   a.v = (const uint8_t*)c.v;

@@ -108,6 +108,11 @@ struct PreArgs {
   uint32_t flags;
   int rot;  // rotating cache: position p lives in row p % cap
   int nrot;  // fp8 cache: dims 64..127 kept as bf16 (n_rot = 64)
+  // fp8 cache, optional: the prefill's bf16 copy [B, Hkv, R, D] of K (dk) and V (dv); each
+  // stored row below R is also written there, decoded (code * 2^e, exact)
+  uint16_t* dk;
+  uint16_t* dv;
+  int R;
 };
 
 template <int D, bool kFp8, bool kI4 = false>
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
   const int lane8 = threadIdx.x & 7;
   const int H = a.Hq + 2 * a.Hkv;
   // fp8 cache row (b, kh, pos) from the bf16 values x[0..2E) of this lane (E = 8)
-  auto store_fp8 = [&](const uint16_t* x, uint16_t* codes16, int8_t* exps, int b_, int kh, int p_) {
+  auto store_fp8 = [&](const uint16_t* x, uint16_t* codes16, int8_t* exps, uint16_t* copy, int b_, int kh, int p_) {
     float m0 = 0.f, m1 = 0.f;
     for (int e = 0; e < E; ++e) {
       m0 = fmaxf(m0, fabsf(bf16_to_f32(x[e])));
@@ -151,9 +156,17 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
     const int e0 = fp8_block_exp(m0);
     const int e1 = a.nrot ? 0 : fp8_block_exp(m1);  // (uniform: all 8 lanes shuffle or none)
     uint8_t* row = (uint8_t*)codes16 + (int64_t)b_ * a.sb + (int64_t)kh * a.sh + (int64_t)p_ * a.sp;
-    *(u32x2*)(row + lane8 * E) = fp8_encode8(x, e0);
+    const u32x2 c0 = fp8_encode8(x, e0);
+    *(u32x2*)(row + lane8 * E) = c0;
+    u32x2 c1 = {0u, 0u};
     if (a.nrot) Vec<E>::store((uint16_t*)(row + HALF) + lane8 * E, x + E);
-    else *(u32x2*)(row + HALF + lane8 * E) = fp8_encode8(x + E, e1);
+    else *(u32x2*)(row + HALF + lane8 * E) = c1 = fp8_encode8(x + E, e1);
+    if (copy && p_ < a.R) {  // the decoded row, as the prefill's decode pass would write it
+      uint16_t* const d = copy + (((int64_t)b_ * a.Hkv + kh) * a.R + p_) * D;
+      *(u32x4*)(d + lane8 * E) = fp8_decode8(c0, e0);
+      if (a.nrot) Vec<E>::store(d + HALF + lane8 * E, x + E);
+      else *(u32x4*)(d + HALF + lane8 * E) = fp8_decode8(c1, e1);
+    }
     if (lane8 == 0) {
       const int64_t r = ((int64_t)b_ * a.Hkv + kh) * a.cap + p_;
       *(uint16_t*)(exps + 2 * r) = (uint16_t)((uint8_t)e0 | ((uint32_t)(uint8_t)e1 << 8));
@@ -179,7 +192,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       if (!in_cap) continue;
       const int kh = h - a.Hq - a.Hkv;
       if (kFp8) {
-        store_fp8(x, a.vc, a.vexp, b, kh, row);
+        store_fp8(x, a.vc, a.vexp, a.dv, b, kh, row);
         continue;
       }
       if (kI4) {
@@ -228,7 +241,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
       for (int e = 0; e < 2 * E; ++e) o[e] = (uint16_t)f32_to_bf16_bits(y[e]);
     }
     if (kFp8 && !is_q) {
-      store_fp8(o, a.kc, a.kexp, b, h - a.Hq, row);
+      store_fp8(o, a.kc, a.kexp, a.dk, b, h - a.Hq, row);
       continue;
     }
     if (kI4 && !is_q) {
@@ -248,7 +261,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreArgs a) {
 int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, const void* kw,
                              float eps, float theta, const int32_t* off, int B, int T, int Hq,
                              int Hkv, int D, uint32_t flags, void* q_out,
-                             const ema_kvcache_desc& c) {
+                             const ema_kvcache_desc& c, void* copy, int copy_rows) {
   PreArgs a;
   a.qkv = (const uint16_t*)qkv;
   a.qw = (const uint16_t*)qw;
@@ -276,6 +289,9 @@ int32_t launch_pre_attention(hipStream_t s, const void* qkv, const void* qw, con
   a.flags = flags;
   a.rot = (c.flags & EMA_KV_ROTATING) != 0;
   a.nrot = c.dtype == EMA_DTYPE_FP8_E4M3 && c.n_rot != 0;
+  a.dk = copy ? (uint16_t*)copy : nullptr;
+  a.dv = copy ? (uint16_t*)copy + (int64_t)B * Hkv * copy_rows * D : nullptr;
+  a.R = copy ? copy_rows : 0;
   const int threads = 256;
   const int64_t blocks = (int64_t)B * T;  // one workgroup per token
   if (blocks > 0x7fffffff) return set_error(EMA_ERR_SHAPE, "ema_pre_attention: too many tokens");

@@ -40,12 +40,13 @@ EMA_DECODE_COUNTER_BYTES = 131072
 EMA_KV_ROTATING = 1
 EMA_PREFILL_CAUSAL = 1
 EMA_PREFILL_CHUNK_ONLY = 2
+EMA_PREFILL_ROWS_DECODED = 4
 
 EXPORTED = (
     "ema_last_error", "ema_version", "ema_kvcache_init", "ema_kvcache_alloc", "ema_kvcache_free",
     "ema_kvcache_init_fp8", "ema_kvcache_alloc_fp8", "ema_kvcache_init_int4", "ema_kvcache_alloc_int4",
     "ema_kvcache_quantize_int4", "ema_kvcache_convert", "ema_position_write",
-    "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_decode_workspace_size",
+    "ema_kvcache_memory_bytes", "ema_pre_attention", "ema_pre_attention_ws", "ema_decode_workspace_size",
     "ema_decode_attention", "ema_decode_step", "ema_decode_step_noalloc", "ema_prefill_attention", "ema_prefill_workspace_size",
     "ema_prefill_attention_ws", "ema_gdn_scan", "ema_gdn_scan_workspace_size", "ema_gdn_scan_ws",
     "ema_quantized_matmul",
@@ -101,6 +102,8 @@ def lib() -> ctypes.CDLL:
             "ema_kvcache_free": (i32, [D]),
             "ema_kvcache_memory_bytes": (i32, [D, ctypes.POINTER(u64)]),
             "ema_pre_attention": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, i32, i32, i32, u32, vp, D]),
+            "ema_pre_attention_ws": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, i32, i32, i32, u32, vp, D, i32, vp,
+                                           u64]),
             "ema_decode_workspace_size": (i32, [i32, i32, i32, i32, i32, ctypes.POINTER(u64)]),
             "ema_decode_attention": (i32, [vp, vp, D, vp, i32, i32, f32, vp, vp, u64]),
             "ema_decode_step": (i32, [vp, vp, vp, vp, f32, f32, vp, i32, i32, u32, f32, D, vp, vp, u64]),
@@ -262,8 +265,12 @@ def position_write(slot, value: int, stream=None) -> None:
 
 
 def pre_attention(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: StaticCache, flags=0,
-                  q_out=None, stream=None):
-    """qkv [B,T,(Hq+2Hkv)*D] bf16; offsets int32 device [B]. Returns q_out [B,Hq,T,D]."""
+                  q_out=None, stream=None, prefill_workspace=None, max_kv_len=None):
+    """qkv [B,T,(Hq+2Hkv)*D] bf16; offsets int32 device [B]. Returns q_out [B,Hq,T,D].
+
+    With prefill_workspace (an FP8 cache: the workspace of prefill_attention for max_kv_len,
+    default the capacity), ema_pre_attention_ws also writes the stored rows, decoded, into
+    its bf16 copy; pass rows_decoded=True to prefill_attention with the same workspace."""
     import torch
 
     B, T, F = qkv.shape
@@ -271,6 +278,14 @@ def pre_attention(qkv, q_norm_w, k_norm_w, eps, theta, offsets, n_heads, cache: 
     Hkv = cache.desc.n_kv_heads
     if q_out is None:
         q_out = torch.empty((B, n_heads, T, D), dtype=torch.bfloat16, device=qkv.device)
+    if prefill_workspace is not None:
+        if max_kv_len is None:
+            max_kv_len = cache.capacity
+        _check(lib().ema_pre_attention_ws(_stream(stream), _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), eps, theta,
+                                          _ptr(offsets), B, T, n_heads, Hkv, D, flags, _ptr(q_out),
+                                          ctypes.byref(cache.desc), max_kv_len, _ptr(prefill_workspace),
+                                          prefill_workspace.numel()), "ema_pre_attention_ws")
+        return q_out
     _check(lib().ema_pre_attention(_stream(stream), _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), eps, theta,
                                    _ptr(offsets), B, T, n_heads, Hkv, D, flags, _ptr(q_out),
                                    ctypes.byref(cache.desc)), "ema_pre_attention")
@@ -352,11 +367,13 @@ def prefill_workspace_size(cache: StaticCache, max_kv_len: int) -> int:
 
 
 def prefill_attention(q, cache: StaticCache, q_offsets, scale=None, causal=True, chunk_only=False, out=None,
-                      stream=None, max_kv_len=None, workspace=None):
+                      stream=None, max_kv_len=None, workspace=None, rows_decoded=False):
     """q [B,Hq,T,D] bf16; q_offsets int32 device [B]. Returns out [B,T,Hq*D].
 
     An FP8 cache goes through ema_prefill_attention_ws: its attended rows (at most
-    max_kv_len per sequence, default the capacity) are decoded into a bf16 workspace."""
+    max_kv_len per sequence, default the capacity) are decoded into a bf16 workspace.
+    rows_decoded: the chunk's rows are in that workspace already (pre_attention with
+    prefill_workspace, EMA_PREFILL_ROWS_DECODED)."""
     import torch
 
     B, Hq, T, D = q.shape
@@ -365,6 +382,7 @@ def prefill_attention(q, cache: StaticCache, q_offsets, scale=None, causal=True,
     if out is None:
         out = torch.empty((B, T, Hq * D), dtype=torch.bfloat16, device=q.device)
     flags = (EMA_PREFILL_CAUSAL if causal else 0) | (EMA_PREFILL_CHUNK_ONLY if chunk_only else 0)
+    flags |= EMA_PREFILL_ROWS_DECODED if rows_decoded else 0
     if cache.dtype == "bf16" and workspace is None:
         _check(lib().ema_prefill_attention(_stream(stream), _ptr(q), ctypes.byref(cache.desc), _ptr(q_offsets), T,
                                            Hq, scale, flags, _ptr(out)), "ema_prefill_attention")

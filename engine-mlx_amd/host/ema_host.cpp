@@ -410,16 +410,26 @@ void attend(const Ctx& ctx, const void* qkv, int32_t T, const std::optional<Arra
   const float scale = 1.0f / std::sqrt((float)D);  // crates/attention/src/gqa.rs:73
   const int32_t* pos = cache.position(ctx, offset);
   if (T > 1) {  // is_prefill (gqa.rs:78): causal over the cache
-    check(ema_pre_attention(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, T, Hq, Hkv, D, flags,
-                            buf.q, &d),
-          "pre_attention");
-    if (d.dtype == EMA_DTYPE_BF16)
+    if (d.dtype == EMA_DTYPE_BF16) {
+      check(ema_pre_attention(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, T, Hq, Hkv, D,
+                              flags, buf.q, &d),
+            "pre_attention");
       check(ema_prefill_attention(ctx.stream, buf.q, &d, pos, T, Hq, scale, EMA_PREFILL_CAUSAL, buf.attn),
             "prefill_attention");
-    else
-      check(ema_prefill_attention_ws(ctx.stream, buf.q, &d, pos, T, Hq, scale, EMA_PREFILL_CAUSAL, buf.attn,
-                                     prefill_rows(d, offset, T), buf.pws, buf.pws_bytes),
+    } else {
+      // FP8: pre-attention also puts the chunk's decoded rows into the prefill's bf16 copy,
+      // so the prefill decodes only earlier rows (none for a static cache's first chunk,
+      // whose keys are the chunk's own)
+      const int32_t rows = prefill_rows(d, offset, T);
+      check(ema_pre_attention_ws(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, pos, 1, T, Hq, Hkv, D,
+                                 flags, buf.q, &d, rows, buf.pws, buf.pws_bytes),
+            "pre_attention_ws");
+      uint32_t pf = EMA_PREFILL_CAUSAL | EMA_PREFILL_ROWS_DECODED;
+      if (offset == 0 && !cache.rotating()) pf |= EMA_PREFILL_CHUNK_ONLY;
+      check(ema_prefill_attention_ws(ctx.stream, buf.q, &d, pos, T, Hq, scale, pf, buf.attn, rows, buf.pws,
+                                     buf.pws_bytes),
             "prefill_attention_ws");
+    }
   } else {  // the decode step writes the row at the offset and attends offset + 1 rows
     const int32_t max_len = offset + 1 < cap ? offset + 1 : cap;
     check(ema_decode_step(ctx.stream, qkv, qw, kw, config.norm_eps, config.rope_theta, const_cast<int32_t*>(pos),

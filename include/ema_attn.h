@@ -135,6 +135,12 @@ extern "C" {
                                      the freshly projected k/v; without this flag the
                                      whole cache [0, q_off+T) is attended, as
                                      gqa_attention does (crates/attention/src/gqa.rs:100-106) */
+#define EMA_PREFILL_ROWS_DECODED 4u /* FP8 cache, ema_prefill_attention_ws: the workspace's
+                                     bf16 copy already holds the chunk's rows
+                                     [q_off, q_off+T), written by ema_pre_attention_ws with
+                                     the same max_kv_len; only the other attended rows are
+                                     decoded (none with EMA_PREFILL_CHUNK_ONLY over a static
+                                     cache, and then no decode pass runs) */
 
 typedef void* ema_stream_t; /* hipStream_t */
 
@@ -255,6 +261,19 @@ EMA_API int32_t ema_pre_attention(ema_stream_t stream, const void* qkv, const vo
                           int32_t batch, int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads,
                           int32_t head_dim, uint32_t flags, void* q_out,
                           const ema_kvcache_desc* cache);
+/* ema_pre_attention over an FP8 cache that also writes each stored K and V row, decoded to
+ * bf16 (code * 2^exp, exact), into the bf16 copy of the ema_prefill_attention_ws workspace
+ * for the same max_kv_len (ema_prefill_workspace_size): row p of the copy for cache row p
+ * (static caches: rows below max_kv_len). An ema_prefill_attention_ws call with
+ * EMA_PREFILL_ROWS_DECODED then decodes only the other rows it attends, none with
+ * EMA_PREFILL_CHUNK_ONLY over a static cache (a fresh prefill: the reference appends the
+ * chunk and attends its round-tripped rows, crates/kvcache/src/fp8.rs:47-68). No
+ * counterpart call in the reference; EMA_ERR_UNSUPPORTED for other caches. */
+EMA_API int32_t ema_pre_attention_ws(ema_stream_t stream, const void* qkv, const void* q_norm_w,
+                                     const void* k_norm_w, float eps, float theta, const int32_t* offsets,
+                                     int32_t batch, int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads,
+                                     int32_t head_dim, uint32_t flags, void* q_out, const ema_kvcache_desc* cache,
+                                     int32_t max_kv_len, void* workspace, uint64_t workspace_bytes);
 
 /* Bytes at the start of every decode workspace that hold the split's arrival counters
  * (one per (sequence, kv head) segment, and one for the grid). They must be zero before a

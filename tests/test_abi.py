@@ -260,6 +260,34 @@ def test_fp8_prefill_is_unsupported(ema):
     assert rc == ema.EMA_ERR_UNSUPPORTED and "fp8" in ema.last_error()
 
 
+def test_pre_attention_ws_and_rows_decoded_flag(ema):
+    """ema_pre_attention_ws takes FP8 caches only and the prefill workspace of its max_kv_len;
+    EMA_PREFILL_ROWS_DECODED is an ema_prefill_attention_ws flag for FP8 caches."""
+    L = ema.lib()
+    g = 0x40000
+    d8 = ema.KvCacheDesc()
+    assert L.ema_kvcache_init_fp8(ctypes.byref(d8), 0x10000, 0x20000, 0x30000, 0x40000, 2, 8, 64, 128, 0) == 0
+    n = ctypes.c_uint64()
+    assert L.ema_prefill_workspace_size(ctypes.byref(d8), 64, ctypes.byref(n)) == 0
+    args = (None, g, g, g, 1e-6, 1e6, g, 2, 8, 16, 8, 128, 0, g)
+    # a bf16 cache has no prefill copy
+    _, d16 = _desc(ema)
+    rc = L.ema_pre_attention_ws(*args, ctypes.byref(d16), 64, g, 1 << 30)
+    assert rc == ema.EMA_ERR_UNSUPPORTED and "FP8" in ema.last_error()
+    # the workspace of the same max_kv_len, no smaller
+    rc = L.ema_pre_attention_ws(*args, ctypes.byref(d8), 64, g, n.value - 16)
+    assert rc == ema.EMA_ERR_WORKSPACE and "workspace" in ema.last_error()
+    # max_kv_len below the chunk
+    rc = L.ema_pre_attention_ws(*args, ctypes.byref(d8), 4, g, n.value)
+    assert rc == ema.EMA_ERR_CAPACITY
+    # the flag: FP8 caches through the workspace entry only
+    rows = ema.EMA_PREFILL_ROWS_DECODED
+    rc = L.ema_prefill_attention_ws(None, g, ctypes.byref(d16), g, 8, 16, 0.088, 1 | rows, g, 64, g, 1 << 30)
+    assert rc == ema.EMA_ERR_INVALID_ARG and "ROWS_DECODED" in ema.last_error()
+    rc = L.ema_prefill_attention(None, g, ctypes.byref(d16), g, 8, 16, 0.088, 1 | rows, g)
+    assert rc == ema.EMA_ERR_INVALID_ARG and "flags" in ema.last_error()
+
+
 def test_unknown_dtype_is_rejected(ema):
     rc, d = _desc(ema)
     d.dtype = 7

@@ -422,3 +422,51 @@ def test_position_write_is_stream_ordered(ema):
         t[0] = t[2]  # a later op on the same stream reads the written value
     torch.cuda.synchronize()
     assert t.cpu().tolist() == [123456, -1, 123456, -1]
+
+
+@pytest.mark.parametrize("rotating,n_rot,first,T,chunk", [
+    (False, 0, 0, 300, False),    # a fresh prefill: the chunk's rows are all it attends
+    (False, 0, 0, 300, True),     # ... with chunk-only keys: no decode pass runs
+    (False, 0, 200, 300, False),  # a second chunk: rows [0, 200) decoded by the pass
+    (False, 0, 200, 300, True),
+    (False, 64, 200, 300, False),  # the RoPE tail kept as bf16
+    (True, 0, 200, 300, False),   # a ring of 384 rows that the second chunk wraps
+    (True, 0, 200, 300, True),
+])
+def test_fp8_prefill_with_rows_from_pre_attention(ema, ora, rotating, n_rot, first, T, chunk):
+    """ema_pre_attention_ws writes the chunk's rows, decoded, into the prefill workspace, and
+    ema_prefill_attention_ws with EMA_PREFILL_ROWS_DECODED then decodes only the other
+    rows: q, the cache and the output are bit-identical to ema_pre_attention followed by
+    the plain FP8 prefill. The workspace starts as NaN, so a row neither writes would show."""
+    import torch
+
+    B, Hq, Hkv, D = 2, 8, 2, 128
+    cap = 384 if rotating else 1024
+    say(f"fp8 prefill rows from pre-attention rot={rotating} n_rot={n_rot} first={first} T={T} chunk={chunk}")
+    qw = ora.normal_bf16(D, seed=901, mean=1.0, std=0.02)
+    kw = ora.normal_bf16(D, seed=902, mean=1.0, std=0.02)
+    F = (Hq + 2 * Hkv) * D
+    c_a = ema.StaticCache(B, Hkv, cap, D, dtype="fp8", rotating=rotating, n_rot=n_rot)
+    c_b = ema.StaticCache(B, Hkv, cap, D, dtype="fp8", rotating=rotating, n_rot=n_rot)
+    if first:  # earlier tokens, written the same way into both caches
+        qkv0 = dev(ora.normal_bf16((B, first, F), seed=903))
+        off0 = dev(np.zeros(B, np.int32))
+        for c in (c_a, c_b):
+            ema.pre_attention(qkv0, dev(qw), dev(kw), 1e-6, 1e6, off0, Hq, c)
+    qkv = dev(ora.normal_bf16((B, T, F), seed=904))
+    off = dev(np.full(B, first, np.int32))
+    mk = cap if rotating else first + T
+    n = ema.prefill_workspace_size(c_a, mk)
+    ws_a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    ws_b = torch.full((n // 2,), 0x7FC0, dtype=torch.int16, device="cuda").view(torch.uint8)  # bf16 NaN
+    q_a = ema.pre_attention(qkv, dev(qw), dev(kw), 1e-6, 1e6, off, Hq, c_a)
+    o_a = ema.prefill_attention(q_a, c_a, off, chunk_only=chunk, max_kv_len=mk, workspace=ws_a)
+    q_b = ema.pre_attention(qkv, dev(qw), dev(kw), 1e-6, 1e6, off, Hq, c_b, prefill_workspace=ws_b, max_kv_len=mk)
+    o_b = ema.prefill_attention(q_b, c_b, off, chunk_only=chunk, max_kv_len=mk, workspace=ws_b, rows_decoded=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q_a), host(q_b))
+    for t_a, t_b in ((c_a.k, c_b.k), (c_a.v, c_b.v), (c_a.k_exp, c_b.k_exp), (c_a.v_exp, c_b.v_exp)):
+        assert torch.equal(t_a, t_b)
+    got = host(o_b)
+    assert np.all(np.isfinite(ora.f32_from_bf16(got))), "a row of the copy was never written"
+    assert np.array_equal(host(o_a), got), "rows from pre-attention == rows from the decode pass"
