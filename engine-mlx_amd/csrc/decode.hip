@@ -1336,16 +1336,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // which reads the offsets, has finished, and no thread here reads them (segment sizes come
 // from the tile prefix).
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (a.adv && e < a.B) {
+  // 32-bit index arithmetic (per-lane 64-bit divisions are long emulations): the grid is
+  // segments * G * kD < 2^31 threads (at most 32767 segments, G <= 16)
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a.adv && e < (uint32_t)a.B) {
     const int o = a.adv[e];
     if (o >= 0 && o < INT32_MAX && (a.rot || o < a.cap)) a.adv[e] = o + 1;
   }
-  const int per_seg = a.G * kD;
-  const int64_t s = e / per_seg;
-  if (s >= (int64_t)a.B * a.Hkv) return;
-  const int gg = (int)(e % per_seg) / kD, d = (int)(e % kD);
-  const int b = (int)(s / a.Hkv), kh = (int)(s % a.Hkv);
+  const uint32_t per_seg = (uint32_t)a.G * kD;
+  const uint32_t s = e / per_seg;
+  if (s >= (uint32_t)(a.B * a.Hkv)) return;
+  const uint32_t r = e - s * per_seg;
+  const int gg = (int)(r / kD), d = (int)(r % kD);
+  const int b = (int)(s / (uint32_t)a.Hkv), kh = (int)(s - (uint32_t)b * a.Hkv);
   const int64_t total = a.hdr[a.B];  // tile prefix published by decode_kernel
   const int nb = (a.hdr[b + 1] - a.hdr[b]) / a.Hkv;  // tiles per kv head of sequence b
   if (nb == 0 || total == 0) return;
