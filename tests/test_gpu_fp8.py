@@ -283,6 +283,28 @@ def test_fp8_decode_shapes(ema, ora, B, G, L, max_len):
     assert_close(host(out), ora.sdpa(q, kd, vd, L, scale_of(D), False), "fp8 decode shapes")
 
 
+@pytest.mark.parametrize("B,cap", [(64, 96), (65, 96), (130, 203)])
+def test_fp8_decode_batch_sizes_around_64(ema, ora, B, cap):
+    """Both sides of the 64-sequence edge between the per-wave length table and the
+    workgroup's, with empty sequences, over whole-8-row exponent groups (96) and row by
+    row (203)."""
+    import torch
+
+    Hkv, G, D = 2, 4, 128
+    Hq = G * Hkv
+    rng = np.random.default_rng(780 + B)
+    L = rng.integers(1, cap + 1, size=B).astype(np.int32)
+    L[::9] = 0
+    L[1] = cap
+    say(f"fp8 decode B={B} cap={cap} sum(L)={int(L.sum())}")
+    (kc, ke, kd), (vc, ve, vd) = quantized_pair(ora, (B, Hkv, cap, D), seed=780 + B)
+    q = ora.normal_bf16((B, Hq, 1, D), seed=783)
+    out = host(ema.decode_attention(dev(q), fp8_cache(ema, kc, ke, vc, ve), dev(L), cap))
+    torch.cuda.synchronize()
+    assert_close(out, ora.sdpa(q, kd, vd, L, scale_of(D), False), f"fp8 decode B={B}")
+    assert not out[::9].any()
+
+
 def test_fp8_graph_replay_matches_eager(ema, ora):
     """The fused fp8 step captured in a HIP graph: every replay, with eager work and
     synchronisation in between, equals the eager result (and rewrites the same row)."""

@@ -312,6 +312,24 @@ def test_decode_qwen3_30b_long_context_shape(ema, ora):
     assert_close(got, ref, "decode 30B long context")
 
 
+@pytest.mark.parametrize("B,cap,bound", [(63, 160, None), (64, 160, None), (65, 160, None), (64, 2048, 2048),
+                                         (200, 160, None), (100, 2048, 2048), (1024, 64, None)])
+def test_decode_batch_sizes_around_64(ema, ora, B, cap, bound):
+    """Up to 64 sequences each wave holds the lengths and tile prefix in its own lanes;
+    larger batches scan them into the workgroup's table (at most 1024 rows). Both sides of
+    that edge, ragged lengths with empty sequences among them, small grids (the merge inside
+    the decode kernel) and full ones (the merge kernel)."""
+    Hq, Hkv, D = 8, 2, 128
+    rng = np.random.default_rng(270 + B + cap)
+    L = rng.integers(1, cap + 1, size=B).astype(np.int32)
+    L[::9] = 0
+    L[1] = cap
+    say(f"decode B={B} cap={cap} bound={bound} sum(L)={int(L.sum())}")
+    got, ref = _decode_case(ema, ora, B, Hq, Hkv, D, cap, L, seed=270 + B, poison=True, max_len=bound)
+    assert_close(got, ref, f"decode B={B}")
+    assert not got[::9].any(), "empty sequences give zeros"
+
+
 # ----------------------------------------------------------------- prefill
 def _prefill_case(ema, ora, B, Hq, Hkv, D, cap, T, q_off, causal, chunk_only, seed, heads=None):
     import torch
@@ -581,6 +599,18 @@ def test_decode_step_fused_small(ema, ora, flags):
     assert np.array_equal(vg, vr), "V rows: bit copy at the offset, untouched elsewhere"
     assert_close(kg, kr, "fused k cache")
     assert_close(got, ref, "fused decode step")
+
+
+def test_decode_step_fused_batch_above_64(ema, ora):
+    """80 sequences (the workgroup-wide length table), offsets from 0 to past the capacity."""
+    B, Hq, Hkv, D, cap = 80, 8, 2, 128, 96
+    off = np.random.default_rng(630).integers(0, cap, size=B).astype(np.int32)
+    off[:4] = [0, cap - 1, cap, cap + 7]
+    say(f"fused decode step B={B} cap={cap}")
+    got, ref, kg, vg, kr, vr, _ = _fused_case(ema, ora, B, Hq, Hkv, D, cap, off, seed=630)
+    assert np.array_equal(vg, vr)
+    assert_close(kg, kr, "fused k cache, B 80")
+    assert_close(got, ref, "fused decode step, B 80")
 
 
 def test_decode_step_fused_out_of_capacity(ema, ora):
