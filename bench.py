@@ -45,7 +45,8 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "primary", "prefill", "decode_long", "decode_b1", "prefill_chunk", "fp8",
-                                      "fp8_tail", "int4", "gdn", "gdn_step", "qmm", "prefill_1p7b", "pre"],
+                                      "fp8_tail", "fp8_prefill", "int4", "gdn", "gdn_step", "qmm", "prefill_1p7b",
+                                      "pre"],
                    default="all")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -654,6 +655,7 @@ def main():
         secondary.append(bench_fp8_step(ctx, ema, "decode_step_B32_32q8kv_fp8_cache"))
         secondary.append(bench_fp8_decode(ctx, ema, "decode_B8_32q4kv_L32768_fp8_cache", 8, 32, 4, 128, 32768,
                                           [32768] * 8))
+    if args.only in ("all", "fp8", "fp8_prefill"):
         secondary.append(bench_fp8_prefill(ctx, ema, "prefill_causal_T2048_32q8kv_fp8_cache", 1, 32, 8, 128, 4096,
                                            2048, 0))
         # the chunk's rows decoded by pre-attention: the prefill call runs no decode pass
