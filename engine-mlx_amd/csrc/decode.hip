@@ -376,18 +376,19 @@ __device__ __forceinline__ void unpack32(const u32x4 (&r)[4], float (&x)[32]) {
 
 // Log-sum-exp merge of segment s = (b, kh), whose pieces are the partial states of
 // workers w0..w1, one thread per (head, dim). Every piece's (m, l, o[dim]) is loaded
-// independently, so a thread's loads are in flight together (one memory round trip per 8
-// pieces).
+// independently, so a thread's loads are in flight together: one memory round trip per
+// kChunk pieces (the merge kernel takes 16 for segments of more than 8 pieces, as a
+// 32k-row segment has, and 8 otherwise, whose loads past the last piece would be wasted).
 // kCoherent: the partial states come from workgroups of the same launch (device-coherent
 // loads); else from a finished launch (plain loads).
-template <bool kCoherent>
+template <bool kCoherent, int kChunk = 8>
 __device__ __forceinline__ void merge_element(const DecodeArgs& a, int b, int kh, int64_t s, int64_t w0, int64_t w1,
                                               int gg, int d) {
     float M = -INFINITY, Lsum = 0.f, acc = 0.f;
-    for (int64_t c0 = w0; c0 <= w1; c0 += 8) {
-      float m[8], l[8], v[8];
+    for (int64_t c0 = w0; c0 <= w1; c0 += kChunk) {
+      float m[kChunk], l[kChunk], v[kChunk];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kChunk; ++i) {
         const int64_t w = c0 + i <= w1 ? c0 + i : w1;  // clamped: duplicates get weight 0 below
         const float* P = a.part + ((w + s) * a.G + gg) * kPieceStride;
         m[i] = kCoherent ? part_load(P) : P[0];
@@ -396,13 +397,13 @@ __device__ __forceinline__ void merge_element(const DecodeArgs& a, int b, int kh
       }
       float Mc = M;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < kChunk; ++i)
         if (c0 + i <= w1) Mc = fmaxf(Mc, m[i]);
       const float r = __builtin_amdgcn_exp2f(M - Mc);
       Lsum *= r;
       acc *= r;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < kChunk; ++i)
         if (c0 + i <= w1) {
           const float sc = __builtin_amdgcn_exp2f(m[i] - Mc);
           Lsum += sc * l[i];
@@ -1357,7 +1358,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int64_t w0 = worker_of(a, seg_first, total, W);
   const int64_t w1 = worker_of(a, seg_first + nb - 1, total, W);
   if (w0 == w1) return;  // written directly by decode_kernel
-  merge_element<false>(a, b, kh, s, w0, w1, gg, d);
+  // (uniform across a workgroup when a segment has at least 256 threads, G >= 2)
+  if (w1 - w0 >= 8) merge_element<false, 16>(a, b, kh, s, w0, w1, gg, d);
+  else merge_element<false, 8>(a, b, kh, s, w0, w1, gg, d);
 }
 
 }  // namespace

@@ -312,6 +312,16 @@ def test_decode_qwen3_30b_long_context_shape(ema, ora):
     assert_close(got, ref, "decode 30B long context")
 
 
+def test_decode_merge_of_many_pieces(ema, ora):
+    """Two long sequences over a full grid: each (sequence, kv head) segment is cut into
+    about 100-160 pieces, which the merge kernel folds 16 at a time (and a remainder)."""
+    B, Hq, Hkv, D, cap = 2, 8, 2, 128, 32768
+    L = [32768, 20001]
+    say(f"decode merge of many pieces L={L}")
+    got, ref = _decode_case(ema, ora, B, Hq, Hkv, D, cap, L, seed=265, max_len=cap)
+    assert_close(got, ref, "decode, many pieces")
+
+
 @pytest.mark.parametrize("B,cap,bound", [(63, 160, None), (64, 160, None), (65, 160, None), (64, 2048, 2048),
                                          (200, 160, None), (100, 2048, 2048), (1024, 64, None)])
 def test_decode_batch_sizes_around_64(ema, ora, B, cap, bound):
