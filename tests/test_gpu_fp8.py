@@ -136,6 +136,7 @@ def test_fp8_write_after_norm_rope(ema, ora, flags):
     (8, [4096, 17, 2500], 4096),
     (1, [64, 65, 3], 96),
     (2, [203, 1, 150, 97], 203),  # capacity not a multiple of 8: exponents loaded row by row
+    (5, [256, 77, 1, 200], 256),  # 5 query heads per kv head (Qwen3-14B)
 ])
 def test_fp8_decode_equals_bf16_decode_of_decoded_cache(ema, ora, G, lengths, cap):
     import torch

@@ -172,6 +172,7 @@ def test_int4_converter(ema, ora, src_row, dst_row, n):
     (8, [4096, 17, 2500], 4096),
     (1, [64, 65, 3, 0], 96),
     (16, [300, 1], 320),
+    (5, [320, 33, 1, 250], 320),  # 5 query heads per kv head (Qwen3-14B)
     (2, [0, 96] + [int(x) for x in np.random.default_rng(820).integers(0, 97, size=68)], 96),  # B 70
 ])
 def test_int4_decode(ema, ora, G, lengths, cap):

@@ -164,7 +164,7 @@ def _decode_case(ema, ora, B, Hq, Hkv, D, cap, lengths, seed, outliers=False, po
     return host(out), ref
 
 
-@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 6, 8, 12, 16])
 def test_decode_small(ema, ora, G):
     B, Hkv, D, cap = 6, 2, 128, 160
     lengths = [1, 31, 32, 33, 100, 160]
@@ -370,7 +370,7 @@ def _prefill_case(ema, ora, B, Hq, Hkv, D, cap, T, q_off, causal, chunk_only, se
     (200, 0, True, False), (200, 37, True, False), (77, 100, True, True), (130, 50, False, False),
     (300, 0, False, True),
 ])
-@pytest.mark.parametrize("G", [1, 2, 8])
+@pytest.mark.parametrize("G", [1, 2, 5, 8])
 def test_prefill_small(ema, ora, T, q_off, causal, chunk, G):
     B, Hkv, D, cap = 2, 2, 128, 512
     say(f"prefill small T={T} q_off={q_off} causal={causal} chunk={chunk} G={G}")
@@ -621,6 +621,27 @@ def test_decode_step_fused_batch_above_64(ema, ora):
     assert np.array_equal(vg, vr)
     assert_close(kg, kr, "fused k cache, B 80")
     assert_close(got, ref, "fused decode step, B 80")
+
+
+def test_decode_step_fused_qwen3_14b_heads(ema, ora):
+    """40 query / 8 kv heads (G = 5, Qwen3-14B): the zero-padded query columns of the QK
+    operand, the fused norm/RoPE of five heads per kv head, ragged offsets."""
+    B, Hq, Hkv, D, cap = 4, 40, 8, 128, 384
+    off = [0, 131, 383, 257]
+    say(f"fused decode step 40q/8kv offsets={off}")
+    got, ref, kg, vg, kr, vr, _ = _fused_case(ema, ora, B, Hq, Hkv, D, cap, off, seed=640)
+    assert np.array_equal(vg, vr)
+    assert_close(kg, kr, "fused k cache, 40q/8kv")
+    assert_close(got, ref, "fused decode step, 40q/8kv")
+
+
+def test_prefill_qwen3_14b_heads_paired(ema, ora):
+    """40 query / 8 kv heads (G = 5) over 2048 tokens: 640 query-block items, so the launch
+    pairs blocks; heads of the first and the last kv group, every row."""
+    say("prefill T=2048 40q/8kv causal (paired), heads 0-4 and 35-39")
+    got, ref = _prefill_case(ema, ora, 1, 40, 8, 128, 2048, 2048, [0], True, False, seed=320,
+                             heads=list(range(5)) + list(range(35, 40)))
+    assert_close(got, ref, "prefill 2k 40q")
 
 
 def test_decode_step_fused_out_of_capacity(ema, ora):

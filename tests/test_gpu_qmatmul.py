@@ -106,6 +106,17 @@ def test_qmatmul_qwen3_8b_qkv_decode_shape(ema, ora, M, N, bits):
     check(ora, y, h, gs, bits, "8B qkv", bar=True)
 
 
+@pytest.mark.parametrize("M,N,bits", [(1, 7168, 4), (32, 7168, 4), (32, 5120, 4), (1, 5120, 8), (32, 7168, 8)])
+def test_qmatmul_qwen3_14b_decode_shape(ema, ora, M, N, bits):
+    # Qwen3-14B: hidden 5120, 40 query / 8 kv heads of 128, so x [M, 5120] -> q|k|v
+    # [M, 7168] or o_proj [M, 5120], group 64 (K / 64 = 80 groups per row)
+    K, gs = 5120, 64
+    say(f"qmatmul Qwen3-14B decode shape M={M} N={N} K={K} bits={bits}")
+    d, h = make(ora, 2, M, N, K, gs, bits)
+    y = ema.quantized_matmul(*d, group_size=gs, bits=bits)
+    check(ora, y, h, gs, bits, "14B qkv", bar=True)
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_qmatmul_one_row_8bit_group_128_many_rows(ema, ora, dtype):
     # one row of x over 6144 weight rows at 8 bits, group 128: enough rows that the one-row
