@@ -291,7 +291,9 @@ EMA_API int32_t ema_decode_workspace_size(int32_t batch, int32_t n_heads, int32_
  *   q        [batch, n_heads, head_dim] bf16 (post norm/RoPE)
  *   lengths  device int32 [batch]: valid positions (offset + 1 after the write);
  *            clamped to [0, capacity]; a sequence with 0 valid positions yields zeros
- *   max_len  host upper bound of lengths (sizes the split; <= capacity)
+ *   max_len  host upper bound of lengths (sizes the split; <= capacity). A bound below
+ *            the true lengths still gives the exact result: the kernels take the split
+ *            from the actual tile count, over the fewer workers the bound planned.
  *   out      [batch, n_heads * head_dim] bf16 (the o_proj input layout)
  * GQA: q head h reads kv head h / (n_heads / n_kv_heads).
  * FP8 cache: K/V rows are decoded exactly to bf16 (code value times 2^exp) and attended

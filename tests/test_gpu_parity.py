@@ -199,6 +199,18 @@ def test_decode_split_invariance(ema, ora, max_len):
     assert_close(got, ref, f"decode max_len={max_len}")
 
 
+@pytest.mark.parametrize("max_len", [1, 100])
+def test_decode_max_len_below_the_lengths(ema, ora, max_len):
+    """A host bound below the true lengths sizes the grid and workspace for fewer tiles; the
+    kernels take the split from the actual tile count (at most the planned workers, each
+    with a longer slice), so the result is still exact."""
+    B, Hq, Hkv, D, cap = 2, 8, 2, 128, 4096
+    lengths = [4000, 3001]
+    say(f"decode with max_len {max_len} below lengths {lengths}")
+    got, ref = _decode_case(ema, ora, B, Hq, Hkv, D, cap, lengths, seed=232, max_len=max_len)
+    assert_close(got, ref, f"decode, max_len {max_len}")
+
+
 def test_decode_workspace_reuse_is_clean(ema, ora):
     """Reusing one workspace across calls with different lengths (stale partial
     slots from earlier calls) gives the same bits as fresh workspaces."""
