@@ -199,6 +199,23 @@ def test_decode_split_invariance(ema, ora, max_len):
     assert_close(got, ref, f"decode max_len={max_len}")
 
 
+def test_decode_lengths_are_clamped_to_the_cache(ema, ora):
+    """Lengths past the capacity attend the whole cache; negative ones give zeros."""
+    import torch
+
+    B, Hq, Hkv, D, cap = 4, 8, 2, 128, 256
+    q = ora.normal_bf16((B, Hq, 1, D), seed=233)
+    kc = ora.normal_bf16((B, Hkv, cap, D), seed=234)
+    vc = ora.normal_bf16((B, Hkv, cap, D), seed=235)
+    given = np.array([cap + 100, -5, cap, 37], np.int32)
+    clamped = np.clip(given, 0, cap).astype(np.int32)
+    say(f"decode lengths {given.tolist()} over capacity {cap}")
+    got = host(ema.decode_attention(dev(q), make_cache(ema, kc, vc), dev(given), cap))
+    torch.cuda.synchronize()
+    assert_close(got, ora.sdpa(q, kc, vc, clamped, scale_of(D), False), "clamped lengths")
+    assert not got[1].any()
+
+
 @pytest.mark.parametrize("max_len", [1, 100])
 def test_decode_max_len_below_the_lengths(ema, ora, max_len):
     """A host bound below the true lengths sizes the grid and workspace for fewer tiles; the
