@@ -9,6 +9,11 @@ its wait would read a register still being loaded, and spill traffic would break
 counts. Scratch use by any other kernel is printed as a warning (it costs time, not
 correctness).
 
+Also fails when a kernel declares more than 80 KiB of static LDS (half of gfx950's 160 KiB):
+a decode variant whose int4 kernel declared 81 952 bytes gave wrong results, while the
+same code at 78 880 bytes was correct. Kernels that need more take it as dynamic LDS,
+with the launch attribute set (the prefill kernel).
+
 usage: check_resources.py <remarks file>
 """
 import re
@@ -24,10 +29,14 @@ def parse(text):
             name = m.group(1)
             kernels[name] = {}
             continue
-        m = re.search(r"remark:\s+(ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill): (\d+)", line)
+        m = re.search(r"remark:\s+(ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill|LDS Size \[bytes/block\]): (\d+)",
+                      line)
         if m and name:
             kernels[name][m.group(1)] = int(m.group(2))
     return kernels
+
+
+MAX_STATIC_LDS = 81920
 
 
 def main():
@@ -36,6 +45,10 @@ def main():
     strict = ("qgemm_dq_kernel",)
     failed = False
     for k, r in kernels.items():
+        if r.get("LDS Size [bytes/block]", 0) > MAX_STATIC_LDS:
+            print(f"{path}: error: kernel {k} declares {r['LDS Size [bytes/block]']} bytes of static LDS, more than "
+                  f"{MAX_STATIC_LDS}", file=sys.stderr)
+            failed = True
         if not (r.get("ScratchSize [bytes/lane]", 0) or r.get("VGPRs Spill", 0)):
             continue
         if any(s in k for s in strict):
