@@ -179,12 +179,16 @@ __device__ __forceinline__ uint32_t fp8_quant_lane(float x, int* e_out, uint16_t
 //     P'_grp[p, g]) with P'_grp = bf16(P s_grp) as the B operand.
 // Both use the exact affine values s * code + b (no bf16 rounding of K and V).
 //
-// (x & m) | c in one v_and_or_b32 (gfx950's VOP3 takes no literal; the constants stay in
-// VGPRs as asm operands).
+// (x & m) | c in one v_and_or_b32. gfx950's VOP3 takes no literal, so the empty asm
+// statements hand the constants over as VGPR values (set once per kernel) and the
+// compiler selects the fused instruction. The instruction itself is left to the compiler:
+// its result feeds MFMA operands, and the hazard recognizer inserts the wait states a VALU
+// write needs before an MFMA reads it only for instructions it emits itself, not for an
+// inline-asm VALU instruction.
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
-  return r;
+  asm("" : "+v"(m));
+  asm("" : "+v"(c));
+  return (x & m) | c;
 }
 // The 8 codes of a word (value i at bits 4i) as the bf16 A-operand registers of one MFMA
 // step, k-slot order (0, 4), (1, 5), (2, 6), (3, 7).

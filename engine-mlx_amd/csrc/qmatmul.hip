@@ -96,12 +96,16 @@ __device__ __forceinline__ uint32_t pair(uint32_t lo, uint32_t hi, uint32_t sel)
 }
 
 // (x & m) | c in one v_and_or_b32. gfx950's VOP3 encoding takes no 32-bit literal, so with
-// literal masks the compiler splits it into v_and + v_or; as operands of the asm the
-// constants are kept in VGPRs, set once per kernel.
+// literal masks the compiler splits it into v_and + v_or; the empty asm statements hand the
+// constants over as VGPR values (set once per kernel) and the compiler selects the fused
+// instruction. The instruction itself is left to the compiler: its result feeds MFMA
+// operands, and the hazard recognizer inserts the wait states a VALU write needs before an
+// MFMA reads it only for instructions it emits itself, not for an inline-asm VALU
+// instruction.
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
-  return r;
+  asm("" : "+v"(m));
+  asm("" : "+v"(c));
+  return (x & m) | c;
 }
 
 template <int BITS, bool F16>
