@@ -189,6 +189,33 @@ def test_decode_zero_length_gives_zeros(ema, ora):
     assert np.all(got[0] == 0) and np.all(got[2] == 0) and np.any(got[1] != 0)
 
 
+@pytest.mark.parametrize("B,Hkv,G,L,cap", [(1, 8, 2, 1024, 4096), (1, 8, 2, 1, 64), (1, 1, 16, 4096, 4096),
+                                            (2, 2, 4, 33, 64), (7, 2, 8, 100, 128), (64, 1, 4, 32, 32),
+                                            (3, 8, 1, 777, 1024)])
+def test_decode_lengths_at_the_bound(ema, ora, B, Hkv, G, L, cap):
+    """Every length equal to the host's bound (the split the plan sized is the one the
+    kernels take), over small grids of one to 64 sequences. Rows past the lengths poisoned
+    with NaN leave the result bit-identical."""
+    lengths = [L] * B
+    say(f"decode at the bound B={B} {Hkv * G}q/{Hkv}kv L={L} cap={cap}")
+    clean, ref = _decode_case(ema, ora, B, Hkv * G, Hkv, 128, cap, lengths, seed=280 + B + L)
+    dirty, _ = _decode_case(ema, ora, B, Hkv * G, Hkv, 128, cap, lengths, seed=280 + B + L, poison=True)
+    assert np.array_equal(clean, dirty)
+    assert_close(clean, ref, f"decode at the bound B={B} L={L}")
+
+
+@pytest.mark.parametrize("bound", [40, 1024])
+def test_decode_equal_lengths_below_the_bound(ema, ora, bound):
+    """Equal lengths below the host's bound: the kernels take the split from the actual tile
+    count, not from the bound (NaN tails stay masked)."""
+    B, Hkv, G, L, cap = 2, 8, 2, 33, 1024
+    say(f"decode, lengths {L} under the bound {bound}")
+    clean, ref = _decode_case(ema, ora, B, Hkv * G, Hkv, 128, cap, [L] * B, seed=290, max_len=bound)
+    dirty, _ = _decode_case(ema, ora, B, Hkv * G, Hkv, 128, cap, [L] * B, seed=290, poison=True, max_len=bound)
+    assert np.array_equal(clean, dirty)
+    assert_close(clean, ref, f"decode, lengths under the bound {bound}")
+
+
 @pytest.mark.parametrize("max_len", [33, 100, 1000, 4096])
 def test_decode_split_invariance(ema, ora, max_len):
     """Different max_len hints change the worker split; results stay within tolerance."""
