@@ -6,8 +6,10 @@ VGPRs: the dequantising GEMM in qmatmul.hip (qgemm_dq_kernel) issues its global 
 inline asm whose register outputs the compiler treats as ready at once, and waits for them
 with fixed vmcnt counts; a spill or a copy of one of those registers between the load and
 its wait would read a register still being loaded, and spill traffic would break the
-counts. Scratch use by any other kernel is printed as a warning (it costs time, not
-correctness).
+counts. SGPR spills fail it too: a spilled SGPR comes back by v_readlane, a VALU write,
+and an asm load reading it fewer than five wait states later (a wait the compiler inserts
+only for the loads it emits itself) could read the old value. Scratch use by any other
+kernel is printed as a warning (it costs time, not correctness).
 
 Also fails when a kernel declares more than 80 KiB of static LDS (half of gfx950's 160 KiB):
 a decode variant whose int4 kernel declared 81 952 bytes gave wrong results, while the
@@ -48,6 +50,10 @@ def main():
         if r.get("LDS Size [bytes/block]", 0) > MAX_STATIC_LDS:
             print(f"{path}: error: kernel {k} declares {r['LDS Size [bytes/block]']} bytes of static LDS, more than "
                   f"{MAX_STATIC_LDS}", file=sys.stderr)
+            failed = True
+        if any(s in k for s in strict) and r.get("SGPRs Spill", 0):
+            print(f"{path}: error: kernel {k} spills SGPRs ({r}); its inline-asm loads read SGPRs that a "
+                  "spill reload would write just before them", file=sys.stderr)
             failed = True
         if not (r.get("ScratchSize [bytes/lane]", 0) or r.get("VGPRs Spill", 0)):
             continue
