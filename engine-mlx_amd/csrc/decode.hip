@@ -253,10 +253,10 @@ __device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
 // (buffer_load_dwordx4 ... lds, non-temporal; the LDS base goes through M0). Issued as asm,
 // untracked by the compiler: the int4 tile loop orders it with explicit vmcnt waits.
 __device__ __forceinline__ void dma16(u32x4 rs, uint32_t voff, uint32_t soff, uint32_t lds) {
-  // s_nop 3: the DMA reads M0 no earlier than one wait state after the SALU write, and an
-  // SGPR operand no earlier than five after a VALU write (a readfirstlane, or the v_readlane
-  // that reloads a spilled SGPR); the compiler inserts neither wait for an asm statement.
-  asm volatile("s_mov_b32 m0, %3\n\ts_nop 3\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
+  // s_nop 0: the DMA reads M0 no earlier than one wait state after the SALU write, a wait
+  // the compiler inserts only for the LDS-DMAs it emits itself. (Its SGPR operands need five
+  // after a VALU write; check_hazards.py fails the build if the compiler places one closer.)
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
                :
                : "v"(voff), "s"(rs), "s"(__builtin_amdgcn_readfirstlane(soff)), "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");

@@ -242,10 +242,10 @@ __global__ __launch_bounds__(256) void gdn_wy_prep_kernel(WyArgs a) {
 // (buffer_load_dwordx4 ... lds, LDS base through M0). Issued as asm, untracked by the
 // compiler: the loop waits for it with an explicit vmcnt(0) before the barrier.
 __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
-  // s_nop 3: the DMA reads M0 no earlier than one wait state after the SALU write, and an
-  // SGPR operand no earlier than five after a VALU write (a readfirstlane, or the v_readlane
-  // that reloads a spilled SGPR); the compiler inserts neither wait for an asm statement.
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 3\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  // s_nop 0: the DMA reads M0 no earlier than one wait state after the SALU write, a wait
+  // the compiler inserts only for the LDS-DMAs it emits itself. (Its SGPR operands need five
+  // after a VALU write; check_hazards.py fails the build if the compiler places one closer.)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
                : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");

@@ -96,10 +96,10 @@ __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
 template <int I>
 __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
   // lds_addr is wave-uniform; readfirstlane keeps it in a scalar register for M0
-  // s_nop 3: the DMA reads M0 no earlier than one wait state after the SALU write, and an
-  // SGPR operand no earlier than five after a VALU write (a readfirstlane, or the v_readlane
-  // that reloads a spilled SGPR); the compiler inserts neither wait for an asm statement.
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 3\n\tbuffer_load_dwordx4 %0, %1, 0 offen offset:%3 lds"
+  // s_nop 0: the DMA reads M0 no earlier than one wait state after the SALU write, a wait
+  // the compiler inserts only for the LDS-DMAs it emits itself. (Its SGPR operands need five
+  // after a VALU write; check_hazards.py fails the build if the compiler places one closer.)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen offset:%3 lds"
                :
                : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "i"(1024 * I)
                : "memory", "m0");
