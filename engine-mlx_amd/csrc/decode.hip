@@ -1491,7 +1491,9 @@ int32_t launch_decode(hipStream_t s, const void* q, const ema_kvcache_desc& c, c
   int32_t rc = check_hip(hipGetLastError(), "ema_decode_attention launch");
   if (rc || a.inline_merge || (plan.workers == 1 && !a.adv)) return rc;
   const int64_t threads = (int64_t)plan.segments * G * kD;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
+  // 64-thread workgroups: the same threads over more CUs (8 x 32k rows: 0.2-0.3 us faster
+  // per call than 256-thread workgroups; the batch-32 step is unchanged)
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((threads + 63) / 64)), dim3(64), 0, s, a);
   return check_hip(hipGetLastError(), "ema_decode_attention merge launch");
 }
 
